@@ -1,0 +1,447 @@
+"""ctypes binding of libdsd_hip.so (the C ABI in include/dsd_hip.h).
+
+Python-side plumbing for tests and bench.py: it forwards every call to the
+HIP library and raises if the library is missing or the call fails -- there
+is no Python or CPU implementation of the decode step here.  Exceptions
+mirror the reference's C++ exception types (include/dsd/cuda_utils.h:43-53,
+src/page_pool.cpp:104-120): InvalidArgument ~ std::invalid_argument,
+OutOfRange ~ std::out_of_range, RuntimeFailure ~ std::runtime_error.
+
+Also provides the synthetic-input helpers bench.py and the tests share
+(reference draw order for context lengths, src/synthetic_data.cpp:29-41).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+
+import numpy as np
+
+PACKAGE_DIR = pathlib.Path(__file__).resolve().parent
+BUILD_DIR = PACKAGE_DIR / "build"
+LIB_PATH = BUILD_DIR / "libdsd_hip.so"
+
+OUTPUT_NONE, OUTPUT_OUTPUTS, OUTPUT_DEBUG = 0, 1, 2
+TIMING_NONE, TIMING_EVENTS = 0, 1
+
+
+class DsdError(Exception):
+    """A non-zero status from libdsd_hip.so."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+class InvalidArgument(DsdError, ValueError):
+    pass
+
+
+class OutOfRange(DsdError, IndexError):
+    pass
+
+
+class RuntimeFailure(DsdError, RuntimeError):
+    pass
+
+
+class HipFailure(RuntimeFailure):
+    pass
+
+
+_ERRORS = {1: InvalidArgument, 2: OutOfRange, 3: RuntimeFailure, 4: HipFailure}
+
+_c_int_p = ctypes.POINTER(ctypes.c_int)
+_c_float_p = ctypes.POINTER(ctypes.c_float)
+_c_i64_p = ctypes.POINTER(ctypes.c_int64)
+_c_u8_p = ctypes.POINTER(ctypes.c_uint8)
+_c_double_p = ctypes.POINTER(ctypes.c_double)
+
+
+class TransferStats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in (
+        "h2d_bytes", "d2h_bytes", "h2d_calls", "d2h_calls",
+        "h2d_large_calls", "d2h_large_calls")]
+
+    def as_dict(self):
+        return {n: int(getattr(self, n)) for n, _ in self._fields_}
+
+
+class StepTimings(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_double) for n in (
+        "score_ms", "topk_ms", "attention_ms", "kernel_ms",
+        "h2d_ms", "d2h_ms", "launch_ms", "sync_ms")]
+
+    def as_dict(self):
+        return {n: float(getattr(self, n)) for n, _ in self._fields_}
+
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "dsd_last_error": (ctypes.c_char_p, []),
+    "dsd_gpu_available": (ctypes.c_int, []),
+    "dsd_device_synchronize": (ctypes.c_int, []),
+    "dsd_pool_create": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_void_p)]),
+    "dsd_pool_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "dsd_pool_reset": (ctypes.c_int, [ctypes.c_void_p]),
+    "dsd_pool_upload_pages": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p, _c_int_p,
+                                             _c_i64_p, _c_float_p, _c_float_p, _c_float_p]),
+    "dsd_pool_upload_tokens": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p, _c_int_p,
+                                              _c_int_p, _c_float_p, _c_float_p, _c_float_p]),
+    "dsd_pool_mark_free": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p]),
+    "dsd_pool_download_page": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_float_p,
+                                              _c_float_p, _c_int_p]),
+    "dsd_pool_download_meta": (ctypes.c_int, [ctypes.c_void_p, _c_int_p, _c_u8_p]),
+    "dsd_pool_download_summaries": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p,
+                                                   _c_float_p]),
+    "dsd_pool_transfer_stats": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(TransferStats)]),
+    "dsd_pool_reset_transfer_stats": (ctypes.c_int, [ctypes.c_void_p]),
+    "dsd_pool_capacity": (ctypes.c_int, [ctypes.c_void_p]),
+    "dsd_sparse_create": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_int] * 4
+                          + [ctypes.POINTER(ctypes.c_void_p)]),
+    "dsd_sparse_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "dsd_sparse_run_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_float_p, _c_int_p,
+                                            _c_int_p, ctypes.c_int, ctypes.c_int, _c_float_p,
+                                            _c_float_p, _c_int_p, _c_int_p,
+                                            ctypes.POINTER(StepTimings)]),
+    "dsd_sparse_run_batch_device": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_int] * 3
+                                    + [ctypes.c_void_p] * 8),
+    "dsd_sparse_replay_stage": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]),
+    "dsd_sparse_stream": (ctypes.c_void_p, [ctypes.c_void_p]),
+    "dsd_dense_run_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_float_p, _c_int_p,
+                                           _c_int_p, _c_float_p, _c_double_p]),
+    "dsd_dense_run_batch_device": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int] + [ctypes.c_void_p] * 5),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+_LIB = None
+
+
+def library_path() -> pathlib.Path:
+    return pathlib.Path(os.environ.get("DSD_HIP_LIB", str(LIB_PATH)))
+
+
+def load_library() -> ctypes.CDLL:
+    """Load libdsd_hip.so; raises FileNotFoundError when it was not built."""
+    global _LIB
+    if _LIB is None:
+        path = library_path()
+        if not path.exists():
+            raise FileNotFoundError(
+                f"{path} is missing: build it with __graft_entry__.build() "
+                f"(make -C 15-618_dynamic_sparse_decode_amd/csrc)")
+        lib = ctypes.CDLL(str(path))
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _LIB = lib
+    return _LIB
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        message = load_library().dsd_last_error().decode()
+        raise _ERRORS.get(status, DsdError)(status, message)
+
+
+def gpu_available() -> bool:
+    return bool(load_library().dsd_gpu_available())
+
+
+def synchronize() -> None:
+    _check(load_library().dsd_device_synchronize())
+
+
+def _ptr(array, ctype):
+    if array is None:
+        return None
+    return array.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _i32(a):
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+class DevicePagePool:
+    """HBM page pool (reference DevicePagePool, include/dsd/device_page_pool.h:17)."""
+
+    def __init__(self, num_heads: int, head_dim: int, page_size: int, capacity_pages: int):
+        self._lib = load_library()
+        handle = ctypes.c_void_p()
+        _check(self._lib.dsd_pool_create(num_heads, head_dim, page_size, capacity_pages,
+                                         ctypes.byref(handle)))
+        self.handle = handle
+        self.num_heads, self.head_dim, self.page_size = num_heads, head_dim, page_size
+        self.capacity = capacity_pages
+        self.elements = num_heads * head_dim
+
+    def close(self) -> None:
+        if self.handle:
+            _check(self._lib.dsd_pool_destroy(self.handle))
+            self.handle = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self) -> None:
+        _check(self._lib.dsd_pool_reset(self.handle))
+
+    def upload_pages(self, page_ids, token_counts, src_offsets, keys, values, summaries=None):
+        ids, counts = _i32(page_ids), _i32(token_counts)
+        offs = np.ascontiguousarray(src_offsets, dtype=np.int64)
+        k, v = _f32(keys), _f32(values)
+        s = None if summaries is None else _f32(summaries)
+        _check(self._lib.dsd_pool_upload_pages(
+            self.handle, len(ids), _ptr(ids, ctypes.c_int), _ptr(counts, ctypes.c_int),
+            _ptr(offs, ctypes.c_int64), _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float),
+            _ptr(s, ctypes.c_float)))
+
+    def upload_tokens(self, page_ids, token_offsets, page_token_counts, keys, values,
+                      summaries=None):
+        ids, offs, counts = _i32(page_ids), _i32(token_offsets), _i32(page_token_counts)
+        k, v = _f32(keys), _f32(values)
+        s = None if summaries is None else _f32(summaries)
+        _check(self._lib.dsd_pool_upload_tokens(
+            self.handle, len(ids), _ptr(ids, ctypes.c_int), _ptr(offs, ctypes.c_int),
+            _ptr(counts, ctypes.c_int), _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float),
+            _ptr(s, ctypes.c_float)))
+
+    def mark_free(self, page_ids) -> None:
+        ids = _i32(page_ids)
+        _check(self._lib.dsd_pool_mark_free(self.handle, len(ids), _ptr(ids, ctypes.c_int)))
+
+    def download_page(self, page_id: int):
+        k = np.empty(self.page_size * self.elements, np.float32)
+        v = np.empty_like(k)
+        count = ctypes.c_int()
+        _check(self._lib.dsd_pool_download_page(self.handle, int(page_id),
+                                                _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float),
+                                                ctypes.byref(count)))
+        n = count.value * self.elements
+        return k[:n].copy(), v[:n].copy()
+
+    def download_meta(self):
+        counts = np.empty(self.capacity, np.int32)
+        live = np.empty(self.capacity, np.uint8)
+        _check(self._lib.dsd_pool_download_meta(self.handle, _ptr(counts, ctypes.c_int),
+                                                _ptr(live, ctypes.c_uint8)))
+        return counts, live
+
+    def download_summaries(self, page_ids):
+        ids = _i32(page_ids)
+        out = np.empty((len(ids), self.elements), np.float32)
+        _check(self._lib.dsd_pool_download_summaries(self.handle, len(ids),
+                                                     _ptr(ids, ctypes.c_int),
+                                                     _ptr(out, ctypes.c_float)))
+        return out
+
+    def transfer_stats(self) -> dict:
+        st = TransferStats()
+        _check(self._lib.dsd_pool_transfer_stats(self.handle, ctypes.byref(st)))
+        return st.as_dict()
+
+    def reset_transfer_stats(self) -> None:
+        _check(self._lib.dsd_pool_reset_transfer_stats(self.handle))
+
+
+class SparseContext:
+    """One sparse decode step per call (reference SparseCudaContext,
+    include/dsd/cuda_sparse_attention.h:50-137)."""
+
+    def __init__(self, pool: DevicePagePool, top_k: int, max_batch: int,
+                 max_total_candidates: int, max_total_selected: int):
+        self._lib = load_library()
+        self.pool = pool
+        self.top_k = top_k
+        handle = ctypes.c_void_p()
+        _check(self._lib.dsd_sparse_create(pool.handle, top_k, max_batch, max_total_candidates,
+                                           max_total_selected, ctypes.byref(handle)))
+        self.handle = handle
+
+    def close(self) -> None:
+        if self.handle:
+            _check(self._lib.dsd_sparse_destroy(self.handle))
+            self.handle = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self) -> int:
+        return self._lib.dsd_sparse_stream(self.handle) or 0
+
+    def run_batch(self, queries, cand_offsets, cand_ids, output_mode=OUTPUT_DEBUG,
+                  timing_mode=TIMING_EVENTS):
+        """Host-buffer step.  Returns a dict with outputs [B][E], and in debug
+        mode scores [P] and selected (a list of per-request id arrays)."""
+        q = _f32(queries).reshape(-1)
+        offs = _i32(cand_offsets)
+        ids = _i32(cand_ids) if len(cand_ids) else np.zeros(1, np.int32)
+        batch = len(offs) - 1
+        total = int(offs[-1]) if batch > 0 else 0
+        E = self.pool.elements
+        out = np.zeros((max(batch, 0), E), np.float32)
+        scores = np.zeros(max(total, 1), np.float32)
+        sel = np.zeros(max(1, batch * max(1, self.top_k)), np.int32)
+        counts = np.zeros(max(batch, 1), np.int32)
+        t = StepTimings()
+        debug = output_mode == OUTPUT_DEBUG
+        _check(self._lib.dsd_sparse_run_batch(
+            self.handle, batch, _ptr(q, ctypes.c_float), _ptr(offs, ctypes.c_int),
+            _ptr(ids, ctypes.c_int), output_mode, timing_mode,
+            _ptr(out, ctypes.c_float) if output_mode != OUTPUT_NONE else None,
+            _ptr(scores, ctypes.c_float) if debug else None,
+            _ptr(sel, ctypes.c_int) if debug else None,
+            _ptr(counts, ctypes.c_int) if debug else None, ctypes.byref(t)))
+        result = {"outputs": out, "timings": t.as_dict()}
+        if debug:
+            result["scores"] = scores[:total].copy()
+            selected, w = [], 0
+            for r in range(batch):
+                c = int(counts[r])
+                selected.append(sel[w:w + c].copy())
+                w += c
+            result["selected"] = selected
+        return result
+
+    def run_batch_device(self, batch, total_candidates, max_candidates, d_queries,
+                         d_cand_offsets, d_cand_ids, d_outputs, d_scores=0, d_selected=0,
+                         d_counts=0, stream=0) -> None:
+        """Device-resident step: integer device addresses, async on `stream`."""
+        _check(self._lib.dsd_sparse_run_batch_device(
+            self.handle, batch, total_candidates, max_candidates, d_queries, d_cand_offsets,
+            d_cand_ids, d_outputs, d_scores or None, d_selected or None, d_counts or None,
+            stream or None))
+
+    def replay_stage(self, stage: int, stream=0) -> None:
+        _check(self._lib.dsd_sparse_replay_stage(self.handle, stage, stream or None))
+
+
+def dense_run_batch(pool: DevicePagePool, queries, cand_offsets, cand_ids):
+    """Dense attention over every candidate page (reference DenseCudaContext)."""
+    lib = load_library()
+    q = _f32(queries).reshape(-1)
+    offs = _i32(cand_offsets)
+    ids = _i32(cand_ids) if len(cand_ids) else np.zeros(1, np.int32)
+    batch = len(offs) - 1
+    out = np.zeros((batch, pool.elements), np.float32)
+    ms = ctypes.c_double()
+    _check(lib.dsd_dense_run_batch(pool.handle, batch, _ptr(q, ctypes.c_float),
+                                   _ptr(offs, ctypes.c_int), _ptr(ids, ctypes.c_int),
+                                   _ptr(out, ctypes.c_float), ctypes.byref(ms)))
+    return out, ms.value
+
+
+def dense_run_batch_device(pool: DevicePagePool, batch, d_queries, d_cand_offsets, d_cand_ids,
+                           d_outputs, stream=0) -> None:
+    _check(load_library().dsd_dense_run_batch_device(pool.handle, batch, d_queries,
+                                                     d_cand_offsets, d_cand_ids, d_outputs,
+                                                     stream or None))
+
+
+# ---------------------------------------------------------------------------
+# Synthetic inputs
+# ---------------------------------------------------------------------------
+def reference_context_lengths(batch: int, lo: int, hi: int, seed: int):
+    """The B context lengths in the reference's draw order: std::mt19937(seed)
+    then std::uniform_int_distribution<int>(lo, hi) (src/synthetic_data.cpp:29-41).
+    libstdc++ (GCC 11+) maps a 32-bit engine output to [lo, hi] with Lemire's
+    multiply-and-reject method (Lemire 2019, "Fast Random Integer Generation in
+    an Interval"); numpy's MT19937 with legacy seeding is the same engine."""
+    bg = np.random.MT19937()
+    bg._legacy_seeding(seed)
+    span = hi - lo + 1
+    out = []
+    for _ in range(batch):
+        prod = int(bg.random_raw()) * span
+        low = prod & 0xFFFFFFFF
+        if low < span:
+            threshold = ((1 << 32) - span) % span
+            while low < threshold:
+                prod = int(bg.random_raw()) * span
+                low = prod & 0xFFFFFFFF
+        out.append(lo + (prod >> 32))
+    return out
+
+
+class SyntheticBatch:
+    """A ragged batch laid out like the reference's BuildSyntheticBatch
+    (src/synthetic_data.cpp:23-68): capacity = total pages, LIFO page ids
+    (the first page allocated is capacity-1, src/page_pool.cpp:36-45), each
+    request's candidates in logical page order.  Values are i.i.d. N(0,1)
+    float32 from numpy's PCG64 stream seeded with `seed` (keys, values, then
+    queries)."""
+
+    def __init__(self, num_heads, head_dim, page_size, context_lengths, seed,
+                 capacity=None, dtype=np.float32):
+        self.num_heads, self.head_dim, self.page_size = num_heads, head_dim, page_size
+        self.elements = E = num_heads * head_dim
+        self.context_lengths = [int(c) for c in context_lengths]
+        pages_per = [(c + page_size - 1) // page_size for c in self.context_lengths]
+        total_pages = sum(pages_per)
+        self.capacity = capacity if capacity is not None else total_pages
+        B = len(self.context_lengths)
+        self.cand_offsets = np.zeros(B + 1, np.int32)
+        self.cand_offsets[1:] = np.cumsum(pages_per)
+        ids = np.arange(total_pages, dtype=np.int32)
+        self.cand_ids = (self.capacity - 1 - ids).astype(np.int32)
+        self.token_counts = np.zeros(self.capacity, np.int32)
+        g = 0
+        for r, c in enumerate(self.context_lengths):
+            for j in range(pages_per[r]):
+                self.token_counts[self.cand_ids[g]] = min(page_size, c - j * page_size)
+                g += 1
+        rng = np.random.default_rng(seed)
+        shape = (self.capacity, page_size, E)
+        self.key_pool = rng.standard_normal(shape, dtype=dtype)
+        self.value_pool = rng.standard_normal(shape, dtype=dtype)
+        self.queries = rng.standard_normal((B, E), dtype=dtype)
+
+    @property
+    def batch(self):
+        return len(self.context_lengths)
+
+    @property
+    def total_candidates(self):
+        return int(self.cand_offsets[-1])
+
+    @property
+    def max_candidates(self):
+        return int(np.max(np.diff(self.cand_offsets))) if self.batch else 0
+
+    def live_page_ids(self):
+        return self.cand_ids.copy()
+
+    def upload(self, pool: DevicePagePool, summaries=None):
+        """Upload every live page; the device computes summaries unless given."""
+        ids = self.live_page_ids()
+        counts = self.token_counts[ids]
+        offs = ids.astype(np.int64) * self.page_size * self.elements
+        pool.upload_pages(ids, counts, offs, self.key_pool.reshape(-1),
+                          self.value_pool.reshape(-1), summaries)

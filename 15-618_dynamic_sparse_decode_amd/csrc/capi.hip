@@ -1,0 +1,922 @@
+// capi.hip -- the extern "C" boundary of libdsd_hip.so (declared in
+// include/dsd_hip.h).  Host-side orchestration only: argument checks with the
+// reference's error semantics, HBM allocation, copies, kernel launches and
+// timing.  All math runs in the kernels of pool_kernels.hip / step_kernels.hip.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "dsd_hip.h"
+#include "dsd_internal.h"
+
+using dsdk::PoolView;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+// Runs f and maps the reference's exception types onto status codes.
+template <typename F>
+int Guard(F&& f) {
+  try {
+    f();
+    return DSD_OK;
+  } catch (const std::invalid_argument& e) {
+    g_last_error = e.what();
+    return DSD_ERR_INVALID_ARGUMENT;
+  } catch (const std::out_of_range& e) {
+    g_last_error = e.what();
+    return DSD_ERR_OUT_OF_RANGE;
+  } catch (const dsdk::HipError& e) {
+    g_last_error = e.what();
+    return DSD_ERR_HIP;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return DSD_ERR_RUNTIME;
+  } catch (...) {
+    g_last_error = "unknown error";
+    return DSD_ERR_RUNTIME;
+  }
+}
+
+void Require(bool ok, const char* message) {
+  if (!ok) throw std::invalid_argument(message);
+}
+
+using Clock = std::chrono::steady_clock;
+double MsSince(Clock::time_point t0) {
+  return std::chrono::duration<double, std::milli>(Clock::now() - t0).count();
+}
+
+// Grow-only device buffer.
+template <typename T>
+struct DeviceBuffer {
+  T* ptr = nullptr;
+  size_t count = 0;
+  DeviceBuffer() = default;
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  ~DeviceBuffer() { Release(); }
+  void Release() {
+    if (ptr != nullptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    count = 0;
+  }
+  void Reserve(size_t n) {
+    if (n <= count) return;
+    Release();
+    DSD_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&ptr), n * sizeof(T)));
+    count = n;
+  }
+};
+
+// Grow-only pinned host buffer (allocated pinned; never registered).
+template <typename T>
+struct PinnedBuffer {
+  T* ptr = nullptr;
+  size_t count = 0;
+  PinnedBuffer() = default;
+  PinnedBuffer(const PinnedBuffer&) = delete;
+  PinnedBuffer& operator=(const PinnedBuffer&) = delete;
+  ~PinnedBuffer() { Release(); }
+  void Release() {
+    if (ptr != nullptr) (void)hipHostFree(ptr);
+    ptr = nullptr;
+    count = 0;
+  }
+  void Reserve(size_t n) {
+    if (n <= count) return;
+    Release();
+    DSD_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&ptr), n * sizeof(T),
+                                hipHostMallocDefault));
+    count = n;
+  }
+};
+
+constexpr uint64_t kLargeCopyBytes = 1ull << 20;  // src/device_page_pool.cpp:13
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Pool
+// ---------------------------------------------------------------------------
+struct dsd_pool {
+  PoolView view;
+  std::vector<int> host_counts;
+  std::vector<uint8_t> host_live;
+  mutable dsd_transfer_stats stats{};
+  hipStream_t stream = nullptr;
+  // staging for metadata / token uploads
+  DeviceBuffer<int> stage_ids, stage_counts, stage_offsets, stage_order, stage_segs;
+  DeviceBuffer<float> stage_rows, stage_keys, stage_values;
+  // dense-path scratch
+  DeviceBuffer<float> dense_q, dense_out;
+  DeviceBuffer<int> dense_offsets, dense_ids;
+  hipEvent_t dense_start = nullptr, dense_stop = nullptr;
+
+  ~dsd_pool() {
+    if (view.keys) (void)hipFree(view.keys);
+    if (view.values) (void)hipFree(view.values);
+    if (view.summaries) (void)hipFree(view.summaries);
+    if (view.token_counts) (void)hipFree(view.token_counts);
+    if (view.live) (void)hipFree(view.live);
+    if (dense_start) (void)hipEventDestroy(dense_start);
+    if (dense_stop) (void)hipEventDestroy(dense_stop);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+
+  void H2D(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return;
+    DSD_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream));
+    stats.h2d_bytes += bytes;
+    ++stats.h2d_calls;
+    if (bytes >= kLargeCopyBytes) ++stats.h2d_large_calls;
+  }
+  void D2H(void* dst, const void* src, size_t bytes) const {
+    if (bytes == 0) return;
+    DSD_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, stream));
+    stats.d2h_bytes += bytes;
+    ++stats.d2h_calls;
+    if (bytes >= kLargeCopyBytes) ++stats.d2h_large_calls;
+  }
+  void Sync() const { DSD_HIP_CHECK(hipStreamSynchronize(stream)); }
+
+  void ValidatePage(int page_id) const {
+    if (page_id < 0 || page_id >= view.capacity) {
+      throw std::out_of_range("invalid page id");
+    }
+  }
+  void ValidateTokenCount(int count) const {
+    if (count <= 0 || count > view.page_size) {
+      throw std::invalid_argument("token_count must be in (0, page_size]");
+    }
+  }
+};
+
+extern "C" {
+
+const char* dsd_last_error(void) { return g_last_error.c_str(); }
+
+int dsd_gpu_available(void) {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return 0;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return 0;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return 0;
+  return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+int dsd_device_synchronize(void) {
+  return Guard([&] { DSD_HIP_CHECK(hipDeviceSynchronize()); });
+}
+
+int dsd_pool_create(int num_heads, int head_dim, int page_size,
+                    int capacity_pages, dsd_pool** out_pool) {
+  return Guard([&] {
+    Require(out_pool != nullptr, "out_pool must be non-null");
+    *out_pool = nullptr;
+    if (capacity_pages < 0) {
+      throw std::invalid_argument("capacity_pages must be non-negative");
+    }
+    Require(num_heads > 0 && head_dim > 0 && page_size > 0,
+            "num_heads, head_dim and page_size must be positive");
+    if (!dsd_gpu_available()) {
+      throw std::runtime_error("no visible gfx950 GPU");
+    }
+    auto pool = std::make_unique<dsd_pool>();
+    PoolView& v = pool->view;
+    v.num_heads = num_heads;
+    v.head_dim = head_dim;
+    v.page_size = page_size;
+    v.elements = num_heads * head_dim;
+    v.capacity = capacity_pages;
+    v.page_elems = static_cast<int64_t>(page_size) * v.elements;
+    DSD_HIP_CHECK(hipStreamCreateWithFlags(&pool->stream, hipStreamNonBlocking));
+    DSD_HIP_CHECK(hipEventCreate(&pool->dense_start));
+    DSD_HIP_CHECK(hipEventCreate(&pool->dense_stop));
+    pool->host_counts.assign(static_cast<size_t>(capacity_pages), 0);
+    pool->host_live.assign(static_cast<size_t>(capacity_pages), 0);
+    if (capacity_pages > 0) {
+      const size_t kv_bytes = static_cast<size_t>(capacity_pages) *
+                              static_cast<size_t>(v.page_elems) * sizeof(float);
+      const size_t sum_bytes = static_cast<size_t>(capacity_pages) *
+                               static_cast<size_t>(v.elements) * sizeof(float);
+      DSD_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&v.keys), kv_bytes));
+      DSD_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&v.values), kv_bytes));
+      DSD_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&v.summaries), sum_bytes));
+      DSD_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&v.token_counts),
+                              sizeof(int) * static_cast<size_t>(capacity_pages)));
+      DSD_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&v.live),
+                              static_cast<size_t>(capacity_pages)));
+      DSD_HIP_CHECK(hipMemsetAsync(v.summaries, 0, sum_bytes, pool->stream));
+      DSD_HIP_CHECK(hipMemsetAsync(v.token_counts, 0,
+                                   sizeof(int) * static_cast<size_t>(capacity_pages),
+                                   pool->stream));
+      DSD_HIP_CHECK(hipMemsetAsync(v.live, 0, static_cast<size_t>(capacity_pages),
+                                   pool->stream));
+      pool->Sync();
+    }
+    *out_pool = pool.release();
+  });
+}
+
+int dsd_pool_destroy(dsd_pool* pool) {
+  return Guard([&] {
+    if (pool != nullptr) {
+      (void)hipStreamSynchronize(pool->stream);
+      delete pool;
+    }
+  });
+}
+
+int dsd_pool_capacity(const dsd_pool* pool) {
+  return pool == nullptr ? 0 : pool->view.capacity;
+}
+
+int dsd_pool_reset(dsd_pool* pool) {
+  return Guard([&] {
+    Require(pool != nullptr, "pool must be non-null");
+    const PoolView& v = pool->view;
+    std::fill(pool->host_counts.begin(), pool->host_counts.end(), 0);
+    std::fill(pool->host_live.begin(), pool->host_live.end(), 0);
+    if (v.capacity > 0) {
+      DSD_HIP_CHECK(hipMemsetAsync(v.summaries, 0,
+                                   sizeof(float) * static_cast<size_t>(v.capacity) *
+                                       static_cast<size_t>(v.elements),
+                                   pool->stream));
+      DSD_HIP_CHECK(hipMemsetAsync(v.token_counts, 0,
+                                   sizeof(int) * static_cast<size_t>(v.capacity),
+                                   pool->stream));
+      DSD_HIP_CHECK(hipMemsetAsync(v.live, 0, static_cast<size_t>(v.capacity),
+                                   pool->stream));
+    }
+    pool->Sync();
+  });
+}
+
+int dsd_pool_upload_pages(dsd_pool* pool, int n, const int* page_ids,
+                          const int* token_counts, const int64_t* src_offsets,
+                          const float* keys, const float* values,
+                          const float* summaries) {
+  return Guard([&] {
+    Require(pool != nullptr, "pool must be non-null");
+    Require(n >= 0, "page count must be non-negative");
+    if (n == 0) return;
+    Require(page_ids != nullptr && token_counts != nullptr && src_offsets != nullptr,
+            "page metadata pointers must be non-null");
+    Require(keys != nullptr && values != nullptr,
+            "host page payload pointers must be non-null");
+    const PoolView& v = pool->view;
+    const int E = v.elements;
+    for (int i = 0; i < n; ++i) {
+      pool->ValidatePage(page_ids[i]);
+      pool->ValidateTokenCount(token_counts[i]);
+      Require(src_offsets[i] >= 0, "source offsets must be non-negative");
+    }
+    // Payload copies: merge runs of full pages that are consecutive both in
+    // the pool and in the source into one copy each.
+    int i = 0;
+    while (i < n) {
+      int run_end = i + 1;
+      if (token_counts[i] == v.page_size) {
+        while (run_end < n && token_counts[run_end] == v.page_size &&
+               page_ids[run_end] == page_ids[run_end - 1] + 1 &&
+               src_offsets[run_end] == src_offsets[run_end - 1] + v.page_elems) {
+          ++run_end;
+        }
+      }
+      const int pages = run_end - i;
+      const size_t elems = pages == 1
+                               ? static_cast<size_t>(token_counts[i]) * E
+                               : static_cast<size_t>(pages) * v.page_elems;
+      const size_t dst = static_cast<size_t>(page_ids[i]) * v.page_elems;
+      pool->H2D(v.keys + dst, keys + src_offsets[i], elems * sizeof(float));
+      pool->H2D(v.values + dst, values + src_offsets[i], elems * sizeof(float));
+      i = run_end;
+    }
+    // Metadata + summaries: one entry per distinct page, the last occurrence
+    // winning (its payload copy was also enqueued last).
+    std::vector<int> last(n, 1);
+    {
+      std::vector<int> idx(n);
+      std::iota(idx.begin(), idx.end(), 0);
+      std::stable_sort(idx.begin(), idx.end(),
+                       [&](int a, int b) { return page_ids[a] < page_ids[b]; });
+      for (int q = 0; q + 1 < n; ++q) {
+        if (page_ids[idx[q]] == page_ids[idx[q + 1]]) last[idx[q]] = 0;
+      }
+    }
+    std::vector<int> ids, counts, rows_src;
+    ids.reserve(n);
+    counts.reserve(n);
+    for (int q = 0; q < n; ++q) {
+      if (!last[q]) continue;
+      ids.push_back(page_ids[q]);
+      counts.push_back(token_counts[q]);
+      rows_src.push_back(q);
+      pool->host_counts[page_ids[q]] = token_counts[q];
+      pool->host_live[page_ids[q]] = 1;
+    }
+    const int m = static_cast<int>(ids.size());
+    pool->stage_ids.Reserve(m);
+    pool->stage_counts.Reserve(m);
+    pool->H2D(pool->stage_ids.ptr, ids.data(), sizeof(int) * m);
+    pool->H2D(pool->stage_counts.ptr, counts.data(), sizeof(int) * m);
+    const float* d_rows = nullptr;
+    if (summaries != nullptr) {
+      std::vector<float> rows(static_cast<size_t>(m) * E);
+      for (int q = 0; q < m; ++q) {
+        std::memcpy(rows.data() + static_cast<size_t>(q) * E,
+                    summaries + static_cast<size_t>(rows_src[q]) * E,
+                    sizeof(float) * E);
+      }
+      pool->stage_rows.Reserve(rows.size());
+      pool->H2D(pool->stage_rows.ptr, rows.data(), sizeof(float) * rows.size());
+      d_rows = pool->stage_rows.ptr;
+    }
+    dsdk::LaunchFinishPageUpload(v, pool->stage_ids.ptr, pool->stage_counts.ptr,
+                                 d_rows, m, pool->stream);
+    pool->Sync();
+  });
+}
+
+int dsd_pool_upload_tokens(dsd_pool* pool, int n, const int* page_ids,
+                           const int* token_offsets,
+                           const int* page_token_counts, const float* keys,
+                           const float* values, const float* summaries) {
+  return Guard([&] {
+    Require(pool != nullptr, "pool must be non-null");
+    Require(n >= 0, "token count must be non-negative");
+    if (n == 0) return;
+    Require(page_ids != nullptr && token_offsets != nullptr &&
+                page_token_counts != nullptr,
+            "token metadata pointers must be non-null");
+    Require(keys != nullptr && values != nullptr,
+            "token payload pointers must be non-null");
+    const PoolView& v = pool->view;
+    const int E = v.elements;
+    for (int i = 0; i < n; ++i) {
+      pool->ValidatePage(page_ids[i]);
+      pool->ValidateTokenCount(page_token_counts[i]);
+      if (token_offsets[i] < 0 || token_offsets[i] >= page_token_counts[i]) {
+        throw std::out_of_range("token_offset is outside the valid page prefix");
+      }
+    }
+    // Segments: tokens sorted by (page, offset), one segment per page.
+    std::vector<int> order(n);
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+      if (page_ids[a] != page_ids[b]) return page_ids[a] < page_ids[b];
+      return token_offsets[a] < token_offsets[b];
+    });
+    std::vector<int> segs;
+    segs.push_back(0);
+    for (int q = 1; q < n; ++q) {
+      if (page_ids[order[q]] != page_ids[order[q - 1]]) segs.push_back(q);
+    }
+    segs.push_back(n);
+    const int nseg = static_cast<int>(segs.size()) - 1;
+    if (summaries == nullptr) {
+      // Device running mean: each page's tokens must extend its current prefix.
+      for (int s = 0; s < nseg; ++s) {
+        const int page = page_ids[order[segs[s]]];
+        int expect = token_offsets[order[segs[s]]] == 0 ? 0 : pool->host_counts[page];
+        for (int q = segs[s]; q < segs[s + 1]; ++q) {
+          if (token_offsets[order[q]] != expect) {
+            throw std::invalid_argument(
+                "device summary update needs tokens that extend the page prefix");
+          }
+          ++expect;
+        }
+      }
+    }
+    for (int q = 0; q < n; ++q) {
+      pool->host_counts[page_ids[q]] = page_token_counts[q];
+      pool->host_live[page_ids[q]] = 1;
+    }
+    const size_t row_elems = static_cast<size_t>(n) * E;
+    pool->stage_keys.Reserve(row_elems);
+    pool->stage_values.Reserve(row_elems);
+    pool->stage_ids.Reserve(n);
+    pool->stage_offsets.Reserve(n);
+    pool->stage_counts.Reserve(n);
+    pool->stage_order.Reserve(n);
+    pool->stage_segs.Reserve(nseg + 1);
+    pool->H2D(pool->stage_keys.ptr, keys, sizeof(float) * row_elems);
+    pool->H2D(pool->stage_values.ptr, values, sizeof(float) * row_elems);
+    pool->H2D(pool->stage_ids.ptr, page_ids, sizeof(int) * n);
+    pool->H2D(pool->stage_offsets.ptr, token_offsets, sizeof(int) * n);
+    pool->H2D(pool->stage_counts.ptr, page_token_counts, sizeof(int) * n);
+    pool->H2D(pool->stage_order.ptr, order.data(), sizeof(int) * n);
+    pool->H2D(pool->stage_segs.ptr, segs.data(), sizeof(int) * (nseg + 1));
+    const float* d_rows = nullptr;
+    if (summaries != nullptr) {
+      pool->stage_rows.Reserve(row_elems);
+      pool->H2D(pool->stage_rows.ptr, summaries, sizeof(float) * row_elems);
+      d_rows = pool->stage_rows.ptr;
+    }
+    dsdk::LaunchAppendTokens(v, pool->stage_segs.ptr, pool->stage_order.ptr,
+                             pool->stage_ids.ptr, pool->stage_offsets.ptr,
+                             pool->stage_counts.ptr, pool->stage_keys.ptr,
+                             pool->stage_values.ptr, d_rows, nseg, pool->stream);
+    pool->Sync();
+  });
+}
+
+int dsd_pool_mark_free(dsd_pool* pool, int n, const int* page_ids) {
+  return Guard([&] {
+    Require(pool != nullptr, "pool must be non-null");
+    Require(n >= 0, "page count must be non-negative");
+    if (n == 0) return;
+    Require(page_ids != nullptr, "page ids must be non-null");
+    std::vector<int> ids(page_ids, page_ids + n);
+    std::sort(ids.begin(), ids.end());
+    ids.erase(std::unique(ids.begin(), ids.end()), ids.end());
+    for (int id : ids) pool->ValidatePage(id);
+    for (int id : ids) {
+      pool->host_counts[id] = 0;
+      pool->host_live[id] = 0;
+    }
+    const int m = static_cast<int>(ids.size());
+    pool->stage_ids.Reserve(m);
+    pool->H2D(pool->stage_ids.ptr, ids.data(), sizeof(int) * m);
+    dsdk::LaunchMarkFree(pool->view, pool->stage_ids.ptr, m, pool->stream);
+    pool->Sync();
+  });
+}
+
+int dsd_pool_download_page(const dsd_pool* pool, int page_id, float* keys,
+                           float* values, int* token_count) {
+  return Guard([&] {
+    Require(pool != nullptr, "pool must be non-null");
+    Require(keys != nullptr && values != nullptr, "download outputs must be non-null");
+    pool->ValidatePage(page_id);
+    const int count = pool->host_counts[page_id];
+    if (pool->host_live[page_id] == 0 || count == 0) {
+      throw std::runtime_error("cannot download a free device page");
+    }
+    const PoolView& v = pool->view;
+    const size_t elems = static_cast<size_t>(count) * v.elements;
+    const size_t off = static_cast<size_t>(page_id) * v.page_elems;
+    pool->D2H(keys, v.keys + off, elems * sizeof(float));
+    pool->D2H(values, v.values + off, elems * sizeof(float));
+    pool->Sync();
+    if (token_count != nullptr) *token_count = count;
+  });
+}
+
+int dsd_pool_download_meta(const dsd_pool* pool, int* token_counts,
+                           uint8_t* live) {
+  return Guard([&] {
+    Require(pool != nullptr, "pool must be non-null");
+    Require(token_counts != nullptr && live != nullptr,
+            "metadata outputs must be non-null");
+    const PoolView& v = pool->view;
+    pool->D2H(token_counts, v.token_counts, sizeof(int) * static_cast<size_t>(v.capacity));
+    pool->D2H(live, v.live, static_cast<size_t>(v.capacity));
+    pool->Sync();
+  });
+}
+
+int dsd_pool_download_summaries(const dsd_pool* pool, int n,
+                                const int* page_ids, float* out) {
+  return Guard([&] {
+    Require(pool != nullptr, "pool must be non-null");
+    Require(n >= 0, "page count must be non-negative");
+    if (n == 0) return;
+    Require(page_ids != nullptr && out != nullptr, "pointers must be non-null");
+    const PoolView& v = pool->view;
+    for (int i = 0; i < n; ++i) pool->ValidatePage(page_ids[i]);
+    for (int i = 0; i < n; ++i) {
+      pool->D2H(out + static_cast<size_t>(i) * v.elements,
+                v.summaries + static_cast<size_t>(page_ids[i]) * v.elements,
+                sizeof(float) * v.elements);
+    }
+    pool->Sync();
+  });
+}
+
+int dsd_pool_transfer_stats(const dsd_pool* pool, dsd_transfer_stats* out) {
+  return Guard([&] {
+    Require(pool != nullptr && out != nullptr, "pointers must be non-null");
+    *out = pool->stats;
+  });
+}
+
+int dsd_pool_reset_transfer_stats(dsd_pool* pool) {
+  return Guard([&] {
+    Require(pool != nullptr, "pool must be non-null");
+    pool->stats = dsd_transfer_stats{};
+  });
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Sparse decode context
+// ---------------------------------------------------------------------------
+struct dsd_sparse_ctx {
+  dsd_pool* pool = nullptr;
+  int top_k = 0;
+  int max_batch = 0;
+  int max_cand = 0;
+  int max_sel = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev[6] = {};
+  DeviceBuffer<float> d_queries, d_scores, d_outputs;
+  DeviceBuffer<int> d_offsets, d_ids, d_selected, d_counts;
+  PinnedBuffer<float> h_queries, h_scores, h_outputs;
+  PinnedBuffer<int> h_offsets, h_ids, h_selected, h_counts;
+
+  struct Launch {
+    bool valid = false;
+    int batch = 0, total = 0, max_n = 0;
+    const float* queries = nullptr;
+    const int* offsets = nullptr;
+    const int* ids = nullptr;
+    float* outputs = nullptr;
+    float* scores = nullptr;
+    int* selected = nullptr;
+    int* counts = nullptr;
+  } last;
+
+  ~dsd_sparse_ctx() {
+    for (hipEvent_t& e : ev) {
+      if (e) (void)hipEventDestroy(e);
+    }
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+
+  float Scale() const {
+    return 1.0f / std::sqrt(static_cast<float>(pool->view.head_dim));
+  }
+
+  void Enqueue(const Launch& L, hipStream_t s, bool timing) {
+    const PoolView& v = pool->view;
+    if (timing) DSD_HIP_CHECK(hipEventRecord(ev[0], s));
+    if (L.total > 0) {
+      dsdk::LaunchScoreExact(v, L.queries, L.offsets, L.ids, L.batch, L.max_n,
+                             Scale(), L.scores, s);
+    }
+    if (timing) DSD_HIP_CHECK(hipEventRecord(ev[1], s));
+    EnqueueSelect(L, s);
+    if (timing) DSD_HIP_CHECK(hipEventRecord(ev[2], s));
+    EnqueueAttention(L, s);
+    if (timing) DSD_HIP_CHECK(hipEventRecord(ev[3], s));
+  }
+  void EnqueueSelect(const Launch& L, hipStream_t s) {
+    dsdk::LaunchSelectTopK(L.scores, L.offsets, L.ids, L.batch, L.max_n, top_k,
+                           L.selected, L.counts, s);
+  }
+  void EnqueueAttention(const Launch& L, hipStream_t s) {
+    dsdk::AttentionArgs a;
+    a.queries = L.queries;
+    a.list_ids = L.selected;
+    a.list_counts = L.counts;
+    a.list_stride = top_k > 0 ? top_k : 1;
+    a.batch = L.batch;
+    a.scale = Scale();
+    a.outputs = L.outputs;
+    dsdk::LaunchAttention(pool->view, a, s);
+  }
+};
+
+extern "C" {
+
+int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
+                      int max_total_candidates, int max_total_selected,
+                      dsd_sparse_ctx** out_ctx) {
+  return Guard([&] {
+    Require(out_ctx != nullptr, "out_ctx must be non-null");
+    *out_ctx = nullptr;
+    Require(pool != nullptr, "pool must be non-null");
+    if (pool->view.head_dim <= 0 || pool->view.head_dim > 128) {
+      throw std::invalid_argument("sparse decode supports head_dim in (0, 128]");
+    }
+    if (max_batch < 0 || max_total_candidates < 0 || max_total_selected < 0) {
+      throw std::invalid_argument("sparse context capacities must be non-negative");
+    }
+    Require(top_k >= 0, "top_k must be non-negative");
+    auto ctx = std::make_unique<dsd_sparse_ctx>();
+    ctx->pool = pool;
+    ctx->top_k = top_k;
+    ctx->max_batch = max_batch;
+    ctx->max_cand = max_total_candidates;
+    ctx->max_sel = max_total_selected;
+    DSD_HIP_CHECK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+    for (hipEvent_t& e : ctx->ev) DSD_HIP_CHECK(hipEventCreate(&e));
+    const size_t E = static_cast<size_t>(pool->view.elements);
+    const size_t B = static_cast<size_t>(std::max(1, max_batch));
+    const size_t P = static_cast<size_t>(std::max(1, max_total_candidates));
+    const size_t K = static_cast<size_t>(std::max(1, top_k));
+    ctx->d_queries.Reserve(B * E);
+    ctx->d_outputs.Reserve(B * E);
+    ctx->d_scores.Reserve(P);
+    ctx->d_offsets.Reserve(B + 1);
+    ctx->d_ids.Reserve(P);
+    ctx->d_selected.Reserve(B * K);
+    ctx->d_counts.Reserve(B);
+    ctx->h_queries.Reserve(B * E);
+    ctx->h_outputs.Reserve(B * E);
+    ctx->h_scores.Reserve(P);
+    ctx->h_offsets.Reserve(B + 1);
+    ctx->h_ids.Reserve(P);
+    ctx->h_selected.Reserve(B * K);
+    ctx->h_counts.Reserve(B);
+    *out_ctx = ctx.release();
+  });
+}
+
+int dsd_sparse_destroy(dsd_sparse_ctx* ctx) {
+  return Guard([&] {
+    if (ctx != nullptr) {
+      (void)hipStreamSynchronize(ctx->stream);
+      delete ctx;
+    }
+  });
+}
+
+void* dsd_sparse_stream(dsd_sparse_ctx* ctx) {
+  return ctx == nullptr ? nullptr : reinterpret_cast<void*>(ctx->stream);
+}
+
+int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
+                         const int* cand_offsets, const int* cand_ids,
+                         int output_mode, int timing_mode, float* outputs,
+                         float* scores, int* selected, int* selected_counts,
+                         dsd_step_timings* timings) {
+  return Guard([&] {
+    Require(ctx != nullptr, "context must be non-null");
+    Require(batch >= 0, "batch must be non-negative");
+    Require(output_mode >= DSD_OUTPUT_NONE && output_mode <= DSD_OUTPUT_DEBUG,
+            "unknown output mode");
+    dsd_step_timings t{};
+    if (timings != nullptr) *timings = t;
+    if (batch == 0) return;
+    Require(queries != nullptr && cand_offsets != nullptr, "inputs must be non-null");
+    const bool want_outputs = output_mode != DSD_OUTPUT_NONE;
+    const bool debug = output_mode == DSD_OUTPUT_DEBUG;
+    const bool timing = timing_mode == DSD_TIMING_EVENTS;
+    if (want_outputs) Require(outputs != nullptr, "outputs must be non-null");
+    if (debug) {
+      Require(scores != nullptr && selected != nullptr && selected_counts != nullptr,
+              "debug outputs must be non-null");
+    }
+    const dsd_pool& pool = *ctx->pool;
+    const int E = pool.view.elements;
+
+    // Shape checks (the reference's PackSparseBatchInto + capacity checks,
+    // src/cuda/sparse_batched_attention.cu:24-96,600-608).
+    Require(cand_offsets[0] == 0, "cand_offsets[0] must be 0");
+    int max_n = 0;
+    int total_sel = 0;
+    for (int r = 0; r < batch; ++r) {
+      const int n = cand_offsets[r + 1] - cand_offsets[r];
+      Require(n >= 0, "cand_offsets must be non-decreasing");
+      max_n = std::max(max_n, n);
+      total_sel += std::min(ctx->top_k, n);
+    }
+    const int total = cand_offsets[batch];
+    if (batch > ctx->max_batch) {
+      throw std::invalid_argument("request batch exceeds sparse context capacity");
+    }
+    if (total > ctx->max_cand) {
+      throw std::invalid_argument("candidate page count exceeds sparse context capacity");
+    }
+    if (total_sel > ctx->max_sel) {
+      throw std::invalid_argument("selected page count exceeds sparse context capacity");
+    }
+    if (total > 0) Require(cand_ids != nullptr, "cand_ids must be non-null");
+    for (int c = 0; c < total; ++c) ctx->pool->ValidatePage(cand_ids[c]);
+
+    // Host -> device through pinned staging.
+    auto t0 = Clock::now();
+    const size_t qn = static_cast<size_t>(batch) * E;
+    std::memcpy(ctx->h_queries.ptr, queries, sizeof(float) * qn);
+    std::memcpy(ctx->h_offsets.ptr, cand_offsets, sizeof(int) * (batch + 1));
+    if (total > 0) std::memcpy(ctx->h_ids.ptr, cand_ids, sizeof(int) * total);
+    DSD_HIP_CHECK(hipMemcpyAsync(ctx->d_queries.ptr, ctx->h_queries.ptr,
+                                 sizeof(float) * qn, hipMemcpyHostToDevice, ctx->stream));
+    DSD_HIP_CHECK(hipMemcpyAsync(ctx->d_offsets.ptr, ctx->h_offsets.ptr,
+                                 sizeof(int) * (batch + 1), hipMemcpyHostToDevice,
+                                 ctx->stream));
+    if (total > 0) {
+      DSD_HIP_CHECK(hipMemcpyAsync(ctx->d_ids.ptr, ctx->h_ids.ptr, sizeof(int) * total,
+                                   hipMemcpyHostToDevice, ctx->stream));
+    }
+    t.h2d_ms = MsSince(t0);
+
+    dsd_sparse_ctx::Launch L;
+    L.valid = true;
+    L.batch = batch;
+    L.total = total;
+    L.max_n = max_n;
+    L.queries = ctx->d_queries.ptr;
+    L.offsets = ctx->d_offsets.ptr;
+    L.ids = ctx->d_ids.ptr;
+    L.outputs = ctx->d_outputs.ptr;
+    L.scores = ctx->d_scores.ptr;
+    L.selected = ctx->d_selected.ptr;
+    L.counts = ctx->d_counts.ptr;
+    t0 = Clock::now();
+    ctx->Enqueue(L, ctx->stream, timing);
+    ctx->last = L;
+    t.launch_ms = MsSince(t0);
+
+    if (want_outputs) {
+      t0 = Clock::now();
+      DSD_HIP_CHECK(hipMemcpyAsync(ctx->h_outputs.ptr, ctx->d_outputs.ptr,
+                                   sizeof(float) * qn, hipMemcpyDeviceToHost, ctx->stream));
+      if (debug) {
+        if (total > 0) {
+          DSD_HIP_CHECK(hipMemcpyAsync(ctx->h_scores.ptr, ctx->d_scores.ptr,
+                                       sizeof(float) * total, hipMemcpyDeviceToHost,
+                                       ctx->stream));
+        }
+        const size_t kk = static_cast<size_t>(std::max(1, ctx->top_k));
+        DSD_HIP_CHECK(hipMemcpyAsync(ctx->h_selected.ptr, ctx->d_selected.ptr,
+                                     sizeof(int) * kk * batch, hipMemcpyDeviceToHost,
+                                     ctx->stream));
+        DSD_HIP_CHECK(hipMemcpyAsync(ctx->h_counts.ptr, ctx->d_counts.ptr,
+                                     sizeof(int) * batch, hipMemcpyDeviceToHost,
+                                     ctx->stream));
+      }
+      t.d2h_ms = MsSince(t0);
+    }
+    t0 = Clock::now();
+    DSD_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    t.sync_ms = MsSince(t0);
+    if (timing) {
+      float a = 0.f, b = 0.f, c = 0.f;
+      DSD_HIP_CHECK(hipEventElapsedTime(&a, ctx->ev[0], ctx->ev[1]));
+      DSD_HIP_CHECK(hipEventElapsedTime(&b, ctx->ev[1], ctx->ev[2]));
+      DSD_HIP_CHECK(hipEventElapsedTime(&c, ctx->ev[2], ctx->ev[3]));
+      t.score_ms = a;
+      t.topk_ms = b;
+      t.attention_ms = c;
+      t.kernel_ms = static_cast<double>(a) + b + c;
+    }
+    if (want_outputs) {
+      std::memcpy(outputs, ctx->h_outputs.ptr, sizeof(float) * qn);
+      if (debug) {
+        if (total > 0) std::memcpy(scores, ctx->h_scores.ptr, sizeof(float) * total);
+        int w = 0;
+        const int kk = std::max(1, ctx->top_k);
+        for (int r = 0; r < batch; ++r) {
+          const int cnt = ctx->h_counts.ptr[r];
+          selected_counts[r] = cnt;
+          for (int q = 0; q < cnt; ++q) selected[w++] = ctx->h_selected.ptr[r * kk + q];
+        }
+      }
+    }
+    if (timings != nullptr) *timings = t;
+  });
+}
+
+int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
+                                int total_candidates, int max_candidates,
+                                const float* d_queries,
+                                const int* d_cand_offsets,
+                                const int* d_cand_ids, float* d_outputs,
+                                float* d_scores, int* d_selected,
+                                int* d_selected_counts, void* stream) {
+  return Guard([&] {
+    Require(ctx != nullptr, "context must be non-null");
+    Require(batch >= 0 && total_candidates >= 0 && max_candidates >= 0,
+            "sizes must be non-negative");
+    if (batch == 0) return;
+    if (batch > ctx->max_batch) {
+      throw std::invalid_argument("request batch exceeds sparse context capacity");
+    }
+    if (total_candidates > ctx->max_cand && d_scores == nullptr) {
+      throw std::invalid_argument("candidate page count exceeds sparse context capacity");
+    }
+    Require(d_queries != nullptr && d_cand_offsets != nullptr && d_outputs != nullptr,
+            "device inputs must be non-null");
+    if (total_candidates > 0) Require(d_cand_ids != nullptr, "cand_ids must be non-null");
+    dsd_sparse_ctx::Launch L;
+    L.valid = true;
+    L.batch = batch;
+    L.total = total_candidates;
+    L.max_n = max_candidates;
+    L.queries = d_queries;
+    L.offsets = d_cand_offsets;
+    L.ids = d_cand_ids;
+    L.outputs = d_outputs;
+    L.scores = d_scores != nullptr ? d_scores : ctx->d_scores.ptr;
+    L.selected = d_selected != nullptr ? d_selected : ctx->d_selected.ptr;
+    L.counts = d_selected_counts != nullptr ? d_selected_counts : ctx->d_counts.ptr;
+    hipStream_t s = stream != nullptr ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
+    ctx->Enqueue(L, s, false);
+    ctx->last = L;
+  });
+}
+
+int dsd_sparse_replay_stage(dsd_sparse_ctx* ctx, int stage, void* stream) {
+  return Guard([&] {
+    Require(ctx != nullptr, "context must be non-null");
+    Require(ctx->last.valid, "no previous step to replay");
+    hipStream_t s = stream != nullptr ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
+    const auto& L = ctx->last;
+    switch (stage) {
+      case 0:
+        if (L.total > 0) {
+          dsdk::LaunchScoreExact(ctx->pool->view, L.queries, L.offsets, L.ids, L.batch,
+                                 L.max_n, ctx->Scale(), L.scores, s);
+        }
+        break;
+      case 1: ctx->EnqueueSelect(L, s); break;
+      case 2: ctx->EnqueueAttention(L, s); break;
+      default: throw std::invalid_argument("stage must be 0, 1 or 2");
+    }
+  });
+}
+
+// ---------------------------------------------------------------------------
+// Dense decode (DenseCudaContext::RunBatch, src/cuda/kernels.cu:197-292).
+// ---------------------------------------------------------------------------
+int dsd_dense_run_batch(dsd_pool* pool, int batch, const float* queries,
+                        const int* cand_offsets, const int* cand_ids,
+                        float* outputs, double* kernel_ms) {
+  return Guard([&] {
+    Require(pool != nullptr, "pool must be non-null");
+    Require(batch >= 0, "batch must be non-negative");
+    if (kernel_ms != nullptr) *kernel_ms = 0.0;
+    if (batch == 0) return;
+    Require(queries != nullptr && cand_offsets != nullptr && outputs != nullptr,
+            "inputs must be non-null");
+    Require(pool->view.head_dim > 0 && pool->view.head_dim <= 256,
+            "head_dim must be in (0, 256]");
+    Require(cand_offsets[0] == 0, "cand_offsets[0] must be 0");
+    for (int r = 0; r < batch; ++r) {
+      Require(cand_offsets[r + 1] >= cand_offsets[r], "cand_offsets must be non-decreasing");
+    }
+    const int total = cand_offsets[batch];
+    if (total > 0) Require(cand_ids != nullptr, "cand_ids must be non-null");
+    for (int c = 0; c < total; ++c) pool->ValidatePage(cand_ids[c]);
+    const size_t qn = static_cast<size_t>(batch) * pool->view.elements;
+    pool->dense_q.Reserve(qn);
+    pool->dense_out.Reserve(qn);
+    pool->dense_offsets.Reserve(batch + 1);
+    pool->dense_ids.Reserve(std::max(1, total));
+    DSD_HIP_CHECK(hipMemcpyAsync(pool->dense_q.ptr, queries, sizeof(float) * qn,
+                                 hipMemcpyHostToDevice, pool->stream));
+    DSD_HIP_CHECK(hipMemcpyAsync(pool->dense_offsets.ptr, cand_offsets,
+                                 sizeof(int) * (batch + 1), hipMemcpyHostToDevice,
+                                 pool->stream));
+    if (total > 0) {
+      DSD_HIP_CHECK(hipMemcpyAsync(pool->dense_ids.ptr, cand_ids, sizeof(int) * total,
+                                   hipMemcpyHostToDevice, pool->stream));
+    }
+    dsdk::AttentionArgs a;
+    a.queries = pool->dense_q.ptr;
+    a.list_ids = pool->dense_ids.ptr;
+    a.list_offsets = pool->dense_offsets.ptr;
+    a.list_stride = 0;
+    a.batch = batch;
+    a.scale = 1.0f / std::sqrt(static_cast<float>(pool->view.head_dim));
+    a.outputs = pool->dense_out.ptr;
+    DSD_HIP_CHECK(hipEventRecord(pool->dense_start, pool->stream));
+    dsdk::LaunchAttention(pool->view, a, pool->stream);
+    DSD_HIP_CHECK(hipEventRecord(pool->dense_stop, pool->stream));
+    DSD_HIP_CHECK(hipMemcpyAsync(outputs, pool->dense_out.ptr, sizeof(float) * qn,
+                                 hipMemcpyDeviceToHost, pool->stream));
+    pool->Sync();
+    if (kernel_ms != nullptr) {
+      float ms = 0.f;
+      DSD_HIP_CHECK(hipEventElapsedTime(&ms, pool->dense_start, pool->dense_stop));
+      *kernel_ms = ms;
+    }
+  });
+}
+
+int dsd_dense_run_batch_device(dsd_pool* pool, int batch,
+                               const float* d_queries,
+                               const int* d_cand_offsets,
+                               const int* d_cand_ids, float* d_outputs,
+                               void* stream) {
+  return Guard([&] {
+    Require(pool != nullptr, "pool must be non-null");
+    Require(batch >= 0, "batch must be non-negative");
+    if (batch == 0) return;
+    Require(d_queries != nullptr && d_cand_offsets != nullptr && d_outputs != nullptr,
+            "device inputs must be non-null");
+    dsdk::AttentionArgs a;
+    a.queries = d_queries;
+    a.list_ids = d_cand_ids;
+    a.list_offsets = d_cand_offsets;
+    a.list_stride = 0;
+    a.batch = batch;
+    a.scale = 1.0f / std::sqrt(static_cast<float>(pool->view.head_dim));
+    a.outputs = d_outputs;
+    dsdk::LaunchAttention(pool->view, a, reinterpret_cast<hipStream_t>(stream));
+  });
+}
+
+}  // extern "C"

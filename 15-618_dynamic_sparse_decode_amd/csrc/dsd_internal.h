@@ -1,0 +1,101 @@
+// dsd_internal.h -- kernel launch interface shared by the HIP translation
+// units of libdsd_hip.so.  Not part of the public ABI (include/dsd_hip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace dsdk {
+
+// Raw view of a device page pool (see the layout in include/dsd_hip.h).
+struct PoolView {
+  float* keys = nullptr;        // [capacity][page_size][E]
+  float* values = nullptr;      // [capacity][page_size][E]
+  float* summaries = nullptr;   // [capacity][E]
+  int* token_counts = nullptr;  // [capacity]
+  uint8_t* live = nullptr;      // [capacity]
+  int num_heads = 0;
+  int head_dim = 0;
+  int page_size = 0;
+  int elements = 0;   // E = num_heads * head_dim
+  int capacity = 0;
+  int64_t page_elems = 0;  // page_size * E
+};
+
+// A HIP runtime failure; the C ABI maps it to DSD_ERR_HIP.
+struct HipError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+inline void CheckHip(hipError_t status, const char* expr) {
+  if (status != hipSuccess) {
+    throw HipError(std::string(expr) + " failed: " + hipGetErrorString(status));
+  }
+}
+
+#define DSD_HIP_CHECK(expr) ::dsdk::CheckHip((expr), #expr)
+
+// ---- pool kernels (pool_kernels.hip) --------------------------------------
+
+// For each of n pages: token count and live flag, then the summary row --
+// copied from rows[n][E] when rows != nullptr, else computed from the page's
+// keys with the host rule (sum in token order, times fl(1/count)).
+void LaunchFinishPageUpload(const PoolView& pool, const int* d_page_ids,
+                            const int* d_token_counts, const float* d_rows,
+                            int n, hipStream_t stream);
+
+// Token append.  Tokens are grouped in segments of one page each (host
+// sorted by (page, offset)): seg_start[nseg+1] indexes order[], order[q] is
+// the token index into the staged rows keys/values[n][E] and the per-token
+// arrays.  Writes K/V rows, then the summary (rows copy or running mean in
+// offset order), token count and live flag.
+void LaunchAppendTokens(const PoolView& pool, const int* d_seg_start,
+                        const int* d_order, const int* d_page_ids,
+                        const int* d_offsets, const int* d_counts,
+                        const float* d_keys, const float* d_values,
+                        const float* d_rows, int num_segments,
+                        hipStream_t stream);
+
+// Clears token count, live flag and summary row of n pages.
+void LaunchMarkFree(const PoolView& pool, const int* d_page_ids, int n,
+                    hipStream_t stream);
+
+// ---- decode-step kernels (step_kernels.hip) --------------------------------
+
+// Exact-order page scores: scores[c] = fl(sum_seq q*s) * scale, bit-equal to
+// the reference's sequential CPU loop.
+void LaunchScoreExact(const PoolView& pool, const float* d_queries,
+                      const int* d_cand_offsets, const int* d_cand_ids,
+                      int batch, int max_candidates, float scale,
+                      float* d_scores, hipStream_t stream);
+
+// Largest next-pow2 candidate count the LDS select handles.
+int SelectMaxCandidates();
+
+// Per-request top-k by (score desc, id asc): selected[r*top_k + j],
+// counts[r] = min(top_k, n_r).
+void LaunchSelectTopK(const float* d_scores, const int* d_cand_offsets,
+                      const int* d_cand_ids, int batch, int max_candidates,
+                      int top_k, int* d_selected, int* d_counts,
+                      hipStream_t stream);
+
+// Fused gather + softmax attention over page lists.  Request r attends over
+// list_ids[start_r .. start_r + count_r): with list_stride > 0, start_r =
+// r*list_stride and count_r = list_counts[r]; otherwise CSR list_offsets.
+struct AttentionArgs {
+  const float* queries = nullptr;  // [batch][E]
+  const int* list_ids = nullptr;
+  const int* list_offsets = nullptr;
+  const int* list_counts = nullptr;
+  int list_stride = 0;
+  int batch = 0;
+  float scale = 0.0f;
+  float* outputs = nullptr;  // [batch][E]
+};
+void LaunchAttention(const PoolView& pool, const AttentionArgs& args,
+                     hipStream_t stream);
+
+}  // namespace dsdk

@@ -1,0 +1,145 @@
+// pool_kernels.hip -- device page pool maintenance kernels (gfx950).
+//
+// Summaries follow the reference's host rule exactly (no FMA contraction, no
+// division shortcut): upload = sum in token order then times fl(1/count)
+// (src/paged_kv_cache.cpp:87-99); append = (s*old + k)/(old+1)
+// (src/paged_kv_cache.cpp:231-238).  The reference's device kernel instead
+// divides by the count (src/device_page_pool.cpp:89-99), which can differ by
+// an ulp; this pool reproduces the host cache bit for bit.
+#include "dsd_internal.h"
+
+namespace dsdk {
+namespace {
+
+constexpr int kPoolThreads = 256;
+
+// One workgroup per uploaded page; threads stride the E summary elements so
+// each token row is read with contiguous, coalesced loads.
+__global__ __launch_bounds__(kPoolThreads) void FinishPageUploadKernel(
+    PoolView pool, const int* __restrict__ page_ids,
+    const int* __restrict__ token_counts, const float* __restrict__ rows,
+    int n) {
+  const int i = blockIdx.x;
+  if (i >= n) return;
+  const int page = page_ids[i];
+  const int count = token_counts[i];
+  const int E = pool.elements;
+  float* summary = pool.summaries + static_cast<size_t>(page) * E;
+  if (rows != nullptr) {
+    const float* src = rows + static_cast<size_t>(i) * E;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) summary[e] = src[e];
+  } else {
+    const float* keys = pool.keys + static_cast<size_t>(page) * pool.page_elems;
+    const float inv = __fdiv_rn(1.0f, static_cast<float>(count));
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      float acc = 0.0f;
+      for (int t = 0; t < count; ++t) {
+        acc = __fadd_rn(acc, keys[static_cast<size_t>(t) * E + e]);
+      }
+      summary[e] = __fmul_rn(acc, inv);
+    }
+  }
+  if (threadIdx.x == 0) {
+    pool.token_counts[page] = count;
+    pool.live[page] = 1;
+  }
+}
+
+// One workgroup per page segment; tokens of a segment are applied in offset
+// order so the running mean matches the host's sequence of updates.
+__global__ __launch_bounds__(kPoolThreads) void AppendTokensKernel(
+    PoolView pool, const int* __restrict__ seg_start,
+    const int* __restrict__ order, const int* __restrict__ page_ids,
+    const int* __restrict__ offsets, const int* __restrict__ counts,
+    const float* __restrict__ keys, const float* __restrict__ values,
+    const float* __restrict__ rows, int num_segments) {
+  const int seg = blockIdx.x;
+  if (seg >= num_segments) return;
+  const int begin = seg_start[seg];
+  const int end = seg_start[seg + 1];
+  const int E = pool.elements;
+  const int page = page_ids[order[begin]];
+  const size_t page_base = static_cast<size_t>(page) * pool.page_elems;
+
+  for (int q = begin; q < end; ++q) {
+    const int tok = order[q];
+    const size_t dst = page_base + static_cast<size_t>(offsets[tok]) * E;
+    const size_t src = static_cast<size_t>(tok) * E;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      pool.keys[dst + e] = keys[src + e];
+      pool.values[dst + e] = values[src + e];
+    }
+  }
+
+  float* summary = pool.summaries + static_cast<size_t>(page) * E;
+  if (rows != nullptr) {
+    const float* src = rows + static_cast<size_t>(order[end - 1]) * E;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) summary[e] = src[e];
+  } else {
+    const bool fresh = offsets[order[begin]] == 0;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      float s = fresh ? 0.0f : summary[e];
+      for (int q = begin; q < end; ++q) {
+        const int tok = order[q];
+        const float old_count = static_cast<float>(offsets[tok]);
+        const float new_count = __fadd_rn(old_count, 1.0f);
+        s = __fdiv_rn(__fadd_rn(__fmul_rn(s, old_count),
+                                keys[static_cast<size_t>(tok) * E + e]),
+                      new_count);
+      }
+      summary[e] = s;
+    }
+  }
+  if (threadIdx.x == 0) {
+    pool.token_counts[page] = counts[order[end - 1]];
+    pool.live[page] = 1;
+  }
+}
+
+__global__ __launch_bounds__(kPoolThreads) void MarkFreeKernel(
+    PoolView pool, const int* __restrict__ page_ids, int n) {
+  const int i = blockIdx.x;
+  if (i >= n) return;
+  const int page = page_ids[i];
+  float* summary = pool.summaries + static_cast<size_t>(page) * pool.elements;
+  for (int e = threadIdx.x; e < pool.elements; e += blockDim.x) summary[e] = 0.0f;
+  if (threadIdx.x == 0) {
+    pool.token_counts[page] = 0;
+    pool.live[page] = 0;
+  }
+}
+
+}  // namespace
+
+void LaunchFinishPageUpload(const PoolView& pool, const int* d_page_ids,
+                            const int* d_token_counts, const float* d_rows,
+                            int n, hipStream_t stream) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(FinishPageUploadKernel, dim3(n), dim3(kPoolThreads), 0,
+                     stream, pool, d_page_ids, d_token_counts, d_rows, n);
+  DSD_HIP_CHECK(hipGetLastError());
+}
+
+void LaunchAppendTokens(const PoolView& pool, const int* d_seg_start,
+                        const int* d_order, const int* d_page_ids,
+                        const int* d_offsets, const int* d_counts,
+                        const float* d_keys, const float* d_values,
+                        const float* d_rows, int num_segments,
+                        hipStream_t stream) {
+  if (num_segments <= 0) return;
+  hipLaunchKernelGGL(AppendTokensKernel, dim3(num_segments), dim3(kPoolThreads),
+                     0, stream, pool, d_seg_start, d_order, d_page_ids,
+                     d_offsets, d_counts, d_keys, d_values, d_rows,
+                     num_segments);
+  DSD_HIP_CHECK(hipGetLastError());
+}
+
+void LaunchMarkFree(const PoolView& pool, const int* d_page_ids, int n,
+                    hipStream_t stream) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(MarkFreeKernel, dim3(n), dim3(kPoolThreads), 0, stream,
+                     pool, d_page_ids, n);
+  DSD_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace dsdk

@@ -1,0 +1,248 @@
+#!/usr/bin/env python3
+"""Decode tokens/s and achieved HBM GB/s of the batched sparse decode step
+(score -> top-k -> fused gather+attention) on one MI355X.
+
+Workload: B=16 requests, context lengths
+U[512, 2048] in the reference's draw order (mt19937 seed 7 -> 1207 pages),
+32 heads x 128 dims, page size 16, top-k 8, FP32 Q/K/V i.i.d. N(0,1).
+A step is one pass of the hot path over the batch with its inputs already in
+HBM; the timed region is K steps on one HIP stream bracketed by HIP events.
+
+    python bench.py [--steps K] [--warmup W] [--config 1|2|3|4]
+
+Prints one JSON line (the driver contract).  `roofline` is the fused
+attention kernel against 8 TB/s, with its average duration measured by HIP
+events around K back-to-back launches on the same stream.  `cpu_baseline`
+times the CPU oracle (a restatement of the reference's sparse_cpu) on the
+same inputs, single-threaded, over a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import pathlib
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+PKG_DIR = ROOT / "15-618_dynamic_sparse_decode_amd"
+
+METRIC = "decode tokens/s + achieved HBM GB/s (sparse path), B=16 ragged ctx, top-k 8"
+HBM_PEAK_GBPS = 8000.0
+
+# name: (batch, ctx_lo, ctx_hi, heads, head_dim, page_size, top_k, seed)
+CONFIGS = {
+    1: (1, 1024, 1024, 32, 128, 16, 8, 7),
+    2: (16, 512, 2048, 32, 128, 16, 8, 7),
+    3: (32, 32768, 32768, 32, 128, 16, 64, 11),
+    4: (64, 4096, 16384, 32, 128, 64, 32, 13),
+}
+
+
+def load_package():
+    spec = importlib.util.spec_from_file_location(
+        "dsd_amd", PKG_DIR / "__init__.py", submodule_search_locations=[str(PKG_DIR)])
+    module = importlib.util.module_from_spec(spec)
+    sys.modules["dsd_amd"] = module
+    spec.loader.exec_module(module)
+    return module
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-sample-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build runs the decode step on a single "
+              "MI355X (--gpus 1); multi-GPU sharding is design-only.", file=sys.stderr)
+        return 2
+
+    # torch first: libdsd_hip.so then binds to the HIP runtime torch loaded,
+    # so the process holds a single runtime and torch streams are valid.
+    import torch
+
+    dsd = load_package()
+    if not dsd.gpu_available():
+        print("no visible gfx950 GPU", file=sys.stderr)
+        return 1
+
+    B, lo, hi, H, D, ps, k, seed = CONFIGS[args.config]
+    E = H * D
+    lengths = dsd.reference_context_lengths(B, lo, hi, seed)
+    t0 = time.time()
+    batch = dsd.SyntheticBatch(H, D, ps, lengths, seed=seed)
+    log(f"config {args.config}: B={B} pages={batch.total_candidates} "
+        f"tokens={sum(lengths)} generated in {time.time() - t0:.1f}s")
+
+    pool = dsd.DevicePagePool(H, D, ps, batch.capacity)
+    t0 = time.time()
+    batch.upload(pool)
+    log(f"uploaded {2 * batch.capacity * ps * E * 4 / 1e9:.2f} GB in {time.time() - t0:.1f}s")
+
+    dev = torch.device("cuda:0")
+    q = torch.from_numpy(batch.queries).to(dev)
+    offs = torch.from_numpy(batch.cand_offsets).to(dev)
+    ids = torch.from_numpy(batch.cand_ids).to(dev)
+    out = torch.zeros_like(q)
+    scores = torch.zeros(max(1, batch.total_candidates), dtype=torch.float32, device=dev)
+    sel = torch.full((B, max(1, k)), -1, dtype=torch.int32, device=dev)
+    counts = torch.zeros(B, dtype=torch.int32, device=dev)
+    sel_total = int(sum(min(k, int(n)) for n in np.diff(batch.cand_offsets)))
+    ctx = dsd.SparseContext(pool, k, B, batch.total_candidates, sel_total)
+    stream = torch.cuda.Stream()
+    sptr = stream.cuda_stream
+
+    def step():
+        ctx.run_batch_device(B, batch.total_candidates, batch.max_candidates, q.data_ptr(),
+                             offs.data_ptr(), ids.data_ptr(), out.data_ptr(), scores.data_ptr(),
+                             sel.data_ptr(), counts.data_ptr(), sptr)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    stop.record(stream)
+    stop.synchronize()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(stop) / args.steps
+    log(f"step {ms_per_step * 1e3:.1f} us over {args.steps} steps")
+
+    # Per-kernel average durations: K back-to-back launches of one stage on
+    # the same stream, bracketed by HIP events.
+    stage_ms = []
+    for stage in range(3):
+        ctx.replay_stage(stage, sptr)
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(args.steps):
+            ctx.replay_stage(stage, sptr)
+        b.record(stream)
+        b.synchronize()
+        stage_ms.append(a.elapsed_time(b) / args.steps)
+    torch.cuda.synchronize()
+    log("stages us: score %.1f select %.1f attention %.1f" % tuple(x * 1e3 for x in stage_ms))
+
+    # Algorithmic bytes per launch (fp32).
+    sel_h = sel.cpu().numpy()
+    cnt_h = counts.cpu().numpy()
+    sel_tokens = int(sum(int(batch.token_counts[sel_h[r, j]])
+                         for r in range(B) for j in range(int(cnt_h[r]))))
+    P = batch.total_candidates
+    score_bytes = B * E * 4 + P * E * 4 + P * 8
+    select_bytes = P * 8 + sel_total * 4
+    attn_bytes = B * E * 4 + sel_tokens * E * 4 * 2 + B * E * 4
+    attn_gbps = attn_bytes / (stage_ms[2] * 1e-3) / 1e9
+    stages = {
+        "score": {"us": stage_ms[0] * 1e3, "bytes": score_bytes,
+                  "GBps": score_bytes / (stage_ms[0] * 1e-3) / 1e9},
+        "select": {"us": stage_ms[1] * 1e3, "bytes": select_bytes,
+                   "GBps": select_bytes / (stage_ms[1] * 1e-3) / 1e9},
+        "attention": {"us": stage_ms[2] * 1e3, "bytes": attn_bytes, "GBps": attn_gbps},
+    }
+    step_bytes = score_bytes + select_bytes + attn_bytes
+
+    result = {
+        "metric": METRIC,
+        "value": B / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: N(0,1) fp32 from numpy PCG64(seed); context lengths in the "
+                "reference draw order (mt19937 + uniform_int)",
+        "config": {
+            "workload": f"BASELINE config {args.config}: sparse decode step, B={B}, ctx "
+                        f"U[{lo},{hi}] (seed {seed}), {H}x{D}, page {ps}, top-k {k}",
+            "batch": B, "pages": P, "selected_tokens": sel_tokens, "context_tokens": sum(lengths),
+            "heads": H, "head_dim": D, "page_size": ps, "top_k": k, "seed": seed,
+        },
+        "step_hbm_GBps": step_bytes / (ms_per_step * 1e-3) / 1e9,
+        "stages": stages,
+        "roofline": {"bound": "hbm", "achieved": attn_gbps, "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": attn_gbps / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": "AttentionKernel<32> (fused gather + online softmax)",
+                     "bytes_per_launch": attn_bytes},
+        "cpu_baseline": None,
+    }
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(dsd, batch, pool, k, out, args.cpu_sample_seconds)
+
+    ctx.close()
+    pool.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_baseline(dsd, batch, pool, k, gpu_out, sample_seconds):
+    """The CPU oracle (restated sparse_cpu, 1 thread) on the same inputs, timed
+    over whole batches until `sample_seconds` have elapsed."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import _oracle as orc
+
+    H, D, ps, E = batch.num_heads, batch.head_dim, batch.page_size, batch.elements
+    live = batch.live_page_ids()
+    summaries = np.zeros((batch.capacity, E), np.float32)
+    summaries[live] = orc.pool_summaries(batch.key_pool, batch.token_counts, E, live)
+    iters, elapsed = 0, 0.0
+    stage = np.zeros(4)
+    outs = None
+    while elapsed < sample_seconds or iters == 0:
+        t0 = time.perf_counter()
+        _, _, outs = orc.sparse_batch(batch.queries, batch.key_pool, batch.value_pool,
+                                      summaries, batch.token_counts, batch.cand_offsets,
+                                      batch.cand_ids, H, D, ps, k, stage_ms=stage)
+        elapsed += time.perf_counter() - t0
+        iters += 1
+    diff = orc.max_abs_diff(gpu_out.cpu().numpy(), outs)
+    return {
+        "value": batch.batch * iters / elapsed,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{iters} full B={batch.batch} sparse_cpu steps ({elapsed:.1f}s) on 1 thread "
+                  f"of {os.cpu_count()} host cores ({cpu_model()})",
+        "ms_per_step": elapsed / iters * 1e3,
+        "stage_ms_per_step": {"score": stage[0] / iters, "topk": stage[1] / iters,
+                              "gather_attention": stage[3] / iters},
+        "gpu_vs_cpu_max_abs_diff": diff,
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

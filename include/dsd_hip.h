@@ -1,0 +1,223 @@
+/*
+ * dsd_hip.h -- C ABI of the MI355X (gfx950) batched page-level sparse decode
+ * library, libdsd_hip.so.
+ *
+ * This is the drop-in boundary.  Every entry point is plain C: opaque
+ * handles, raw pointers and sizes, an int status.  The reference's C++ API
+ * (PagePool / PagedKvCache / DevicePagePool / SparseCudaContext::RunBatch /
+ * DenseCudaContext, the headers under include/dsd/) is implemented in host C++ on top
+ * of these calls only; each entry below names the reference interface it
+ * replaces (/root/reference/<file>:<line>).
+ *
+ * Status codes map 1:1 onto the reference's exception types; the message of
+ * the last failure on the calling thread is returned by dsd_last_error().
+ *
+ * Device memory layout (HBM), owned by a pool handle:
+ *   keys, values   float[capacity][page_size][E]   token-major, E = H*D
+ *   summaries      float[capacity][E]              per-page key mean
+ *   token_counts   int32[capacity]
+ *   live           uint8[capacity]
+ * Element (page p, token t, head h, dim d) is at p*page_size*E + t*E + h*D + d
+ * (reference src/page_pool.cpp:58-59, src/cuda/sparse_batched_attention.cu:330).
+ *
+ * Threading: a handle is not thread-safe.  Pool calls are synchronous with
+ * respect to the host (the reference's pool copies are blocking cudaMemcpy,
+ * src/device_page_pool.cpp:1138-1166).  Sparse/dense host-buffer calls return
+ * after their outputs are in host memory; *_device calls are asynchronous on
+ * the given stream.
+ */
+#ifndef DSD_HIP_H_
+#define DSD_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status ------------------------------------------------------------ */
+enum {
+  DSD_OK = 0,
+  DSD_ERR_INVALID_ARGUMENT = 1, /* reference: std::invalid_argument */
+  DSD_ERR_OUT_OF_RANGE = 2,     /* reference: std::out_of_range */
+  DSD_ERR_RUNTIME = 3,          /* reference: std::runtime_error */
+  DSD_ERR_HIP = 4               /* HIP runtime failure (reference: DSD_CUDA_CHECK,
+                                   include/dsd/cuda_utils.h:43-53) */
+};
+
+/* Message of the last failure on this thread ("" if none). */
+const char* dsd_last_error(void);
+
+/* 1 when a gfx950-class device is visible, else 0.
+ * Replaces SparseAttentionCudaAvailable / DenseAttentionCudaAvailable
+ * (include/dsd/cuda_sparse_attention.h:17, cuda_dense_attention.h:16). */
+int dsd_gpu_available(void);
+
+/* Wait for all work on the current device. */
+int dsd_device_synchronize(void);
+
+/* ---- device page pool -------------------------------------------------- */
+/* Replaces dsd::DevicePagePool (include/dsd/device_page_pool.h:17-140). */
+typedef struct dsd_pool dsd_pool;
+
+typedef struct dsd_transfer_stats {
+  uint64_t h2d_bytes;
+  uint64_t d2h_bytes;
+  uint64_t h2d_calls;
+  uint64_t d2h_calls;
+  uint64_t h2d_large_calls; /* >= 1 MiB, as src/device_page_pool.cpp:13 */
+  uint64_t d2h_large_calls;
+} dsd_transfer_stats; /* include/dsd/types.h:50-57 */
+
+/* DevicePagePool(config, capacity_pages) (device_page_pool.h:19). */
+int dsd_pool_create(int num_heads, int head_dim, int page_size,
+                    int capacity_pages, dsd_pool** out_pool);
+int dsd_pool_destroy(dsd_pool* pool);
+
+/* Reset(): all pages free, counts/live/summaries zero (device_page_pool.h:21). */
+int dsd_pool_reset(dsd_pool* pool);
+
+/* Upload n whole pages from host memory.  Page i gets id page_ids[i] and
+ * token_counts[i] in (0, page_size] tokens whose K/V rows are the
+ * token_counts[i]*E contiguous floats starting at element src_offsets[i] of
+ * keys / values.  summaries: NULL => the device computes each page summary
+ * with the host rule (sum in token order, then times fl(1/count));
+ * otherwise [n][E] rows copied verbatim.
+ * Covers UploadPage (device_page_pool.h:23-27), UploadPagesFromCache
+ * (:31-33, with src_offsets = id*page_size*E into the cache pools and the
+ * cache's summary rows) and UploadPromptDirect (:37-42, src_offsets = first
+ * prompt token of each page * E). */
+int dsd_pool_upload_pages(dsd_pool* pool, int n, const int* page_ids,
+                          const int* token_counts, const int64_t* src_offsets,
+                          const float* keys, const float* values,
+                          const float* summaries);
+
+/* Upload n single tokens: token i's K/V rows ([n][E] in keys/values) go to
+ * (page_ids[i], token_offsets[i]); the page's token count becomes
+ * page_token_counts[i].  summaries: NULL => the device applies the
+ * running-mean update s = (s*old + k)/(old+1) in offset order (requires
+ * each page's first offset to equal its current device count); otherwise
+ * [n][E] rows copied.  Replaces UploadTokensFromCache / UploadTokensDirect
+ * (device_page_pool.h:55-63). */
+int dsd_pool_upload_tokens(dsd_pool* pool, int n, const int* page_ids,
+                           const int* token_offsets,
+                           const int* page_token_counts, const float* keys,
+                           const float* values, const float* summaries);
+
+/* MarkPagesFree (device_page_pool.h:71-72): counts, live flags and summary
+ * rows of the listed pages are cleared on the device. */
+int dsd_pool_mark_free(dsd_pool* pool, int n, const int* page_ids);
+
+/* DownloadPage (device_page_pool.h:74-77): copies token_count*E floats of
+ * K and V; *token_count receives the count.  Free page => DSD_ERR_RUNTIME. */
+int dsd_pool_download_page(const dsd_pool* pool, int page_id, float* keys,
+                           float* values, int* token_count);
+
+/* DownloadMetadata (device_page_pool.h:79-81): capacity entries each. */
+int dsd_pool_download_meta(const dsd_pool* pool, int* token_counts,
+                           uint8_t* live);
+
+/* Device summary rows of n pages into out[n][E] (parity checks). */
+int dsd_pool_download_summaries(const dsd_pool* pool, int n,
+                                const int* page_ids, float* out);
+
+/* transfer_stats / ResetTransferStats (device_page_pool.h:85-86). */
+int dsd_pool_transfer_stats(const dsd_pool* pool, dsd_transfer_stats* out);
+int dsd_pool_reset_transfer_stats(dsd_pool* pool);
+
+int dsd_pool_capacity(const dsd_pool* pool);
+
+/* ---- sparse decode step ------------------------------------------------ */
+/* Replaces dsd::SparseCudaContext (include/dsd/cuda_sparse_attention.h:50-137). */
+typedef struct dsd_sparse_ctx dsd_sparse_ctx;
+
+enum {
+  DSD_OUTPUT_NONE = 0,    /* SparseBatchOutputMode::kNoOutputs   (:19-23) */
+  DSD_OUTPUT_OUTPUTS = 1, /* SparseBatchOutputMode::kOutputsOnly */
+  DSD_OUTPUT_DEBUG = 2    /* SparseBatchOutputMode::kDebugTensors */
+};
+enum {
+  DSD_TIMING_NONE = 0,  /* SparseBatchTimingMode::kNone (:25-28) */
+  DSD_TIMING_EVENTS = 1 /* SparseBatchTimingMode::kKernelEvents */
+};
+
+/* Per-call timings, ms (StageTimings + RuntimeOverheadTimings,
+ * include/dsd/types.h:40-48,65-71). */
+typedef struct dsd_step_timings {
+  double score_ms;
+  double topk_ms;
+  double attention_ms;
+  double kernel_ms;
+  double h2d_ms;
+  double d2h_ms;
+  double launch_ms;
+  double sync_ms;
+} dsd_step_timings;
+
+/* SparseCudaContext(cache, config, max_batch_size, max_total_candidates,
+ * max_total_selected_pages) (cuda_sparse_attention.h:52-57).  The context
+ * reads pages from `pool`, which must outlive it.  top_k >= 0. */
+int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
+                      int max_total_candidates, int max_total_selected,
+                      dsd_sparse_ctx** out_ctx);
+int dsd_sparse_destroy(dsd_sparse_ctx* ctx);
+
+/* RunBatch (cuda_sparse_attention.h:60-68) over host buffers.
+ *   queries      [batch][E]
+ *   cand_offsets [batch+1]   CSR offsets into cand_ids (cand_offsets[0] == 0)
+ *   cand_ids     [cand_offsets[batch]] candidate page ids per request
+ * Outputs (host; may be NULL when not requested by output_mode):
+ *   outputs          [batch][E]
+ *   scores           [total candidates]             (DSD_OUTPUT_DEBUG)
+ *   selected         [sum min(k, n_r)] compact       (DSD_OUTPUT_DEBUG)
+ *   selected_counts  [batch]                         (DSD_OUTPUT_DEBUG)
+ * Selected ids equal the reference sparse_cpu selection bit-exactly.
+ * timings may be NULL. */
+int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
+                         const int* cand_offsets, const int* cand_ids,
+                         int output_mode, int timing_mode, float* outputs,
+                         float* scores, int* selected, int* selected_counts,
+                         dsd_step_timings* timings);
+
+/* Device-resident step: every pointer is device memory and the call only
+ * enqueues work on `stream` (a hipStream_t; NULL = the context's stream).
+ * total_candidates and max_candidates (largest n_r) must describe the CSR.
+ * selected ([batch][top_k], unused slots untouched), selected_counts,
+ * scores may be NULL (context scratch is used). */
+int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
+                                int total_candidates, int max_candidates,
+                                const float* d_queries,
+                                const int* d_cand_offsets,
+                                const int* d_cand_ids, float* d_outputs,
+                                float* d_scores, int* d_selected,
+                                int* d_selected_counts, void* stream);
+
+/* Re-enqueue one stage of the last dsd_sparse_run_batch_device call on the
+ * same buffers (stage 0 = score, 1 = select, 2 = attention).  For per-kernel
+ * timing of the hot loop. */
+int dsd_sparse_replay_stage(dsd_sparse_ctx* ctx, int stage, void* stream);
+
+/* The context's own stream (hipStream_t). */
+void* dsd_sparse_stream(dsd_sparse_ctx* ctx);
+
+/* ---- dense decode step ------------------------------------------------- */
+/* DenseCudaContext::RunBatch (include/dsd/cuda_dense_attention.h:18-44):
+ * attention over every candidate page, host buffers as above.
+ * kernel_ms may be NULL. */
+int dsd_dense_run_batch(dsd_pool* pool, int batch, const float* queries,
+                        const int* cand_offsets, const int* cand_ids,
+                        float* outputs, double* kernel_ms);
+
+/* Device-resident dense step on `stream` (NULL = default stream). */
+int dsd_dense_run_batch_device(dsd_pool* pool, int batch,
+                               const float* d_queries,
+                               const int* d_cand_offsets,
+                               const int* d_cand_ids, float* d_outputs,
+                               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSD_HIP_H_ */

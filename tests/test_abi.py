@@ -1,0 +1,64 @@
+"""The C-ABI boundary (include/dsd_hip.h) on a machine without a GPU: the
+library loads, exports every declared entry point, maps errors to the
+reference's exception types, and does not contain the oracle."""
+from __future__ import annotations
+
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "dsd_hip.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dsd_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_symbols()
+    for required in ("dsd_pool_create", "dsd_pool_upload_pages", "dsd_pool_upload_tokens",
+                     "dsd_pool_mark_free", "dsd_pool_download_page", "dsd_sparse_create",
+                     "dsd_sparse_run_batch", "dsd_sparse_run_batch_device",
+                     "dsd_dense_run_batch", "dsd_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(dsd):
+    lib = dsd.load_library()
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, missing
+    # the ctypes binding covers the whole header
+    assert sorted(dsd.EXPORTED_SYMBOLS) == declared_symbols()
+
+
+def test_exported_dynamic_symbols_are_the_c_abi(dsd):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(dsd.library_path())],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert set(declared_symbols()) <= exported
+    # the product never carries the checker
+    assert not any(s.startswith("oracle_") or s.startswith("ref_") for s in exported)
+
+
+def test_product_does_not_link_the_oracle(dsd):
+    out = subprocess.run(["ldd", str(dsd.library_path())], capture_output=True, text=True).stdout
+    assert "oracle" not in out and "dsd_ref" not in out
+
+
+def test_errors_without_gpu(dsd):
+    if dsd.gpu_available():
+        pytest.skip("a GPU is visible; the no-GPU error path does not apply")
+    with pytest.raises(dsd.RuntimeFailure, match="gfx950"):
+        dsd.DevicePagePool(2, 4, 4, 4)
+
+
+def test_invalid_arguments_are_checked_before_the_device(dsd):
+    with pytest.raises(dsd.InvalidArgument, match="capacity_pages"):
+        dsd.DevicePagePool(2, 4, 4, -1)
+    with pytest.raises(dsd.InvalidArgument):
+        dsd.DevicePagePool(0, 4, 4, 4)
