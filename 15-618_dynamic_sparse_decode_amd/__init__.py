@@ -24,6 +24,7 @@ BUILD_DIR = PACKAGE_DIR / "build"
 LIB_PATH = BUILD_DIR / "libdsd_hip.so"
 
 OUTPUT_NONE, OUTPUT_OUTPUTS, OUTPUT_DEBUG = 0, 1, 2
+SCORE_CERTIFIED, SCORE_EXACT = 0, 1
 TIMING_NONE, TIMING_EVENTS = 0, 1
 
 
@@ -110,6 +111,10 @@ _SIGNATURES = {
                                     + [ctypes.c_void_p] * 8),
     "dsd_sparse_replay_stage": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]),
     "dsd_sparse_stream": (ctypes.c_void_p, [ctypes.c_void_p]),
+    "dsd_sparse_set_score_mode": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "dsd_sparse_score_bounds": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_float_p,
+                                               _c_float_p, _c_float_p]),
+    "dsd_sparse_exact_rescored_pages": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p]),
     "dsd_dense_run_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_float_p, _c_int_p,
                                            _c_int_p, _c_float_p, _c_double_p]),
     "dsd_dense_run_batch_device": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int] + [ctypes.c_void_p] * 5),
@@ -297,9 +302,10 @@ class SparseContext:
         return self._lib.dsd_sparse_stream(self.handle) or 0
 
     def run_batch(self, queries, cand_offsets, cand_ids, output_mode=OUTPUT_DEBUG,
-                  timing_mode=TIMING_EVENTS):
-        """Host-buffer step.  Returns a dict with outputs [B][E], and in debug
-        mode scores [P] and selected (a list of per-request id arrays)."""
+                  timing_mode=TIMING_EVENTS, want_ids=False):
+        """Host-buffer step.  Returns a dict with outputs [B][E], in debug mode
+        scores [P], and selected (a list of per-request id arrays) in debug
+        mode or when want_ids is set with OUTPUT_OUTPUTS."""
         q = _f32(queries).reshape(-1)
         offs = _i32(cand_offsets)
         ids = _i32(cand_ids) if len(cand_ids) else np.zeros(1, np.int32)
@@ -312,16 +318,18 @@ class SparseContext:
         counts = np.zeros(max(batch, 1), np.int32)
         t = StepTimings()
         debug = output_mode == OUTPUT_DEBUG
+        ids_out = debug or (want_ids and output_mode == OUTPUT_OUTPUTS)
         _check(self._lib.dsd_sparse_run_batch(
             self.handle, batch, _ptr(q, ctypes.c_float), _ptr(offs, ctypes.c_int),
             _ptr(ids, ctypes.c_int), output_mode, timing_mode,
             _ptr(out, ctypes.c_float) if output_mode != OUTPUT_NONE else None,
             _ptr(scores, ctypes.c_float) if debug else None,
-            _ptr(sel, ctypes.c_int) if debug else None,
-            _ptr(counts, ctypes.c_int) if debug else None, ctypes.byref(t)))
+            _ptr(sel, ctypes.c_int) if ids_out else None,
+            _ptr(counts, ctypes.c_int) if ids_out else None, ctypes.byref(t)))
         result = {"outputs": out, "timings": t.as_dict()}
         if debug:
             result["scores"] = scores[:total].copy()
+        if ids_out:
             selected, w = [], 0
             for r in range(batch):
                 c = int(counts[r])
@@ -338,6 +346,23 @@ class SparseContext:
             self.handle, batch, total_candidates, max_candidates, d_queries, d_cand_offsets,
             d_cand_ids, d_outputs, d_scores or None, d_selected or None, d_counts or None,
             stream or None))
+
+    def set_score_mode(self, mode: int) -> None:
+        _check(self._lib.dsd_sparse_set_score_mode(self.handle, mode))
+
+    def score_bounds(self, n: int):
+        """(mid, lo, hi) certified intervals of the last step's first n candidates."""
+        mid, lo, hi = (np.empty(n, np.float32) for _ in range(3))
+        _check(self._lib.dsd_sparse_score_bounds(self.handle, n, _ptr(mid, ctypes.c_float),
+                                                 _ptr(lo, ctypes.c_float),
+                                                 _ptr(hi, ctypes.c_float)))
+        return mid, lo, hi
+
+    def exact_rescored_pages(self, reset: bool = False) -> int:
+        out = ctypes.c_int()
+        _check(self._lib.dsd_sparse_exact_rescored_pages(self.handle, int(reset),
+                                                         ctypes.byref(out)))
+        return out.value
 
     def replay_stage(self, stage: int, stream=0) -> None:
         _check(self._lib.dsd_sparse_replay_stage(self.handle, stage, stream or None))

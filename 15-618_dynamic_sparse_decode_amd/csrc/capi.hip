@@ -529,13 +529,15 @@ struct dsd_sparse_ctx {
   int max_sel = 0;
   hipStream_t stream = nullptr;
   hipEvent_t ev[6] = {};
-  DeviceBuffer<float> d_queries, d_scores, d_outputs;
-  DeviceBuffer<int> d_offsets, d_ids, d_selected, d_counts;
+  DeviceBuffer<float> d_queries, d_scores, d_outputs, d_lo, d_hi;
+  DeviceBuffer<int> d_offsets, d_ids, d_selected, d_counts, d_exact_pages;
+  int score_mode = DSD_SCORE_CERTIFIED;
   PinnedBuffer<float> h_queries, h_scores, h_outputs;
   PinnedBuffer<int> h_offsets, h_ids, h_selected, h_counts;
 
   struct Launch {
     bool valid = false;
+    bool certified = false;
     int batch = 0, total = 0, max_n = 0;
     const float* queries = nullptr;
     const int* offsets = nullptr;
@@ -557,13 +559,25 @@ struct dsd_sparse_ctx {
     return 1.0f / std::sqrt(static_cast<float>(pool->view.head_dim));
   }
 
-  void Enqueue(const Launch& L, hipStream_t s, bool timing) {
-    const PoolView& v = pool->view;
-    if (timing) DSD_HIP_CHECK(hipEventRecord(ev[0], s));
-    if (L.total > 0) {
-      dsdk::LaunchScoreExact(v, L.queries, L.offsets, L.ids, L.batch, L.max_n,
+  // Certified scoring unless exact scores are requested or the shape is
+  // outside what the certified kernels handle.
+  bool UseCertified(int max_n, bool need_exact_scores) const {
+    return score_mode == DSD_SCORE_CERTIFIED && !need_exact_scores &&
+           dsdk::CertifiedScoringSupported(pool->view.elements, max_n);
+  }
+  void EnqueueScore(const Launch& L, hipStream_t s) {
+    if (L.total <= 0) return;
+    if (L.certified) {
+      dsdk::LaunchScoreBounds(pool->view, L.queries, L.offsets, L.ids, L.batch, L.total,
+                              L.max_n, Scale(), L.scores, d_lo.ptr, d_hi.ptr, s);
+    } else {
+      dsdk::LaunchScoreExact(pool->view, L.queries, L.offsets, L.ids, L.batch, L.max_n,
                              Scale(), L.scores, s);
     }
+  }
+  void Enqueue(const Launch& L, hipStream_t s, bool timing) {
+    if (timing) DSD_HIP_CHECK(hipEventRecord(ev[0], s));
+    EnqueueScore(L, s);
     if (timing) DSD_HIP_CHECK(hipEventRecord(ev[1], s));
     EnqueueSelect(L, s);
     if (timing) DSD_HIP_CHECK(hipEventRecord(ev[2], s));
@@ -571,8 +585,14 @@ struct dsd_sparse_ctx {
     if (timing) DSD_HIP_CHECK(hipEventRecord(ev[3], s));
   }
   void EnqueueSelect(const Launch& L, hipStream_t s) {
-    dsdk::LaunchSelectTopK(L.scores, L.offsets, L.ids, L.batch, L.max_n, top_k,
-                           L.selected, L.counts, s);
+    if (L.certified) {
+      dsdk::LaunchSelectCertified(pool->view, L.scores, d_lo.ptr, d_hi.ptr, L.queries,
+                                  L.offsets, L.ids, L.batch, L.max_n, Scale(), top_k,
+                                  L.selected, L.counts, d_exact_pages.ptr, s);
+    } else {
+      dsdk::LaunchSelectTopK(L.scores, L.offsets, L.ids, L.batch, L.max_n, top_k,
+                             L.selected, L.counts, s);
+    }
   }
   void EnqueueAttention(const Launch& L, hipStream_t s) {
     dsdk::AttentionArgs a;
@@ -622,6 +642,10 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     ctx->d_ids.Reserve(P);
     ctx->d_selected.Reserve(B * K);
     ctx->d_counts.Reserve(B);
+    ctx->d_lo.Reserve(P);
+    ctx->d_hi.Reserve(P);
+    ctx->d_exact_pages.Reserve(1);
+    DSD_HIP_CHECK(hipMemset(ctx->d_exact_pages.ptr, 0, sizeof(int)));
     ctx->h_queries.Reserve(B * E);
     ctx->h_outputs.Reserve(B * E);
     ctx->h_scores.Reserve(P);
@@ -662,6 +686,9 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
     Require(queries != nullptr && cand_offsets != nullptr, "inputs must be non-null");
     const bool want_outputs = output_mode != DSD_OUTPUT_NONE;
     const bool debug = output_mode == DSD_OUTPUT_DEBUG;
+    // Ids are returned in debug mode, or in outputs mode when buffers are given.
+    const bool want_ids =
+        debug || (want_outputs && selected != nullptr && selected_counts != nullptr);
     const bool timing = timing_mode == DSD_TIMING_EVENTS;
     if (want_outputs) Require(outputs != nullptr, "outputs must be non-null");
     if (debug) {
@@ -714,6 +741,7 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
 
     dsd_sparse_ctx::Launch L;
     L.valid = true;
+    L.certified = ctx->UseCertified(max_n, debug);
     L.batch = batch;
     L.total = total;
     L.max_n = max_n;
@@ -733,12 +761,12 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
       t0 = Clock::now();
       DSD_HIP_CHECK(hipMemcpyAsync(ctx->h_outputs.ptr, ctx->d_outputs.ptr,
                                    sizeof(float) * qn, hipMemcpyDeviceToHost, ctx->stream));
-      if (debug) {
-        if (total > 0) {
-          DSD_HIP_CHECK(hipMemcpyAsync(ctx->h_scores.ptr, ctx->d_scores.ptr,
-                                       sizeof(float) * total, hipMemcpyDeviceToHost,
-                                       ctx->stream));
-        }
+      if (debug && total > 0) {
+        DSD_HIP_CHECK(hipMemcpyAsync(ctx->h_scores.ptr, ctx->d_scores.ptr,
+                                     sizeof(float) * total, hipMemcpyDeviceToHost,
+                                     ctx->stream));
+      }
+      if (want_ids) {
         const size_t kk = static_cast<size_t>(std::max(1, ctx->top_k));
         DSD_HIP_CHECK(hipMemcpyAsync(ctx->h_selected.ptr, ctx->d_selected.ptr,
                                      sizeof(int) * kk * batch, hipMemcpyDeviceToHost,
@@ -764,8 +792,8 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
     }
     if (want_outputs) {
       std::memcpy(outputs, ctx->h_outputs.ptr, sizeof(float) * qn);
-      if (debug) {
-        if (total > 0) std::memcpy(scores, ctx->h_scores.ptr, sizeof(float) * total);
+      if (debug && total > 0) std::memcpy(scores, ctx->h_scores.ptr, sizeof(float) * total);
+      if (want_ids) {
         int w = 0;
         const int kk = std::max(1, ctx->top_k);
         for (int r = 0; r < batch; ++r) {
@@ -794,7 +822,7 @@ int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
     if (batch > ctx->max_batch) {
       throw std::invalid_argument("request batch exceeds sparse context capacity");
     }
-    if (total_candidates > ctx->max_cand && d_scores == nullptr) {
+    if (total_candidates > ctx->max_cand) {
       throw std::invalid_argument("candidate page count exceeds sparse context capacity");
     }
     Require(d_queries != nullptr && d_cand_offsets != nullptr && d_outputs != nullptr,
@@ -802,6 +830,7 @@ int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
     if (total_candidates > 0) Require(d_cand_ids != nullptr, "cand_ids must be non-null");
     dsd_sparse_ctx::Launch L;
     L.valid = true;
+    L.certified = ctx->UseCertified(max_candidates, false);
     L.batch = batch;
     L.total = total_candidates;
     L.max_n = max_candidates;
@@ -825,16 +854,42 @@ int dsd_sparse_replay_stage(dsd_sparse_ctx* ctx, int stage, void* stream) {
     hipStream_t s = stream != nullptr ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
     const auto& L = ctx->last;
     switch (stage) {
-      case 0:
-        if (L.total > 0) {
-          dsdk::LaunchScoreExact(ctx->pool->view, L.queries, L.offsets, L.ids, L.batch,
-                                 L.max_n, ctx->Scale(), L.scores, s);
-        }
-        break;
+      case 0: ctx->EnqueueScore(L, s); break;
       case 1: ctx->EnqueueSelect(L, s); break;
       case 2: ctx->EnqueueAttention(L, s); break;
       default: throw std::invalid_argument("stage must be 0, 1 or 2");
     }
+  });
+}
+
+int dsd_sparse_set_score_mode(dsd_sparse_ctx* ctx, int mode) {
+  return Guard([&] {
+    Require(ctx != nullptr, "context must be non-null");
+    Require(mode == DSD_SCORE_CERTIFIED || mode == DSD_SCORE_EXACT, "unknown score mode");
+    ctx->score_mode = mode;
+  });
+}
+
+int dsd_sparse_score_bounds(dsd_sparse_ctx* ctx, int n, float* mid, float* lo, float* hi) {
+  return Guard([&] {
+    Require(ctx != nullptr, "context must be non-null");
+    Require(ctx->last.valid && ctx->last.certified,
+            "the last step did not use certified scoring");
+    Require(n >= 0 && n <= ctx->last.total, "n exceeds the last step's candidate count");
+    Require(mid != nullptr && lo != nullptr && hi != nullptr, "outputs must be non-null");
+    DSD_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    DSD_HIP_CHECK(hipMemcpy(mid, ctx->last.scores, sizeof(float) * n, hipMemcpyDeviceToHost));
+    DSD_HIP_CHECK(hipMemcpy(lo, ctx->d_lo.ptr, sizeof(float) * n, hipMemcpyDeviceToHost));
+    DSD_HIP_CHECK(hipMemcpy(hi, ctx->d_hi.ptr, sizeof(float) * n, hipMemcpyDeviceToHost));
+  });
+}
+
+int dsd_sparse_exact_rescored_pages(dsd_sparse_ctx* ctx, int reset, int* out) {
+  return Guard([&] {
+    Require(ctx != nullptr && out != nullptr, "pointers must be non-null");
+    DSD_HIP_CHECK(hipDeviceSynchronize());
+    DSD_HIP_CHECK(hipMemcpy(out, ctx->d_exact_pages.ptr, sizeof(int), hipMemcpyDeviceToHost));
+    if (reset) DSD_HIP_CHECK(hipMemset(ctx->d_exact_pages.ptr, 0, sizeof(int)));
   });
 }
 

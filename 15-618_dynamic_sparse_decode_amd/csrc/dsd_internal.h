@@ -72,6 +72,24 @@ void LaunchScoreExact(const PoolView& pool, const float* d_queries,
                       int batch, int max_candidates, float scale,
                       float* d_scores, hipStream_t stream);
 
+// Certified scoring: per candidate an interval [lo, hi] that provably holds
+// the reference's sequential-fp32 score, and its midpoint.  Needs E % 64 == 0
+// and at most 2048 candidates per request (next power of two).
+bool CertifiedScoringSupported(int elements, int max_candidates);
+void LaunchScoreBounds(const PoolView& pool, const float* d_queries,
+                       const int* d_cand_offsets, const int* d_cand_ids, int batch,
+                       int total_candidates, int max_candidates, float scale, float* d_mid,
+                       float* d_lo, float* d_hi, hipStream_t stream);
+
+// Top-k from certified intervals; candidates whose order is not decided by
+// disjoint intervals are rescored with the exact sequential chain.  Adds the
+// number of rescored pages to *d_exact_pages when non-null.
+void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float* d_lo,
+                           const float* d_hi, const float* d_queries,
+                           const int* d_cand_offsets, const int* d_cand_ids, int batch,
+                           int max_candidates, float scale, int top_k, int* d_selected,
+                           int* d_counts, int* d_exact_pages, hipStream_t stream);
+
 // Largest next-pow2 candidate count the LDS select handles.
 int SelectMaxCandidates();
 

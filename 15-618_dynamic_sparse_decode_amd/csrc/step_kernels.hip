@@ -5,6 +5,8 @@
 // Dense attention (reference DenseAttentionCpu, :196-203) reuses kernel 3
 // with every candidate page as the list.
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 
 #include "dsd_internal.h"
 
@@ -63,6 +65,238 @@ __global__ __launch_bounds__(kWave) void ScoreExactKernel(
     }
   }
   if (active) scores[c] = __fmul_rn(acc, scale);
+}
+
+// ---------------------------------------------------------------------------
+// 1b. Certified scoring (the fast path).
+//
+// The sequential chain above is latency-bound (4096 dependent adds per page).
+// Instead, each page gets one wave that forms the same fp32 products
+// p_i = fl(q_i*s_i), sums them in double, and bounds how far the reference's
+// sequential fp32 sum can be from that sum:
+//   acc_i = fl(acc_{i-1} + p_i)  =>  |acc_n - S| <= u * sum_i |T_i| / (1 - n u)
+// with S = sum p_i, T_i the exact prefix sums and u = 2^-24 (plus 2^-150 per
+// step for subnormal results).  Each lane owns a contiguous block of BL
+// products: pass 1 sums the block, a wave exclusive scan gives the block's
+// starting prefix, pass 2 accumulates |T_i|.  Double rounding of the scan is
+// covered by generous slack terms.  The page's score interval
+// [fl(lo*scale), fl(hi*scale)] (lo/hi rounded outward to float) provably
+// contains the reference score, because fl(x*scale) is monotone in x.
+// ---------------------------------------------------------------------------
+constexpr int kBoundWaves = 4;
+
+__device__ __forceinline__ float NextDown(float x) {
+  if (x == 0.0f) return -0x1p-149f;
+  uint32_t b = __float_as_uint(x);
+  b = (b & 0x80000000u) ? b + 1u : b - 1u;
+  return __uint_as_float(b);
+}
+
+__device__ __forceinline__ float NextUp(float x) {
+  if (x == 0.0f) return 0x1p-149f;
+  uint32_t b = __float_as_uint(x);
+  b = (b & 0x80000000u) ? b - 1u : b + 1u;
+  return __uint_as_float(b);
+}
+
+__device__ __forceinline__ double WaveSum(double v) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Lane 0 turns the wave's sums into the certified interval.
+__device__ __forceinline__ void WriteBounds(double s_hat, double abs_prefix, double abs_p,
+                                            int n, float scale, float* mid_out,
+                                            float* lo_out, float* hi_out, int c) {
+  const double dn = static_cast<double>(n);
+  const double u = 0x1p-24;
+  const double at_up = abs_prefix * (1.0 + 0x1p-40) + dn * dn * 0x1p-52 * abs_p;
+  double err = u * at_up / (1.0 - dn * u) + dn * 0x1p-52 * abs_p + dn * 0x1p-149;
+  err *= 1.001;
+  float lo, hi, mid;
+  if (isfinite(s_hat) && isfinite(err)) {
+    lo = NextDown(__double2float_rd(s_hat - err));
+    hi = NextUp(__double2float_ru(s_hat + err));
+    mid = __double2float_rn(s_hat);
+    if (!(mid >= lo)) mid = lo;
+    if (!(mid <= hi)) mid = hi;
+    lo = __fmul_rn(lo, scale);
+    hi = __fmul_rn(hi, scale);
+    mid = __fmul_rn(mid, scale);
+  } else {
+    // Non-finite sums: an unbounded interval forces the exact path.
+    lo = -INFINITY;
+    hi = INFINITY;
+    mid = 0.0f;
+  }
+  mid_out[c] = mid;
+  lo_out[c] = lo;
+  hi_out[c] = hi;
+}
+
+// Orders this wave's LDS writes before its later LDS reads of other lanes'
+// data (a wave-scope release/acquire around a wave barrier).
+__device__ __forceinline__ void WaveSync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// E = 4096, one 256-thread workgroup per candidate page (grid = candidates):
+// wave w covers elements [1024w, 1024w + 1024), lane l the contiguous block
+// [1024w + 16l, +16).  Rows are loaded coalesced and transposed through LDS
+// as above; the waves' partial sums meet in LDS for the carries.
+constexpr int kPageThreads = 256;
+constexpr int kPageWaves = kPageThreads / kWave;
+constexpr int kPageBlock = 4096 / kPageThreads;  // 16 products per lane
+constexpr int kPageStride = kPageBlock + 4;
+
+__device__ __forceinline__ int RequestOf(const int* __restrict__ cand_offsets, int batch,
+                                         int c) {
+  int lo = 0, hi = batch;  // cand_offsets[lo] <= c < cand_offsets[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (cand_offsets[mid] <= c) lo = mid;
+    else hi = mid;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(kPageThreads) void ScoreBoundPageKernel(
+    const float* __restrict__ queries, const float* __restrict__ summaries,
+    const int* __restrict__ token_counts, const int* __restrict__ cand_offsets,
+    const int* __restrict__ cand_ids, int batch, float scale, float* __restrict__ mid_out,
+    float* __restrict__ lo_out, float* __restrict__ hi_out) {
+  constexpr int E = 4096;
+  __shared__ __align__(16) float lds[kPageWaves][kWave * kPageStride];
+  __shared__ double s_total[kPageWaves];
+  __shared__ double s_abs[kPageWaves];
+  __shared__ float s_absp[kPageWaves];
+  const int c = blockIdx.x;
+  const int r = RequestOf(cand_offsets, batch, c);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int page = cand_ids[c];
+  const bool zero = token_counts[page] == 0;
+  const float4* __restrict__ q4 =
+      reinterpret_cast<const float4*>(queries + static_cast<size_t>(r) * E) + wave * 256;
+  const float4* __restrict__ s4 =
+      reinterpret_cast<const float4*>(summaries + static_cast<size_t>(page) * E) + wave * 256;
+  float* my = lds[wave];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {  // 4 rows of 256 elements
+    const float4 qv = q4[j * kWave + lane];
+    const float4 sv = zero ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : s4[j * kWave + lane];
+    float4 pv;
+    pv.x = __fmul_rn(qv.x, sv.x);
+    pv.y = __fmul_rn(qv.y, sv.y);
+    pv.z = __fmul_rn(qv.z, sv.z);
+    pv.w = __fmul_rn(qv.w, sv.w);
+    const int e = j * 4 * kWave + 4 * lane;
+    const int owner = e / kPageBlock;
+    *reinterpret_cast<float4*>(my + owner * kPageStride + (e - owner * kPageBlock)) = pv;
+  }
+  WaveSync();
+  float p[kPageBlock];
+#pragma unroll
+  for (int i = 0; i < kPageBlock; i += 4) {
+    const float4 pv = *reinterpret_cast<const float4*>(my + lane * kPageStride + i);
+    p[i + 0] = pv.x;
+    p[i + 1] = pv.y;
+    p[i + 2] = pv.z;
+    p[i + 3] = pv.w;
+  }
+  double block = 0.0;
+  float abs_p = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kPageBlock; ++i) {
+    block += static_cast<double>(p[i]);
+    abs_p += fabsf(p[i]);
+  }
+  double incl = block;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const double t = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += t;
+  }
+  if (lane == kWave - 1) s_total[wave] = incl;
+  __syncthreads();
+  double carry = 0.0;
+  for (int w = 0; w < wave; ++w) carry += s_total[w];
+  double prefix = __shfl_up(incl, 1, kWave);
+  if (lane == 0) prefix = 0.0;
+  prefix += carry;
+  double abs_prefix = 0.0;
+#pragma unroll
+  for (int i = 0; i < kPageBlock; ++i) {
+    prefix += static_cast<double>(p[i]);
+    abs_prefix += fabs(prefix);
+  }
+  double absp = static_cast<double>(abs_p);
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {  // both wave sums in one shuffle sequence
+    abs_prefix += __shfl_xor(abs_prefix, o, kWave);
+    absp += __shfl_xor(absp, o, kWave);
+  }
+  if (lane == 0) {
+    s_abs[wave] = abs_prefix;
+    s_absp[wave] = static_cast<float>(absp);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double s_hat = 0.0, at = 0.0, ap = 0.0;
+    for (int w = 0; w < kPageWaves; ++w) {
+      s_hat += s_total[w];
+      at += s_abs[w];
+      ap += s_absp[w];
+    }
+    // |p| sums carry float rounding (< 2^-17 relative); doubled to stay an
+    // upper bound for the slack terms they feed.
+    WriteBounds(s_hat, at, 2.0 * ap, E, scale, mid_out, lo_out, hi_out, c);
+  }
+}
+
+// Any E that is a multiple of 64: runtime block length, products re-formed
+// from the (cache-resident) operands in pass 2.
+__global__ __launch_bounds__(kBoundWaves * kWave) void ScoreBoundGenericKernel(
+    const float* __restrict__ queries, const float* __restrict__ summaries,
+    const int* __restrict__ token_counts, const int* __restrict__ cand_offsets,
+    const int* __restrict__ cand_ids, int E, float scale, float* __restrict__ mid_out,
+    float* __restrict__ lo_out, float* __restrict__ hi_out) {
+  const int BL = E / kWave;
+  const int r = blockIdx.y;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int begin = cand_offsets[r];
+  const int c = begin + blockIdx.x * kBoundWaves + wave;
+  if (c >= cand_offsets[r + 1]) return;
+  const int page = cand_ids[c];
+  const bool zero = token_counts[page] == 0;
+  const float* __restrict__ q = queries + static_cast<size_t>(r) * E + lane * BL;
+  const float* __restrict__ s = summaries + static_cast<size_t>(page) * E + lane * BL;
+  double block = 0.0, abs_p = 0.0;
+  for (int i = 0; i < BL; ++i) {
+    const float pi = __fmul_rn(q[i], zero ? 0.0f : s[i]);
+    block += static_cast<double>(pi);
+    abs_p += fabs(static_cast<double>(pi));
+  }
+  double incl = block;
+  for (int o = 1; o < kWave; o <<= 1) {
+    const double t = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += t;
+  }
+  double prefix = __shfl_up(incl, 1, kWave);
+  if (lane == 0) prefix = 0.0;
+  double abs_prefix = 0.0;
+  for (int i = 0; i < BL; ++i) {
+    prefix += static_cast<double>(__fmul_rn(q[i], zero ? 0.0f : s[i]));
+    abs_prefix += fabs(prefix);
+  }
+  const double s_hat = __shfl(incl, kWave - 1, kWave);
+  abs_prefix = WaveSum(abs_prefix);
+  abs_p = WaveSum(abs_p);
+  if (lane == 0) WriteBounds(s_hat, abs_prefix, abs_p, E, scale, mid_out, lo_out, hi_out, c);
 }
 
 // ---------------------------------------------------------------------------
@@ -132,6 +366,341 @@ __global__ __launch_bounds__(256) void SelectTopKKernel(
   }
   int* out = selected + static_cast<size_t>(r) * top_k;
   for (int i = threadIdx.x; i < kk; i += blockDim.x) out[i] = KeyPage(keys[i]);
+  if (threadIdx.x == 0) counts[r] = kk;
+}
+
+// Bitonic sort of (key, idx) pairs, descending, over m = 2^log_m entries.
+__device__ void BitonicSortDesc(uint64_t* keys, int* idx, int m, int log_m) {
+  const int half = m >> 1;
+  for (int log_size = 1; log_size <= log_m; ++log_size) {
+    const int size = 1 << log_size;
+    for (int log_stride = log_size - 1; log_stride >= 0; --log_stride) {
+      const int stride = 1 << log_stride;
+      for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        const int lo = ((i >> log_stride) << (log_stride + 1)) | (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool descending = (lo & size) == 0;
+        const uint64_t a = keys[lo];
+        const uint64_t b = keys[hi];
+        if ((a < b) == descending) {
+          keys[lo] = b;
+          keys[hi] = a;
+          const int t = idx[lo];
+          idx[lo] = idx[hi];
+          idx[hi] = t;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2b. Certified top-k select.
+//
+// Candidates are sorted by (interval midpoint desc, id asc).  With T the
+// first k, a candidate needs its exact score only if its interval overlaps
+// another relevant one: an outsider whose hi reaches min(lo over T), or a
+// member of T whose interval meets an outsider's or another member's.  Every
+// other comparison is already decided by disjoint intervals, so replacing the
+// flagged candidates' keys by their exact scores and sorting again yields the
+// reference order exactly.  Exact scores come from the reference's sequential
+// chain: all threads form the fp32 products of up to kChainPages flagged
+// pages into LDS, then one lane per page runs the dependent adds.
+// ---------------------------------------------------------------------------
+constexpr int kCertMaxKeys = 2048;   // next-pow2 candidates per request
+constexpr int kChainPages = 8;
+constexpr int kSelectLdsBytes = 64 * 1024;
+
+__global__ __launch_bounds__(256) void SelectCertifiedKernel(
+    const float* __restrict__ mid, const float* __restrict__ lo,
+    const float* __restrict__ hi, const float* __restrict__ queries,
+    const float* __restrict__ summaries, const int* __restrict__ token_counts,
+    const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int E,
+    float scale, int top_k, int chain_floats, int* __restrict__ selected,
+    int* __restrict__ counts, int* __restrict__ exact_pages) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  __shared__ float s_red[2][4];
+  __shared__ int s_nflag;
+  const int r = blockIdx.x;
+  const int begin = cand_offsets[r];
+  const int n = cand_offsets[r + 1] - begin;
+  const int kk = top_k <= 0 ? 0 : (top_k < n ? top_k : n);
+  if (kk == 0) {
+    if (threadIdx.x == 0) counts[r] = 0;
+    return;
+  }
+  int m = 1, log_m = 0;
+  while (m < n) {
+    m <<= 1;
+    ++log_m;
+  }
+  uint64_t* keys = reinterpret_cast<uint64_t*>(smem_raw);
+  int* idx = reinterpret_cast<int*>(keys + m);
+  int* flagged = idx + m;
+  float* s_lo = reinterpret_cast<float*>(flagged + m);
+  float* s_hi = s_lo + m;
+  float* tile = reinterpret_cast<float*>(
+      smem_raw + ((static_cast<size_t>(m) * 24 + 15) & ~static_cast<size_t>(15)));
+
+  for (int i = threadIdx.x; i < m; i += blockDim.x) {
+    if (i < n) {
+      keys[i] = SelectKey(mid[begin + i], cand_ids[begin + i]);
+      idx[i] = i;
+      s_lo[i] = lo[begin + i];
+      s_hi[i] = hi[begin + i];
+    } else {
+      keys[i] = 0ull;
+      idx[i] = -1;
+    }
+  }
+  if (threadIdx.x == 0) s_nflag = 0;
+  __syncthreads();
+  BitonicSortDesc(keys, idx, m, log_m);
+
+  // min lo over T and max hi over the outsiders.
+  float my_min = INFINITY, my_max = -INFINITY;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int cnd = idx[i];
+    if (i < kk) my_min = fminf(my_min, s_lo[cnd]);
+    else my_max = fmaxf(my_max, s_hi[cnd]);
+  }
+  for (int o = 1; o < kWave; o <<= 1) {
+    my_min = fminf(my_min, __shfl_xor(my_min, o, kWave));
+    my_max = fmaxf(my_max, __shfl_xor(my_max, o, kWave));
+  }
+  const int wave = threadIdx.x / kWave;
+  const int nwaves = (blockDim.x + kWave - 1) / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    s_red[0][wave] = my_min;
+    s_red[1][wave] = my_max;
+  }
+  __syncthreads();
+  float min_t_lo = INFINITY, max_o_hi = -INFINITY;
+  for (int w = 0; w < nwaves; ++w) {
+    min_t_lo = fminf(min_t_lo, s_red[0][w]);
+    max_o_hi = fmaxf(max_o_hi, s_red[1][w]);
+  }
+
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int cnd = idx[i];
+    const float l = s_lo[cnd];
+    const float h = s_hi[cnd];
+    bool flag;
+    if (i >= kk) {
+      flag = h >= min_t_lo;
+    } else {
+      flag = l <= max_o_hi;
+      for (int j = 0; j < kk && !flag; ++j) {
+        if (j == i) continue;
+        const int c2 = idx[j];
+        flag = l <= s_hi[c2] && s_lo[c2] <= h;
+      }
+    }
+    if (flag) flagged[atomicAdd(&s_nflag, 1)] = i;
+  }
+  __syncthreads();
+  const int nflag = s_nflag;
+  if (nflag > 0) {
+    if (threadIdx.x == 0 && exact_pages != nullptr) atomicAdd(exact_pages, nflag);
+    const float* __restrict__ q = queries + static_cast<size_t>(r) * E;
+    for (int g0 = 0; g0 < nflag; g0 += kChainPages) {
+      const int G = nflag - g0 < kChainPages ? nflag - g0 : kChainPages;
+      int tile_len = (chain_floats / G - 4) & ~3;
+      if (tile_len > E) tile_len = E;
+      const int stride = tile_len + 4;  // padded rows: conflict-free b128 reads
+      float acc = 0.0f;
+      for (int t0 = 0; t0 < E; t0 += tile_len) {
+        const int len = E - t0 < tile_len ? E - t0 : tile_len;
+        for (int x = threadIdx.x; x < G * len; x += blockDim.x) {
+          const int f = x / len;
+          const int e = x - f * len;
+          const int page = cand_ids[begin + idx[flagged[g0 + f]]];
+          const float sv = token_counts[page] == 0
+                               ? 0.0f
+                               : summaries[static_cast<size_t>(page) * E + t0 + e];
+          tile[f * stride + e] = __fmul_rn(q[t0 + e], sv);
+        }
+        __syncthreads();
+        if (static_cast<int>(threadIdx.x) < G) {
+          const float* row = tile + threadIdx.x * stride;
+          int e = 0;
+          for (; e + 4 <= len; e += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(row + e);
+            acc = __fadd_rn(acc, v.x);
+            acc = __fadd_rn(acc, v.y);
+            acc = __fadd_rn(acc, v.z);
+            acc = __fadd_rn(acc, v.w);
+          }
+          for (; e < len; ++e) acc = __fadd_rn(acc, row[e]);
+        }
+        __syncthreads();
+      }
+      if (static_cast<int>(threadIdx.x) < G) {
+        const int pos = flagged[g0 + threadIdx.x];
+        keys[pos] = SelectKey(__fmul_rn(acc, scale), cand_ids[begin + idx[pos]]);
+      }
+      __syncthreads();
+    }
+    BitonicSortDesc(keys, idx, m, log_m);
+  }
+  int* out = selected + static_cast<size_t>(r) * top_k;
+  for (int i = threadIdx.x; i < kk; i += blockDim.x) out[i] = KeyPage(keys[i]);
+  if (threadIdx.x == 0) counts[r] = kk;
+}
+
+// Exact sequential-chain scores for `nflag` candidates of request r (their
+// candidate indices in flagged[]), written as select keys into keys[].  All
+// threads form the fp32 products of up to kChainPages pages per tile in LDS;
+// one lane per page then runs the dependent adds, so the cost is one chain's
+// latency per group of pages.  Must be called by the whole workgroup.
+constexpr int kRankTile = 1024;
+constexpr int kRankTileStride = kRankTile + 4;
+
+__device__ void RescoreExact(const int* flagged, int nflag, const float* __restrict__ q,
+                             const float* __restrict__ summaries,
+                             const int* __restrict__ token_counts,
+                             const int* __restrict__ cand_ids, int begin, int E, float scale,
+                             float* tile, uint64_t* keys) {
+  for (int g0 = 0; g0 < nflag; g0 += kChainPages) {
+    const int G = nflag - g0 < kChainPages ? nflag - g0 : kChainPages;
+    float acc = 0.0f;
+    for (int t0 = 0; t0 < E; t0 += kRankTile) {
+      const int len = E - t0 < kRankTile ? E - t0 : kRankTile;
+      for (int x = threadIdx.x; x < G * len; x += blockDim.x) {
+        const int f = x / len;
+        const int e = x - f * len;
+        const int page = cand_ids[begin + flagged[g0 + f]];
+        const float sv = token_counts[page] == 0
+                             ? 0.0f
+                             : summaries[static_cast<size_t>(page) * E + t0 + e];
+        tile[f * kRankTileStride + e] = __fmul_rn(q[t0 + e], sv);
+      }
+      __syncthreads();
+      if (static_cast<int>(threadIdx.x) < G) {
+        const float* row = tile + threadIdx.x * kRankTileStride;
+        int e = 0;
+        for (; e + 4 <= len; e += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(row + e);
+          acc = __fadd_rn(acc, v.x);
+          acc = __fadd_rn(acc, v.y);
+          acc = __fadd_rn(acc, v.z);
+          acc = __fadd_rn(acc, v.w);
+        }
+        for (; e < len; ++e) acc = __fadd_rn(acc, row[e]);
+      }
+      __syncthreads();
+    }
+    if (static_cast<int>(threadIdx.x) < G) {
+      const int i = flagged[g0 + threadIdx.x];
+      keys[i] = SelectKey(__fmul_rn(acc, scale), cand_ids[begin + i]);
+    }
+    __syncthreads();
+  }
+}
+
+// Certified select for up to 256 candidates per request: thread i owns
+// candidate i and finds its rank by counting larger keys (broadcast LDS reads,
+// no barrier chain), ties broken by position so ranks are distinct.
+constexpr int kRankMax = 256;
+
+__global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
+    const float* __restrict__ mid, const float* __restrict__ lo,
+    const float* __restrict__ hi, const float* __restrict__ queries,
+    const float* __restrict__ summaries, const int* __restrict__ token_counts,
+    const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int E,
+    float scale, int top_k, int* __restrict__ selected, int* __restrict__ counts,
+    int* __restrict__ exact_pages) {
+  __shared__ uint64_t s_key[kRankMax];
+  __shared__ float s_lo[kRankMax];
+  __shared__ float s_hi[kRankMax];
+  __shared__ int s_top[kRankMax];
+  __shared__ int s_flag[kRankMax];
+  __shared__ float s_red[2][kRankMax / kWave];
+  __shared__ int s_nflag;
+  __shared__ __align__(16) float tile[kChainPages * kRankTileStride];
+  const int r = blockIdx.x;
+  const int begin = cand_offsets[r];
+  const int n = cand_offsets[r + 1] - begin;
+  const int kk = top_k <= 0 ? 0 : (top_k < n ? top_k : n);
+  if (kk == 0) {
+    if (threadIdx.x == 0) counts[r] = 0;
+    return;
+  }
+  const int i = threadIdx.x;
+  const bool active = i < n;
+  if (active) {
+    s_key[i] = SelectKey(mid[begin + i], cand_ids[begin + i]);
+    s_lo[i] = lo[begin + i];
+    s_hi[i] = hi[begin + i];
+  }
+  if (i == 0) s_nflag = 0;
+  __syncthreads();
+  // Keys are read 8 at a time (independent broadcast LDS reads in flight).
+  auto rank_of = [&](int me) {
+    const uint64_t key = s_key[me];
+    int rank = 0;
+    int j = 0;
+    for (; j + 8 <= n; j += 8) {
+      uint64_t kj[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) kj[u] = s_key[j + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        rank += (kj[u] > key || (kj[u] == key && j + u < me)) ? 1 : 0;
+      }
+    }
+    for (; j < n; ++j) {
+      const uint64_t kj = s_key[j];
+      rank += (kj > key || (kj == key && j < me)) ? 1 : 0;
+    }
+    return rank;
+  };
+  int rank = active ? rank_of(i) : n;
+  if (active && rank < kk) s_top[rank] = i;
+  float my_min = (active && rank < kk) ? s_lo[i] : INFINITY;
+  float my_max = (active && rank >= kk) ? s_hi[i] : -INFINITY;
+  for (int o = 1; o < kWave; o <<= 1) {
+    my_min = fminf(my_min, __shfl_xor(my_min, o, kWave));
+    my_max = fmaxf(my_max, __shfl_xor(my_max, o, kWave));
+  }
+  const int wave = threadIdx.x / kWave;
+  const int nwaves = (blockDim.x + kWave - 1) / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    s_red[0][wave] = my_min;
+    s_red[1][wave] = my_max;
+  }
+  __syncthreads();
+  float min_t_lo = INFINITY, max_o_hi = -INFINITY;
+  for (int w = 0; w < nwaves; ++w) {
+    min_t_lo = fminf(min_t_lo, s_red[0][w]);
+    max_o_hi = fmaxf(max_o_hi, s_red[1][w]);
+  }
+  if (active) {
+    const float l = s_lo[i];
+    const float h = s_hi[i];
+    bool flag;
+    if (rank >= kk) {
+      flag = h >= min_t_lo;
+    } else {
+      flag = l <= max_o_hi;
+      for (int j = 0; j < kk && !flag; ++j) {
+        if (j == rank) continue;
+        const int c2 = s_top[j];
+        flag = l <= s_hi[c2] && s_lo[c2] <= h;
+      }
+    }
+    if (flag) s_flag[atomicAdd(&s_nflag, 1)] = i;
+  }
+  __syncthreads();
+  const int nflag = s_nflag;
+  if (nflag > 0) {
+    if (threadIdx.x == 0 && exact_pages != nullptr) atomicAdd(exact_pages, nflag);
+    RescoreExact(s_flag, nflag, queries + static_cast<size_t>(r) * E, summaries,
+                 token_counts, cand_ids, begin, E, scale, tile, s_key);
+    rank = active ? rank_of(i) : n;
+  }
+  if (active && rank < kk) selected[static_cast<size_t>(r) * top_k + rank] = cand_ids[begin + i];
   if (threadIdx.x == 0) counts[r] = kk;
 }
 
@@ -327,6 +896,169 @@ __global__ __launch_bounds__(kAttnThreads) void AttentionKernel(
   }
 }
 
+// Fixed-D variant for the hot shape (D = 128) with the lane split, the
+// waves per workgroup and the chunks in flight per wave as parameters:
+// LPT lanes per token (each owns D/LPT contiguous dims), 64/LPT tokens per
+// chunk, UNROLL chunks whose K and V rows are all requested before any is
+// consumed (bytes in flight per wave = UNROLL * 64/LPT * 2 * D * 4).
+template <int D, int LPT, int WAVES, int UNROLL>
+__global__ __launch_bounds__(WAVES * kWave) void AttentionFastKernel(
+    PoolView pool, AttentionArgs args) {
+  constexpr int DQ = D / LPT;
+  constexpr int TPC = kWave / LPT;
+  static_assert(DQ % 4 == 0, "float4 rows");
+  const int h = blockIdx.x;
+  const int r = blockIdx.y;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int g = lane / LPT;
+  const int j = lane % LPT;
+  const int E = pool.elements;
+  const int ps = pool.page_size;
+  int start, count;
+  if (args.list_stride > 0) {
+    start = r * args.list_stride;
+    count = args.list_counts[r];
+  } else {
+    start = args.list_offsets[r];
+    count = args.list_offsets[r + 1] - start;
+  }
+  const int head_off = h * D + j * DQ;
+  float q[DQ];
+  float acc[DQ];
+  {
+    const float qscale = args.scale * kLog2e;
+    LoadDims<DQ>(args.queries + static_cast<size_t>(r) * E + head_off, q);
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) {
+      q[i] *= qscale;
+      acc[i] = 0.0f;
+    }
+  }
+  float m = -INFINITY;
+  float l = 0.0f;
+  const int total = count * ps;
+  for (int base = wave * TPC * UNROLL; base < total; base += WAVES * TPC * UNROLL) {
+    float kv[UNROLL][DQ];
+    float vv[UNROLL][DQ];
+    bool valid[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int f = base + u * TPC + g;
+      valid[u] = false;
+      if (f < total) {
+        const int slot = f / ps;
+        const int t = f - slot * ps;
+        const int page = args.list_ids[start + slot];
+        valid[u] = t < pool.token_counts[page];
+        if (valid[u]) {
+          const size_t off = static_cast<size_t>(page) * pool.page_elems +
+                             static_cast<size_t>(t) * E + head_off;
+          LoadDims<DQ>(pool.keys + off, kv[u]);
+          LoadDims<DQ>(pool.values + off, vv[u]);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      float dot = 0.0f;
+      if (valid[u]) {
+#pragma unroll
+        for (int i = 0; i < DQ; ++i) dot = fmaf(q[i], kv[u][i], dot);
+      }
+#pragma unroll
+      for (int o = 1; o < LPT; o <<= 1) dot += __shfl_xor(dot, o, kWave);
+      if (valid[u]) {
+        const float m_new = fmaxf(m, dot);
+        const float alpha = Exp2(m - m_new);
+        const float beta = Exp2(dot - m_new);
+        l = fmaf(l, alpha, beta);
+#pragma unroll
+        for (int i = 0; i < DQ; ++i) acc[i] = fmaf(acc[i], alpha, beta * vv[u][i]);
+        m = m_new;
+      }
+    }
+  }
+  // merge the TPC token-slot streams of this wave
+  float wm = m;
+#pragma unroll
+  for (int o = LPT; o < kWave; o <<= 1) wm = fmaxf(wm, __shfl_xor(wm, o, kWave));
+  const float sc = (m == -INFINITY) ? 0.0f : Exp2(m - wm);
+  float wl = l * sc;
+#pragma unroll
+  for (int i = 0; i < DQ; ++i) acc[i] *= sc;
+#pragma unroll
+  for (int o = LPT; o < kWave; o <<= 1) {
+    wl += __shfl_xor(wl, o, kWave);
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) acc[i] += __shfl_xor(acc[i], o, kWave);
+  }
+  __shared__ float s_m[WAVES];
+  __shared__ float s_l[WAVES];
+  __shared__ __align__(16) float s_acc[WAVES][D];
+  if (g == 0) {
+    if (j == 0) {
+      s_m[wave] = wm;
+      s_l[wave] = wl;
+    }
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) s_acc[wave][j * DQ + i] = acc[i];
+  }
+  __syncthreads();
+  float mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, s_m[w]);
+  float* out = args.outputs + static_cast<size_t>(r) * E + static_cast<size_t>(h) * D;
+  for (int d = threadIdx.x; d < D; d += WAVES * kWave) {
+    float lt = 0.0f;
+    float at = 0.0f;
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        const float sw = (s_m[w] == -INFINITY) ? 0.0f : Exp2(s_m[w] - mx);
+        lt = fmaf(s_l[w], sw, lt);
+        at = fmaf(s_acc[w][d], sw, at);
+      }
+    }
+    out[d] = lt == 0.0f ? 0.0f : at / lt;
+  }
+}
+
+using AttnKernelFn = void (*)(PoolView, AttentionArgs);
+
+struct AttnVariant {
+  int lpt, waves, unroll;
+  AttnKernelFn fn;
+};
+
+#define DSD_ATTN_VARIANT(L, W, U) \
+  AttnVariant{L, W, U, AttentionFastKernel<128, L, W, U>}
+const AttnVariant kAttnVariants[] = {
+    DSD_ATTN_VARIANT(4, 4, 1),  DSD_ATTN_VARIANT(4, 4, 2),  DSD_ATTN_VARIANT(4, 8, 1),
+    DSD_ATTN_VARIANT(8, 4, 1),  DSD_ATTN_VARIANT(8, 4, 2),  DSD_ATTN_VARIANT(8, 4, 4),
+    DSD_ATTN_VARIANT(8, 8, 1),  DSD_ATTN_VARIANT(8, 8, 2),  DSD_ATTN_VARIANT(16, 4, 2),
+    DSD_ATTN_VARIANT(16, 4, 4), DSD_ATTN_VARIANT(16, 8, 2), DSD_ATTN_VARIANT(16, 8, 4),
+};
+#undef DSD_ATTN_VARIANT
+
+// The D = 128 variant in use: DSD_ATTN_VARIANT="LPTxWAVESxUNROLL" selects
+// one of kAttnVariants (a tuning knob); otherwise the measured default.
+const AttnVariant& SelectAttnVariant() {
+  int lpt = 16, waves = 8, unroll = 4;
+  if (const char* env = std::getenv("DSD_ATTN_VARIANT")) {
+    int a = 0, b = 0, c = 0;
+    if (std::sscanf(env, "%dx%dx%d", &a, &b, &c) == 3) {
+      lpt = a;
+      waves = b;
+      unroll = c;
+    }
+  }
+  for (const auto& v : kAttnVariants) {
+    if (v.lpt == lpt && v.waves == waves && v.unroll == unroll) return v;
+  }
+  throw std::invalid_argument("unknown DSD_ATTN_VARIANT");
+}
+
 template <int DQ>
 void LaunchAttentionT(const PoolView& pool, const AttentionArgs& args,
                       hipStream_t stream) {
@@ -352,6 +1084,70 @@ void LaunchScoreExact(const PoolView& pool, const float* d_queries,
                        d_queries, pool.summaries, pool.token_counts,
                        d_cand_offsets, d_cand_ids, pool.elements, scale, d_scores);
   }
+  DSD_HIP_CHECK(hipGetLastError());
+}
+
+bool CertifiedScoringSupported(int elements, int max_candidates) {
+  int m = 1;
+  while (m < max_candidates) m <<= 1;
+  return elements % kWave == 0 && elements >= kWave && m <= kCertMaxKeys;
+}
+
+void LaunchScoreBounds(const PoolView& pool, const float* d_queries,
+                       const int* d_cand_offsets, const int* d_cand_ids, int batch,
+                       int total_candidates, int max_candidates, float scale, float* d_mid,
+                       float* d_lo, float* d_hi, hipStream_t stream) {
+  if (batch <= 0 || max_candidates <= 0) return;
+  const dim3 grid((max_candidates + kBoundWaves - 1) / kBoundWaves, batch);
+  const dim3 block(kBoundWaves * kWave);
+  if (pool.elements == 4096 && total_candidates > 0) {
+    hipLaunchKernelGGL(ScoreBoundPageKernel, dim3(total_candidates), dim3(kPageThreads), 0,
+                       stream, d_queries, pool.summaries, pool.token_counts, d_cand_offsets,
+                       d_cand_ids, batch, scale, d_mid, d_lo, d_hi);
+  } else if (pool.elements == 4096) {
+    return;
+  } else {
+    hipLaunchKernelGGL(ScoreBoundGenericKernel, grid, block, 0, stream, d_queries,
+                       pool.summaries, pool.token_counts, d_cand_offsets, d_cand_ids,
+                       pool.elements, scale, d_mid, d_lo, d_hi);
+  }
+  DSD_HIP_CHECK(hipGetLastError());
+}
+
+void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float* d_lo,
+                           const float* d_hi, const float* d_queries,
+                           const int* d_cand_offsets, const int* d_cand_ids, int batch,
+                           int max_candidates, float scale, int top_k, int* d_selected,
+                           int* d_counts, int* d_exact_pages, hipStream_t stream) {
+  if (batch <= 0) return;
+  if (max_candidates <= kRankMax) {
+    int threads = ((max_candidates + kWave - 1) / kWave) * kWave;
+    if (threads < kWave) threads = kWave;
+    hipLaunchKernelGGL(SelectCertifiedRankKernel, dim3(batch), dim3(threads), 0, stream,
+                       d_mid, d_lo, d_hi, d_queries, pool.summaries, pool.token_counts,
+                       d_cand_offsets, d_cand_ids, pool.elements, scale, top_k, d_selected,
+                       d_counts, d_exact_pages);
+    DSD_HIP_CHECK(hipGetLastError());
+    return;
+  }
+  int m = 1;
+  while (m < max_candidates) m <<= 1;
+  if (m > kCertMaxKeys) {
+    throw std::invalid_argument("certified select supports up to " +
+                                std::to_string(kCertMaxKeys) + " candidates per request");
+  }
+  int threads = m / 2;
+  if (threads < kWave) threads = kWave;
+  if (threads > 256) threads = 256;
+  // keys/idx/flag lists and staged bounds, then the rest of 64 KiB for
+  // product tiles.
+  const size_t list_bytes = (static_cast<size_t>(m) * 24 + 15) & ~static_cast<size_t>(15);
+  const int chain_floats = static_cast<int>((kSelectLdsBytes - 256 - list_bytes) / sizeof(float));
+  const size_t lds = list_bytes + sizeof(float) * static_cast<size_t>(chain_floats);
+  hipLaunchKernelGGL(SelectCertifiedKernel, dim3(batch), dim3(threads), lds, stream, d_mid,
+                     d_lo, d_hi, d_queries, pool.summaries, pool.token_counts, d_cand_offsets,
+                     d_cand_ids, pool.elements, scale, top_k, chain_floats, d_selected,
+                     d_counts, d_exact_pages);
   DSD_HIP_CHECK(hipGetLastError());
 }
 
@@ -384,6 +1180,13 @@ void LaunchAttention(const PoolView& pool, const AttentionArgs& args,
   const int D = pool.head_dim;
   if (D <= 0 || D > 256) {
     throw std::invalid_argument("head_dim must be in (0, 256]");
+  }
+  if (D == 128) {
+    const AttnVariant& v = SelectAttnVariant();
+    hipLaunchKernelGGL(v.fn, dim3(pool.num_heads, args.batch), dim3(v.waves * kWave), 0,
+                       stream, pool, args);
+    DSD_HIP_CHECK(hipGetLastError());
+    return;
   }
   switch (D % 4 == 0 ? D / 4 : 0) {
     case 1: LaunchAttentionT<1>(pool, args, stream); break;

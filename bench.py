@@ -124,6 +124,7 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    ctx.exact_rescored_pages(reset=True)
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record(stream)
@@ -133,7 +134,9 @@ def main() -> int:
     stop.synchronize()
     torch.cuda.synchronize()
     ms_per_step = start.elapsed_time(stop) / args.steps
-    log(f"step {ms_per_step * 1e3:.1f} us over {args.steps} steps")
+    rescored = ctx.exact_rescored_pages(reset=True)
+    log(f"step {ms_per_step * 1e3:.1f} us over {args.steps} steps; "
+        f"{rescored} pages rescored exactly")
 
     # Per-kernel average durations: K back-to-back launches of one stage on
     # the same stream, bracketed by HIP events.
@@ -192,6 +195,8 @@ def main() -> int:
             "heads": H, "head_dim": D, "page_size": ps, "top_k": k, "seed": seed,
         },
         "step_hbm_GBps": step_bytes / (ms_per_step * 1e-3) / 1e9,
+        "selection": {"mode": "certified intervals + exact sequential rescoring",
+                      "exact_rescored_pages_per_step": rescored / args.steps},
         "stages": stages,
         "roofline": {"bound": "hbm", "achieved": attn_gbps, "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": attn_gbps / HBM_PEAK_GBPS, "traffic": None,

@@ -170,8 +170,9 @@ int dsd_sparse_destroy(dsd_sparse_ctx* ctx);
  * Outputs (host; may be NULL when not requested by output_mode):
  *   outputs          [batch][E]
  *   scores           [total candidates]             (DSD_OUTPUT_DEBUG)
- *   selected         [sum min(k, n_r)] compact       (DSD_OUTPUT_DEBUG)
- *   selected_counts  [batch]                         (DSD_OUTPUT_DEBUG)
+ *   selected         [sum min(k, n_r)] compact       (DSD_OUTPUT_DEBUG, or
+ *   selected_counts  [batch]                          DSD_OUTPUT_OUTPUTS when
+ *                                                     both are non-NULL)
  * Selected ids equal the reference sparse_cpu selection bit-exactly.
  * timings may be NULL. */
 int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
@@ -200,6 +201,26 @@ int dsd_sparse_replay_stage(dsd_sparse_ctx* ctx, int stage, void* stream);
 
 /* The context's own stream (hipStream_t). */
 void* dsd_sparse_stream(dsd_sparse_ctx* ctx);
+
+/* Scoring mode (no counterpart in the reference, whose GPU scores are a
+ * tree-reduced approximation, src/cuda/sparse_batched_attention.cu:133-151):
+ *   DSD_SCORE_CERTIFIED (default) -- every page gets a rigorous interval
+ *     around its sequential-fp32 score from an HBM-bound parallel kernel;
+ *     only pages whose order the intervals leave open are rescored with the
+ *     sequential chain.  Selection equals sparse_cpu bit for bit.
+ *   DSD_SCORE_EXACT -- every page is scored with the sequential chain.
+ * DSD_OUTPUT_DEBUG always uses exact scores (they are returned). */
+enum { DSD_SCORE_CERTIFIED = 0, DSD_SCORE_EXACT = 1 };
+int dsd_sparse_set_score_mode(dsd_sparse_ctx* ctx, int mode);
+
+/* The first n certified score intervals of the last step (midpoint, lower
+ * and upper bound per candidate, in CSR order).  For verification. */
+int dsd_sparse_score_bounds(dsd_sparse_ctx* ctx, int n, float* mid, float* lo,
+                            float* hi);
+
+/* Pages rescored with the exact chain by certified selects so far (*out);
+ * reset != 0 zeroes the counter.  Synchronizes the device. */
+int dsd_sparse_exact_rescored_pages(dsd_sparse_ctx* ctx, int reset, int* out);
 
 /* ---- dense decode step ------------------------------------------------- */
 /* DenseCudaContext::RunBatch (include/dsd/cuda_dense_attention.h:18-44):

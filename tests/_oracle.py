@@ -125,7 +125,7 @@ def sparse_batch(queries, key_pool, value_pool, summaries, token_counts, cand_of
                               head_dim, page_size, int(top_k), P(scores), P(sel), P(counts),
                               P(outs), P(ms))
     if stage_ms is not None:
-        stage_ms[:] = ms
+        stage_ms += ms
     selected = [sel[r * kk: r * kk + counts[r]].copy() for r in range(B)]
     return scores[:total].copy(), selected, outs
 

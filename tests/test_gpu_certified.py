@@ -1,0 +1,142 @@
+"""Certified scoring (the default selection path) against the oracle.
+
+The certified kernels never compute the reference's sequential score for
+most pages; they bound it.  These tests pin the two claims that make the
+selection exact: (1) every interval contains the exact sparse_cpu score,
+(2) the selected ids equal sparse_cpu's, including inputs built so that
+intervals overlap and the exact fallback must decide (permuted summaries:
+same products in another order, so the sequential sums differ only by
+rounding; duplicated summaries: exactly equal scores)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import _oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def selected_total(offsets, k):
+    return int(sum(min(k, int(n)) for n in np.diff(offsets)))
+
+
+def run_both_paths(gpu, pool, queries, offs, ids, k):
+    total = int(offs[-1])
+    with gpu.SparseContext(pool, k, len(offs) - 1, total, selected_total(offs, k)) as ctx:
+        cert = ctx.run_batch(queries, offs, ids, output_mode=gpu.OUTPUT_OUTPUTS, want_ids=True)
+        bounds = ctx.score_bounds(total)
+        rescored = ctx.exact_rescored_pages()
+        exact = ctx.run_batch(queries, offs, ids, output_mode=gpu.OUTPUT_DEBUG)
+    return cert, bounds, rescored, exact
+
+
+@pytest.mark.parametrize("seed", [7, 8, 9, 10, 11])
+def test_certified_config2_matches_exact_and_oracle(gpu, seed):
+    lengths = gpu.reference_context_lengths(16, 512, 2048, seed)
+    batch = gpu.SyntheticBatch(32, 128, 16, lengths, seed=seed)
+    pool = gpu.DevicePagePool(32, 128, 16, batch.capacity)
+    batch.upload(pool)
+    cert, (mid, lo, hi), rescored, exact = run_both_paths(
+        gpu, pool, batch.queries, batch.cand_offsets, batch.cand_ids, 8)
+    ex = exact["scores"]
+    assert np.all(lo <= ex) and np.all(ex <= hi), "an interval misses the exact score"
+    assert np.all(lo <= mid) and np.all(mid <= hi)
+    for r in range(batch.batch):
+        assert cert["selected"][r].tolist() == exact["selected"][r].tolist(), (seed, r)
+    assert np.array_equal(cert["outputs"].view(np.uint32), exact["outputs"].view(np.uint32))
+    # against the oracle as well
+    summ = np.zeros((batch.capacity, 4096), np.float32)
+    live = batch.live_page_ids()
+    summ[live] = orc.pool_summaries(batch.key_pool, batch.token_counts, 4096, live)
+    _, selected, outs = orc.sparse_batch(batch.queries, batch.key_pool, batch.value_pool, summ,
+                                         batch.token_counts, batch.cand_offsets, batch.cand_ids,
+                                         32, 128, 16, 8)
+    for r in range(batch.batch):
+        assert cert["selected"][r].tolist() == selected[r].tolist()
+    assert orc.max_abs_diff(cert["outputs"], outs) <= 1e-4
+    pool.close()
+
+
+@pytest.mark.parametrize("H,D,ps,k,lengths", [
+    (4, 16, 16, 3, [33, 97, 60, 41]),       # E = 64: generic certified kernel
+    (2, 64, 8, 4, [17, 45, 30]),             # E = 128
+    (8, 32, 4, 16, [400, 250, 3]),           # k > 16
+    (32, 128, 64, 32, [4100, 9000]),         # page 64, k 32
+])
+def test_certified_small_shapes_match_oracle(gpu, H, D, ps, k, lengths):
+    batch = gpu.SyntheticBatch(H, D, ps, lengths, seed=sum(lengths))
+    E = H * D
+    pool = gpu.DevicePagePool(H, D, ps, batch.capacity)
+    batch.upload(pool)
+    cert, (mid, lo, hi), _, exact = run_both_paths(gpu, pool, batch.queries, batch.cand_offsets,
+                                                   batch.cand_ids, k)
+    assert np.all(lo <= exact["scores"]) and np.all(exact["scores"] <= hi)
+    summ = np.zeros((batch.capacity, E), np.float32)
+    live = batch.live_page_ids()
+    summ[live] = orc.pool_summaries(batch.key_pool, batch.token_counts, E, live)
+    _, selected, outs = orc.sparse_batch(batch.queries, batch.key_pool, batch.value_pool, summ,
+                                         batch.token_counts, batch.cand_offsets, batch.cand_ids,
+                                         H, D, ps, k)
+    for r in range(batch.batch):
+        assert cert["selected"][r].tolist() == selected[r].tolist(), r
+    assert orc.max_abs_diff(cert["outputs"], outs) <= 1e-4
+
+
+def adversarial_pool(gpu, rng, H=32, D=128, ps=16, groups=6, copies=4):
+    """Pages whose summaries are permutations / copies of a few base rows."""
+    E = H * D
+    cap = groups * copies
+    keys = np.empty((cap, ps, E), np.float32)
+    base = rng.standard_normal((groups, ps, E)).astype(np.float32)
+    for g in range(groups):
+        for c in range(copies):
+            p = g * copies + c
+            if c == 0 or c == 3:
+                keys[p] = base[g]                      # identical summaries -> exact ties
+            else:
+                perm = rng.permutation(E)               # same multiset of values,
+                keys[p] = base[g][:, perm]              # other order
+    values = rng.standard_normal((cap, ps, E)).astype(np.float32)
+    pool = gpu.DevicePagePool(H, D, ps, cap)
+    ids = np.arange(cap, dtype=np.int32)
+    pool.upload_pages(ids, np.full(cap, ps, np.int32), ids.astype(np.int64) * ps * E, keys, values)
+    return pool, keys, values
+
+
+def test_certified_adversarial_near_ties_take_the_exact_path(gpu):
+    rng = np.random.default_rng(99)
+    H, D, ps = 32, 128, 16
+    E = H * D
+    pool, keys, values = adversarial_pool(gpu, rng)
+    cap = keys.shape[0]
+    # queries constant within permutation groups make permuted pages' scores
+    # equal in exact arithmetic; a second query is generic.
+    q = np.stack([np.full(E, 0.37, np.float32), rng.standard_normal(E).astype(np.float32)])
+    cand = rng.permutation(cap).astype(np.int32)
+    offs = np.array([0, cap, 2 * cap], np.int32)
+    ids = np.concatenate([cand, cand[::-1]]).astype(np.int32)
+    for k in (1, 3, 5, 8, 13):
+        cert, (mid, lo, hi), rescored, exact = run_both_paths(gpu, pool, q, offs, ids, k)
+        assert np.all(lo <= exact["scores"]) and np.all(exact["scores"] <= hi)
+        summ = orc.pool_summaries(keys, np.full(cap, ps, np.int32), E)
+        _, selected, outs = orc.sparse_batch(q, keys, values, summ, np.full(cap, ps, np.int32),
+                                             offs, ids, H, D, ps, k)
+        for r in range(2):
+            assert cert["selected"][r].tolist() == selected[r].tolist(), (k, r)
+            assert exact["selected"][r].tolist() == selected[r].tolist(), (k, r)
+        assert orc.max_abs_diff(cert["outputs"], outs) <= 1e-4
+        assert rescored > 0, "near ties should have needed the exact chain"
+
+
+def test_certified_all_zero_query_ties_resolve_by_page_id(gpu):
+    # Every score is exactly +0: all intervals overlap, every relevant page is
+    # rescored, and the smallest ids win (test_sparse_cuda.cpp:134-169 at scale).
+    rng = np.random.default_rng(5)
+    pool, keys, values = adversarial_pool(gpu, rng, groups=3, copies=4)
+    cap = keys.shape[0]
+    cand = rng.permutation(cap).astype(np.int32)
+    with gpu.SparseContext(pool, 4, 1, cap, 4) as ctx:
+        res = ctx.run_batch(np.zeros((1, 4096), np.float32), np.array([0, cap], np.int32), cand,
+                            output_mode=gpu.OUTPUT_OUTPUTS, want_ids=True)
+    assert res["selected"][0].tolist() == [0, 1, 2, 3]
