@@ -70,6 +70,13 @@ class TransferStats(ctypes.Structure):
         return {n: int(getattr(self, n)) for n, _ in self._fields_}
 
 
+class PoolArrays(ctypes.Structure):
+    _fields_ = [("keys", ctypes.c_void_p), ("values", ctypes.c_void_p),
+                ("summaries", ctypes.c_void_p), ("token_counts", ctypes.c_void_p),
+                ("live", ctypes.c_void_p), ("k_offsets", ctypes.c_void_p),
+                ("v_offsets", ctypes.c_void_p)]
+
+
 class StepTimings(ctypes.Structure):
     _fields_ = [(n, ctypes.c_double) for n in (
         "score_ms", "topk_ms", "attention_ms", "kernel_ms",
@@ -97,6 +104,10 @@ _SIGNATURES = {
     "dsd_pool_download_meta": (ctypes.c_int, [ctypes.c_void_p, _c_int_p, _c_u8_p]),
     "dsd_pool_download_summaries": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p,
                                                    _c_float_p]),
+    "dsd_pool_device_arrays": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(PoolArrays)]),
+    "dsd_pool_prefill_synthetic": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p,
+                                                  _c_int_p, ctypes.c_int]),
+    "dsd_pool_append_synthetic": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int] + [_c_int_p] * 5),
     "dsd_pool_transfer_stats": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(TransferStats)]),
     "dsd_pool_reset_transfer_stats": (ctypes.c_int, [ctypes.c_void_p]),
     "dsd_pool_capacity": (ctypes.c_int, [ctypes.c_void_p]),
@@ -256,6 +267,23 @@ class DevicePagePool:
                                                      _ptr(ids, ctypes.c_int),
                                                      _ptr(out, ctypes.c_float)))
         return out
+
+    def device_arrays(self) -> dict:
+        arr = PoolArrays()
+        _check(self._lib.dsd_pool_device_arrays(self.handle, ctypes.byref(arr)))
+        return {n: int(getattr(arr, n) or 0) for n, _ in arr._fields_}
+
+    def prefill_synthetic(self, page_ids, token_counts, request_id: int) -> None:
+        ids, counts = _i32(page_ids), _i32(token_counts)
+        _check(self._lib.dsd_pool_prefill_synthetic(self.handle, len(ids), _ptr(ids, ctypes.c_int),
+                                                    _ptr(counts, ctypes.c_int), request_id))
+
+    def append_synthetic(self, page_ids, token_offsets, page_token_counts, request_ids,
+                         decode_steps) -> None:
+        arrs = [_i32(a) for a in (page_ids, token_offsets, page_token_counts, request_ids,
+                                  decode_steps)]
+        _check(self._lib.dsd_pool_append_synthetic(self.handle, len(arrs[0]),
+                                                   *[_ptr(a, ctypes.c_int) for a in arrs]))
 
     def transfer_stats(self) -> dict:
         st = TransferStats()

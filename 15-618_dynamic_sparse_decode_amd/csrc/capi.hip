@@ -113,13 +113,18 @@ struct dsd_pool {
   hipStream_t stream = nullptr;
   // staging for metadata / token uploads
   DeviceBuffer<int> stage_ids, stage_counts, stage_offsets, stage_order, stage_segs;
+  DeviceBuffer<int> stage_req, stage_steps;
   DeviceBuffer<float> stage_rows, stage_keys, stage_values;
   // dense-path scratch
   DeviceBuffer<float> dense_q, dense_out;
   DeviceBuffer<int> dense_offsets, dense_ids;
   hipEvent_t dense_start = nullptr, dense_stop = nullptr;
+  uint64_t* k_offsets = nullptr;  // [capacity] element offset of each page
+  uint64_t* v_offsets = nullptr;
 
   ~dsd_pool() {
+    if (k_offsets) (void)hipFree(k_offsets);
+    if (v_offsets) (void)hipFree(v_offsets);
     if (view.keys) (void)hipFree(view.keys);
     if (view.values) (void)hipFree(view.values);
     if (view.summaries) (void)hipFree(view.summaries);
@@ -220,6 +225,15 @@ int dsd_pool_create(int num_heads, int head_dim, int page_size,
                                    pool->stream));
       DSD_HIP_CHECK(hipMemsetAsync(v.live, 0, static_cast<size_t>(capacity_pages),
                                    pool->stream));
+      std::vector<uint64_t> offsets(static_cast<size_t>(capacity_pages));
+      for (int p = 0; p < capacity_pages; ++p) {
+        offsets[p] = static_cast<uint64_t>(p) * static_cast<uint64_t>(v.page_elems);
+      }
+      const size_t off_bytes = sizeof(uint64_t) * offsets.size();
+      DSD_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&pool->k_offsets), off_bytes));
+      DSD_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&pool->v_offsets), off_bytes));
+      DSD_HIP_CHECK(hipMemcpy(pool->k_offsets, offsets.data(), off_bytes, hipMemcpyHostToDevice));
+      DSD_HIP_CHECK(hipMemcpy(pool->v_offsets, offsets.data(), off_bytes, hipMemcpyHostToDevice));
       pool->Sync();
     }
     *out_pool = pool.release();
@@ -498,6 +512,99 @@ int dsd_pool_download_summaries(const dsd_pool* pool, int n,
                 v.summaries + static_cast<size_t>(page_ids[i]) * v.elements,
                 sizeof(float) * v.elements);
     }
+    pool->Sync();
+  });
+}
+
+int dsd_pool_device_arrays(const dsd_pool* pool, dsd_pool_arrays* out) {
+  return Guard([&] {
+    Require(pool != nullptr && out != nullptr, "pointers must be non-null");
+    out->keys = pool->view.keys;
+    out->values = pool->view.values;
+    out->summaries = pool->view.summaries;
+    out->token_counts = pool->view.token_counts;
+    out->live = pool->view.live;
+    out->k_offsets = pool->k_offsets;
+    out->v_offsets = pool->v_offsets;
+  });
+}
+
+int dsd_pool_prefill_synthetic(dsd_pool* pool, int n, const int* page_ids,
+                               const int* token_counts, int request_id) {
+  return Guard([&] {
+    Require(pool != nullptr, "pool must be non-null");
+    Require(n >= 0, "page count must be non-negative");
+    if (n == 0) return;
+    Require(page_ids != nullptr && token_counts != nullptr, "pointers must be non-null");
+    for (int i = 0; i < n; ++i) {
+      pool->ValidatePage(page_ids[i]);
+      pool->ValidateTokenCount(token_counts[i]);
+    }
+    for (int i = 0; i < n; ++i) {
+      pool->host_counts[page_ids[i]] = token_counts[i];
+      pool->host_live[page_ids[i]] = 1;
+    }
+    pool->stage_ids.Reserve(n);
+    pool->stage_counts.Reserve(n);
+    pool->H2D(pool->stage_ids.ptr, page_ids, sizeof(int) * n);
+    pool->H2D(pool->stage_counts.ptr, token_counts, sizeof(int) * n);
+    dsdk::LaunchPrefillSynthetic(pool->view, pool->stage_ids.ptr, pool->stage_counts.ptr, n,
+                                 request_id, pool->stream);
+    pool->Sync();
+  });
+}
+
+int dsd_pool_append_synthetic(dsd_pool* pool, int n, const int* page_ids,
+                              const int* token_offsets, const int* page_token_counts,
+                              const int* request_ids, const int* decode_steps) {
+  return Guard([&] {
+    Require(pool != nullptr, "pool must be non-null");
+    Require(n >= 0, "token count must be non-negative");
+    if (n == 0) return;
+    Require(page_ids != nullptr && token_offsets != nullptr && page_token_counts != nullptr &&
+                request_ids != nullptr && decode_steps != nullptr,
+            "pointers must be non-null");
+    for (int i = 0; i < n; ++i) {
+      pool->ValidatePage(page_ids[i]);
+      pool->ValidateTokenCount(page_token_counts[i]);
+      if (token_offsets[i] < 0 || token_offsets[i] >= page_token_counts[i]) {
+        throw std::out_of_range("token_offset is outside the valid page prefix");
+      }
+    }
+    std::vector<int> order(n);
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+      if (page_ids[a] != page_ids[b]) return page_ids[a] < page_ids[b];
+      return token_offsets[a] < token_offsets[b];
+    });
+    std::vector<int> segs{0};
+    for (int q = 1; q < n; ++q) {
+      if (page_ids[order[q]] != page_ids[order[q - 1]]) segs.push_back(q);
+    }
+    segs.push_back(n);
+    const int nseg = static_cast<int>(segs.size()) - 1;
+    for (int q = 0; q < n; ++q) {
+      pool->host_counts[page_ids[q]] = page_token_counts[q];
+      pool->host_live[page_ids[q]] = 1;
+    }
+    pool->stage_ids.Reserve(n);
+    pool->stage_offsets.Reserve(n);
+    pool->stage_counts.Reserve(n);
+    pool->stage_order.Reserve(n);
+    pool->stage_segs.Reserve(nseg + 1);
+    pool->stage_req.Reserve(n);
+    pool->stage_steps.Reserve(n);
+    pool->H2D(pool->stage_ids.ptr, page_ids, sizeof(int) * n);
+    pool->H2D(pool->stage_offsets.ptr, token_offsets, sizeof(int) * n);
+    pool->H2D(pool->stage_counts.ptr, page_token_counts, sizeof(int) * n);
+    pool->H2D(pool->stage_order.ptr, order.data(), sizeof(int) * n);
+    pool->H2D(pool->stage_segs.ptr, segs.data(), sizeof(int) * (nseg + 1));
+    pool->H2D(pool->stage_req.ptr, request_ids, sizeof(int) * n);
+    pool->H2D(pool->stage_steps.ptr, decode_steps, sizeof(int) * n);
+    dsdk::LaunchAppendSynthetic(pool->view, pool->stage_segs.ptr, pool->stage_order.ptr,
+                                pool->stage_ids.ptr, pool->stage_offsets.ptr,
+                                pool->stage_counts.ptr, pool->stage_req.ptr,
+                                pool->stage_steps.ptr, nseg, pool->stream);
     pool->Sync();
   });
 }

@@ -59,6 +59,15 @@ void LaunchAppendTokens(const PoolView& pool, const int* d_seg_start,
                         const float* d_rows, int num_segments,
                         hipStream_t stream);
 
+// Synthetic GPU-resident admission (integer-hash payloads).
+void LaunchPrefillSynthetic(const PoolView& pool, const int* d_page_ids,
+                            const int* d_token_counts, int n, int request_id,
+                            hipStream_t stream);
+void LaunchAppendSynthetic(const PoolView& pool, const int* d_seg_start, const int* d_order,
+                           const int* d_page_ids, const int* d_offsets, const int* d_counts,
+                           const int* d_request_ids, const int* d_decode_steps,
+                           int num_segments, hipStream_t stream);
+
 // Clears token count, live flag and summary row of n pages.
 void LaunchMarkFree(const PoolView& pool, const int* d_page_ids, int n,
                     hipStream_t stream);

@@ -1,0 +1,667 @@
+// continuous_batching.cpp -- the continuous-batching serving loop (behaviour
+// of reference src/continuous_batching.cpp:24-1039): workload generation,
+// the three prompt admission modes, per-step RunBatch over the active set,
+// decode-token append (host payloads, or device-generated in the synthetic
+// mode), page release, and the step statistics.  Every device-side update
+// goes through SparseCudaContext / DenseCudaContext (libdsd_hip.so).
+#include "dsd/continuous_batching.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdint>
+#include <deque>
+#include <numeric>
+#include <random>
+#include <stdexcept>
+#include <unordered_set>
+#include <utility>
+
+#include "dsd/cuda_dense_attention.h"
+#include "dsd/paged_kv_cache.h"
+#include "dsd/reference_kernels.h"
+
+namespace dsd {
+
+namespace {
+
+using Clock = std::chrono::steady_clock;
+
+double Ms(Clock::time_point a, Clock::time_point b) {
+  return std::chrono::duration<double, std::milli>(b - a).count();
+}
+
+int Ept(const ModelConfig& c) { return c.num_heads * c.head_dim; }
+
+int PagesFor(const ModelConfig& c, int tokens) {
+  return tokens <= 0 ? 0 : (tokens + c.page_size - 1) / c.page_size;
+}
+
+std::vector<float> Uniform(int count, std::mt19937& rng) {
+  std::uniform_real_distribution<float> dist(-1.0f, 1.0f);
+  std::vector<float> v(static_cast<std::size_t>(count));
+  for (float& x : v) x = dist(rng);
+  return v;
+}
+
+// Seed of the per-(request, step, stream) decode payload generator
+// (reference src/continuous_batching.cpp:44-59); streams 0 = next query,
+// 1 = key, 2 = value.
+std::uint32_t StepSeed(int request_id, int decode_step, int stream) {
+  std::uint32_t x = 0x9e3779b9u;
+  x ^= static_cast<std::uint32_t>(request_id) + 0x85ebca6bu + (x << 6) + (x >> 2);
+  x ^= static_cast<std::uint32_t>(decode_step) + 0xc2b2ae35u + (x << 6) + (x >> 2);
+  x ^= static_cast<std::uint32_t>(stream) + 0x27d4eb2fu + (x << 6) + (x >> 2);
+  return x;
+}
+
+std::vector<float> TokenVector(int count, int request_id, int decode_step, int stream) {
+  std::mt19937 rng(StepSeed(request_id, decode_step, stream));
+  return Uniform(count, rng);
+}
+
+int CapacityFor(const ModelConfig& c, const std::vector<ContinuousRequestSpec>& specs) {
+  int pages = 0;
+  for (const auto& s : specs) pages += PagesFor(c, s.prompt_tokens) + PagesFor(c, s.decode_steps);
+  return std::max(pages, 1);
+}
+
+int MaxPagesPerRequest(const ModelConfig& c, const std::vector<ContinuousRequestSpec>& specs) {
+  int m = 0;
+  for (const auto& s : specs) {
+    m = std::max(m, PagesFor(c, s.prompt_tokens) + PagesFor(c, s.decode_steps));
+  }
+  return std::max(m, 1);
+}
+
+void Add(StageTimings* d, const StageTimings& s) {
+  d->page_scoring_ms += s.page_scoring_ms;
+  d->topk_ms += s.topk_ms;
+  d->gather_ms += s.gather_ms;
+  d->attention_ms += s.attention_ms;
+  d->total_ms += s.total_ms;
+}
+
+void Add(RuntimeOverheadTimings* d, const RuntimeOverheadTimings& s) {
+  d->time_malloc_ms += s.time_malloc_ms;
+  d->time_memcpy_h2d_ms += s.time_memcpy_h2d_ms;
+  d->time_memcpy_d2h_ms += s.time_memcpy_d2h_ms;
+  d->time_free_ms += s.time_free_ms;
+  d->time_kernel_launch_ms += s.time_kernel_launch_ms;
+  d->time_sync_ms += s.time_sync_ms;
+  d->time_prepare_sparse_layout_ms += s.time_prepare_sparse_layout_ms;
+}
+
+void Add(DeviceTransferStats* d, const DeviceTransferStats& s) {
+  d->h2d_bytes += s.h2d_bytes;
+  d->d2h_bytes += s.d2h_bytes;
+  d->h2d_calls += s.h2d_calls;
+  d->d2h_calls += s.d2h_calls;
+  d->h2d_large_calls += s.h2d_large_calls;
+  d->d2h_large_calls += s.d2h_large_calls;
+}
+
+void Scale(StageTimings* t, double f) {
+  t->page_scoring_ms *= f;
+  t->topk_ms *= f;
+  t->gather_ms *= f;
+  t->attention_ms *= f;
+  t->total_ms *= f;
+}
+
+void Scale(RuntimeOverheadTimings* t, double f) {
+  t->time_malloc_ms *= f;
+  t->time_memcpy_h2d_ms *= f;
+  t->time_memcpy_d2h_ms *= f;
+  t->time_free_ms *= f;
+  t->time_kernel_launch_ms *= f;
+  t->time_sync_ms *= f;
+  t->time_prepare_sparse_layout_ms *= f;
+}
+
+double Percentile(std::vector<double> v, double q) {
+  if (v.empty()) return 0.0;
+  std::sort(v.begin(), v.end());
+  const double pos = q * static_cast<double>(v.size() - 1);
+  const auto lo = static_cast<std::size_t>(std::floor(pos));
+  const auto hi = static_cast<std::size_t>(std::ceil(pos));
+  if (lo == hi) return v[lo];
+  const double f = pos - static_cast<double>(lo);
+  return v[lo] * (1.0 - f) + v[hi] * f;
+}
+
+void Validate(const ModelConfig& c, const std::vector<ContinuousRequestSpec>& specs) {
+  const int E = Ept(c);
+  std::unordered_set<int> ids;
+  for (const auto& s : specs) {
+    if (s.request_id < 0) throw std::invalid_argument("request_id must be non-negative");
+    if (s.arrival_step < 0 || s.prompt_tokens < 0 || s.decode_steps < 0) {
+      throw std::invalid_argument("continuous request counts must be non-negative");
+    }
+    const std::size_t n = static_cast<std::size_t>(s.prompt_tokens) * E;
+    if (s.prompt_keys.size() != n || s.prompt_values.size() != n) {
+      throw std::invalid_argument("prompt payload size does not match prompt_tokens");
+    }
+    if (static_cast<int>(s.initial_query.size()) != E) {
+      throw std::invalid_argument("initial query size does not match model config");
+    }
+  }
+  for (const auto& s : specs) {
+    if (!ids.insert(s.request_id).second) {
+      throw std::invalid_argument("continuous workload request_id values must be unique");
+    }
+  }
+}
+
+std::vector<int> PromptPageCounts(const ModelConfig& c, const ContinuousRequestSpec& s) {
+  std::vector<int> counts;
+  for (int t = 0; t < s.prompt_tokens; t += c.page_size) {
+    counts.push_back(std::min(c.page_size, s.prompt_tokens - t));
+  }
+  return counts;
+}
+
+// kCpuCache admission: pages appended to the host cache.  A tail page that
+// will receive decode tokens keeps a summary (reference :167-193).
+std::vector<PageId> AdmitToCache(const ModelConfig& c, const ContinuousRequestSpec& s,
+                                 PagedKvCache* cache) {
+  const int E = Ept(c);
+  std::vector<PageId> ids;
+  for (int t = 0; t < s.prompt_tokens; t += c.page_size) {
+    const int n = std::min(c.page_size, s.prompt_tokens - t);
+    const bool tail = t + n == s.prompt_tokens;
+    const bool summary = tail && n < c.page_size && s.decode_steps > 0;
+    const std::size_t at = static_cast<std::size_t>(t) * E;
+    ids.push_back(cache->AppendPage(s.request_id, s.prompt_keys.data() + at,
+                                    s.prompt_values.data() + at, n, summary));
+  }
+  return ids;
+}
+
+std::vector<PageId> AdmitPrompt(const ModelConfig& c, const ContinuousRequestSpec& s,
+                                ContinuousPromptAdmissionMode mode, PagedKvCache* cache,
+                                SparseCudaContext* ctx) {
+  if (mode == ContinuousPromptAdmissionMode::kCpuCache) {
+    auto ids = AdmitToCache(c, s, cache);
+    ctx->SyncPagesFromCache(*cache, ids);
+    return ids;
+  }
+  const auto counts = PromptPageCounts(c, s);
+  auto ids = cache->ReservePagesForRequest(s.request_id, counts);
+  if (mode == ContinuousPromptAdmissionMode::kDirectGpuUpload) {
+    ctx->SyncPromptDirect(*cache, ids, counts, s.prompt_keys.data(), s.prompt_values.data());
+    return ids;
+  }
+  if (mode == ContinuousPromptAdmissionMode::kSyntheticGpuPrefill) {
+    ctx->PrefillPromptSynthetic(*cache, ids, counts, s.request_id);
+    return ids;
+  }
+  throw std::invalid_argument("unknown prompt admission mode");
+}
+
+struct DecodePayloads {
+  std::vector<std::vector<float>> next_queries, keys, values;
+};
+
+DecodePayloads BuildPayloads(const ModelConfig& c,
+                             const std::vector<ContinuousRequestSpec>& specs, bool kv) {
+  const int E = Ept(c);
+  DecodePayloads p;
+  p.next_queries.resize(specs.size());
+  if (kv) {
+    p.keys.resize(specs.size());
+    p.values.resize(specs.size());
+  }
+  for (std::size_t i = 0; i < specs.size(); ++i) {
+    const auto& s = specs[i];
+    for (int step = 0; step < s.decode_steps; ++step) {
+      auto q = TokenVector(E, s.request_id, step + 1, 0);
+      p.next_queries[i].insert(p.next_queries[i].end(), q.begin(), q.end());
+      if (kv) {
+        auto k = TokenVector(E, s.request_id, step, 1);
+        auto v = TokenVector(E, s.request_id, step, 2);
+        p.keys[i].insert(p.keys[i].end(), k.begin(), k.end());
+        p.values[i].insert(p.values[i].end(), v.begin(), v.end());
+      }
+    }
+  }
+  return p;
+}
+
+const float* Row(const std::vector<float>& v, int step, int E) {
+  return v.data() + static_cast<std::size_t>(step) * static_cast<std::size_t>(E);
+}
+
+void FinishStats(ContinuousBatchStats* stats, Clock::time_point wall_start,
+                 const std::vector<double>& step_ms, const StageTimings& timings,
+                 const RuntimeOverheadTimings& overheads, int steps, int batch_sum) {
+  stats->total_wall_ms = Ms(wall_start, Clock::now());
+  stats->tokens_per_second = stats->total_wall_ms > 0.0
+                                 ? stats->total_generated_tokens / (stats->total_wall_ms / 1e3)
+                                 : 0.0;
+  stats->outside_run_batch_ms = std::max(0.0, stats->total_wall_ms - stats->run_batch_wall_ms);
+  stats->serving_loop_other_ms =
+      std::max(0.0, stats->total_wall_ms - stats->run_batch_wall_ms -
+                        stats->runtime_admission_ms - stats->append_sync_ms -
+                        stats->release_sync_ms);
+  stats->measured_end_to_end_ms =
+      stats->decode_payload_prep_ms + stats->prompt_preadmit_ms + stats->total_wall_ms;
+  stats->avg_step_ms =
+      step_ms.empty() ? 0.0
+                      : std::accumulate(step_ms.begin(), step_ms.end(), 0.0) /
+                            static_cast<double>(step_ms.size());
+  stats->p50_step_ms = Percentile(step_ms, 0.50);
+  stats->p95_step_ms = Percentile(step_ms, 0.95);
+  stats->avg_active_batch_size =
+      steps > 0 ? static_cast<double>(batch_sum) / static_cast<double>(steps) : 0.0;
+  if (steps > 0) {
+    stats->avg_sparse_timings = timings;
+    Scale(&stats->avg_sparse_timings, 1.0 / steps);
+    stats->avg_runtime_overheads = overheads;
+    Scale(&stats->avg_runtime_overheads, 1.0 / steps);
+  }
+}
+
+}  // namespace
+
+std::vector<ContinuousRequestSpec> BuildSyntheticContinuousWorkload(
+    const ModelConfig& config, int num_requests, int arrival_window, int min_prompt_tokens,
+    int max_prompt_tokens, int min_decode_steps, int max_decode_steps, int seed) {
+  if (num_requests < 0 || arrival_window < 0 || min_prompt_tokens < 0 ||
+      max_prompt_tokens < min_prompt_tokens || min_decode_steps < 0 ||
+      max_decode_steps < min_decode_steps) {
+    throw std::invalid_argument("invalid continuous workload parameters");
+  }
+  std::mt19937 rng(static_cast<std::mt19937::result_type>(seed));
+  std::uniform_int_distribution<int> arrival(0, std::max(0, arrival_window));
+  std::uniform_int_distribution<int> prompt(min_prompt_tokens, max_prompt_tokens);
+  std::uniform_int_distribution<int> decode(min_decode_steps, max_decode_steps);
+  const int E = Ept(config);
+  std::vector<ContinuousRequestSpec> specs;
+  specs.reserve(static_cast<std::size_t>(num_requests));
+  for (int id = 0; id < num_requests; ++id) {
+    ContinuousRequestSpec s;
+    s.request_id = id;
+    s.arrival_step = arrival(rng);
+    s.prompt_tokens = prompt(rng);
+    s.decode_steps = decode(rng);
+    s.prompt_keys = Uniform(s.prompt_tokens * E, rng);
+    s.prompt_values = Uniform(s.prompt_tokens * E, rng);
+    s.initial_query = Uniform(E, rng);
+    specs.push_back(std::move(s));
+  }
+  std::sort(specs.begin(), specs.end(),
+            [](const ContinuousRequestSpec& a, const ContinuousRequestSpec& b) {
+              if (a.arrival_step == b.arrival_step) return a.request_id < b.request_id;
+              return a.arrival_step < b.arrival_step;
+            });
+  return specs;
+}
+
+ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
+                                               const std::vector<ContinuousRequestSpec>& specs,
+                                               int max_active_requests) {
+  ContinuousDecodeOptions options;
+  options.max_active_requests = max_active_requests;
+  return RunContinuousSparseDecode(config, specs, options);
+}
+
+ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
+                                               const std::vector<ContinuousRequestSpec>& specs,
+                                               const ContinuousDecodeOptions& options) {
+  if (options.max_active_requests <= 0) {
+    throw std::invalid_argument("max_active_requests must be positive");
+  }
+  if (!SparseAttentionCudaAvailable()) {
+    throw std::runtime_error("continuous sparse decode requires a visible gfx950 GPU");
+  }
+  if (options.gpu_synthetic_decode_append &&
+      options.prompt_admission_mode == ContinuousPromptAdmissionMode::kCpuCache) {
+    throw std::invalid_argument(
+        "gpu_synthetic_decode_append requires a GPU-resident prompt admission mode");
+  }
+  Validate(config, specs);
+  const int E = Ept(config);
+  const int total_pages = CapacityFor(config, specs);
+  const int max_pages = MaxPagesPerRequest(config, specs);
+  const int window_pages = std::max(1, options.max_active_requests * max_pages);
+  const int capacity =
+      options.preadmit_prompts ? total_pages : std::min(total_pages, window_pages);
+  const int max_candidates = options.max_active_requests * max_pages;
+  const int max_selected =
+      options.max_active_requests * std::min(config.top_k_pages, max_pages);
+  const bool metadata_only =
+      options.prompt_admission_mode != ContinuousPromptAdmissionMode::kCpuCache;
+  PagedKvCache cache(config, capacity, !metadata_only);
+  SparseCudaContext ctx(cache, config, options.max_active_requests, max_candidates,
+                        max_selected);
+  ctx.ResetDeviceTransferStats();
+
+  ContinuousBatchStats stats;
+  DecodePayloads payloads;
+  if (options.precompute_decode_payloads) {
+    const auto t0 = Clock::now();
+    payloads = BuildPayloads(config, specs, !options.gpu_synthetic_decode_append);
+    stats.decode_payload_prep_ms = Ms(t0, Clock::now());
+  }
+  std::vector<double> step_ms;
+  StageTimings timings;
+  RuntimeOverheadTimings overheads;
+  int steps_run = 0;
+  int batch_sum = 0;
+  std::deque<std::size_t> pending;
+  std::vector<ActiveDecodeRequest> active;
+  active.reserve(static_cast<std::size_t>(options.max_active_requests));
+  std::vector<const RequestState*> batch;
+  std::vector<std::uint8_t> admitted(specs.size(), 0);
+
+  if (options.preadmit_prompts) {
+    for (std::size_t i = 0; i < specs.size(); ++i) {
+      const auto t0 = Clock::now();
+      AdmitPrompt(config, specs[i], options.prompt_admission_mode, &cache, &ctx);
+      const double ms = Ms(t0, Clock::now());
+      stats.admission_ms += ms;
+      stats.prompt_preadmit_ms += ms;
+      admitted[i] = 1;
+    }
+    stats.admission_device_transfer_stats = ctx.DeviceTransfers();
+    ctx.ResetDeviceTransferStats();
+  }
+
+  std::size_t next = 0;
+  int step = 0;
+  const auto wall_start = Clock::now();
+  while (next < specs.size() || !pending.empty() || !active.empty()) {
+    if (active.empty() && pending.empty() && next < specs.size() &&
+        step < specs[next].arrival_step) {
+      step = specs[next].arrival_step;
+    }
+    while (next < specs.size() && specs[next].arrival_step <= step) pending.push_back(next++);
+    while (static_cast<int>(active.size()) < options.max_active_requests && !pending.empty()) {
+      const std::size_t i = pending.front();
+      pending.pop_front();
+      const auto& s = specs[i];
+      if (!admitted[i]) {
+        const auto t0 = Clock::now();
+        AdmitPrompt(config, s, options.prompt_admission_mode, &cache, &ctx);
+        const double ms = Ms(t0, Clock::now());
+        stats.admission_ms += ms;
+        stats.runtime_admission_ms += ms;
+        admitted[i] = 1;
+      }
+      if (s.decode_steps > 0) {
+        ActiveDecodeRequest a;
+        a.state = MakeRequestState(s.request_id, s.initial_query, cache, s.prompt_tokens);
+        a.remaining_decode_steps = s.decode_steps;
+        a.spec_index = i;
+        active.push_back(std::move(a));
+      } else {
+        const auto freed = cache.ReleaseRequest(s.request_id);
+        if (!options.lazy_release) ctx.SyncFreedPages(freed);
+      }
+    }
+    if (active.empty()) {
+      ++step;
+      continue;
+    }
+
+    const auto t_step = Clock::now();
+    batch.clear();
+    for (const auto& a : active) batch.push_back(&a.state);
+    SparseRunBatchOptions run;
+    run.output_mode = options.run_batch_output_mode;
+    run.timing_mode = options.run_batch_timing_mode;
+    const auto result = ctx.RunBatch(batch, run);
+    const double ms = Ms(t_step, Clock::now());
+    stats.run_batch_wall_ms += ms;
+    step_ms.push_back(ms);
+    Add(&timings, result.aggregate_timings);
+    Add(&overheads, result.runtime_overheads);
+    ++steps_run;
+    batch_sum += static_cast<int>(active.size());
+
+    std::vector<AppendTokenResult> appended;
+    std::vector<float> keys, values;
+    std::vector<int> synth_requests, synth_steps;
+    for (auto& a : active) {
+      const int id = a.state.request_id;
+      const int dstep = a.decode_step_index;
+      std::vector<float> gk, gv;
+      const float* k = nullptr;
+      const float* v = nullptr;
+      if (!options.gpu_synthetic_decode_append) {
+        if (options.precompute_decode_payloads) {
+          k = Row(payloads.keys[a.spec_index], dstep, E);
+          v = Row(payloads.values[a.spec_index], dstep, E);
+        } else {
+          gk = TokenVector(E, id, dstep, 1);
+          gv = TokenVector(E, id, dstep, 2);
+          k = gk.data();
+          v = gv.data();
+        }
+      }
+      // Decode tokens of GPU-admitted prompts start a fresh page (:614-616).
+      const bool force_new = metadata_only && dstep == 0;
+      const auto r = options.gpu_synthetic_decode_append
+                         ? cache.AppendTokenMetadataOnly(id, force_new)
+                         : (metadata_only ? cache.AppendTokenMetadataOnly(id, k, force_new)
+                                          : cache.AppendToken(id, k, v, force_new));
+      // The last decode token is never attended to, so it is not uploaded.
+      if (a.remaining_decode_steps > 1) {
+        appended.push_back(r);
+        if (options.gpu_synthetic_decode_append) {
+          synth_requests.push_back(id);
+          synth_steps.push_back(dstep);
+        } else if (metadata_only) {
+          keys.insert(keys.end(), k, k + E);
+          values.insert(values.end(), v, v + E);
+        }
+      }
+      ++a.state.context_tokens;
+      const auto& pages = cache.GetRequestPages(id);
+      a.state.candidate_page_ids.assign(pages.begin(), pages.end());
+      if (options.precompute_decode_payloads) {
+        const float* q = Row(payloads.next_queries[a.spec_index], dstep, E);
+        a.state.query.assign(q, q + E);
+      } else {
+        a.state.query = TokenVector(E, id, dstep + 1, 0);
+      }
+      ++a.decode_step_index;
+      --a.remaining_decode_steps;
+      ++stats.total_generated_tokens;
+    }
+    const auto t_append = Clock::now();
+    if (options.gpu_synthetic_decode_append) {
+      ctx.AppendSyntheticTokens(cache, appended, synth_requests, synth_steps);
+    } else if (metadata_only) {
+      ctx.SyncAppendedTokensDirect(cache, appended, keys, values);
+    } else {
+      ctx.SyncAppendedTokens(cache, appended);
+    }
+    stats.append_sync_ms += Ms(t_append, Clock::now());
+
+    std::vector<PageId> freed;
+    active.erase(std::remove_if(active.begin(), active.end(),
+                                [&](const ActiveDecodeRequest& a) {
+                                  if (a.remaining_decode_steps > 0) return false;
+                                  const auto ids = cache.ReleaseRequest(a.state.request_id);
+                                  freed.insert(freed.end(), ids.begin(), ids.end());
+                                  return true;
+                                }),
+                 active.end());
+    const auto t_release = Clock::now();
+    if (!options.lazy_release) ctx.SyncFreedPages(freed);
+    stats.release_sync_ms += Ms(t_release, Clock::now());
+    ++step;
+  }
+  FinishStats(&stats, wall_start, step_ms, timings, overheads, steps_run, batch_sum);
+  Add(&stats.device_transfer_stats, ctx.DeviceTransfers());
+  return stats;
+}
+
+ContinuousBatchStats RunContinuousDenseGpuDecode(
+    const ModelConfig& config, const std::vector<ContinuousRequestSpec>& specs,
+    int max_active_requests) {
+  ContinuousDecodeOptions options;
+  options.max_active_requests = max_active_requests;
+  return RunContinuousDenseGpuDecode(config, specs, options);
+}
+
+ContinuousBatchStats RunContinuousDenseGpuDecode(
+    const ModelConfig& config, const std::vector<ContinuousRequestSpec>& specs,
+    const ContinuousDecodeOptions& options) {
+  if (options.max_active_requests <= 0) {
+    throw std::invalid_argument("max_active_requests must be positive");
+  }
+  if (!DenseAttentionCudaAvailable()) {
+    throw std::runtime_error("continuous dense decode requires a visible gfx950 GPU");
+  }
+  Validate(config, specs);
+  const int E = Ept(config);
+  PagedKvCache cache(config, CapacityFor(config, specs), true);
+  DenseCudaContext ctx(cache, config);
+  ContinuousBatchStats stats;
+  DecodePayloads payloads;
+  if (options.precompute_decode_payloads) {
+    const auto t0 = Clock::now();
+    payloads = BuildPayloads(config, specs, true);
+    stats.decode_payload_prep_ms = Ms(t0, Clock::now());
+  }
+  std::vector<double> step_ms;
+  StageTimings timings;
+  RuntimeOverheadTimings overheads;
+  int steps_run = 0;
+  int batch_sum = 0;
+  std::deque<std::size_t> pending;
+  std::vector<ActiveDecodeRequest> active;
+  std::vector<RequestState> batch;
+  std::vector<std::uint8_t> admitted(specs.size(), 0);
+  auto admit = [&](std::size_t i, double* sink) {
+    const auto t0 = Clock::now();
+    ctx.SyncPagesFromCache(cache, AdmitToCache(config, specs[i], &cache));
+    const double ms = Ms(t0, Clock::now());
+    stats.admission_ms += ms;
+    *sink += ms;
+    admitted[i] = 1;
+  };
+  if (options.preadmit_prompts) {
+    for (std::size_t i = 0; i < specs.size(); ++i) admit(i, &stats.prompt_preadmit_ms);
+  }
+  std::size_t next = 0;
+  int step = 0;
+  const auto wall_start = Clock::now();
+  while (next < specs.size() || !pending.empty() || !active.empty()) {
+    if (active.empty() && pending.empty() && next < specs.size() &&
+        step < specs[next].arrival_step) {
+      step = specs[next].arrival_step;
+    }
+    while (next < specs.size() && specs[next].arrival_step <= step) pending.push_back(next++);
+    while (static_cast<int>(active.size()) < options.max_active_requests && !pending.empty()) {
+      const std::size_t i = pending.front();
+      pending.pop_front();
+      if (!admitted[i]) admit(i, &stats.runtime_admission_ms);
+      const auto& s = specs[i];
+      if (s.decode_steps > 0) {
+        ActiveDecodeRequest a;
+        a.state = MakeRequestState(s.request_id, s.initial_query, cache, s.prompt_tokens);
+        a.remaining_decode_steps = s.decode_steps;
+        a.spec_index = i;
+        active.push_back(std::move(a));
+      } else {
+        const auto freed = cache.ReleaseRequest(s.request_id);
+        if (!options.lazy_release) ctx.SyncFreedPages(freed);
+      }
+    }
+    if (active.empty()) {
+      ++step;
+      continue;
+    }
+    const auto t_step = Clock::now();
+    batch.clear();
+    for (const auto& a : active) batch.push_back(a.state);
+    const auto result = ctx.RunBatch(batch);
+    const double ms = Ms(t_step, Clock::now());
+    stats.run_batch_wall_ms += ms;
+    step_ms.push_back(ms);
+    timings.attention_ms += result.kernel_ms;
+    timings.total_ms += result.kernel_ms;
+    Add(&overheads, result.runtime_overheads);
+    ++steps_run;
+    batch_sum += static_cast<int>(active.size());
+
+    std::vector<AppendTokenResult> appended;
+    for (auto& a : active) {
+      const int id = a.state.request_id;
+      const int dstep = a.decode_step_index;
+      std::vector<float> gk, gv;
+      const float* k;
+      const float* v;
+      if (options.precompute_decode_payloads) {
+        k = Row(payloads.keys[a.spec_index], dstep, E);
+        v = Row(payloads.values[a.spec_index], dstep, E);
+      } else {
+        gk = TokenVector(E, id, dstep, 1);
+        gv = TokenVector(E, id, dstep, 2);
+        k = gk.data();
+        v = gv.data();
+      }
+      const auto r = cache.AppendToken(id, k, v, false);
+      if (a.remaining_decode_steps > 1) appended.push_back(r);
+      ++a.state.context_tokens;
+      const auto& pages = cache.GetRequestPages(id);
+      a.state.candidate_page_ids.assign(pages.begin(), pages.end());
+      if (options.precompute_decode_payloads) {
+        const float* q = Row(payloads.next_queries[a.spec_index], dstep, E);
+        a.state.query.assign(q, q + E);
+      } else {
+        a.state.query = TokenVector(E, id, dstep + 1, 0);
+      }
+      ++a.decode_step_index;
+      --a.remaining_decode_steps;
+      ++stats.total_generated_tokens;
+    }
+    const auto t_append = Clock::now();
+    ctx.SyncAppendedTokens(cache, appended);
+    stats.append_sync_ms += Ms(t_append, Clock::now());
+    std::vector<PageId> freed;
+    active.erase(std::remove_if(active.begin(), active.end(),
+                                [&](const ActiveDecodeRequest& a) {
+                                  if (a.remaining_decode_steps > 0) return false;
+                                  const auto ids = cache.ReleaseRequest(a.state.request_id);
+                                  freed.insert(freed.end(), ids.begin(), ids.end());
+                                  return true;
+                                }),
+                 active.end());
+    const auto t_release = Clock::now();
+    if (!options.lazy_release) ctx.SyncFreedPages(freed);
+    stats.release_sync_ms += Ms(t_release, Clock::now());
+    ++step;
+  }
+  FinishStats(&stats, wall_start, step_ms, timings, overheads, steps_run, batch_sum);
+  return stats;
+}
+
+ContinuousBenchmarkResult RunContinuousSparseBenchmark(
+    const ModelConfig& config, const std::vector<ContinuousRequestSpec>& specs,
+    int max_active_requests) {
+  ContinuousDecodeOptions options;
+  options.max_active_requests = max_active_requests;
+  return RunContinuousSparseBenchmark(config, specs, options);
+}
+
+ContinuousBenchmarkResult RunContinuousSparseBenchmark(
+    const ModelConfig& config, const std::vector<ContinuousRequestSpec>& specs,
+    const ContinuousDecodeOptions& options) {
+  ContinuousBenchmarkResult result;
+  result.continuous_sparse = RunContinuousSparseDecode(config, specs, options);
+  ContinuousDecodeOptions serial = options;
+  serial.max_active_requests = 1;
+  result.serial_sparse = RunContinuousSparseDecode(config, specs, serial);
+  result.continuous_vs_serial_speedup =
+      result.serial_sparse.tokens_per_second > 0.0
+          ? result.continuous_sparse.tokens_per_second / result.serial_sparse.tokens_per_second
+          : 0.0;
+  return result;
+}
+
+}  // namespace dsd

@@ -109,6 +109,107 @@ __global__ __launch_bounds__(kPoolThreads) void MarkFreeKernel(
   }
 }
 
+// Integer-hash synthetic payloads for the GPU-resident admission modes.  The
+// mixing sequence and the value map (x % 2001 - 1000) / 1000 follow
+// src/device_page_pool.cpp:102-138 so that a workload generated here is the
+// same workload the reference generates.
+__device__ __forceinline__ uint32_t HashMix(uint32_t x, int v, uint32_t salt) {
+  return x ^ (static_cast<uint32_t>(v) + salt + (x << 6) + (x >> 2));
+}
+
+__device__ __forceinline__ float HashValue(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return static_cast<float>(static_cast<int>(x % 2001u) - 1000) / 1000.0f;
+}
+
+__device__ __forceinline__ float PromptValue(int request_id, int page_idx, int token,
+                                             int element, int stream) {
+  uint32_t x = 0x9e3779b9u;
+  x = HashMix(x, request_id, 0x85ebca6bu);
+  x = HashMix(x, page_idx, 0xc2b2ae35u);
+  x = HashMix(x, token, 0x27d4eb2fu);
+  x = HashMix(x, element, 0x165667b1u);
+  x = HashMix(x, stream, 0xd3a2646cu);
+  return HashValue(x);
+}
+
+__device__ __forceinline__ float DecodeValue(int request_id, int decode_step, int element,
+                                             int stream) {
+  uint32_t x = 0x9e3779b9u;
+  x = HashMix(x, request_id, 0x85ebca6bu);
+  x = HashMix(x, decode_step, 0xc2b2ae35u);
+  x = HashMix(x, element, 0x165667b1u);
+  x = HashMix(x, stream, 0xd3a2646cu);
+  return HashValue(x);
+}
+
+// One workgroup per prompt page: K/V from the hash, summary by the host rule.
+__global__ __launch_bounds__(kPoolThreads) void PrefillSyntheticKernel(
+    PoolView pool, const int* __restrict__ page_ids, const int* __restrict__ token_counts,
+    int n, int request_id) {
+  const int i = blockIdx.x;
+  if (i >= n) return;
+  const int page = page_ids[i];
+  const int count = token_counts[i];
+  const int E = pool.elements;
+  const size_t base = static_cast<size_t>(page) * pool.page_elems;
+  const float inv = __fdiv_rn(1.0f, static_cast<float>(count));
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    float acc = 0.0f;
+    for (int t = 0; t < count; ++t) {
+      const float k = PromptValue(request_id, i, t, e, 1);
+      const float v = PromptValue(request_id, i, t, e, 2);
+      pool.keys[base + static_cast<size_t>(t) * E + e] = k;
+      pool.values[base + static_cast<size_t>(t) * E + e] = v;
+      acc = __fadd_rn(acc, k);
+    }
+    pool.summaries[static_cast<size_t>(page) * E + e] = __fmul_rn(acc, inv);
+  }
+  if (threadIdx.x == 0) {
+    pool.token_counts[page] = count;
+    pool.live[page] = 1;
+  }
+}
+
+// One workgroup per page segment (tokens in offset order), running mean.
+__global__ __launch_bounds__(kPoolThreads) void AppendSyntheticKernel(
+    PoolView pool, const int* __restrict__ seg_start, const int* __restrict__ order,
+    const int* __restrict__ page_ids, const int* __restrict__ offsets,
+    const int* __restrict__ counts, const int* __restrict__ request_ids,
+    const int* __restrict__ decode_steps, int num_segments) {
+  const int seg = blockIdx.x;
+  if (seg >= num_segments) return;
+  const int begin = seg_start[seg];
+  const int end = seg_start[seg + 1];
+  const int E = pool.elements;
+  const int page = page_ids[order[begin]];
+  const size_t base = static_cast<size_t>(page) * pool.page_elems;
+  float* summary = pool.summaries + static_cast<size_t>(page) * E;
+  const bool fresh = offsets[order[begin]] == 0;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    float s = fresh ? 0.0f : summary[e];
+    for (int q = begin; q < end; ++q) {
+      const int tok = order[q];
+      const float k = DecodeValue(request_ids[tok], decode_steps[tok], e, 1);
+      const float v = DecodeValue(request_ids[tok], decode_steps[tok], e, 2);
+      const size_t dst = base + static_cast<size_t>(offsets[tok]) * E + e;
+      pool.keys[dst] = k;
+      pool.values[dst] = v;
+      const float old_count = static_cast<float>(offsets[tok]);
+      s = __fdiv_rn(__fadd_rn(__fmul_rn(s, old_count), k), __fadd_rn(old_count, 1.0f));
+    }
+    summary[e] = s;
+  }
+  if (threadIdx.x == 0) {
+    pool.token_counts[page] = counts[order[end - 1]];
+    pool.live[page] = 1;
+  }
+}
+
 }  // namespace
 
 void LaunchFinishPageUpload(const PoolView& pool, const int* d_page_ids,
@@ -131,6 +232,26 @@ void LaunchAppendTokens(const PoolView& pool, const int* d_seg_start,
                      0, stream, pool, d_seg_start, d_order, d_page_ids,
                      d_offsets, d_counts, d_keys, d_values, d_rows,
                      num_segments);
+  DSD_HIP_CHECK(hipGetLastError());
+}
+
+void LaunchPrefillSynthetic(const PoolView& pool, const int* d_page_ids,
+                            const int* d_token_counts, int n, int request_id,
+                            hipStream_t stream) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(PrefillSyntheticKernel, dim3(n), dim3(kPoolThreads), 0, stream, pool,
+                     d_page_ids, d_token_counts, n, request_id);
+  DSD_HIP_CHECK(hipGetLastError());
+}
+
+void LaunchAppendSynthetic(const PoolView& pool, const int* d_seg_start, const int* d_order,
+                           const int* d_page_ids, const int* d_offsets, const int* d_counts,
+                           const int* d_request_ids, const int* d_decode_steps,
+                           int num_segments, hipStream_t stream) {
+  if (num_segments <= 0) return;
+  hipLaunchKernelGGL(AppendSyntheticKernel, dim3(num_segments), dim3(kPoolThreads), 0, stream,
+                     pool, d_seg_start, d_order, d_page_ids, d_offsets, d_counts,
+                     d_request_ids, d_decode_steps, num_segments);
   DSD_HIP_CHECK(hipGetLastError());
 }
 

@@ -122,6 +122,36 @@ int dsd_pool_download_meta(const dsd_pool* pool, int* token_counts,
 int dsd_pool_download_summaries(const dsd_pool* pool, int n,
                                 const int* page_ids, float* out);
 
+/* Device addresses of the pool arrays (key_base_device, value_base_device,
+ * page_summary_base_device, page_token_counts_device, page_live_mask_device,
+ * page_k_offsets_device, page_v_offsets_device, device_page_pool.h:92-100).
+ * k_offsets[p] = v_offsets[p] = p * page_size * E. */
+typedef struct dsd_pool_arrays {
+  float* keys;
+  float* values;
+  float* summaries;
+  int* token_counts;
+  uint8_t* live;
+  uint64_t* k_offsets;
+  uint64_t* v_offsets;
+} dsd_pool_arrays;
+int dsd_pool_device_arrays(const dsd_pool* pool, dsd_pool_arrays* out);
+
+/* PrefillPromptSynthetic (device_page_pool.h:44-48): K/V of n prompt pages of
+ * request_id generated on the device from the reference's integer hash
+ * (src/device_page_pool.cpp:102-120; page i of the call is prompt page i),
+ * summaries by the host rule. */
+int dsd_pool_prefill_synthetic(dsd_pool* pool, int n, const int* page_ids,
+                               const int* token_counts, int request_id);
+
+/* AppendTokensSynthetic (device_page_pool.h:65-69): token i's K/V generated
+ * from (request_ids[i], decode_steps[i]) (src/device_page_pool.cpp:122-138),
+ * written at (page_ids[i], token_offsets[i]), running-mean summary. */
+int dsd_pool_append_synthetic(dsd_pool* pool, int n, const int* page_ids,
+                              const int* token_offsets,
+                              const int* page_token_counts,
+                              const int* request_ids, const int* decode_steps);
+
 /* transfer_stats / ResetTransferStats (device_page_pool.h:85-86). */
 int dsd_pool_transfer_stats(const dsd_pool* pool, dsd_transfer_stats* out);
 int dsd_pool_reset_transfer_stats(dsd_pool* pool);

@@ -62,3 +62,35 @@ def test_invalid_arguments_are_checked_before_the_device(dsd):
         dsd.DevicePagePool(2, 4, 4, -1)
     with pytest.raises(dsd.InvalidArgument):
         dsd.DevicePagePool(0, 4, 4, 4)
+
+
+CPP_LIB = ROOT / "15-618_dynamic_sparse_decode_amd" / "build" / "libdsd.so"
+
+
+def cpp_exports():
+    if not CPP_LIB.exists():
+        pytest.skip("libdsd.so not built")
+    out = subprocess.run(["nm", "-DC", "--defined-only", str(CPP_LIB)],
+                         capture_output=True, text=True, check=True).stdout
+    return {line.split(" ", 2)[2] for line in out.splitlines() if " T " in line}
+
+
+def test_cpp_library_exports_the_reference_api():
+    names = cpp_exports()
+    for sig in ("dsd::PagePool::allocate_page()", "dsd::PagedKvCache::AppendToken(",
+                "dsd::DevicePagePool::UploadPage(", "dsd::SparseCudaContext::RunBatch(",
+                "dsd::DenseCudaContext::RunBatch(", "dsd::SparseDecodeCuda(",
+                "dsd::DenseAttentionCudaBatch(", "dsd::BuildSyntheticBatch(",
+                "dsd::RunContinuousSparseDecode(", "dsd::MakeRequestState("):
+        assert any(n.startswith(sig) for n in names), sig
+
+
+def test_cpp_library_carries_no_cpu_compute_path():
+    # the CPU rows live only in the checker (oracle/liboracle_cpu.so)
+    names = cpp_exports()
+    for cpu in ("dsd::ScorePagesCpu", "dsd::SelectTopKPagesCpu", "dsd::SparseAttentionCpu",
+                "dsd::DenseAttentionCpu", "dsd::DecodePipeline::RunNaiveSparseStep(",
+                "dsd::DecodePipeline::RunDenseStep("):
+        assert not any(n.startswith(cpu) for n in names), cpu
+    out = subprocess.run(["ldd", str(CPP_LIB)], capture_output=True, text=True).stdout
+    assert "oracle" not in out and "libdsd_hip.so" in out

@@ -1,0 +1,78 @@
+"""The drop-in check: the reference's own test programs, benchmark and demo,
+compiled unchanged against include/dsd/ and linked to libdsd.so (with the
+CPU rows from oracle/liboracle_cpu.so), must pass as they do against the
+reference's library.
+
+The binaries are built in this container by `make -C oracle dropin` from the
+reference's sources where they lie (outputs only under oracle/_ref/dropin/,
+which is git-ignored and travels to the GPU box prebuilt).  Where they were
+not built (no reference tree), the tests skip.
+
+  tests/test_page_pool.cpp, tests/test_reference.cpp    CPU
+  tests/test_device_page_pool.cpp, test_dense_cuda.cpp,
+  test_sparse_cuda.cpp, test_continuous_batching.cpp     GPU (they print
+      "skipped: no visible sm90 GPU" and exit 0 without one, so the GPU
+      marker is what makes them meaningful)
+  benchmarks/bench_decode.cpp                            GPU: its accuracy
+      lines (sparse_gpu vs sparse_cpu, dense_gpu vs dense_cpu) are checked
+"""
+from __future__ import annotations
+
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+DROPIN = ROOT / "oracle" / "_ref" / "dropin"
+
+
+def run(name, *args, timeout=300):
+    exe = DROPIN / name
+    if not exe.exists():
+        pytest.skip(f"{exe} not built (needs the reference tree: make -C oracle dropin)")
+    print(f"[dropin] {name} {' '.join(args)}", flush=True)
+    proc = subprocess.run([str(exe), *args], capture_output=True, text=True, timeout=timeout)
+    return proc
+
+
+@pytest.mark.parametrize("name,expect", [
+    ("test_page_pool", "page pool tests passed"),
+    ("test_reference", "reference tests passed"),
+])
+def test_reference_cpu_tests_pass_against_libdsd(name, expect):
+    proc = run(name)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    assert expect in proc.stdout
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,expect", [
+    ("test_device_page_pool", "device page pool tests passed"),
+    ("test_dense_cuda", "dense cuda tests passed"),
+    ("test_sparse_cuda", "sparse cuda tests passed"),
+    ("test_continuous_batching", "continuous batching tests passed"),
+])
+def test_reference_gpu_tests_pass_against_libdsd(name, expect):
+    proc = run(name)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    assert "skipped" not in proc.stdout, proc.stdout
+    assert expect in proc.stdout, proc.stdout
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("args", [
+    # top_k batch min max seed iters warmup heads head_dim page  (argv order)
+    ("8", "4", "64", "300", "7", "1", "0", "4", "16", "16"),
+    ("8", "4", "512", "1024", "3", "1", "0", "32", "128", "16"),
+])
+def test_reference_bench_decode_accuracy_lines(args):
+    proc = run("bench_decode", *args)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    out = proc.stdout
+    diffs = dict(re.findall(r"(avg_max_abs_diff_\w+)=([-+0-9.eE]+)", out))
+    assert "avg_max_abs_diff_sparse_gpu_vs_sparse_cpu" in diffs, out
+    assert float(diffs["avg_max_abs_diff_sparse_gpu_vs_sparse_cpu"]) <= 1e-4
+    if "avg_max_abs_diff_dense_gpu_vs_dense_cpu" in diffs:
+        assert float(diffs["avg_max_abs_diff_dense_gpu_vs_dense_cpu"]) <= 1e-4
