@@ -5,6 +5,8 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <numeric>
@@ -638,13 +640,23 @@ struct dsd_sparse_ctx {
   hipEvent_t ev[6] = {};
   DeviceBuffer<float> d_queries, d_scores, d_outputs, d_lo, d_hi;
   DeviceBuffer<int> d_offsets, d_ids, d_selected, d_counts, d_exact_pages;
+  // fused-step publication words (see fused_step.hip) and per-workgroup
+  // clock stamps for the timing mode
+  DeviceBuffer<unsigned long long> d_rec, d_stamps;
+  DeviceBuffer<int> d_arrivals;
+  unsigned epoch = 0;
+  double wall_khz = 0.0;  // wall_clock64() rate
   int score_mode = DSD_SCORE_CERTIFIED;
+  bool fused_enabled = true;
   PinnedBuffer<float> h_queries, h_scores, h_outputs;
-  PinnedBuffer<int> h_offsets, h_ids, h_selected, h_counts;
+  PinnedBuffer<int> h_offsets, h_ids, h_selected, h_counts, h_fail;
+  PinnedBuffer<unsigned long long> h_stamps;
+  int stamp_grid = 0;  // workgroups stamped by the last timed fused launch
 
   struct Launch {
     bool valid = false;
     bool certified = false;
+    bool fused = false;
     int batch = 0, total = 0, max_n = 0;
     const float* queries = nullptr;
     const int* offsets = nullptr;
@@ -682,7 +694,77 @@ struct dsd_sparse_ctx {
                              Scale(), L.scores, s);
     }
   }
+  // The single-launch step covers certified selection on the hot shape.
+  bool UseFused(bool certified, int max_n) const {
+    return certified && fused_enabled && max_batch <= 512 &&
+           dsdk::FusedStepSupported(pool->view, max_n, top_k);
+  }
+  void EnqueueFused(const Launch& L, hipStream_t s, bool stamp) {
+    dsdk::FusedArgs a;
+    a.queries = L.queries;
+    a.cand_offsets = L.offsets;
+    a.cand_ids = L.ids;
+    a.batch = L.batch;
+    a.total = L.total;
+    a.top_k = top_k;
+    a.sel_stride = top_k > 0 ? top_k : 1;
+    a.scale = Scale();
+    a.mid = L.scores;
+    a.lo = d_lo.ptr;
+    a.hi = d_hi.ptr;
+    a.selected = L.selected;
+    a.counts = L.counts;
+    a.outputs = L.outputs;
+    a.rec = d_rec.ptr;
+    a.arrivals = d_arrivals.ptr;
+    a.max_batch = std::max(1, max_batch);
+    if (++epoch == 0) epoch = 1;  // words start at 0: never tag with epoch 0
+    a.epoch = epoch;
+    a.exact_pages = d_exact_pages.ptr;
+    a.fail_flag = h_fail.ptr;
+    if (stamp) {
+      stamp_grid = dsdk::FusedStepGrid(pool->view, L.batch, L.total);
+      a.stamps = d_stamps.ptr;
+    }
+    dsdk::LaunchFusedStep(pool->view, a, s);
+    if (stamp) {
+      DSD_HIP_CHECK(hipMemcpyAsync(h_stamps.ptr, d_stamps.ptr,
+                                   4 * sizeof(unsigned long long) * stamp_grid,
+                                   hipMemcpyDeviceToHost, s));
+    }
+  }
+  // Phase split of the last timed fused launch from its workgroup stamps:
+  // first start, last score item end, last selection done, last end.
+  void FusedPhases(int total, double* score_ms, double* select_ms,
+                   double* attention_ms) const {
+    *score_ms = *select_ms = *attention_ms = 0.0;
+    if (stamp_grid <= 0 || wall_khz <= 0.0) return;
+    const int score_items = dsdk::FusedStepScoreItems(total);
+    const unsigned long long* st = h_stamps.ptr;
+    unsigned long long t0 = ~0ull, t_score = 0, t_select = 0, t_end = 0;
+    for (int g = 0; g < stamp_grid; ++g) {
+      t0 = std::min(t0, st[4 * g]);
+      if (g < score_items) {
+        t_score = std::max(t_score, st[4 * g + 3]);
+      } else {
+        t_select = std::max(t_select, st[4 * g + 2]);
+        t_end = std::max(t_end, st[4 * g + 3]);
+      }
+    }
+    t_score = std::max(t_score, t0);
+    t_select = std::max(t_select, t_score);
+    t_end = std::max(t_end, t_select);
+    *score_ms = static_cast<double>(t_score - t0) / wall_khz;
+    *select_ms = static_cast<double>(t_select - t_score) / wall_khz;
+    *attention_ms = static_cast<double>(t_end - t_select) / wall_khz;
+  }
   void Enqueue(const Launch& L, hipStream_t s, bool timing) {
+    if (L.fused) {
+      if (timing) DSD_HIP_CHECK(hipEventRecord(ev[0], s));
+      EnqueueFused(L, s, timing);
+      if (timing) DSD_HIP_CHECK(hipEventRecord(ev[3], s));
+      return;
+    }
     if (timing) DSD_HIP_CHECK(hipEventRecord(ev[0], s));
     EnqueueScore(L, s);
     if (timing) DSD_HIP_CHECK(hipEventRecord(ev[1], s));
@@ -690,6 +772,19 @@ struct dsd_sparse_ctx {
     if (timing) DSD_HIP_CHECK(hipEventRecord(ev[2], s));
     EnqueueAttention(L, s);
     if (timing) DSD_HIP_CHECK(hipEventRecord(ev[3], s));
+  }
+  // After the stream has synchronised: a fused step that reported a failure
+  // (a timed-out wait, or a request beyond max_candidates) left zeros.
+  void CheckTimeout() {
+    if (h_fail.ptr != nullptr && h_fail.ptr[0] != 0) {
+      const int code = h_fail.ptr[0];
+      h_fail.ptr[0] = 0;
+      if (code == 2) {
+        throw std::invalid_argument(
+            "a request has more candidates than the max_candidates the step was given");
+      }
+      throw std::runtime_error("fused decode step: wait for page selection timed out");
+    }
   }
   void EnqueueSelect(const Launch& L, hipStream_t s) {
     if (L.certified) {
@@ -753,6 +848,30 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     ctx->d_hi.Reserve(P);
     ctx->d_exact_pages.Reserve(1);
     DSD_HIP_CHECK(hipMemset(ctx->d_exact_pages.ptr, 0, sizeof(int)));
+    {
+      const size_t rec = 3 * P;
+      const size_t grid =
+          static_cast<size_t>(dsdk::FusedStepGrid(pool->view, static_cast<int>(B),
+                                                  static_cast<int>(P)));
+      ctx->d_rec.Reserve(rec);
+      ctx->d_stamps.Reserve(4 * grid);
+      ctx->h_stamps.Reserve(4 * grid);
+      DSD_HIP_CHECK(hipMemset(ctx->d_rec.ptr, 0, rec * sizeof(unsigned long long)));
+      const size_t arrivals = 2 * B * 32;
+      ctx->d_arrivals.Reserve(arrivals);
+      DSD_HIP_CHECK(hipMemset(ctx->d_arrivals.ptr, 0, arrivals * sizeof(int)));
+    }
+    ctx->h_fail.Reserve(1);
+    ctx->h_fail.ptr[0] = 0;
+    {
+      int device = 0, khz = 0;
+      DSD_HIP_CHECK(hipGetDevice(&device));
+      DSD_HIP_CHECK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device));
+      ctx->wall_khz = static_cast<double>(khz);
+    }
+    if (const char* env = std::getenv("DSD_FUSED_STEP")) {
+      ctx->fused_enabled = std::strcmp(env, "0") != 0;
+    }
     ctx->h_queries.Reserve(B * E);
     ctx->h_outputs.Reserve(B * E);
     ctx->h_scores.Reserve(P);
@@ -849,6 +968,7 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
     dsd_sparse_ctx::Launch L;
     L.valid = true;
     L.certified = ctx->UseCertified(max_n, debug);
+    L.fused = ctx->UseFused(L.certified, max_n);
     L.batch = batch;
     L.total = total;
     L.max_n = max_n;
@@ -887,7 +1007,14 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
     t0 = Clock::now();
     DSD_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     t.sync_ms = MsSince(t0);
-    if (timing) {
+    if (L.fused) ctx->CheckTimeout();
+    if (timing && L.fused) {
+      // One kernel: its event time, split at the workgroup clock stamps.
+      float k = 0.f;
+      DSD_HIP_CHECK(hipEventElapsedTime(&k, ctx->ev[0], ctx->ev[3]));
+      ctx->FusedPhases(L.total, &t.score_ms, &t.topk_ms, &t.attention_ms);
+      t.kernel_ms = k;
+    } else if (timing) {
       float a = 0.f, b = 0.f, c = 0.f;
       DSD_HIP_CHECK(hipEventElapsedTime(&a, ctx->ev[0], ctx->ev[1]));
       DSD_HIP_CHECK(hipEventElapsedTime(&b, ctx->ev[1], ctx->ev[2]));
@@ -938,6 +1065,7 @@ int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
     dsd_sparse_ctx::Launch L;
     L.valid = true;
     L.certified = ctx->UseCertified(max_candidates, false);
+    L.fused = ctx->UseFused(L.certified, max_candidates);
     L.batch = batch;
     L.total = total_candidates;
     L.max_n = max_candidates;
@@ -964,7 +1092,11 @@ int dsd_sparse_replay_stage(dsd_sparse_ctx* ctx, int stage, void* stream) {
       case 0: ctx->EnqueueScore(L, s); break;
       case 1: ctx->EnqueueSelect(L, s); break;
       case 2: ctx->EnqueueAttention(L, s); break;
-      default: throw std::invalid_argument("stage must be 0, 1 or 2");
+      case 3:
+        Require(L.fused, "the last step did not use the single-launch kernel");
+        ctx->EnqueueFused(L, s, false);
+        break;
+      default: throw std::invalid_argument("stage must be 0, 1, 2 or 3");
     }
   });
 }
@@ -995,6 +1127,7 @@ int dsd_sparse_exact_rescored_pages(dsd_sparse_ctx* ctx, int reset, int* out) {
   return Guard([&] {
     Require(ctx != nullptr && out != nullptr, "pointers must be non-null");
     DSD_HIP_CHECK(hipDeviceSynchronize());
+    ctx->CheckTimeout();
     DSD_HIP_CHECK(hipMemcpy(out, ctx->d_exact_pages.ptr, sizeof(int), hipMemcpyDeviceToHost));
     if (reset) DSD_HIP_CHECK(hipMemset(ctx->d_exact_pages.ptr, 0, sizeof(int)));
   });

@@ -125,4 +125,43 @@ struct AttentionArgs {
 void LaunchAttention(const PoolView& pool, const AttentionArgs& args,
                      hipStream_t stream);
 
+// ---- the fused single-launch step (fused_step.hip) --------------------------
+
+// Arguments of the one-launch decode step.  Intervals cross workgroups as
+// epoch-tagged 64-bit words in context-owned device memory (zero at
+// creation): rec[total][3] = (mid, lo, hi) of each candidate.  epoch is
+// non-zero and differs between consecutive launches on the context.
+struct FusedArgs {
+  const float* queries = nullptr;     // [batch][E]
+  const int* cand_offsets = nullptr;  // [batch + 1]
+  const int* cand_ids = nullptr;      // [total]
+  int batch = 0;
+  int total = 0;
+  int top_k = 0;
+  int sel_stride = 1;                 // row stride of selected
+  float scale = 0.0f;
+  float* mid = nullptr;               // [total] certified intervals (caller copy)
+  float* lo = nullptr;
+  float* hi = nullptr;
+  int* selected = nullptr;            // [batch][sel_stride] (caller copy)
+  int* counts = nullptr;              // [batch]
+  float* outputs = nullptr;           // [batch][E]
+  unsigned long long* rec = nullptr;
+  int* arrivals = nullptr;            // [2][max_batch][32] counters, zero at creation
+  int max_batch = 0;                  // <= 512
+  unsigned epoch = 0;
+  int* exact_pages = nullptr;         // may be null
+  int* fail_flag = nullptr;           // host-visible: 1 wait timed out, 2 CSR overflow
+  unsigned long long* stamps = nullptr;  // null, or [grid][4] clocks: start,
+                                         // counter ready, selection done, end
+};
+
+// E = 4096, head_dim = 128, max_candidates <= 256, top_k <= 256.
+bool FusedStepSupported(const PoolView& pool, int max_candidates, int top_k);
+// Workgroups of one launch: score items (8 candidates each), then
+// batch * num_heads / 2 attention items.
+int FusedStepScoreItems(int total_candidates);
+int FusedStepGrid(const PoolView& pool, int batch, int total_candidates);
+void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t stream);
+
 }  // namespace dsdk

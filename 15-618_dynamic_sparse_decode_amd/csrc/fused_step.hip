@@ -1,0 +1,613 @@
+// fused_step.hip -- the whole sparse decode step in one launch (gfx950).
+//
+// For the hot shape (E = 4096, head_dim 128, at most 256 candidates and
+// top_k <= 256 per request, certified selection) the three stages of the
+// step -- page scoring (reference ScorePagesCpu, src/reference_kernels.cpp:
+// 59-80), top-k (SelectTopKPagesCpu, :82-107) and gather + attention
+// (GatherPagesCpu + SparseAttentionCpu, :109-194) -- run in one kernel, so the
+// step pays one launch and no kernel boundary between dependent stages.
+//
+// Work items, by workgroup id:
+//   [0, S)          score items, S = ceil(P / 8): the certified intervals of
+//                   candidates 8s .. 8s+7 (two waves per page)
+//   [S, S + B*H/2)  attention items (request r, heads 2i and 2i+1),
+//                   request-major: each selects its request's top-k from the
+//                   intervals (the H/2 items of a request compute the same
+//                   selection; the first writes it out), then attends over
+//                   the selected pages, eight waves per head.
+// Workgroups have 1024 threads, one per CU, so the score items and the
+// first attention items start together and every attention item is
+// resident by the time the score items finish.
+// An attention item waits for its request's intervals, i.e. only for lower
+// workgroup ids.  Each XCD dispatches its share of a grid in id order, so
+// every score item has started (or finished) before any attention item
+// starts, and score items never wait: every wait ends.  The spins are
+// bounded anyway (a timeout is reported to the host and gives zeros, never a
+// hang).
+//
+// Publication without fences.  Each interval crosses workgroups as three
+// 64-bit words (mid, lo, hi) whose high half is this launch's epoch (a
+// per-context counter, never 0) and whose low half is the float: written
+// with relaxed agent-scope atomic stores, read with relaxed agent-scope
+// atomic loads until the epoch matches.  A word is valid exactly when its
+// tag is current, so no ordering between words is needed and there is no
+// release/acquire (each would write back or invalidate the XCD's L2).
+// Waiting is cheap: each score item adds its pages to its request's arrival
+// counter (one counter per 128-byte line, so requests never share a line;
+// read-modify-writes on one line serialise device-wide), and one thread per
+// attention item polls that counter; only then are the interval words read
+// (and re-read if a tag is not yet current: the counter is a wake-up hint,
+// never trusted for the data).  Counters are double-buffered by epoch
+// parity; each launch clears the set the next launch will use.
+#include "dsd_internal.h"
+#include "step_common.h"
+
+namespace dsdk {
+namespace {
+
+constexpr int kFThreads = 1024;             // one workgroup per CU
+constexpr int kFWaves = kFThreads / kWave;  // 16
+constexpr int kFE = 4096;
+constexpr int kFD = 128;
+constexpr int kFPagesPerItem = 8;           // score item = 8 pages, 2 waves each
+constexpr int kFHeadsPerItem = 2;           // attention item = 2 heads, 8 waves each
+constexpr int kFHeadWaves = kFWaves / kFHeadsPerItem;
+constexpr int kFPageLanes = 2 * kWave;      // 128 lanes per page
+constexpr int kFPerLane = kFE / kFPageLanes;  // 32 consecutive products per lane
+constexpr int kFMaxCand = 256;
+constexpr int kFMaxK = 256;
+constexpr int kFLpt = 16;                 // lanes per token row (8 dims each)
+constexpr int kFDq = kFD / kFLpt;         // 8
+constexpr int kFTpc = kWave / kFLpt;      // 4 token rows per wave per chunk
+constexpr int kFUnroll = 4;               // chunks in flight per wave
+constexpr unsigned kSpinLimit = 1u << 24;  // polls of ~1 us each at most
+constexpr int kCounterStride = 32;         // ints: one 128-byte line per counter
+constexpr int kStampsPerGroup = 4;         // start, counter ready, selected, end
+
+struct FusedShared {
+  // score item (per wave): float total (the carry into wave 2p+1), double
+  // sum of the group sums, bound sums
+  float wave_total[kFWaves];
+  double total[kFWaves];
+  double abs_prefix[kFWaves];
+  double abs_p[kFWaves];
+  int fail;
+  int nflag;
+  // selection (attention item)
+  uint64_t key[kFMaxCand];
+  float lo[kFMaxCand];
+  float hi[kFMaxCand];
+  int top[kFMaxCand];
+  int flag[kFMaxCand];
+  int rank[kFMaxCand];
+  float tlo[kFMaxK];    // intervals of the top-k members, in rank order
+  float thi[kFMaxK];
+  float red[2][kFWaves];
+  alignas(16) float tile[kChainPages * kRankTileStride];
+  // attention
+  int page[kFMaxK];
+  int ntok[kFMaxK];
+  float m[kFWaves];
+  float l[kFWaves];
+  alignas(16) float acc[kFWaves][kFD];
+};
+
+__device__ __forceinline__ uint64_t Now() { return static_cast<uint64_t>(wall_clock64()); }
+
+__device__ __forceinline__ void PutTagged(unsigned long long* p, unsigned epoch,
+                                          uint32_t payload) {
+  __hip_atomic_store(p, (static_cast<unsigned long long>(epoch) << 32) | payload,
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned long long LoadWord(unsigned long long* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool Current(unsigned long long w, unsigned epoch) {
+  return static_cast<unsigned>(w >> 32) == epoch;
+}
+
+__device__ __forceinline__ void ReportFailure(const FusedArgs& a, int code) {
+  __hip_atomic_store(a.fail_flag, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Index of the request holding candidate c: the number of requests whose
+// candidate range ends at or before c (cand_offsets is non-decreasing).  One
+// wave-wide load per 64 requests instead of a dependent binary search.
+__device__ __forceinline__ int RequestOfBallot(const int* __restrict__ offs, int batch, int c) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int r = 0;
+  for (int base = 0; base < batch; base += kWave) {
+    const int i = base + lane;
+    const int end = i < batch ? offs[i + 1] : 0x7fffffff;
+    const int cnt = __popcll(__ballot(end <= c));
+    r += cnt;
+    if (cnt < kWave) break;
+  }
+  return r;
+}
+
+// Arrival counter of request r for the launch with this epoch.
+__device__ __forceinline__ int* ArrivalCounter(const FusedArgs& a, unsigned epoch, int r) {
+  return a.arrivals + (static_cast<size_t>(epoch & 1u) * a.max_batch + r) * kCounterStride;
+}
+
+// Ranks of the n <= 256 keys in sh.key (descending; equal keys by position)
+// into sh.rank: tpc threads per candidate count disjoint slices of the keys
+// (broadcast LDS reads, 8 in flight) and add their counts with shuffles.
+// Must be called by the whole workgroup; ends with a barrier.
+__device__ void ParallelRanks(FusedShared& sh, int n) {
+  const int tpc = n <= kFThreads / 8 ? 8 : 4;
+  const int t = threadIdx.x;
+  const int cand = t / tpc;
+  const int part = t - cand * tpc;
+  int partial = 0;
+  if (cand < n) {
+    const uint64_t key = sh.key[cand];
+    const int m = (n + tpc - 1) / tpc;
+    const int j0 = part * m;
+    const int j1 = j0 + m < n ? j0 + m : n;
+    int j = j0;
+    for (; j + 8 <= j1; j += 8) {
+      uint64_t kj[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) kj[u] = sh.key[j + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        partial += (kj[u] > key || (kj[u] == key && j + u < cand)) ? 1 : 0;
+      }
+    }
+    for (; j < j1; ++j) partial += (sh.key[j] > key || (sh.key[j] == key && j < cand)) ? 1 : 0;
+  }
+  partial += __shfl_xor(partial, 1, kWave);
+  partial += __shfl_xor(partial, 2, kWave);
+  if (tpc == 8) partial += __shfl_xor(partial, 4, kWave);
+  if (cand < n && part == 0) sh.rank[cand] = partial;
+  __syncthreads();
+}
+
+// Score item s: certified intervals of candidates 8s .. 8s+7.  Waves 2p and
+// 2p+1 take page p, wave 2p+h the elements [2048h, 2048h + 2048) as 8 rows
+// of 64 float4: lane l of row j holds float4 number 512h + 64j + l, so every
+// load instruction reads 1 KiB contiguously.  Each lane's float4 is a group
+// of 4 consecutive products (L = 4): the lane forms the group's local prefix
+// sums in float; a float scan of the group sums along the row (plus the
+// rows before, plus wave 2p's total for h = 1) gives the group's starting
+// prefix; the group sums also meet in double for s_hat.
+__device__ void ScoreItem(const PoolView& pool, const FusedArgs& a, int s, FusedShared& sh) {
+  constexpr int kRows = kFPerLane / 4;  // 8
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int half = wave & 1;
+  const int c = s * kFPagesPerItem + (wave >> 1);
+  const bool active = c < a.total;  // uniform per wave
+  float row_sum[kRows];   // float sums of the rows, all lanes
+  float excl[kRows];      // this lane's exclusive prefix within row j
+  float loc_abs = 0.0f;   // sum of |loc| over this lane's groups
+  float p_abs = 0.0f;
+  double s_lane = 0.0;
+  int r = 0;
+  if (active) {
+    const int page = a.cand_ids[c];
+    r = RequestOfBallot(a.cand_offsets, a.batch, c);
+    const float4* q4 = reinterpret_cast<const float4*>(a.queries + static_cast<size_t>(r) * kFE) +
+                       half * 512 + lane;
+    const float4* s4 =
+        reinterpret_cast<const float4*>(pool.summaries + static_cast<size_t>(page) * kFE) +
+        half * 512 + lane;
+    const int count = pool.token_counts[page];
+    float4 qv[kRows];
+    float4 sv[kRows];
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) {
+      qv[j] = q4[j * kWave];
+      sv[j] = s4[j * kWave];
+    }
+    // A page holding no tokens reads as an all-zero summary
+    // (src/paged_kv_cache.cpp:457-459); the products q*0 are still formed.
+    if (count == 0) {
+#pragma unroll
+      for (int j = 0; j < kRows; ++j) sv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) {
+      const float p0 = __fmul_rn(qv[j].x, sv[j].x);
+      const float p1 = __fmul_rn(qv[j].y, sv[j].y);
+      const float p2 = __fmul_rn(qv[j].z, sv[j].z);
+      const float p3 = __fmul_rn(qv[j].w, sv[j].w);
+      const float l1 = p0;
+      const float l2 = __fadd_rn(l1, p1);
+      const float l3 = __fadd_rn(l2, p2);
+      const float l4 = __fadd_rn(l3, p3);
+      loc_abs = __fadd_rn(loc_abs, __fadd_rn(__fadd_rn(fabsf(l1), fabsf(l2)),
+                                             __fadd_rn(fabsf(l3), fabsf(l4))));
+      p_abs = __fadd_rn(p_abs, __fadd_rn(__fadd_rn(fabsf(p0), fabsf(p1)),
+                                         __fadd_rn(fabsf(p2), fabsf(p3))));
+      s_lane += static_cast<double>(l4);
+      // row scan of the group sums (float)
+      float incl = l4;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const float t = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl = __fadd_rn(incl, t);
+      }
+      row_sum[j] = __shfl(incl, kWave - 1, kWave);
+      excl[j] = __fsub_rn(incl, l4);
+    }
+    if (lane == 0) {
+      float total = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kRows; ++j) total = __fadd_rn(total, row_sum[j]);
+      sh.wave_total[wave] = total;
+    }
+  }
+  __syncthreads();
+  if (active) {
+    // Starting prefix of each of this lane's groups, and the bound sums.
+    float base = half ? sh.wave_total[wave - 1] : 0.0f;
+    float tl = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) {
+      const float start = __fadd_rn(base, excl[j]);
+      tl = __fadd_rn(tl, 4.0f * fabsf(start));
+      base = __fadd_rn(base, row_sum[j]);
+    }
+    double tsum = static_cast<double>(tl) + static_cast<double>(loc_abs);
+    double absp = static_cast<double>(p_abs);
+    double sl = s_lane;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      tsum += __shfl_xor(tsum, o, kWave);
+      absp += __shfl_xor(absp, o, kWave);
+      sl += __shfl_xor(sl, o, kWave);
+    }
+    if (lane == 0) {
+      sh.total[wave] = sl;
+      sh.abs_prefix[wave] = tsum;
+      sh.abs_p[wave] = absp;
+    }
+  }
+  __syncthreads();
+  if (s == 0 && static_cast<int>(threadIdx.x) < a.max_batch) {
+    // Clear the arrival counters the next launch uses.
+    __hip_atomic_store(ArrivalCounter(a, a.epoch + 1, threadIdx.x), 0, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (active && half == 0 && lane == 0) {
+    const double s_hat = sh.total[wave] + sh.total[wave + 1];
+    const double tsum = sh.abs_prefix[wave] + sh.abs_prefix[wave + 1];
+    const double ap = sh.abs_p[wave] + sh.abs_p[wave + 1];
+    // Roundings on any term's path into a group's starting prefix: 6 scan
+    // steps, 1 subtraction, 8 additions into wave 2p's total, 8 row
+    // additions, 1 final addition (24; 40 used).  The float |p| sums carry
+    // < 2^-19 relative error; doubled to stay an upper bound.
+    float mid, lo, hi;
+    WriteBoundsBlocked(s_hat, tsum, 2.0 * ap, kFE, 4, 40, a.scale, &mid, &lo, &hi);
+    a.mid[c] = mid;
+    a.lo[c] = lo;
+    a.hi[c] = hi;
+    // Publish the interval, then count the page into its request.
+    unsigned long long* rec = a.rec + 3 * static_cast<size_t>(c);
+    PutTagged(rec + 0, a.epoch, __float_as_uint(mid));
+    PutTagged(rec + 1, a.epoch, __float_as_uint(lo));
+    PutTagged(rec + 2, a.epoch, __float_as_uint(hi));
+    __hip_atomic_fetch_add(ArrivalCounter(a, a.epoch, r), 1, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Top-k of request r (n candidates from `begin`) from the published
+// intervals into sh.page / sh.ntok; returns the count (0 on failure).
+// Candidates whose order the intervals do not decide are rescored with the
+// exact sequential chain (as SelectCertifiedRankKernel).  The workgroup of
+// head 0 also writes the selection out for the caller.
+__device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r, int begin,
+                                int n, bool writer, FusedShared& sh) {
+  int kk = a.top_k <= 0 ? 0 : (a.top_k < n ? a.top_k : n);
+  if (n > kFMaxCand) {
+    // The caller's max_candidates understated the CSR: select nothing (the
+    // outputs are zeros) and report it to the host.
+    if (writer && threadIdx.x == 0) ReportFailure(a, 2);
+    kk = 0;
+  }
+  const int i = threadIdx.x;
+  const bool active = kk > 0 && i < n;
+  // Ids and token counts do not depend on the scores: fetch them first.
+  int my_page = 0, my_ntok = 0;
+  if (active) {
+    my_page = a.cand_ids[begin + i];
+    my_ntok = pool.token_counts[my_page];
+  }
+  if (i == 0) {
+    sh.fail = 0;
+    sh.nflag = 0;
+    if (kk > 0) {
+      // One poller per workgroup: wait until every page of the request has
+      // arrived (a hint; the tags below decide).
+      int* counter = ArrivalCounter(a, a.epoch, r);
+      unsigned spins = 0;
+      while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < n) {
+        __builtin_amdgcn_s_sleep(2);
+        if (++spins >= kSpinLimit) {
+          sh.fail = 1;
+          break;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (a.stamps != nullptr && threadIdx.x == 0) {
+    a.stamps[kStampsPerGroup * static_cast<size_t>(blockIdx.x) + 1] = Now();
+  }
+  if (active && !sh.fail) {
+    unsigned long long* rec = a.rec + 3 * static_cast<size_t>(begin + i);
+    // First an ordinary (L2-cached) read, shared by the workgroups of this
+    // request on the XCD; a word whose tag is not current (not yet visible,
+    // or a stale cached line) is then polled coherently.
+    unsigned long long w0 = rec[0], w1 = rec[1], w2 = rec[2];
+    unsigned spins = 0;
+    while (!(Current(w0, a.epoch) && Current(w1, a.epoch) && Current(w2, a.epoch))) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins >= kSpinLimit) {
+        sh.fail = 1;
+        break;
+      }
+      w0 = LoadWord(rec + 0);
+      w1 = LoadWord(rec + 1);
+      w2 = LoadWord(rec + 2);
+    }
+    sh.key[i] = SelectKey(__uint_as_float(static_cast<uint32_t>(w0)), my_page);
+    sh.lo[i] = __uint_as_float(static_cast<uint32_t>(w1));
+    sh.hi[i] = __uint_as_float(static_cast<uint32_t>(w2));
+  }
+  __syncthreads();
+  if (sh.fail) {
+    if (threadIdx.x == 0) ReportFailure(a, 1);
+    kk = 0;
+  }
+  if (kk > 0) {
+    const bool mine = i < n;
+    ParallelRanks(sh, n);
+    int rank = mine ? sh.rank[i] : n;
+    if (mine && rank < kk) {
+      sh.top[rank] = i;
+      sh.tlo[rank] = sh.lo[i];
+      sh.thi[rank] = sh.hi[i];
+    }
+    float my_min = (mine && rank < kk) ? sh.lo[i] : INFINITY;
+    float my_max = (mine && rank >= kk) ? sh.hi[i] : -INFINITY;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      my_min = fminf(my_min, __shfl_xor(my_min, o, kWave));
+      my_max = fmaxf(my_max, __shfl_xor(my_max, o, kWave));
+    }
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+      sh.red[0][wave] = my_min;
+      sh.red[1][wave] = my_max;
+    }
+    __syncthreads();
+    float min_t_lo = INFINITY, max_o_hi = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kFWaves; ++w) {
+      min_t_lo = fminf(min_t_lo, sh.red[0][w]);
+      max_o_hi = fmaxf(max_o_hi, sh.red[1][w]);
+    }
+    if (mine) {
+      const float l = sh.lo[i];
+      const float h = sh.hi[i];
+      bool flag;
+      if (rank >= kk) {
+        flag = h >= min_t_lo;
+      } else {
+        // Overlap with any other member (intervals in rank order: independent
+        // reads), or with the best outsider.
+        flag = l <= max_o_hi;
+#pragma unroll 4
+        for (int j = 0; j < kk; ++j) {
+          flag = flag || (j != rank && l <= sh.thi[j] && sh.tlo[j] <= h);
+        }
+      }
+      if (flag) sh.flag[atomicAdd(&sh.nflag, 1)] = i;
+    }
+    __syncthreads();
+    const int nflag = sh.nflag;
+    if (nflag > 0) {
+      if (writer && threadIdx.x == 0 && a.exact_pages != nullptr) {
+        atomicAdd(a.exact_pages, nflag);
+      }
+      RescoreExact(sh.flag, nflag, a.queries + static_cast<size_t>(r) * kFE, pool.summaries,
+                   pool.token_counts, a.cand_ids, begin, kFE, a.scale, sh.tile, sh.key);
+      ParallelRanks(sh, n);
+      rank = mine ? sh.rank[i] : n;
+    }
+    if (mine && rank < kk) {
+      sh.page[rank] = my_page;
+      sh.ntok[rank] = my_ntok;
+      if (writer) a.selected[static_cast<size_t>(r) * a.sel_stride + rank] = my_page;
+    }
+  }
+  if (writer && threadIdx.x == 0) a.counts[r] = kk;
+  __syncthreads();
+  return kk;
+}
+
+// Attention item (request r, heads h0 and h0+1): select, then per head
+// softmax(q_h K^T * scale) V over the selected pages' valid tokens; waves
+// 0-7 take head h0 and waves 8-15 head h0+1, each as
+// AttentionFastKernel<128, 16, 8, 4>.
+__device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, int h0,
+                              FusedShared& sh, uint64_t* t_selected) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int hw = wave % kFHeadWaves;   // wave within its head
+  const int h = h0 + wave / kFHeadWaves;
+  const int g = lane / kFLpt;
+  const int j = lane % kFLpt;
+  const int head_off = h * kFD + j * kFDq;
+  const int begin = a.cand_offsets[r];
+  const int n = a.cand_offsets[r + 1] - begin;
+  float q[kFDq];
+  float acc[kFDq];
+  {
+    const float qscale = a.scale * kLog2e;
+    LoadDims<kFDq>(a.queries + static_cast<size_t>(r) * kFE + head_off, q);
+#pragma unroll
+    for (int i = 0; i < kFDq; ++i) {
+      q[i] *= qscale;
+      acc[i] = 0.0f;
+    }
+  }
+  const int kk = SelectForRequest(pool, a, r, begin, n, h0 == 0, sh);
+  if (a.stamps != nullptr && threadIdx.x == 0) *t_selected = Now();
+  if (kk == 0) {
+    // Nothing selected: zeros (src/cuda/sparse_batched_attention.cu:621-627).
+    if (threadIdx.x < kFHeadsPerItem * kFD) {
+      a.outputs[static_cast<size_t>(r) * kFE + static_cast<size_t>(h0) * kFD + threadIdx.x] =
+          0.0f;
+    }
+    return;
+  }
+
+  const int E = kFE;
+  const int ps = pool.page_size;
+  const int total = kk * ps;
+  float m = -INFINITY;
+  float l = 0.0f;
+  for (int base = hw * kFTpc * kFUnroll; base < total;
+       base += kFHeadWaves * kFTpc * kFUnroll) {
+    float kv[kFUnroll][kFDq];
+    float vv[kFUnroll][kFDq];
+    bool valid[kFUnroll];
+#pragma unroll
+    for (int u = 0; u < kFUnroll; ++u) {
+      const int f = base + u * kFTpc + g;
+      valid[u] = false;
+      if (f < total) {
+        const int slot = f / ps;
+        const int t = f - slot * ps;
+        valid[u] = t < sh.ntok[slot];
+        if (valid[u]) {
+          const size_t off = static_cast<size_t>(sh.page[slot]) * pool.page_elems +
+                             static_cast<size_t>(t) * E + head_off;
+          LoadDims<kFDq>(pool.keys + off, kv[u]);
+          LoadDims<kFDq>(pool.values + off, vv[u]);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kFUnroll; ++u) {
+      float dot = 0.0f;
+      if (valid[u]) {
+#pragma unroll
+        for (int i = 0; i < kFDq; ++i) dot = fmaf(q[i], kv[u][i], dot);
+      }
+#pragma unroll
+      for (int o = 1; o < kFLpt; o <<= 1) dot += __shfl_xor(dot, o, kWave);
+      if (valid[u]) {
+        const float m_new = fmaxf(m, dot);
+        const float alpha = Exp2(m - m_new);
+        const float beta = Exp2(dot - m_new);
+        l = fmaf(l, alpha, beta);
+#pragma unroll
+        for (int i = 0; i < kFDq; ++i) acc[i] = fmaf(acc[i], alpha, beta * vv[u][i]);
+        m = m_new;
+      }
+    }
+  }
+  // Merge the 4 token-slot streams of this wave, then the 8 waves of each
+  // head in LDS.
+  float wm = m;
+#pragma unroll
+  for (int o = kFLpt; o < kWave; o <<= 1) wm = fmaxf(wm, __shfl_xor(wm, o, kWave));
+  const float sc = (m == -INFINITY) ? 0.0f : Exp2(m - wm);
+  float wl = l * sc;
+#pragma unroll
+  for (int i = 0; i < kFDq; ++i) acc[i] *= sc;
+#pragma unroll
+  for (int o = kFLpt; o < kWave; o <<= 1) {
+    wl += __shfl_xor(wl, o, kWave);
+#pragma unroll
+    for (int i = 0; i < kFDq; ++i) acc[i] += __shfl_xor(acc[i], o, kWave);
+  }
+  if (g == 0) {
+    if (j == 0) {
+      sh.m[wave] = wm;
+      sh.l[wave] = wl;
+    }
+#pragma unroll
+    for (int i = 0; i < kFDq; ++i) sh.acc[wave][j * kFDq + i] = acc[i];
+  }
+  __syncthreads();
+  if (threadIdx.x < kFHeadsPerItem * kFD) {
+    const int hh = threadIdx.x / kFD;  // which of the two heads
+    const int d = threadIdx.x - hh * kFD;
+    const int w0 = hh * kFHeadWaves;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kFHeadWaves; ++w) mx = fmaxf(mx, sh.m[w0 + w]);
+    float lt = 0.0f;
+    float at = 0.0f;
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kFHeadWaves; ++w) {
+        const float sw = (sh.m[w0 + w] == -INFINITY) ? 0.0f : Exp2(sh.m[w0 + w] - mx);
+        lt = fmaf(sh.l[w0 + w], sw, lt);
+        at = fmaf(sh.acc[w0 + w][d], sw, at);
+      }
+    }
+    // No valid token at all: zeros, as the reference.
+    a.outputs[static_cast<size_t>(r) * kFE + static_cast<size_t>(h0 + hh) * kFD + d] =
+        lt == 0.0f ? 0.0f : at / lt;
+  }
+}
+
+__global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, FusedArgs a) {
+  __shared__ FusedShared sh;
+  const int id = blockIdx.x;
+  const int score_items = (a.total + kFPagesPerItem - 1) / kFPagesPerItem;
+  uint64_t t_start = 0, t_selected = 0;
+  if (a.stamps != nullptr && threadIdx.x == 0) t_start = Now();
+  if (id < score_items) {
+    ScoreItem(pool, a, id, sh);
+  } else {
+    const int pairs = pool.num_heads / kFHeadsPerItem;
+    const int item = id - score_items;
+    const int r = item / pairs;
+    AttentionItem(pool, a, r, (item - r * pairs) * kFHeadsPerItem, sh, &t_selected);
+  }
+  if (a.stamps != nullptr && threadIdx.x == 0) {
+    // Per-workgroup start, [counter ready: written by the selection],
+    // selection done (attention items) and end, at distinct addresses;
+    // reduced on the host.
+    a.stamps[kStampsPerGroup * static_cast<size_t>(id) + 0] = t_start;
+    a.stamps[kStampsPerGroup * static_cast<size_t>(id) + 2] = t_selected;
+    a.stamps[kStampsPerGroup * static_cast<size_t>(id) + 3] = Now();
+  }
+}
+
+}  // namespace
+
+bool FusedStepSupported(const PoolView& pool, int max_candidates, int top_k) {
+  return pool.elements == kFE && pool.head_dim == kFD && pool.page_size > 0 &&
+         pool.num_heads % kFHeadsPerItem == 0 && max_candidates <= kFMaxCand &&
+         top_k <= kFMaxK;
+}
+
+int FusedStepScoreItems(int total_candidates) {
+  return (total_candidates + kFPagesPerItem - 1) / kFPagesPerItem;
+}
+
+int FusedStepGrid(const PoolView& pool, int batch, int total_candidates) {
+  return FusedStepScoreItems(total_candidates) + batch * (pool.num_heads / kFHeadsPerItem);
+}
+
+void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t stream) {
+  if (args.batch <= 0) return;
+  const int grid = FusedStepGrid(pool, args.batch, args.total);
+  hipLaunchKernelGGL(FusedStepKernel, dim3(grid), dim3(kFThreads), 0, stream, pool, args);
+  DSD_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace dsdk

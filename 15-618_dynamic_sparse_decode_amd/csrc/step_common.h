@@ -1,0 +1,225 @@
+// step_common.h -- device helpers shared by the decode-step kernels
+// (step_kernels.hip) and the fused single-launch step (fused_step.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+namespace dsdk {
+namespace {
+
+constexpr int kWave = 64;
+
+// ---- certified score intervals ---------------------------------------------
+// The reference score is acc = fl(acc + fl(q_i*s_i)) over i = 0..E-1, then
+// fl(acc*scale).  A workgroup forms the same fp32 products, sums them in
+// double (s_hat) and accumulates |T_i| over the exact prefix sums T_i; the
+// sequential fp32 sum then lies within u*sum|T_i|/(1 - n*u) (u = 2^-24) of
+// the exact sum, plus n*2^-149 for subnormal steps, plus slack for the
+// double rounding of s_hat and the T_i.  WriteBounds turns that into an
+// outward-rounded float interval times scale (fl(x*scale) is monotone in x).
+
+__device__ __forceinline__ float NextDown(float x) {
+  if (x == 0.0f) return -0x1p-149f;
+  uint32_t b = __float_as_uint(x);
+  b = (b & 0x80000000u) ? b + 1u : b - 1u;
+  return __uint_as_float(b);
+}
+
+__device__ __forceinline__ float NextUp(float x) {
+  if (x == 0.0f) return 0x1p-149f;
+  uint32_t b = __float_as_uint(x);
+  b = (b & 0x80000000u) ? b - 1u : b + 1u;
+  return __uint_as_float(b);
+}
+
+__device__ __forceinline__ double WaveSum(double v) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// The certified interval [fl(lo*scale), fl(hi*scale)] around s_hat*scale
+// for an error bound err on the unscaled sum.
+__device__ __forceinline__ void WriteInterval(double s_hat, double err, float scale,
+                                              float* mid_out, float* lo_out, float* hi_out,
+                                              int c) {
+  float lo, hi, mid;
+  if (isfinite(s_hat) && isfinite(err)) {
+    lo = NextDown(__double2float_rd(s_hat - err));
+    hi = NextUp(__double2float_ru(s_hat + err));
+    mid = __double2float_rn(s_hat);
+    if (!(mid >= lo)) mid = lo;
+    if (!(mid <= hi)) mid = hi;
+    lo = __fmul_rn(lo, scale);
+    hi = __fmul_rn(hi, scale);
+    mid = __fmul_rn(mid, scale);
+  } else {
+    // Non-finite sums: an unbounded interval forces the exact path.
+    lo = -INFINITY;
+    hi = INFINITY;
+    mid = 0.0f;
+  }
+  mid_out[c] = mid;
+  lo_out[c] = lo;
+  hi_out[c] = hi;
+}
+
+// Interval from exact-order prefix sums: abs_prefix = sum_i |T_i| formed in
+// double, abs_p an upper bound of sum_i |p_i|.
+__device__ __forceinline__ void WriteBounds(double s_hat, double abs_prefix, double abs_p,
+                                            int n, float scale, float* mid_out,
+                                            float* lo_out, float* hi_out, int c) {
+  const double dn = static_cast<double>(n);
+  const double u = 0x1p-24;
+  const double at_up = abs_prefix * (1.0 + 0x1p-40) + dn * dn * 0x1p-52 * abs_p;
+  double err = u * at_up / (1.0 - dn * u) + dn * 0x1p-52 * abs_p + dn * 0x1p-149;
+  err *= 1.001;
+  WriteInterval(s_hat, err, scale, mid_out, lo_out, hi_out, c);
+}
+
+// Interval from groups of L consecutive products.  Within a group the local
+// prefix sums loc_j are formed in float (recursive summation); P_k is the
+// computed prefix at the start of group k, formed from the float group sums
+// with at most `depth` roundings in any precision no coarser than float.
+// Inputs: s_hat = the double sum of the float group sums, tsum = sum_k
+// (L*|P_k| + sum_j |loc_j|) (accumulated with float rounding at worst),
+// abs_p = an upper bound of sum |p_i|.  With g_m = gamma_m = m*u/(1 - m*u)
+// (Higham, Accuracy and Stability, 2nd ed., Lemma 3.1 and eq. 4.4):
+//   |loc_j - t_j| <= g_L * sum|p|     (t_j: exact local prefix),
+//   |P_k - exact prefix at group k| <= (g_depth + g_L) * sum|p|,
+// so the exact prefix sums satisfy, by the triangle inequality,
+//   sum_i |T_i| <= tsum + n*(g_depth + 2*g_L)*sum|p|,
+// and |s_hat - S| <= g_L*sum|p| + double rounding.  Both feed the
+// sequential-sum bound u*sum|T_i|/(1 - n*u) (eq. 4.3).  4*n*2^-149 covers
+// subnormal steps (absolute error 2^-150 each) of the reference chain and of
+// the local sums; n^2*2^-52*sum|p| the double rounding; (1 + 2^-16) the
+// float rounding of tsum.
+__device__ __forceinline__ void WriteBoundsBlocked(double s_hat, double tsum, double abs_p,
+                                                   int n, int L, int depth, float scale,
+                                                   float* mid, float* lo, float* hi) {
+  const double dn = static_cast<double>(n);
+  const double u = 0x1p-24;
+  const double gl = static_cast<double>(L) * u / (1.0 - static_cast<double>(L) * u);
+  const double gd = static_cast<double>(depth) * u / (1.0 - static_cast<double>(depth) * u);
+  const double t_up = tsum * (1.0 + 0x1p-16) + dn * (gd + 2.0 * gl) * abs_p +
+                      dn * dn * 0x1p-52 * abs_p;
+  double err = u * t_up / (1.0 - dn * u) + gl * abs_p + dn * 0x1p-52 * abs_p +
+               4.0 * dn * 0x1p-149;
+  err *= 1.001;
+  WriteInterval(s_hat, err, scale, mid, lo, hi, 0);
+}
+
+// Orders this wave's LDS writes before its later LDS reads of other lanes'
+// data (a wave-scope release/acquire around a wave barrier).
+__device__ __forceinline__ void WaveSync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---- select keys ------------------------------------------------------------
+// One 64-bit key per candidate whose unsigned order is the reference's
+// comparator (src/reference_kernels.cpp:94-99): high word = order-preserving
+// image of the score (-0.0 folded onto +0.0, since the reference compares
+// with ==), low word = ~page_id so that a smaller id wins a tie.
+
+__device__ __forceinline__ uint64_t SelectKey(float score, int page_id) {
+  uint32_t bits = __float_as_uint(score);
+  if (bits == 0x80000000u) bits = 0u;
+  const uint32_t ord = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+  return (static_cast<uint64_t>(ord) << 32) |
+         static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(page_id));
+}
+
+__device__ __forceinline__ int KeyPage(uint64_t key) {
+  return static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(key & 0xFFFFFFFFull));
+}
+
+// ---- exact rescoring --------------------------------------------------------
+constexpr int kChainPages = 8;
+
+// Exact sequential-chain scores for `nflag` candidates of request r (their
+// candidate indices in flagged[]), written as select keys into keys[].  All
+// threads form the fp32 products of up to kChainPages pages per tile in LDS;
+// one lane per page then runs the dependent adds, so the cost is one chain's
+// latency per group of pages.  Must be called by the whole workgroup.
+constexpr int kRankTile = 1024;
+constexpr int kRankTileStride = kRankTile + 4;
+
+__device__ void RescoreExact(const int* flagged, int nflag, const float* __restrict__ q,
+                             const float* __restrict__ summaries,
+                             const int* __restrict__ token_counts,
+                             const int* __restrict__ cand_ids, int begin, int E, float scale,
+                             float* tile, uint64_t* keys) {
+  for (int g0 = 0; g0 < nflag; g0 += kChainPages) {
+    const int G = nflag - g0 < kChainPages ? nflag - g0 : kChainPages;
+    float acc = 0.0f;
+    for (int t0 = 0; t0 < E; t0 += kRankTile) {
+      const int len = E - t0 < kRankTile ? E - t0 : kRankTile;
+      for (int x = threadIdx.x; x < G * len; x += blockDim.x) {
+        const int f = x / len;
+        const int e = x - f * len;
+        const int page = cand_ids[begin + flagged[g0 + f]];
+        const float sv = token_counts[page] == 0
+                             ? 0.0f
+                             : summaries[static_cast<size_t>(page) * E + t0 + e];
+        tile[f * kRankTileStride + e] = __fmul_rn(q[t0 + e], sv);
+      }
+      __syncthreads();
+      if (static_cast<int>(threadIdx.x) < G) {
+        const float* row = tile + threadIdx.x * kRankTileStride;
+        int e = 0;
+        for (; e + 4 <= len; e += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(row + e);
+          acc = __fadd_rn(acc, v.x);
+          acc = __fadd_rn(acc, v.y);
+          acc = __fadd_rn(acc, v.z);
+          acc = __fadd_rn(acc, v.w);
+        }
+        for (; e < len; ++e) acc = __fadd_rn(acc, row[e]);
+      }
+      __syncthreads();
+    }
+    if (static_cast<int>(threadIdx.x) < G) {
+      const int i = flagged[g0 + threadIdx.x];
+      keys[i] = SelectKey(__fmul_rn(acc, scale), cand_ids[begin + i]);
+    }
+    __syncthreads();
+  }
+}
+
+// ---- attention helpers ------------------------------------------------------
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <int DQ>
+__device__ __forceinline__ void LoadDims(const float* __restrict__ p,
+                                         float (&v)[DQ]) {
+  if constexpr (DQ % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < DQ / 4; ++i) {
+      const float4 x = reinterpret_cast<const float4*>(p)[i];
+      v[4 * i + 0] = x.x;
+      v[4 * i + 1] = x.y;
+      v[4 * i + 2] = x.z;
+      v[4 * i + 3] = x.w;
+    }
+  } else if constexpr (DQ % 2 == 0) {
+#pragma unroll
+    for (int i = 0; i < DQ / 2; ++i) {
+      const float2 x = reinterpret_cast<const float2*>(p)[i];
+      v[2 * i + 0] = x.x;
+      v[2 * i + 1] = x.y;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) v[i] = p[i];
+  }
+}
+
+__device__ __forceinline__ float Exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace
+}  // namespace dsdk

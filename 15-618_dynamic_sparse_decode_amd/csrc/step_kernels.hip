@@ -9,11 +9,10 @@
 #include <cstdlib>
 
 #include "dsd_internal.h"
+#include "step_common.h"
 
 namespace dsdk {
 namespace {
-
-constexpr int kWave = 64;
 
 // ---------------------------------------------------------------------------
 // 1. Exact-order scoring.
@@ -84,64 +83,6 @@ __global__ __launch_bounds__(kWave) void ScoreExactKernel(
 // contains the reference score, because fl(x*scale) is monotone in x.
 // ---------------------------------------------------------------------------
 constexpr int kBoundWaves = 4;
-
-__device__ __forceinline__ float NextDown(float x) {
-  if (x == 0.0f) return -0x1p-149f;
-  uint32_t b = __float_as_uint(x);
-  b = (b & 0x80000000u) ? b + 1u : b - 1u;
-  return __uint_as_float(b);
-}
-
-__device__ __forceinline__ float NextUp(float x) {
-  if (x == 0.0f) return 0x1p-149f;
-  uint32_t b = __float_as_uint(x);
-  b = (b & 0x80000000u) ? b - 1u : b + 1u;
-  return __uint_as_float(b);
-}
-
-__device__ __forceinline__ double WaveSum(double v) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
-
-// Lane 0 turns the wave's sums into the certified interval.
-__device__ __forceinline__ void WriteBounds(double s_hat, double abs_prefix, double abs_p,
-                                            int n, float scale, float* mid_out,
-                                            float* lo_out, float* hi_out, int c) {
-  const double dn = static_cast<double>(n);
-  const double u = 0x1p-24;
-  const double at_up = abs_prefix * (1.0 + 0x1p-40) + dn * dn * 0x1p-52 * abs_p;
-  double err = u * at_up / (1.0 - dn * u) + dn * 0x1p-52 * abs_p + dn * 0x1p-149;
-  err *= 1.001;
-  float lo, hi, mid;
-  if (isfinite(s_hat) && isfinite(err)) {
-    lo = NextDown(__double2float_rd(s_hat - err));
-    hi = NextUp(__double2float_ru(s_hat + err));
-    mid = __double2float_rn(s_hat);
-    if (!(mid >= lo)) mid = lo;
-    if (!(mid <= hi)) mid = hi;
-    lo = __fmul_rn(lo, scale);
-    hi = __fmul_rn(hi, scale);
-    mid = __fmul_rn(mid, scale);
-  } else {
-    // Non-finite sums: an unbounded interval forces the exact path.
-    lo = -INFINITY;
-    hi = INFINITY;
-    mid = 0.0f;
-  }
-  mid_out[c] = mid;
-  lo_out[c] = lo;
-  hi_out[c] = hi;
-}
-
-// Orders this wave's LDS writes before its later LDS reads of other lanes'
-// data (a wave-scope release/acquire around a wave barrier).
-__device__ __forceinline__ void WaveSync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // E = 4096, one 256-thread workgroup per candidate page (grid = candidates):
 // wave w covers elements [1024w, 1024w + 1024), lane l the contiguous block
@@ -310,18 +251,6 @@ __global__ __launch_bounds__(kBoundWaves * kWave) void ScoreBoundGenericKernel(
 // ---------------------------------------------------------------------------
 constexpr int kSelectMaxKeys = 8192;  // 64 KiB of LDS
 
-__device__ __forceinline__ uint64_t SelectKey(float score, int page_id) {
-  uint32_t bits = __float_as_uint(score);
-  if (bits == 0x80000000u) bits = 0u;
-  const uint32_t ord = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
-  return (static_cast<uint64_t>(ord) << 32) |
-         static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(page_id));
-}
-
-__device__ __forceinline__ int KeyPage(uint64_t key) {
-  return static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(key & 0xFFFFFFFFull));
-}
-
 __global__ __launch_bounds__(256) void SelectTopKKernel(
     const float* __restrict__ scores, const int* __restrict__ cand_offsets,
     const int* __restrict__ cand_ids, int top_k, int* __restrict__ selected,
@@ -409,7 +338,6 @@ __device__ void BitonicSortDesc(uint64_t* keys, int* idx, int m, int log_m) {
 // pages into LDS, then one lane per page runs the dependent adds.
 // ---------------------------------------------------------------------------
 constexpr int kCertMaxKeys = 2048;   // next-pow2 candidates per request
-constexpr int kChainPages = 8;
 constexpr int kSelectLdsBytes = 64 * 1024;
 
 __global__ __launch_bounds__(256) void SelectCertifiedKernel(
@@ -549,56 +477,6 @@ __global__ __launch_bounds__(256) void SelectCertifiedKernel(
   if (threadIdx.x == 0) counts[r] = kk;
 }
 
-// Exact sequential-chain scores for `nflag` candidates of request r (their
-// candidate indices in flagged[]), written as select keys into keys[].  All
-// threads form the fp32 products of up to kChainPages pages per tile in LDS;
-// one lane per page then runs the dependent adds, so the cost is one chain's
-// latency per group of pages.  Must be called by the whole workgroup.
-constexpr int kRankTile = 1024;
-constexpr int kRankTileStride = kRankTile + 4;
-
-__device__ void RescoreExact(const int* flagged, int nflag, const float* __restrict__ q,
-                             const float* __restrict__ summaries,
-                             const int* __restrict__ token_counts,
-                             const int* __restrict__ cand_ids, int begin, int E, float scale,
-                             float* tile, uint64_t* keys) {
-  for (int g0 = 0; g0 < nflag; g0 += kChainPages) {
-    const int G = nflag - g0 < kChainPages ? nflag - g0 : kChainPages;
-    float acc = 0.0f;
-    for (int t0 = 0; t0 < E; t0 += kRankTile) {
-      const int len = E - t0 < kRankTile ? E - t0 : kRankTile;
-      for (int x = threadIdx.x; x < G * len; x += blockDim.x) {
-        const int f = x / len;
-        const int e = x - f * len;
-        const int page = cand_ids[begin + flagged[g0 + f]];
-        const float sv = token_counts[page] == 0
-                             ? 0.0f
-                             : summaries[static_cast<size_t>(page) * E + t0 + e];
-        tile[f * kRankTileStride + e] = __fmul_rn(q[t0 + e], sv);
-      }
-      __syncthreads();
-      if (static_cast<int>(threadIdx.x) < G) {
-        const float* row = tile + threadIdx.x * kRankTileStride;
-        int e = 0;
-        for (; e + 4 <= len; e += 4) {
-          const float4 v = *reinterpret_cast<const float4*>(row + e);
-          acc = __fadd_rn(acc, v.x);
-          acc = __fadd_rn(acc, v.y);
-          acc = __fadd_rn(acc, v.z);
-          acc = __fadd_rn(acc, v.w);
-        }
-        for (; e < len; ++e) acc = __fadd_rn(acc, row[e]);
-      }
-      __syncthreads();
-    }
-    if (static_cast<int>(threadIdx.x) < G) {
-      const int i = flagged[g0 + threadIdx.x];
-      keys[i] = SelectKey(__fmul_rn(acc, scale), cand_ids[begin + i]);
-    }
-    __syncthreads();
-  }
-}
-
 // Certified select for up to 256 candidates per request: thread i owns
 // candidate i and finds its rank by counting larger keys (broadcast LDS reads,
 // no barrier chain), ties broken by position so ranks are distinct.
@@ -721,35 +599,6 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
 constexpr int kAttnWaves = 4;
 constexpr int kAttnThreads = kAttnWaves * kWave;
 constexpr int kChunk = 16;
-constexpr float kLog2e = 1.4426950408889634f;
-
-template <int DQ>
-__device__ __forceinline__ void LoadDims(const float* __restrict__ p,
-                                         float (&v)[DQ]) {
-  if constexpr (DQ % 4 == 0) {
-#pragma unroll
-    for (int i = 0; i < DQ / 4; ++i) {
-      const float4 x = reinterpret_cast<const float4*>(p)[i];
-      v[4 * i + 0] = x.x;
-      v[4 * i + 1] = x.y;
-      v[4 * i + 2] = x.z;
-      v[4 * i + 3] = x.w;
-    }
-  } else if constexpr (DQ % 2 == 0) {
-#pragma unroll
-    for (int i = 0; i < DQ / 2; ++i) {
-      const float2 x = reinterpret_cast<const float2*>(p)[i];
-      v[2 * i + 0] = x.x;
-      v[2 * i + 1] = x.y;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < DQ; ++i) v[i] = p[i];
-  }
-}
-
-__device__ __forceinline__ float Exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
 // DQ > 0: head_dim == 4*DQ, lane j covers dims [j*DQ, (j+1)*DQ).
 // DQ == 0: generic head_dim <= 256, lane j covers dims j, j+4, j+8, ...
 template <int DQ>

@@ -138,10 +138,11 @@ def main() -> int:
     log(f"step {ms_per_step * 1e3:.1f} us over {args.steps} steps; "
         f"{rescored} pages rescored exactly")
 
-    # Per-kernel average durations: K back-to-back launches of one stage on
-    # the same stream, bracketed by HIP events.
-    stage_ms = []
-    for stage in range(3):
+    # Per-kernel average durations: K back-to-back launches of one kernel on
+    # the same stream, bracketed by HIP events.  Stages 0-2 are the
+    # three-kernel step (score, select, attention); stage 3 is the
+    # single-launch fused step the default path runs.
+    def replay_ms(stage):
         ctx.replay_stage(stage, sptr)
         torch.cuda.synchronize()
         a = torch.cuda.Event(enable_timing=True)
@@ -151,9 +152,38 @@ def main() -> int:
             ctx.replay_stage(stage, sptr)
         b.record(stream)
         b.synchronize()
-        stage_ms.append(a.elapsed_time(b) / args.steps)
+        return a.elapsed_time(b) / args.steps
+
+    stage_ms = [replay_ms(stage) for stage in range(3)]
+    try:
+        fused_ms = replay_ms(3)
+    except dsd.DsdError:
+        fused_ms = None
     torch.cuda.synchronize()
-    log("stages us: score %.1f select %.1f attention %.1f" % tuple(x * 1e3 for x in stage_ms))
+    log("three-kernel stages us: score %.1f select %.1f attention %.1f"
+        % tuple(x * 1e3 for x in stage_ms))
+    if fused_ms is not None:
+        log(f"fused single-launch step kernel: {fused_ms * 1e3:.1f} us")
+
+    # PCIe-inclusive rate: the host-buffer entry point (queries and CSR in,
+    # outputs out through pinned staging), as the reference's RunBatch.
+    host_steps = max(1, min(args.steps, 20))
+    ctx.run_batch(batch.queries, batch.cand_offsets, batch.cand_ids,
+                  output_mode=dsd.OUTPUT_OUTPUTS, timing_mode=dsd.TIMING_NONE)
+    t0 = time.perf_counter()
+    for _ in range(host_steps):
+        ctx.run_batch(batch.queries, batch.cand_offsets, batch.cand_ids,
+                      output_mode=dsd.OUTPUT_OUTPUTS, timing_mode=dsd.TIMING_NONE)
+    host_ms = (time.perf_counter() - t0) * 1e3 / host_steps
+    log(f"host-buffer step (PCIe-inclusive): {host_ms * 1e3:.1f} us")
+    # In-kernel phase split of one step (timing-events mode): the fused
+    # kernel stamps its first start, last score item, last selection and
+    # last attention item.
+    phases = ctx.run_batch(batch.queries, batch.cand_offsets, batch.cand_ids,
+                           output_mode=dsd.OUTPUT_OUTPUTS,
+                           timing_mode=dsd.TIMING_EVENTS)["timings"]
+    log("timed host step phases us: score %.1f select %.1f attention %.1f kernel %.1f"
+        % tuple(phases[k] * 1e3 for k in ("score_ms", "topk_ms", "attention_ms", "kernel_ms")))
 
     # Algorithmic bytes per launch (fp32).
     sel_h = sel.cpu().numpy()
@@ -173,6 +203,16 @@ def main() -> int:
         "attention": {"us": stage_ms[2] * 1e3, "bytes": attn_bytes, "GBps": attn_gbps},
     }
     step_bytes = score_bytes + select_bytes + attn_bytes
+    if fused_ms is not None:
+        stages["fused_step"] = {"us": fused_ms * 1e3, "bytes": step_bytes,
+                                "GBps": step_bytes / (fused_ms * 1e-3) / 1e9}
+        roof_kernel = ("FusedStepKernel: page scoring + certified top-k + fused gather/"
+                       "attention in one launch")
+        roof_bytes, roof_ms = step_bytes, fused_ms
+    else:
+        roof_kernel = "AttentionFastKernel<128,16,8,4> (fused gather + online softmax)"
+        roof_bytes, roof_ms = attn_bytes, stage_ms[2]
+    roof_gbps = roof_bytes / (roof_ms * 1e-3) / 1e9
 
     result = {
         "metric": METRIC,
@@ -198,10 +238,15 @@ def main() -> int:
         "selection": {"mode": "certified intervals + exact sequential rescoring",
                       "exact_rescored_pages_per_step": rescored / args.steps},
         "stages": stages,
-        "roofline": {"bound": "hbm", "achieved": attn_gbps, "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": attn_gbps / HBM_PEAK_GBPS, "traffic": None,
-                     "kernel": "AttentionKernel<32> (fused gather + online softmax)",
-                     "bytes_per_launch": attn_bytes},
+        "roofline": {"bound": "hbm", "achieved": roof_gbps, "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": roof_gbps / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": roof_kernel, "bytes_per_launch": roof_bytes,
+                     "us_per_launch": roof_ms * 1e3},
+        "step_phases_us": {k[:-3]: phases[k] * 1e3
+                           for k in ("score_ms", "topk_ms", "attention_ms", "kernel_ms")},
+        "host_path": {"us_per_step": host_ms * 1e3, "tokens_per_s": B / (host_ms * 1e-3),
+                      "note": "dsd_sparse_run_batch with host buffers (PCIe-inclusive); "
+                              "not the headline value"},
         "cpu_baseline": None,
     }
 

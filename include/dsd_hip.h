@@ -225,8 +225,9 @@ int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
                                 int* d_selected_counts, void* stream);
 
 /* Re-enqueue one stage of the last dsd_sparse_run_batch_device call on the
- * same buffers (stage 0 = score, 1 = select, 2 = attention).  For per-kernel
- * timing of the hot loop. */
+ * same buffers (stage 0 = score, 1 = select, 2 = attention, each as its own
+ * kernel; 3 = the single-launch fused step, when the last call used it).
+ * For per-kernel timing of the hot loop. */
 int dsd_sparse_replay_stage(dsd_sparse_ctx* ctx, int stage, void* stream);
 
 /* The context's own stream (hipStream_t). */
