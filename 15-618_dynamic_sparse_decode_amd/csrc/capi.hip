@@ -783,6 +783,9 @@ struct dsd_sparse_ctx {
         throw std::invalid_argument(
             "a request has more candidates than the max_candidates the step was given");
       }
+      if (code == 3) {
+        throw std::runtime_error("fused decode step: a selected page id was out of range");
+      }
       throw std::runtime_error("fused decode step: wait for page selection timed out");
     }
   }

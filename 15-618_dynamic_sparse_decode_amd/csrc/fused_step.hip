@@ -74,12 +74,15 @@ struct FusedShared {
   int fail;
   int nflag;
   // selection (attention item)
+  float mid[kFMaxCand];
   uint64_t key[kFMaxCand];
   float lo[kFMaxCand];
   float hi[kFMaxCand];
   int top[kFMaxCand];
   int flag[kFMaxCand];
   int rank[kFMaxCand];
+  int cpage[kFMaxCand];  // page id and token count of candidate i
+  int cntok[kFMaxCand];
   float tlo[kFMaxK];    // intervals of the top-k members, in rank order
   float thi[kFMaxK];
   float red[2][kFWaves];
@@ -133,37 +136,89 @@ __device__ __forceinline__ int* ArrivalCounter(const FusedArgs& a, unsigned epoc
   return a.arrivals + (static_cast<size_t>(epoch & 1u) * a.max_batch + r) * kCounterStride;
 }
 
-// Ranks of the n <= 256 keys in sh.key (descending; equal keys by position)
-// into sh.rank: tpc threads per candidate count disjoint slices of the keys
-// (broadcast LDS reads, 8 in flight) and add their counts with shuffles.
-// Must be called by the whole workgroup; ends with a barrier.
-__device__ void ParallelRanks(FusedShared& sh, int n) {
-  const int tpc = n <= kFThreads / 8 ? 8 : 4;
+// Ranks of the n <= 256 keys in sh.key (descending; equal keys by position):
+// kTpc threads per candidate count interleaved slices of the keys
+// (candidate j is read by part j % kTpc: contiguous LDS words per
+// instruction) and add their counts with shuffles.  Returns the rank to the
+// candidate's first thread (part 0), n elsewhere.  No barrier.
+constexpr int kTpc = 4;
+// Every candidate below kFMaxCand has a lead thread in both rank passes.
+static_assert(kFThreads / kTpc >= kFMaxCand, "PartialRanks must cover kFMaxCand");
+static_assert(kFThreads / 4 >= kFMaxCand, "FloatRanks must cover kFMaxCand");
+
+__device__ __forceinline__ int PartialRanks(const FusedShared& sh, int n, int* cand_out) {
   const int t = threadIdx.x;
-  const int cand = t / tpc;
-  const int part = t - cand * tpc;
+  const int cand = t / kTpc;
+  const int part = t - cand * kTpc;
   int partial = 0;
   if (cand < n) {
     const uint64_t key = sh.key[cand];
-    const int m = (n + tpc - 1) / tpc;
-    const int j0 = part * m;
-    const int j1 = j0 + m < n ? j0 + m : n;
-    int j = j0;
-    for (; j + 8 <= j1; j += 8) {
+    int j = part;
+    for (; j + 7 * kTpc < n; j += 8 * kTpc) {
       uint64_t kj[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) kj[u] = sh.key[j + u];
+      for (int u = 0; u < 8; ++u) kj[u] = sh.key[j + u * kTpc];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        partial += (kj[u] > key || (kj[u] == key && j + u < cand)) ? 1 : 0;
+        partial += (kj[u] > key || (kj[u] == key && j + u * kTpc < cand)) ? 1 : 0;
       }
     }
-    for (; j < j1; ++j) partial += (sh.key[j] > key || (sh.key[j] == key && j < cand)) ? 1 : 0;
+    for (; j < n; j += kTpc) {
+      partial += (sh.key[j] > key || (sh.key[j] == key && j < cand)) ? 1 : 0;
+    }
   }
-  partial += __shfl_xor(partial, 1, kWave);
-  partial += __shfl_xor(partial, 2, kWave);
-  if (tpc == 8) partial += __shfl_xor(partial, 4, kWave);
-  if (cand < n && part == 0) sh.rank[cand] = partial;
+#pragma unroll
+  for (int o = 1; o < kTpc; o <<= 1) partial += __shfl_xor(partial, o, kWave);
+  *cand_out = cand;
+  return (cand < n && part == 0) ? partial : n;
+}
+
+// The common case of the same ranks from the float scores alone: tpc
+// threads per candidate (as many as the workgroup allows for n: every
+// candidate below n must get a lead thread) count the midpoints strictly
+// above its own (two instructions per midpoint instead of a 64-bit key
+// comparison).  That is the rank whenever no two candidates have equal
+// midpoints; equal ones are counted into *ties (including itself), and the
+// caller falls back to the key ranks when any candidate has one.
+__device__ __forceinline__ int FloatRanks(const FusedShared& sh, int n, int* cand_out,
+                                          int* ties) {
+  const int tpc = n <= kFThreads / 16 ? 16 : (n <= kFThreads / 8 ? 8 : 4);
+  const int t = threadIdx.x;
+  const int cand = t / tpc;
+  const int part = t - cand * tpc;
+  int gt = 0, eq = 0;
+  if (cand < n) {
+    const float m = sh.mid[cand];
+    int j = part;
+    for (; j + 7 * tpc < n; j += 8 * tpc) {
+      float mj[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) mj[u] = sh.mid[j + u * tpc];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        gt += mj[u] > m ? 1 : 0;
+        eq += mj[u] == m ? 1 : 0;
+      }
+    }
+    for (; j < n; j += tpc) {
+      gt += sh.mid[j] > m ? 1 : 0;
+      eq += sh.mid[j] == m ? 1 : 0;
+    }
+  }
+  for (int o = 1; o < tpc; o <<= 1) {  // tpc is uniform: every lane shuffles
+    gt += __shfl_xor(gt, o, kWave);
+    eq += __shfl_xor(eq, o, kWave);
+  }
+  *cand_out = cand;
+  *ties = eq;
+  return (cand < n && part == 0) ? gt : n;
+}
+
+// Ranks of the keys into sh.rank (whole workgroup; ends with a barrier).
+__device__ void ParallelRanks(FusedShared& sh, int n) {
+  int cand;
+  const int rank = PartialRanks(sh, n, &cand);
+  if (rank < n) sh.rank[cand] = rank;
   __syncthreads();
 }
 
@@ -300,8 +355,8 @@ __device__ void ScoreItem(const PoolView& pool, const FusedArgs& a, int s, Fused
 // Top-k of request r (n candidates from `begin`) from the published
 // intervals into sh.page / sh.ntok; returns the count (0 on failure).
 // Candidates whose order the intervals do not decide are rescored with the
-// exact sequential chain (as SelectCertifiedRankKernel).  The workgroup of
-// head 0 also writes the selection out for the caller.
+// exact sequential chain (as SelectCertifiedRankKernel).  The workgroup with
+// `writer` set also writes the selection out for the caller.
 __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r, int begin,
                                 int n, bool writer, FusedShared& sh) {
   int kk = a.top_k <= 0 ? 0 : (a.top_k < n ? a.top_k : n);
@@ -312,10 +367,10 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     kk = 0;
   }
   const int i = threadIdx.x;
-  const bool active = kk > 0 && i < n;
+  const bool mine = kk > 0 && i < n;
   // Ids and token counts do not depend on the scores: fetch them first.
   int my_page = 0, my_ntok = 0;
-  if (active) {
+  if (mine) {
     my_page = a.cand_ids[begin + i];
     my_ntok = pool.token_counts[my_page];
   }
@@ -340,7 +395,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
   if (a.stamps != nullptr && threadIdx.x == 0) {
     a.stamps[kStampsPerGroup * static_cast<size_t>(blockIdx.x) + 1] = Now();
   }
-  if (active && !sh.fail) {
+  if (mine && !sh.fail) {
     unsigned long long* rec = a.rec + 3 * static_cast<size_t>(begin + i);
     // First an ordinary (L2-cached) read, shared by the workgroups of this
     // request on the XCD; a word whose tag is not current (not yet visible,
@@ -357,9 +412,12 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
       w1 = LoadWord(rec + 1);
       w2 = LoadWord(rec + 2);
     }
-    sh.key[i] = SelectKey(__uint_as_float(static_cast<uint32_t>(w0)), my_page);
+    sh.mid[i] = __uint_as_float(static_cast<uint32_t>(w0));
+    sh.key[i] = SelectKey(sh.mid[i], my_page);
     sh.lo[i] = __uint_as_float(static_cast<uint32_t>(w1));
     sh.hi[i] = __uint_as_float(static_cast<uint32_t>(w2));
+    sh.cpage[i] = my_page;
+    sh.cntok[i] = my_ntok;
   }
   __syncthreads();
   if (sh.fail) {
@@ -367,16 +425,29 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     kk = 0;
   }
   if (kk > 0) {
-    const bool mine = i < n;
-    ParallelRanks(sh, n);
-    int rank = mine ? sh.rank[i] : n;
-    if (mine && rank < kk) {
-      sh.top[rank] = i;
-      sh.tlo[rank] = sh.lo[i];
-      sh.thi[rank] = sh.hi[i];
+    // Ranks, with everything the flag test needs published in the same
+    // pass: rank per candidate, the members' intervals in rank order, the
+    // members' pages (speculatively: rewritten if rescoring reorders), and
+    // per-wave min(lo of members) / max(hi of outsiders).  Midpoints decide
+    // the ranks unless two are equal; then the (score, page id) keys do.
+    int cand, ties;
+    int lead_rank = FloatRanks(sh, n, &cand, &ties);
+    if (__syncthreads_or(lead_rank < n && ties > 1)) {
+      lead_rank = PartialRanks(sh, n, &cand);
     }
-    float my_min = (mine && rank < kk) ? sh.lo[i] : INFINITY;
-    float my_max = (mine && rank >= kk) ? sh.hi[i] : -INFINITY;
+    float my_min = INFINITY, my_max = -INFINITY;
+    if (lead_rank < n) {
+      sh.rank[cand] = lead_rank;
+      if (lead_rank < kk) {
+        sh.tlo[lead_rank] = sh.lo[cand];
+        sh.thi[lead_rank] = sh.hi[cand];
+        sh.page[lead_rank] = sh.cpage[cand];
+        sh.ntok[lead_rank] = sh.cntok[cand];
+        my_min = sh.lo[cand];
+      } else {
+        my_max = sh.hi[cand];
+      }
+    }
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
       my_min = fminf(my_min, __shfl_xor(my_min, o, kWave));
@@ -388,48 +459,62 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
       sh.red[1][wave] = my_max;
     }
     __syncthreads();
-    float min_t_lo = INFINITY, max_o_hi = -INFINITY;
+    bool flag = false;
+    if (i < n) {
+      float min_t_lo = INFINITY, max_o_hi = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kFWaves; ++w) {
-      min_t_lo = fminf(min_t_lo, sh.red[0][w]);
-      max_o_hi = fmaxf(max_o_hi, sh.red[1][w]);
-    }
-    if (mine) {
+      for (int w = 0; w < kFWaves; ++w) {
+        min_t_lo = fminf(min_t_lo, sh.red[0][w]);
+        max_o_hi = fmaxf(max_o_hi, sh.red[1][w]);
+      }
+      const int rank = sh.rank[i];
       const float l = sh.lo[i];
       const float h = sh.hi[i];
-      bool flag;
       if (rank >= kk) {
         flag = h >= min_t_lo;
       } else {
-        // Overlap with any other member (intervals in rank order: independent
-        // reads), or with the best outsider.
-        flag = l <= max_o_hi;
+        // Overlap with any other member, or with the best outsider.  The
+        // members are in midpoint order, so a member ranked above overlaps
+        // iff its lo <= this hi, one ranked below iff its hi >= this lo.
+        float above_lo = INFINITY, below_hi = -INFINITY;
 #pragma unroll 4
         for (int j = 0; j < kk; ++j) {
-          flag = flag || (j != rank && l <= sh.thi[j] && sh.tlo[j] <= h);
+          const float tl = sh.tlo[j];
+          const float th = sh.thi[j];
+          above_lo = j < rank ? fminf(above_lo, tl) : above_lo;
+          below_hi = j > rank ? fmaxf(below_hi, th) : below_hi;
         }
+        flag = l <= max_o_hi || above_lo <= h || below_hi >= l;
       }
-      if (flag) sh.flag[atomicAdd(&sh.nflag, 1)] = i;
     }
-    __syncthreads();
-    const int nflag = sh.nflag;
-    if (nflag > 0) {
+    if (__syncthreads_or(flag ? 1 : 0)) {
+      // Some order is not decided by the intervals: rescore those pages
+      // with the exact chain, rank again and rewrite the members.
+      if (flag) sh.flag[atomicAdd(&sh.nflag, 1)] = i;
+      __syncthreads();
+      const int nflag = sh.nflag;
       if (writer && threadIdx.x == 0 && a.exact_pages != nullptr) {
         atomicAdd(a.exact_pages, nflag);
       }
       RescoreExact(sh.flag, nflag, a.queries + static_cast<size_t>(r) * kFE, pool.summaries,
                    pool.token_counts, a.cand_ids, begin, kFE, a.scale, sh.tile, sh.key);
       ParallelRanks(sh, n);
-      rank = mine ? sh.rank[i] : n;
+      if (i < n && sh.rank[i] < kk) {
+        sh.page[sh.rank[i]] = sh.cpage[i];
+        sh.ntok[sh.rank[i]] = sh.cntok[i];
+      }
+      __syncthreads();
     }
-    if (mine && rank < kk) {
-      sh.page[rank] = my_page;
-      sh.ntok[rank] = my_ntok;
-      if (writer) a.selected[static_cast<size_t>(r) * a.sel_stride + rank] = my_page;
+    // Every member slot holds a candidate's page id; one outside the pool
+    // would be a selection bug: drop it (no K/V access) and report it.
+    if (i < kk && (sh.page[i] < 0 || sh.page[i] >= pool.capacity)) {
+      sh.ntok[i] = 0;
+      ReportFailure(a, 3);
     }
+    __syncthreads();
+    if (writer && i < kk) a.selected[static_cast<size_t>(r) * a.sel_stride + i] = sh.page[i];
   }
   if (writer && threadIdx.x == 0) a.counts[r] = kk;
-  __syncthreads();
   return kk;
 }
 
