@@ -728,6 +728,8 @@ struct dsd_sparse_ctx {
     }
     dsdk::LaunchFusedStep(pool->view, a, s);
     if (stamp) {
+      // The kernel's own end, before the stamps travel back.
+      DSD_HIP_CHECK(hipEventRecord(ev[3], s));
       DSD_HIP_CHECK(hipMemcpyAsync(h_stamps.ptr, d_stamps.ptr,
                                    4 * sizeof(unsigned long long) * stamp_grid,
                                    hipMemcpyDeviceToHost, s));
@@ -761,8 +763,7 @@ struct dsd_sparse_ctx {
   void Enqueue(const Launch& L, hipStream_t s, bool timing) {
     if (L.fused) {
       if (timing) DSD_HIP_CHECK(hipEventRecord(ev[0], s));
-      EnqueueFused(L, s, timing);
-      if (timing) DSD_HIP_CHECK(hipEventRecord(ev[3], s));
+      EnqueueFused(L, s, timing);  // records ev[3] at the kernel's end
       return;
     }
     if (timing) DSD_HIP_CHECK(hipEventRecord(ev[0], s));

@@ -74,6 +74,9 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     ap.add_argument("--cpu-sample-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB, 5 times (the "
+                         "known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -84,6 +87,16 @@ def main() -> int:
     # torch first: libdsd_hip.so then binds to the HIP runtime torch loaded,
     # so the process holds a single runtime and torch streams are valid.
     import torch
+
+    if args.copy_calibration > 0:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n * 4, "copies": 5}), flush=True)
+        return 0
 
     dsd = load_package()
     if not dsd.gpu_available():
@@ -239,7 +252,10 @@ def main() -> int:
                       "exact_rescored_pages_per_step": rescored / args.steps},
         "stages": stages,
         "roofline": {"bound": "hbm", "achieved": roof_gbps, "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": roof_gbps / HBM_PEAK_GBPS, "traffic": None,
+                     "unit": "GB/s", "frac": roof_gbps / HBM_PEAK_GBPS,
+                     "traffic": measured_traffic(args.config, roof_kernel),
+                     "traffic_source": f"profiles/decode_step_config{args.config}_traffic.md "
+                                       "(FETCH_SIZE/WRITE_SIZE per launch, copy-calibrated)",
                      "kernel": roof_kernel, "bytes_per_launch": roof_bytes,
                      "us_per_launch": roof_ms * 1e3},
         "step_phases_us": {k[:-3]: phases[k] * 1e3
@@ -257,6 +273,20 @@ def main() -> int:
     pool.close()
     print(json.dumps(result), flush=True)
     return 0
+
+
+def measured_traffic(config, roof_kernel):
+    """HBM bytes per launch of the roofline kernel from the committed counter
+    summary for this config (two rocprofv3 --pmc passes, FETCH_SIZE and
+    WRITE_SIZE, scaled by a plain copy of known size), or None."""
+    path = ROOT / "profiles" / f"decode_step_config{config}_traffic.json"
+    if not path.exists():
+        return None
+    kernels = json.loads(path.read_text()).get("kernels", {})
+    for name, entry in kernels.items():
+        if roof_kernel.startswith(name.split("<")[0]):
+            return entry["traffic_bytes"]
+    return None
 
 
 def cpu_baseline(dsd, batch, pool, k, gpu_out, sample_seconds):
