@@ -723,7 +723,7 @@ struct dsd_sparse_ctx {
     a.exact_pages = d_exact_pages.ptr;
     a.fail_flag = h_fail.ptr;
     if (stamp) {
-      stamp_grid = dsdk::FusedStepGrid(pool->view, L.batch, L.total);
+      stamp_grid = dsdk::FusedStepGrid(pool->view, L.batch);
       a.stamps = d_stamps.ptr;
     }
     dsdk::LaunchFusedStep(pool->view, a, s);
@@ -731,27 +731,25 @@ struct dsd_sparse_ctx {
       // The kernel's own end, before the stamps travel back.
       DSD_HIP_CHECK(hipEventRecord(ev[3], s));
       DSD_HIP_CHECK(hipMemcpyAsync(h_stamps.ptr, d_stamps.ptr,
-                                   4 * sizeof(unsigned long long) * stamp_grid,
+                                   sizeof(unsigned long long) * stamp_grid *
+                                       dsdk::FusedStepStampsPerGroup(),
                                    hipMemcpyDeviceToHost, s));
     }
   }
-  // Phase split of the last timed fused launch from its workgroup stamps:
-  // first start, last score item end, last selection done, last end.
-  void FusedPhases(int total, double* score_ms, double* select_ms,
-                   double* attention_ms) const {
+  // Phase split of the last timed fused launch from its workgroup stamps
+  // (start, slice scored, counter ready, records read, ranked, selected,
+  // end): first start -> last slice scored -> last selection -> last end.
+  void FusedPhases(double* score_ms, double* select_ms, double* attention_ms) const {
     *score_ms = *select_ms = *attention_ms = 0.0;
     if (stamp_grid <= 0 || wall_khz <= 0.0) return;
-    const int score_items = dsdk::FusedStepScoreItems(total);
+    const int per = dsdk::FusedStepStampsPerGroup();
     const unsigned long long* st = h_stamps.ptr;
     unsigned long long t0 = ~0ull, t_score = 0, t_select = 0, t_end = 0;
     for (int g = 0; g < stamp_grid; ++g) {
-      t0 = std::min(t0, st[4 * g]);
-      if (g < score_items) {
-        t_score = std::max(t_score, st[4 * g + 3]);
-      } else {
-        t_select = std::max(t_select, st[4 * g + 2]);
-        t_end = std::max(t_end, st[4 * g + 3]);
-      }
+      t0 = std::min(t0, st[per * g + 0]);
+      t_score = std::max(t_score, st[per * g + 1]);
+      t_select = std::max(t_select, st[per * g + 5]);
+      t_end = std::max(t_end, st[per * g + 6]);
     }
     t_score = std::max(t_score, t0);
     t_select = std::max(t_select, t_score);
@@ -854,12 +852,12 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     DSD_HIP_CHECK(hipMemset(ctx->d_exact_pages.ptr, 0, sizeof(int)));
     {
       const size_t rec = 3 * P;
-      const size_t grid =
-          static_cast<size_t>(dsdk::FusedStepGrid(pool->view, static_cast<int>(B),
-                                                  static_cast<int>(P)));
+      const size_t stamps =
+          static_cast<size_t>(dsdk::FusedStepGrid(pool->view, static_cast<int>(B))) *
+          dsdk::FusedStepStampsPerGroup();
       ctx->d_rec.Reserve(rec);
-      ctx->d_stamps.Reserve(4 * grid);
-      ctx->h_stamps.Reserve(4 * grid);
+      ctx->d_stamps.Reserve(stamps);
+      ctx->h_stamps.Reserve(stamps);
       DSD_HIP_CHECK(hipMemset(ctx->d_rec.ptr, 0, rec * sizeof(unsigned long long)));
       const size_t arrivals = 2 * B * 32;
       ctx->d_arrivals.Reserve(arrivals);
@@ -1016,7 +1014,7 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
       // One kernel: its event time, split at the workgroup clock stamps.
       float k = 0.f;
       DSD_HIP_CHECK(hipEventElapsedTime(&k, ctx->ev[0], ctx->ev[3]));
-      ctx->FusedPhases(L.total, &t.score_ms, &t.topk_ms, &t.attention_ms);
+      ctx->FusedPhases(&t.score_ms, &t.topk_ms, &t.attention_ms);
       t.kernel_ms = k;
     } else if (timing) {
       float a = 0.f, b = 0.f, c = 0.f;

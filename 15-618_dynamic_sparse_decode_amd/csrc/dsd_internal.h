@@ -152,16 +152,17 @@ struct FusedArgs {
   unsigned epoch = 0;
   int* exact_pages = nullptr;         // may be null
   int* fail_flag = nullptr;           // host-visible: 1 wait timed out, 2 CSR overflow
-  unsigned long long* stamps = nullptr;  // null, or [grid][4] clocks: start,
-                                         // counter ready, selection done, end
+  unsigned long long* stamps = nullptr;  // null, or [grid][FusedStepStampsPerGroup()]:
+                                         // clocks at start, slice scored, counter
+                                         // ready, records read, ranked, selected,
+                                         // end; then the hardware ids
 };
 
 // E = 4096, head_dim = 128, max_candidates <= 256, top_k <= 256.
 bool FusedStepSupported(const PoolView& pool, int max_candidates, int top_k);
-// Workgroups of one launch: score items (8 candidates each), then
-// batch * num_heads / 2 attention items.
-int FusedStepScoreItems(int total_candidates);
-int FusedStepGrid(const PoolView& pool, int batch, int total_candidates);
+// Workgroups of one launch: num_heads / 2 per request.
+int FusedStepGrid(const PoolView& pool, int batch);
+int FusedStepStampsPerGroup();
 void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t stream);
 
 }  // namespace dsdk

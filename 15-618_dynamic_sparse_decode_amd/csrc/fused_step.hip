@@ -7,38 +7,30 @@
 // (GatherPagesCpu + SparseAttentionCpu, :109-194) -- run in one kernel, so the
 // step pays one launch and no kernel boundary between dependent stages.
 //
-// Work items, by workgroup id:
-//   [0, S)          score items, S = ceil(P / 8): the certified intervals of
-//                   candidates 8s .. 8s+7 (two waves per page)
-//   [S, S + B*H/2)  attention items (request r, heads 2i and 2i+1),
-//                   request-major: each selects its request's top-k from the
-//                   intervals (the H/2 items of a request compute the same
-//                   selection; the first writes it out), then attends over
-//                   the selected pages, eight waves per head.
-// Workgroups have 1024 threads, one per CU, so the score items and the
-// first attention items start together and every attention item is
-// resident by the time the score items finish.
-// An attention item waits for its request's intervals, i.e. only for lower
-// workgroup ids.  Each XCD dispatches its share of a grid in id order, so
-// every score item has started (or finished) before any attention item
-// starts, and score items never wait: every wait ends.  The spins are
-// bounded anyway (a timeout is reported to the host and gives zeros, never a
-// hang).
+// Work items.  Request r owns the G = H/2 consecutive workgroups
+// [r*G, r*G + G); workgroup (r, g) takes heads 2g and 2g+1.  Each does:
+//   1. score: the certified intervals of its slice of the request's
+//      candidates, [n*g/G, n*(g+1)/G), eight pages per pass, two waves per
+//      page; publishes them and counts itself into the request's arrival
+//      counter;
+//   2. select: waits until the G workgroups of its request have arrived,
+//      then computes the request's top-k from the intervals (the G
+//      workgroups compute the same selection; g = 0 writes it out);
+//   3. attend: eight waves per head over the selected pages.
+// Workgroups have 1024 threads (one per CU at this kernel's register use),
+// so at B*H/2 <= 256 the whole step is one dispatch wave.
 //
-// Publication without fences.  Each interval crosses workgroups as three
-// 64-bit words (mid, lo, hi) whose high half is this launch's epoch (a
-// per-context counter, never 0) and whose low half is the float: written
-// with relaxed agent-scope atomic stores, read with relaxed agent-scope
-// atomic loads until the epoch matches.  A word is valid exactly when its
-// tag is current, so no ordering between words is needed and there is no
-// release/acquire (each would write back or invalidate the XCD's L2).
-// Waiting is cheap: each score item adds its pages to its request's arrival
-// counter (one counter per 128-byte line, so requests never share a line;
-// read-modify-writes on one line serialise device-wide), and one thread per
-// attention item polls that counter; only then are the interval words read
-// (and re-read if a tag is not yet current: the counter is a wake-up hint,
-// never trusted for the data).  Counters are double-buffered by epoch
-// parity; each launch clears the set the next launch will use.
+// Every wait ends.  A workgroup waits only for the workgroups of its own
+// request, which have adjacent ids.  Workgroup i goes to XCD i mod 8 and each
+// XCD dispatches its share in id order.  Take the lowest-id unfinished
+// workgroup u (request r): everything below u has finished, so any workgroup
+// of r that an XCD has not dispatched yet is queued behind at most the other
+// members of r on that XCD (ceil(G/8) in all), and an XCD that can hold that
+// many workgroups dispatches it.  The members of r never wait for anything
+// outside r and score before they wait, so u finishes; by induction every
+// workgroup does.  The spins are bounded anyway (a timeout is reported to the
+// host and gives zeros, never a hang).
+//
 #include "dsd_internal.h"
 #include "step_common.h"
 
@@ -49,8 +41,8 @@ constexpr int kFThreads = 1024;             // one workgroup per CU
 constexpr int kFWaves = kFThreads / kWave;  // 16
 constexpr int kFE = 4096;
 constexpr int kFD = 128;
-constexpr int kFPagesPerItem = 8;           // score item = 8 pages, 2 waves each
-constexpr int kFHeadsPerItem = 2;           // attention item = 2 heads, 8 waves each
+constexpr int kFPagesPerPass = 8;           // score pass = 8 pages, 2 waves each
+constexpr int kFHeadsPerItem = 2;           // workgroup = 2 heads, 8 waves each
 constexpr int kFHeadWaves = kFWaves / kFHeadsPerItem;
 constexpr int kFPageLanes = 2 * kWave;      // 128 lanes per page
 constexpr int kFPerLane = kFE / kFPageLanes;  // 32 consecutive products per lane
@@ -62,15 +54,18 @@ constexpr int kFTpc = kWave / kFLpt;      // 4 token rows per wave per chunk
 constexpr int kFUnroll = 4;               // chunks in flight per wave
 constexpr unsigned kSpinLimit = 1u << 24;  // polls of ~1 us each at most
 constexpr int kCounterStride = 32;         // ints: one 128-byte line per counter
-constexpr int kStampsPerGroup = 4;         // start, counter ready, selected, end
+// Timing mode: per-workgroup wall clocks at start, slice scored, counter
+// ready, records read, ranked, selected, end; then the hardware ids.
+constexpr int kStampsPerGroup = 8;
+enum Stamp { kStart, kScored, kReady, kRecords, kRanked, kSelected, kEnd, kHwId };
 
 struct FusedShared {
-  // score item (per wave): float total (the carry into wave 2p+1), double
-  // sum of the group sums, bound sums
+  uint64_t stamp[kStampsPerGroup];  // timing mode: thread 0's clocks
+  // score pass (per wave): float total (the carry into wave 2p+1) and the
+  // bound sums
   float wave_total[kFWaves];
-  double total[kFWaves];
-  double abs_prefix[kFWaves];
-  double abs_p[kFWaves];
+  float abs_prefix[kFWaves];
+  float abs_p[kFWaves];
   int fail;
   int nflag;
   // selection (attention item)
@@ -97,6 +92,13 @@ struct FusedShared {
 
 __device__ __forceinline__ uint64_t Now() { return static_cast<uint64_t>(wall_clock64()); }
 
+// Timing mode only: thread 0 records the wall clock for stamp `which` in
+// LDS (a global store here would make the next barrier wait for it); the
+// kernel's end writes them out.
+__device__ __forceinline__ void StampAt(const FusedArgs& a, FusedShared& sh, int which) {
+  if (a.stamps != nullptr && threadIdx.x == 0) sh.stamp[which] = Now();
+}
+
 __device__ __forceinline__ void PutTagged(unsigned long long* p, unsigned epoch,
                                           uint32_t payload) {
   __hip_atomic_store(p, (static_cast<unsigned long long>(epoch) << 32) | payload,
@@ -113,22 +115,6 @@ __device__ __forceinline__ bool Current(unsigned long long w, unsigned epoch) {
 
 __device__ __forceinline__ void ReportFailure(const FusedArgs& a, int code) {
   __hip_atomic_store(a.fail_flag, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-
-// Index of the request holding candidate c: the number of requests whose
-// candidate range ends at or before c (cand_offsets is non-decreasing).  One
-// wave-wide load per 64 requests instead of a dependent binary search.
-__device__ __forceinline__ int RequestOfBallot(const int* __restrict__ offs, int batch, int c) {
-  const int lane = threadIdx.x & (kWave - 1);
-  int r = 0;
-  for (int base = 0; base < batch; base += kWave) {
-    const int i = base + lane;
-    const int end = i < batch ? offs[i + 1] : 0x7fffffff;
-    const int cnt = __popcll(__ballot(end <= c));
-    r += cnt;
-    if (cnt < kWave) break;
-  }
-  return r;
 }
 
 // Arrival counter of request r for the launch with this epoch.
@@ -222,30 +208,32 @@ __device__ void ParallelRanks(FusedShared& sh, int n) {
   __syncthreads();
 }
 
-// Score item s: certified intervals of candidates 8s .. 8s+7.  Waves 2p and
-// 2p+1 take page p, wave 2p+h the elements [2048h, 2048h + 2048) as 8 rows
-// of 64 float4: lane l of row j holds float4 number 512h + 64j + l, so every
-// load instruction reads 1 KiB contiguously.  Each lane's float4 is a group
-// of 4 consecutive products (L = 4): the lane forms the group's local prefix
-// sums in float; a float scan of the group sums along the row (plus the
-// rows before, plus wave 2p's total for h = 1) gives the group's starting
-// prefix; the group sums also meet in double for s_hat.
-__device__ void ScoreItem(const PoolView& pool, const FusedArgs& a, int s, FusedShared& sh) {
+// One score pass: certified intervals of candidates first + p, p < 8, below
+// end (all of request r).  Waves 2p and 2p+1 take candidate first + p, wave
+// 2p+h the elements [2048h, 2048h + 2048) as 8 rows of 64 float4: lane l of
+// row j holds float4 number 512h + 64j + l, so every load instruction reads
+// 1 KiB contiguously.  Each lane's float4 is a group of L = 4 consecutive
+// products: the lane forms the group's local prefix sums; a DPP scan of the
+// group sums along the row, plus the sums of the rows before, plus wave 2p's
+// total for h = 1, gives the group's starting prefix.  All in float; the
+// rounding depth on any product's path into a group's starting prefix or
+// into the page sum is at most 3 local + 6 scan + 8 rows of wave 2p + 8 rows
+// of wave 2p+1 + 1 = 26 (40 is used in the bound).  Called by the whole
+// workgroup.
+__device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int r, int first, int end,
+                          FusedShared& sh) {
   constexpr int kRows = kFPerLane / 4;  // 8
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int half = wave & 1;
-  const int c = s * kFPagesPerItem + (wave >> 1);
-  const bool active = c < a.total;  // uniform per wave
-  float row_sum[kRows];   // float sums of the rows, all lanes
-  float excl[kRows];      // this lane's exclusive prefix within row j
+  const int c = first + (wave >> 1);
+  const bool active = c < end;  // uniform per wave
+  float row_sum[kRows];   // float sums of the rows (wave-uniform)
+  float excl[kRows];      // sum of the group sums of the lanes below, row j
   float loc_abs = 0.0f;   // sum of |loc| over this lane's groups
   float p_abs = 0.0f;
-  double s_lane = 0.0;
-  int r = 0;
   if (active) {
     const int page = a.cand_ids[c];
-    r = RequestOfBallot(a.cand_offsets, a.batch, c);
     const float4* q4 = reinterpret_cast<const float4*>(a.queries + static_cast<size_t>(r) * kFE) +
                        half * 512 + lane;
     const float4* s4 =
@@ -271,24 +259,16 @@ __device__ void ScoreItem(const PoolView& pool, const FusedArgs& a, int s, Fused
       const float p1 = __fmul_rn(qv[j].y, sv[j].y);
       const float p2 = __fmul_rn(qv[j].z, sv[j].z);
       const float p3 = __fmul_rn(qv[j].w, sv[j].w);
-      const float l1 = p0;
-      const float l2 = __fadd_rn(l1, p1);
+      const float l2 = __fadd_rn(p0, p1);
       const float l3 = __fadd_rn(l2, p2);
       const float l4 = __fadd_rn(l3, p3);
-      loc_abs = __fadd_rn(loc_abs, __fadd_rn(__fadd_rn(fabsf(l1), fabsf(l2)),
+      loc_abs = __fadd_rn(loc_abs, __fadd_rn(__fadd_rn(fabsf(p0), fabsf(l2)),
                                              __fadd_rn(fabsf(l3), fabsf(l4))));
       p_abs = __fadd_rn(p_abs, __fadd_rn(__fadd_rn(fabsf(p0), fabsf(p1)),
                                          __fadd_rn(fabsf(p2), fabsf(p3))));
-      s_lane += static_cast<double>(l4);
-      // row scan of the group sums (float)
-      float incl = l4;
-#pragma unroll
-      for (int o = 1; o < kWave; o <<= 1) {
-        const float t = __shfl_up(incl, o, kWave);
-        if (lane >= o) incl = __fadd_rn(incl, t);
-      }
-      row_sum[j] = __shfl(incl, kWave - 1, kWave);
-      excl[j] = __fsub_rn(incl, l4);
+      const float incl = WaveInclusiveScan(l4);
+      row_sum[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(incl), kWave - 1));
+      excl[j] = DppMove<kWaveShr1>(incl);  // exact: the inclusive sum of lane - 1
     }
     if (lane == 0) {
       float total = 0.0f;
@@ -308,57 +288,52 @@ __device__ void ScoreItem(const PoolView& pool, const FusedArgs& a, int s, Fused
       tl = __fadd_rn(tl, 4.0f * fabsf(start));
       base = __fadd_rn(base, row_sum[j]);
     }
-    double tsum = static_cast<double>(tl) + static_cast<double>(loc_abs);
-    double absp = static_cast<double>(p_abs);
-    double sl = s_lane;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      tsum += __shfl_xor(tsum, o, kWave);
-      absp += __shfl_xor(absp, o, kWave);
-      sl += __shfl_xor(sl, o, kWave);
-    }
+    const float tsum = WaveTotal(__fadd_rn(tl, loc_abs));
+    const float absp = WaveTotal(p_abs);
     if (lane == 0) {
-      sh.total[wave] = sl;
       sh.abs_prefix[wave] = tsum;
       sh.abs_p[wave] = absp;
     }
   }
   __syncthreads();
-  if (s == 0 && static_cast<int>(threadIdx.x) < a.max_batch) {
-    // Clear the arrival counters the next launch uses.
-    __hip_atomic_store(ArrivalCounter(a, a.epoch + 1, threadIdx.x), 0, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  }
   if (active && half == 0 && lane == 0) {
-    const double s_hat = sh.total[wave] + sh.total[wave + 1];
-    const double tsum = sh.abs_prefix[wave] + sh.abs_prefix[wave + 1];
-    const double ap = sh.abs_p[wave] + sh.abs_p[wave + 1];
-    // Roundings on any term's path into a group's starting prefix: 6 scan
-    // steps, 1 subtraction, 8 additions into wave 2p's total, 8 row
-    // additions, 1 final addition (24; 40 used).  The float |p| sums carry
-    // < 2^-19 relative error; doubled to stay an upper bound.
+    const float s_hat = __fadd_rn(sh.wave_total[wave], sh.wave_total[wave + 1]);
+    const float tsum = __fadd_rn(sh.abs_prefix[wave], sh.abs_prefix[wave + 1]);
+    const float ap = __fadd_rn(sh.abs_p[wave], sh.abs_p[wave + 1]);
     float mid, lo, hi;
-    WriteBoundsBlocked(s_hat, tsum, 2.0 * ap, kFE, 4, 40, a.scale, &mid, &lo, &hi);
+    WriteBoundsFloat(s_hat, tsum, ap, kFE, 4, 40, a.scale, &mid, &lo, &hi);
     a.mid[c] = mid;
     a.lo[c] = lo;
     a.hi[c] = hi;
-    // Publish the interval, then count the page into its request.
     unsigned long long* rec = a.rec + 3 * static_cast<size_t>(c);
     PutTagged(rec + 0, a.epoch, __float_as_uint(mid));
     PutTagged(rec + 1, a.epoch, __float_as_uint(lo));
     PutTagged(rec + 2, a.epoch, __float_as_uint(hi));
+  }
+}
+
+// The candidates [c0, c1) of request r, eight per pass; then this workgroup
+// counts itself into the request's arrival counter.
+__device__ void ScoreSlice(const PoolView& pool, const FusedArgs& a, int r, int c0, int c1,
+                           FusedShared& sh) {
+  for (int first = c0; first < c1; first += kFPagesPerPass) {
+    ScorePass(pool, a, r, first, c1, sh);
+  }
+  __syncthreads();  // the slice's words are issued before the count
+  if (threadIdx.x == 0) {
     __hip_atomic_fetch_add(ArrivalCounter(a, a.epoch, r), 1, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 // Top-k of request r (n candidates from `begin`) from the published
-// intervals into sh.page / sh.ntok; returns the count (0 on failure).
+// intervals into sh.page / sh.ntok, once all `groups` workgroups of the
+// request have counted in; returns the count (0 on failure).
 // Candidates whose order the intervals do not decide are rescored with the
 // exact sequential chain (as SelectCertifiedRankKernel).  The workgroup with
 // `writer` set also writes the selection out for the caller.
 __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r, int begin,
-                                int n, bool writer, FusedShared& sh) {
+                                int n, int groups, bool writer, FusedShared& sh) {
   int kk = a.top_k <= 0 ? 0 : (a.top_k < n ? a.top_k : n);
   if (n > kFMaxCand) {
     // The caller's max_candidates understated the CSR: select nothing (the
@@ -378,11 +353,11 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     sh.fail = 0;
     sh.nflag = 0;
     if (kk > 0) {
-      // One poller per workgroup: wait until every page of the request has
-      // arrived (a hint; the tags below decide).
+      // One poller per workgroup: wait until every workgroup of the request
+      // has published its slice (a hint; the tags below decide).
       int* counter = ArrivalCounter(a, a.epoch, r);
       unsigned spins = 0;
-      while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < n) {
+      while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < groups) {
         __builtin_amdgcn_s_sleep(2);
         if (++spins >= kSpinLimit) {
           sh.fail = 1;
@@ -392,9 +367,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     }
   }
   __syncthreads();
-  if (a.stamps != nullptr && threadIdx.x == 0) {
-    a.stamps[kStampsPerGroup * static_cast<size_t>(blockIdx.x) + 1] = Now();
-  }
+  StampAt(a, sh, kReady);
   if (mine && !sh.fail) {
     unsigned long long* rec = a.rec + 3 * static_cast<size_t>(begin + i);
     // First an ordinary (L2-cached) read, shared by the workgroups of this
@@ -420,6 +393,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     sh.cntok[i] = my_ntok;
   }
   __syncthreads();
+  StampAt(a, sh, kRecords);
   if (sh.fail) {
     if (threadIdx.x == 0) ReportFailure(a, 1);
     kk = 0;
@@ -435,6 +409,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     if (__syncthreads_or(lead_rank < n && ties > 1)) {
       lead_rank = PartialRanks(sh, n, &cand);
     }
+    StampAt(a, sh, kRanked);
     float my_min = INFINITY, my_max = -INFINITY;
     if (lead_rank < n) {
       sh.rank[cand] = lead_rank;
@@ -518,12 +493,13 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
   return kk;
 }
 
-// Attention item (request r, heads h0 and h0+1): select, then per head
-// softmax(q_h K^T * scale) V over the selected pages' valid tokens; waves
-// 0-7 take head h0 and waves 8-15 head h0+1, each as
+// Attention of workgroup (r, g), heads h0 = 2g and h0+1: select, then per
+// head softmax(q_h K^T * scale) V over the selected pages' valid tokens;
+// waves 0-7 take head h0 and waves 8-15 head h0+1, each as
 // AttentionFastKernel<128, 16, 8, 4>.
-__device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, int h0,
-                              FusedShared& sh, uint64_t* t_selected) {
+__device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, int begin, int n,
+                              int group, int groups, FusedShared& sh) {
+  const int h0 = group * kFHeadsPerItem;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int hw = wave % kFHeadWaves;   // wave within its head
@@ -531,8 +507,6 @@ __device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, i
   const int g = lane / kFLpt;
   const int j = lane % kFLpt;
   const int head_off = h * kFD + j * kFDq;
-  const int begin = a.cand_offsets[r];
-  const int n = a.cand_offsets[r + 1] - begin;
   float q[kFDq];
   float acc[kFDq];
   {
@@ -544,8 +518,8 @@ __device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, i
       acc[i] = 0.0f;
     }
   }
-  const int kk = SelectForRequest(pool, a, r, begin, n, h0 == 0, sh);
-  if (a.stamps != nullptr && threadIdx.x == 0) *t_selected = Now();
+  const int kk = SelectForRequest(pool, a, r, begin, n, groups, group == 0, sh);
+  StampAt(a, sh, kSelected);
   if (kk == 0) {
     // Nothing selected: zeros (src/cuda/sparse_batched_attention.cu:621-627).
     if (threadIdx.x < kFHeadsPerItem * kFD) {
@@ -650,25 +624,36 @@ __device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, i
 
 __global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, FusedArgs a) {
   __shared__ FusedShared sh;
-  const int id = blockIdx.x;
-  const int score_items = (a.total + kFPagesPerItem - 1) / kFPagesPerItem;
-  uint64_t t_start = 0, t_selected = 0;
-  if (a.stamps != nullptr && threadIdx.x == 0) t_start = Now();
-  if (id < score_items) {
-    ScoreItem(pool, a, id, sh);
-  } else {
-    const int pairs = pool.num_heads / kFHeadsPerItem;
-    const int item = id - score_items;
-    const int r = item / pairs;
-    AttentionItem(pool, a, r, (item - r * pairs) * kFHeadsPerItem, sh, &t_selected);
-  }
   if (a.stamps != nullptr && threadIdx.x == 0) {
-    // Per-workgroup start, [counter ready: written by the selection],
-    // selection done (attention items) and end, at distinct addresses;
-    // reduced on the host.
-    a.stamps[kStampsPerGroup * static_cast<size_t>(id) + 0] = t_start;
-    a.stamps[kStampsPerGroup * static_cast<size_t>(id) + 2] = t_selected;
-    a.stamps[kStampsPerGroup * static_cast<size_t>(id) + 3] = Now();
+    for (int i = 0; i < kStampsPerGroup; ++i) sh.stamp[i] = 0;
+  }
+  StampAt(a, sh, kStart);
+  const int groups = pool.num_heads / kFHeadsPerItem;
+  const int r = blockIdx.x / groups;
+  const int g = blockIdx.x - r * groups;
+  if (blockIdx.x == 0 && static_cast<int>(threadIdx.x) < a.max_batch) {
+    // Clear the arrival counters the next launch uses.
+    __hip_atomic_store(ArrivalCounter(a, a.epoch + 1, threadIdx.x), 0, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const int begin = a.cand_offsets[r];
+  const int n = a.cand_offsets[r + 1] - begin;
+  // A request beyond kFMaxCand selects nothing (reported by the selection):
+  // its slices are not scored.
+  if (n <= kFMaxCand) {
+    ScoreSlice(pool, a, r, begin + (g * n) / groups, begin + ((g + 1) * n) / groups, sh);
+  }
+  StampAt(a, sh, kScored);
+  AttentionItem(pool, a, r, begin, n, g, groups, sh);
+  StampAt(a, sh, kEnd);
+  if (a.stamps != nullptr && threadIdx.x == 0) {
+    // HW_ID (wave slot, SIMD, CU, shader array, shader engine) and XCC_ID.
+    const uint64_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+    const uint64_t xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);
+    sh.stamp[kHwId] = (xcc << 32) | hw;
+    for (int i = 0; i < kStampsPerGroup; ++i) {
+      a.stamps[kStampsPerGroup * static_cast<size_t>(blockIdx.x) + i] = sh.stamp[i];
+    }
   }
 }
 
@@ -680,17 +665,15 @@ bool FusedStepSupported(const PoolView& pool, int max_candidates, int top_k) {
          top_k <= kFMaxK;
 }
 
-int FusedStepScoreItems(int total_candidates) {
-  return (total_candidates + kFPagesPerItem - 1) / kFPagesPerItem;
+int FusedStepGrid(const PoolView& pool, int batch) {
+  return batch * (pool.num_heads / kFHeadsPerItem);
 }
 
-int FusedStepGrid(const PoolView& pool, int batch, int total_candidates) {
-  return FusedStepScoreItems(total_candidates) + batch * (pool.num_heads / kFHeadsPerItem);
-}
+int FusedStepStampsPerGroup() { return kStampsPerGroup; }
 
 void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t stream) {
   if (args.batch <= 0) return;
-  const int grid = FusedStepGrid(pool, args.batch, args.total);
+  const int grid = FusedStepGrid(pool, args.batch);
   hipLaunchKernelGGL(FusedStepKernel, dim3(grid), dim3(kFThreads), 0, stream, pool, args);
   DSD_HIP_CHECK(hipGetLastError());
 }

@@ -80,36 +80,67 @@ __device__ __forceinline__ void WriteBounds(double s_hat, double abs_prefix, dou
   WriteInterval(s_hat, err, scale, mid_out, lo_out, hi_out, c);
 }
 
-// Interval from groups of L consecutive products.  Within a group the local
-// prefix sums loc_j are formed in float (recursive summation); P_k is the
-// computed prefix at the start of group k, formed from the float group sums
-// with at most `depth` roundings in any precision no coarser than float.
-// Inputs: s_hat = the double sum of the float group sums, tsum = sum_k
-// (L*|P_k| + sum_j |loc_j|) (accumulated with float rounding at worst),
-// abs_p = an upper bound of sum |p_i|.  With g_m = gamma_m = m*u/(1 - m*u)
+// Interval from a float evaluation in groups of L consecutive products.
+// Within a group the local prefix sums loc_j are formed in float (recursive
+// summation); P_k, the computed prefix at the start of group k, and s_hat,
+// the computed sum of all products, come from float additions of the group
+// sums in some tree.  `depth` bounds the roundings on any product's path
+// into any P_k or into s_hat, the L - 1 local ones included.  Inputs:
+// tsum >= sum_k (L*|P_k| + sum_j |loc_j|) and abs_p >= sum_i |p_i|, each
+// summed in float with at most 64 roundings on any path (relative error
+// below 2^-17, covered by the factor 1 + 2^-16).  With g_m = m*u/(1 - m*u)
 // (Higham, Accuracy and Stability, 2nd ed., Lemma 3.1 and eq. 4.4):
-//   |loc_j - t_j| <= g_L * sum|p|     (t_j: exact local prefix),
-//   |P_k - exact prefix at group k| <= (g_depth + g_L) * sum|p|,
+//   |loc_j - t_j| <= g_L * sum|p|       (t_j: exact local prefix),
+//   |P_k - exact prefix at group k| <= g_depth * sum|p|,
+//   |s_hat - S| <= g_depth * sum|p|     (S: exact sum),
 // so the exact prefix sums satisfy, by the triangle inequality,
-//   sum_i |T_i| <= tsum + n*(g_depth + 2*g_L)*sum|p|,
-// and |s_hat - S| <= g_L*sum|p| + double rounding.  Both feed the
-// sequential-sum bound u*sum|T_i|/(1 - n*u) (eq. 4.3).  4*n*2^-149 covers
-// subnormal steps (absolute error 2^-150 each) of the reference chain and of
-// the local sums; n^2*2^-52*sum|p| the double rounding; (1 + 2^-16) the
-// float rounding of tsum.
-__device__ __forceinline__ void WriteBoundsBlocked(double s_hat, double tsum, double abs_p,
-                                                   int n, int L, int depth, float scale,
-                                                   float* mid, float* lo, float* hi) {
+//   sum_i |T_i| <= tsum + n*(g_depth + g_L)*sum|p|,
+// which feeds the sequential-sum bound u*sum|T_i|/(1 - n*u) (eq. 4.3) for
+// the reference chain.  Float additions are exact in the subnormal range and
+// the products are the reference's own, so no subnormal term is needed;
+// 4*n*2^-149 is kept as slack, and 1.001 covers this function's own double
+// arithmetic.
+__device__ __forceinline__ void WriteBoundsFloat(float s_hat, float tsum, float abs_p, int n,
+                                                 int L, int depth, float scale, float* mid,
+                                                 float* lo, float* hi) {
   const double dn = static_cast<double>(n);
   const double u = 0x1p-24;
   const double gl = static_cast<double>(L) * u / (1.0 - static_cast<double>(L) * u);
   const double gd = static_cast<double>(depth) * u / (1.0 - static_cast<double>(depth) * u);
-  const double t_up = tsum * (1.0 + 0x1p-16) + dn * (gd + 2.0 * gl) * abs_p +
-                      dn * dn * 0x1p-52 * abs_p;
-  double err = u * t_up / (1.0 - dn * u) + gl * abs_p + dn * 0x1p-52 * abs_p +
-               4.0 * dn * 0x1p-149;
+  const double ap = static_cast<double>(abs_p) * (1.0 + 0x1p-16);
+  const double t_up = static_cast<double>(tsum) * (1.0 + 0x1p-16) + dn * (gd + gl) * ap;
+  double err = u * t_up / (1.0 - dn * u) + gd * ap + 4.0 * dn * 0x1p-149;
   err *= 1.001;
-  WriteInterval(s_hat, err, scale, mid, lo, hi, 0);
+  WriteInterval(static_cast<double>(s_hat), err, scale, mid, lo, hi, 0);
+}
+
+// ---- wave scans with DPP -----------------------------------------------------
+// x from lane `lane - shift` in its row of 16 (row_shr), lane 15 of the row
+// below (row_bcast:15, rows 1 and 3), lane 31 (row_bcast:31, rows 2 and 3),
+// or the lane below across the wave (wave_shr:1); lanes with no source read 0.
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ float DppMove(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, kRowMask, 0xf, true));
+}
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143, kWaveShr1 = 0x138;
+
+// Inclusive prefix sum over the 64 lanes in float (Hillis-Steele): every
+// input reaches every output through at most 6 additions.
+__device__ __forceinline__ float WaveInclusiveScan(float x) {
+  x = __fadd_rn(x, DppMove<kRowShr1>(x));
+  x = __fadd_rn(x, DppMove<kRowShr2>(x));
+  x = __fadd_rn(x, DppMove<kRowShr4>(x));
+  x = __fadd_rn(x, DppMove<kRowShr8>(x));
+  x = __fadd_rn(x, DppMove<kRowBcast15, 0xa>(x));
+  x = __fadd_rn(x, DppMove<kRowBcast31, 0xc>(x));
+  return x;
+}
+
+// Sum over the 64 lanes (at most 6 roundings per input), in every lane.
+__device__ __forceinline__ float WaveTotal(float x) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(WaveInclusiveScan(x)), 63));
 }
 
 // Orders this wave's LDS writes before its later LDS reads of other lanes'
