@@ -643,7 +643,6 @@ struct dsd_sparse_ctx {
   // fused-step publication words (see fused_step.hip) and per-workgroup
   // clock stamps for the timing mode
   DeviceBuffer<unsigned long long> d_rec, d_stamps;
-  DeviceBuffer<int> d_arrivals;
   unsigned epoch = 0;
   double wall_khz = 0.0;  // wall_clock64() rate
   int score_mode = DSD_SCORE_CERTIFIED;
@@ -696,7 +695,7 @@ struct dsd_sparse_ctx {
   }
   // The single-launch step covers certified selection on the hot shape.
   bool UseFused(bool certified, int max_n) const {
-    return certified && fused_enabled && max_batch <= 512 &&
+    return certified && fused_enabled &&
            dsdk::FusedStepSupported(pool->view, max_n, top_k);
   }
   void EnqueueFused(const Launch& L, hipStream_t s, bool stamp) {
@@ -716,8 +715,6 @@ struct dsd_sparse_ctx {
     a.counts = L.counts;
     a.outputs = L.outputs;
     a.rec = d_rec.ptr;
-    a.arrivals = d_arrivals.ptr;
-    a.max_batch = std::max(1, max_batch);
     if (++epoch == 0) epoch = 1;  // words start at 0: never tag with epoch 0
     a.epoch = epoch;
     a.exact_pages = d_exact_pages.ptr;
@@ -859,9 +856,6 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
       ctx->d_stamps.Reserve(stamps);
       ctx->h_stamps.Reserve(stamps);
       DSD_HIP_CHECK(hipMemset(ctx->d_rec.ptr, 0, rec * sizeof(unsigned long long)));
-      const size_t arrivals = 2 * B * 32;
-      ctx->d_arrivals.Reserve(arrivals);
-      DSD_HIP_CHECK(hipMemset(ctx->d_arrivals.ptr, 0, arrivals * sizeof(int)));
     }
     ctx->h_fail.Reserve(1);
     ctx->h_fail.ptr[0] = 0;

@@ -147,11 +147,10 @@ struct FusedArgs {
   int* counts = nullptr;              // [batch]
   float* outputs = nullptr;           // [batch][E]
   unsigned long long* rec = nullptr;
-  int* arrivals = nullptr;            // [2][max_batch][32] counters, zero at creation
-  int max_batch = 0;                  // <= 512
   unsigned epoch = 0;
   int* exact_pages = nullptr;         // may be null
-  int* fail_flag = nullptr;           // host-visible: 1 wait timed out, 2 CSR overflow
+  int* fail_flag = nullptr;           // host-visible: 1 wait timed out, 2 CSR overflow,
+                                      // 3 page id outside the pool
   unsigned long long* stamps = nullptr;  // null, or [grid][FusedStepStampsPerGroup()]:
                                          // clocks at start, slice scored, counter
                                          // ready, records read, ranked, selected,

@@ -11,11 +11,10 @@
 // [r*G, r*G + G); workgroup (r, g) takes heads 2g and 2g+1.  Each does:
 //   1. score: the certified intervals of its slice of the request's
 //      candidates, [n*g/G, n*(g+1)/G), eight pages per pass, two waves per
-//      page; publishes them and counts itself into the request's arrival
-//      counter;
-//   2. select: waits until the G workgroups of its request have arrived,
-//      then computes the request's top-k from the intervals (the G
-//      workgroups compute the same selection; g = 0 writes it out);
+//      page, published as tagged words (below);
+//   2. select: waits until every interval of its request is published,
+//      then computes the request's top-k from them (the G workgroups
+//      compute the same selection; g = 0 writes it out);
 //   3. attend: eight waves per head over the selected pages.
 // Workgroups have 1024 threads (one per CU at this kernel's register use),
 // so at B*H/2 <= 256 the whole step is one dispatch wave.
@@ -31,6 +30,16 @@
 // workgroup does.  The spins are bounded anyway (a timeout is reported to the
 // host and gives zeros, never a hang).
 //
+// Publication without fences.  Each interval crosses workgroups as three
+// 64-bit words (mid, lo, hi) whose high half is this launch's epoch (a
+// per-context counter, never 0) and whose low half is the float: written
+// with relaxed agent-scope atomic stores, read with relaxed agent-scope
+// atomic loads until the epoch matches.  A word is valid exactly when its
+// tag is current, so no ordering between words is needed and there is no
+// release/acquire (each would write back or invalidate the XCD's L2).  Wave
+// 0 of each workgroup polls its request's words directly (a cached read
+// first, then coherent re-reads of the words whose tag is not yet current,
+// with a short sleep between rounds) and shares them through LDS.
 #include "dsd_internal.h"
 #include "step_common.h"
 
@@ -52,8 +61,9 @@ constexpr int kFLpt = 16;                 // lanes per token row (8 dims each)
 constexpr int kFDq = kFD / kFLpt;         // 8
 constexpr int kFTpc = kWave / kFLpt;      // 4 token rows per wave per chunk
 constexpr int kFUnroll = 4;               // chunks in flight per wave
-constexpr unsigned kSpinLimit = 1u << 24;  // polls of ~1 us each at most
-constexpr int kCounterStride = 32;         // ints: one 128-byte line per counter
+constexpr unsigned kSpinLimit = 1u << 22;  // polls (about 1 us each) before a timeout
+constexpr int kFSlots = kFMaxCand / kWave;  // candidates (or ranks) per lane: l + 64m
+static_assert(kFMaxK <= kFMaxCand, "rank slots cover the candidate slots");
 // Timing mode: per-workgroup wall clocks at start, slice scored, counter
 // ready, records read, ranked, selected, end; then the hardware ids.
 constexpr int kStampsPerGroup = 8;
@@ -117,20 +127,14 @@ __device__ __forceinline__ void ReportFailure(const FusedArgs& a, int code) {
   __hip_atomic_store(a.fail_flag, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// Arrival counter of request r for the launch with this epoch.
-__device__ __forceinline__ int* ArrivalCounter(const FusedArgs& a, unsigned epoch, int r) {
-  return a.arrivals + (static_cast<size_t>(epoch & 1u) * a.max_batch + r) * kCounterStride;
-}
-
 // Ranks of the n <= 256 keys in sh.key (descending; equal keys by position):
 // kTpc threads per candidate count interleaved slices of the keys
 // (candidate j is read by part j % kTpc: contiguous LDS words per
 // instruction) and add their counts with shuffles.  Returns the rank to the
 // candidate's first thread (part 0), n elsewhere.  No barrier.
 constexpr int kTpc = 4;
-// Every candidate below kFMaxCand has a lead thread in both rank passes.
+// Every candidate below kFMaxCand has a lead thread.
 static_assert(kFThreads / kTpc >= kFMaxCand, "PartialRanks must cover kFMaxCand");
-static_assert(kFThreads / 4 >= kFMaxCand, "FloatRanks must cover kFMaxCand");
 
 __device__ __forceinline__ int PartialRanks(const FusedShared& sh, int n, int* cand_out) {
   const int t = threadIdx.x;
@@ -157,47 +161,6 @@ __device__ __forceinline__ int PartialRanks(const FusedShared& sh, int n, int* c
   for (int o = 1; o < kTpc; o <<= 1) partial += __shfl_xor(partial, o, kWave);
   *cand_out = cand;
   return (cand < n && part == 0) ? partial : n;
-}
-
-// The common case of the same ranks from the float scores alone: tpc
-// threads per candidate (as many as the workgroup allows for n: every
-// candidate below n must get a lead thread) count the midpoints strictly
-// above its own (two instructions per midpoint instead of a 64-bit key
-// comparison).  That is the rank whenever no two candidates have equal
-// midpoints; equal ones are counted into *ties (including itself), and the
-// caller falls back to the key ranks when any candidate has one.
-__device__ __forceinline__ int FloatRanks(const FusedShared& sh, int n, int* cand_out,
-                                          int* ties) {
-  const int tpc = n <= kFThreads / 16 ? 16 : (n <= kFThreads / 8 ? 8 : 4);
-  const int t = threadIdx.x;
-  const int cand = t / tpc;
-  const int part = t - cand * tpc;
-  int gt = 0, eq = 0;
-  if (cand < n) {
-    const float m = sh.mid[cand];
-    int j = part;
-    for (; j + 7 * tpc < n; j += 8 * tpc) {
-      float mj[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) mj[u] = sh.mid[j + u * tpc];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        gt += mj[u] > m ? 1 : 0;
-        eq += mj[u] == m ? 1 : 0;
-      }
-    }
-    for (; j < n; j += tpc) {
-      gt += sh.mid[j] > m ? 1 : 0;
-      eq += sh.mid[j] == m ? 1 : 0;
-    }
-  }
-  for (int o = 1; o < tpc; o <<= 1) {  // tpc is uniform: every lane shuffles
-    gt += __shfl_xor(gt, o, kWave);
-    eq += __shfl_xor(eq, o, kWave);
-  }
-  *cand_out = cand;
-  *ties = eq;
-  return (cand < n && part == 0) ? gt : n;
 }
 
 // Ranks of the keys into sh.rank (whole workgroup; ends with a barrier).
@@ -233,13 +196,20 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int r, int f
   float loc_abs = 0.0f;   // sum of |loc| over this lane's groups
   float p_abs = 0.0f;
   if (active) {
-    const int page = a.cand_ids[c];
+    int page = a.cand_ids[c];
+    int count = 0;
+    if (page >= 0 && page < pool.capacity) {
+      count = pool.token_counts[page];
+    } else {
+      // An id outside the pool scores as an empty page and is reported.
+      if (half == 0 && lane == 0) ReportFailure(a, 3);
+      page = 0;
+    }
     const float4* q4 = reinterpret_cast<const float4*>(a.queries + static_cast<size_t>(r) * kFE) +
                        half * 512 + lane;
     const float4* s4 =
         reinterpret_cast<const float4*>(pool.summaries + static_cast<size_t>(page) * kFE) +
         half * 512 + lane;
-    const int count = pool.token_counts[page];
     float4 qv[kRows];
     float4 sv[kRows];
 #pragma unroll
@@ -312,28 +282,79 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int r, int f
   }
 }
 
-// The candidates [c0, c1) of request r, eight per pass; then this workgroup
-// counts itself into the request's arrival counter.
+// The candidates [c0, c1) of request r, eight per pass.
 __device__ void ScoreSlice(const PoolView& pool, const FusedArgs& a, int r, int c0, int c1,
                            FusedShared& sh) {
   for (int first = c0; first < c1; first += kFPagesPerPass) {
     ScorePass(pool, a, r, first, c1, sh);
   }
-  __syncthreads();  // the slice's words are issued before the count
-  if (threadIdx.x == 0) {
-    __hip_atomic_fetch_add(ArrivalCounter(a, a.epoch, r), 1, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-  }
 }
 
+// ---- selection helpers: wave scans with identities (lanes with no source
+// keep the identity) -----------------------------------------------------------
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ float DppOr(float x, float identity) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(identity), __float_as_int(x),
+                                                    kCtrl, kRowMask, 0xf, false));
+}
+constexpr int kRowShl1 = 0x101, kRowShl2 = 0x102, kRowShl4 = 0x104, kRowShl8 = 0x108;
+constexpr int kWaveShl1 = 0x130;
+
+__device__ __forceinline__ float ReadLane(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+// Inclusive minimum over lanes 0..l.
+__device__ __forceinline__ float WaveMinPrefix(float x) {
+  x = fminf(x, DppOr<kRowShr1>(x, INFINITY));
+  x = fminf(x, DppOr<kRowShr2>(x, INFINITY));
+  x = fminf(x, DppOr<kRowShr4>(x, INFINITY));
+  x = fminf(x, DppOr<kRowShr8>(x, INFINITY));
+  x = fminf(x, DppOr<kRowBcast15, 0xa>(x, INFINITY));
+  x = fminf(x, DppOr<kRowBcast31, 0xc>(x, INFINITY));
+  return x;
+}
+
+// Inclusive maximum over lanes l..63: within each row of 16 by row shifts
+// toward lane 0, then the rows above through their first lanes.
+__device__ __forceinline__ float WaveMaxSuffix(float x) {
+  x = fmaxf(x, DppOr<kRowShl1>(x, -INFINITY));
+  x = fmaxf(x, DppOr<kRowShl2>(x, -INFINITY));
+  x = fmaxf(x, DppOr<kRowShl4>(x, -INFINITY));
+  x = fmaxf(x, DppOr<kRowShl8>(x, -INFINITY));
+  const float r3 = ReadLane(x, 48);
+  const float r2 = fmaxf(ReadLane(x, 32), r3);
+  const float r1 = fmaxf(ReadLane(x, 16), r2);
+  const int row = (threadIdx.x & (kWave - 1)) >> 4;
+  const float above = row == 0 ? r1 : (row == 1 ? r2 : (row == 2 ? r3 : -INFINITY));
+  return fmaxf(x, above);
+}
+
+__device__ __forceinline__ float WaveMax(float x) { return ReadLane(WaveMaxSuffix(x), 0); }
+
+__device__ __forceinline__ int Popc(uint64_t m) { return __popcll(m); }
+
 // Top-k of request r (n candidates from `begin`) from the published
-// intervals into sh.page / sh.ntok, once all `groups` workgroups of the
-// request have counted in; returns the count (0 on failure).
-// Candidates whose order the intervals do not decide are rescored with the
-// exact sequential chain (as SelectCertifiedRankKernel).  The workgroup with
-// `writer` set also writes the selection out for the caller.
+// intervals into sh.page / sh.ntok (rank order); returns the count (0 on
+// failure).  The order is that of the (score desc, page id asc) key of the
+// reference comparator; equal keys (a page listed twice) by position.
+//   1. Every lane holds candidates l + 64m (id, token count); wave 0 polls
+//      the interval words and shares them in LDS; one barrier.
+//   2. Ranks by ballots: rank(i) = #{j : mid_j > mid_i} + #{j : mid_j ==
+//      mid_i and (page_j, j) < (page_i, i)}.  Wave w ranks the candidates
+//      whose lane is w mod 16 and writes the members' rank slots; one
+//      barrier.
+//   3. Certification, computed identically by every wave (no barrier): an
+//      outsider is flagged when its hi reaches the members' smallest lo; a
+//      member when its lo reaches the outsiders' largest hi, or when it
+//      overlaps a member ranked above (prefix minimum of lo) or below
+//      (suffix maximum of hi).  The members are in midpoint order, so these
+//      cover every overlapping pair.
+//   4. Only if some pair is flagged: those pages are rescored with the exact
+//      sequential chain (as SelectCertifiedRankKernel) and ranked again.
+// The workgroup with `writer` set also writes the selection out.
 __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r, int begin,
-                                int n, int groups, bool writer, FusedShared& sh) {
+                                int n, bool writer, FusedShared& sh) {
   int kk = a.top_k <= 0 ? 0 : (a.top_k < n ? a.top_k : n);
   if (n > kFMaxCand) {
     // The caller's max_candidates understated the CSR: select nothing (the
@@ -341,56 +362,73 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     if (writer && threadIdx.x == 0) ReportFailure(a, 2);
     kk = 0;
   }
-  const int i = threadIdx.x;
-  const bool mine = kk > 0 && i < n;
-  // Ids and token counts do not depend on the scores: fetch them first.
-  int my_page = 0, my_ntok = 0;
-  if (mine) {
-    my_page = a.cand_ids[begin + i];
-    my_ntok = pool.token_counts[my_page];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  // Ids and token counts do not depend on the scores: every wave loads them
+  // for all candidates first.  An id outside the pool keeps no tokens (the
+  // score pass reported it).
+  int page[kFSlots], ntok[kFSlots];
+#pragma unroll
+  for (int m = 0; m < kFSlots; ++m) {
+    const int i = lane + kWave * m;
+    page[m] = 0x7fffffff;
+    ntok[m] = 0;
+    if (kk > 0 && i < n) {
+      page[m] = a.cand_ids[begin + i];
+      if (page[m] >= 0 && page[m] < pool.capacity) ntok[m] = pool.token_counts[page[m]];
+    }
   }
-  if (i == 0) {
-    sh.fail = 0;
-    sh.nflag = 0;
-    if (kk > 0) {
-      // One poller per workgroup: wait until every workgroup of the request
-      // has published its slice (a hint; the tags below decide).
-      int* counter = ArrivalCounter(a, a.epoch, r);
-      unsigned spins = 0;
-      while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < groups) {
-        __builtin_amdgcn_s_sleep(2);
-        if (++spins >= kSpinLimit) {
-          sh.fail = 1;
-          break;
+  if (threadIdx.x == 0) sh.fail = 0;
+  if (wave == 0 && kk > 0) {
+    // First an ordinary (L2-cached) read; words whose tag is not current
+    // (not yet visible, or a stale cached line) are then polled coherently.
+    unsigned long long w[kFSlots][3];
+    bool ok = true;
+#pragma unroll
+    for (int m = 0; m < kFSlots; ++m) {
+      const int i = lane + kWave * m;
+      w[m][0] = w[m][1] = w[m][2] = static_cast<unsigned long long>(a.epoch) << 32;
+      if (i < n) {
+        const unsigned long long* rec = a.rec + 3 * static_cast<size_t>(begin + i);
+        w[m][0] = rec[0];
+        w[m][1] = rec[1];
+        w[m][2] = rec[2];
+        ok = ok && Current(w[m][0], a.epoch) && Current(w[m][1], a.epoch) &&
+             Current(w[m][2], a.epoch);
+      }
+    }
+    unsigned spins = 0;
+    while (__ballot(!ok) != 0) {
+      if (++spins >= kSpinLimit) {
+        if (lane == 0) sh.fail = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      ok = true;
+#pragma unroll
+      for (int m = 0; m < kFSlots; ++m) {
+        const int i = lane + kWave * m;
+        if (i < n) {
+          unsigned long long* rec = a.rec + 3 * static_cast<size_t>(begin + i);
+#pragma unroll
+          for (int x = 0; x < 3; ++x) {
+            if (!Current(w[m][x], a.epoch)) w[m][x] = LoadWord(rec + x);
+          }
+          ok = ok && Current(w[m][0], a.epoch) && Current(w[m][1], a.epoch) &&
+               Current(w[m][2], a.epoch);
         }
       }
     }
-  }
-  __syncthreads();
-  StampAt(a, sh, kReady);
-  if (mine && !sh.fail) {
-    unsigned long long* rec = a.rec + 3 * static_cast<size_t>(begin + i);
-    // First an ordinary (L2-cached) read, shared by the workgroups of this
-    // request on the XCD; a word whose tag is not current (not yet visible,
-    // or a stale cached line) is then polled coherently.
-    unsigned long long w0 = rec[0], w1 = rec[1], w2 = rec[2];
-    unsigned spins = 0;
-    while (!(Current(w0, a.epoch) && Current(w1, a.epoch) && Current(w2, a.epoch))) {
-      __builtin_amdgcn_s_sleep(1);
-      if (++spins >= kSpinLimit) {
-        sh.fail = 1;
-        break;
+#pragma unroll
+    for (int m = 0; m < kFSlots; ++m) {
+      const int i = lane + kWave * m;
+      if (i < n) {
+        sh.mid[i] = __uint_as_float(static_cast<uint32_t>(w[m][0]));
+        sh.lo[i] = __uint_as_float(static_cast<uint32_t>(w[m][1]));
+        sh.hi[i] = __uint_as_float(static_cast<uint32_t>(w[m][2]));
       }
-      w0 = LoadWord(rec + 0);
-      w1 = LoadWord(rec + 1);
-      w2 = LoadWord(rec + 2);
     }
-    sh.mid[i] = __uint_as_float(static_cast<uint32_t>(w0));
-    sh.key[i] = SelectKey(sh.mid[i], my_page);
-    sh.lo[i] = __uint_as_float(static_cast<uint32_t>(w1));
-    sh.hi[i] = __uint_as_float(static_cast<uint32_t>(w2));
-    sh.cpage[i] = my_page;
-    sh.cntok[i] = my_ntok;
+    StampAt(a, sh, kReady);
   }
   __syncthreads();
   StampAt(a, sh, kRecords);
@@ -399,95 +437,154 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     kk = 0;
   }
   if (kk > 0) {
-    // Ranks, with everything the flag test needs published in the same
-    // pass: rank per candidate, the members' intervals in rank order, the
-    // members' pages (speculatively: rewritten if rescoring reorders), and
-    // per-wave min(lo of members) / max(hi of outsiders).  Midpoints decide
-    // the ranks unless two are equal; then the (score, page id) keys do.
-    int cand, ties;
-    int lead_rank = FloatRanks(sh, n, &cand, &ties);
-    if (__syncthreads_or(lead_rank < n && ties > 1)) {
-      lead_rank = PartialRanks(sh, n, &cand);
+    float mid[kFSlots], lo[kFSlots], hi[kFSlots];
+#pragma unroll
+    for (int m = 0; m < kFSlots; ++m) {
+      const int i = lane + kWave * m;  // < kFMaxCand: the LDS reads stay in bounds
+      const bool in = i < n;
+      const float x = sh.mid[i], l = sh.lo[i], h = sh.hi[i];
+      // Midpoints are finite; -inf marks the empty slots.
+      mid[m] = in ? x : -INFINITY;
+      lo[m] = in ? l : INFINITY;
+      hi[m] = in ? h : -INFINITY;
     }
-    StampAt(a, sh, kRanked);
-    float my_min = INFINITY, my_max = -INFINITY;
-    if (lead_rank < n) {
-      sh.rank[cand] = lead_rank;
-      if (lead_rank < kk) {
-        sh.tlo[lead_rank] = sh.lo[cand];
-        sh.thi[lead_rank] = sh.hi[cand];
-        sh.page[lead_rank] = sh.cpage[cand];
-        sh.ntok[lead_rank] = sh.cntok[cand];
-        my_min = sh.lo[cand];
-      } else {
-        my_max = sh.hi[cand];
+    // 2. ranks: wave w ranks candidate i = 64m + l for l = w + 16q and keeps
+    // the rank in lane l (a uniform loop: ballots need every lane).
+    int my_rank[kFSlots];
+#pragma unroll
+    for (int m = 0; m < kFSlots; ++m) {
+      my_rank[m] = n;
+      if (kWave * m >= n) continue;
+#pragma unroll
+      for (int q = 0; q < kWave / kFWaves; ++q) {
+        const int l = wave + kFWaves * q;
+        const int i = kWave * m + l;
+        const float s_mid = ReadLane(mid[m], l);
+        int above = 0, equal = 0;
+#pragma unroll
+        for (int m2 = 0; m2 < kFSlots; ++m2) {
+          if (kWave * m2 >= n) continue;
+          above += Popc(__ballot(mid[m2] > s_mid));
+          equal += Popc(__ballot(mid[m2] == s_mid));
+        }
+        if (equal > 1) {
+          // Equal midpoints (rare): order them by (page id, position).
+          const int s_page = __builtin_amdgcn_readlane(page[m], l);
+#pragma unroll
+          for (int m2 = 0; m2 < kFSlots; ++m2) {
+            if (kWave * m2 >= n) continue;
+            const int j = kWave * m2 + lane;
+            const bool tie_before = (mid[m2] == s_mid) &
+                                    ((page[m2] < s_page) | ((page[m2] == s_page) & (j < i)));
+            above += Popc(__ballot(tie_before));
+          }
+        }
+        my_rank[m] = (lane == l && i < n) ? above : my_rank[m];
       }
     }
 #pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      my_min = fminf(my_min, __shfl_xor(my_min, o, kWave));
-      my_max = fmaxf(my_max, __shfl_xor(my_max, o, kWave));
-    }
-    const int wave = threadIdx.x / kWave;
-    if ((threadIdx.x & (kWave - 1)) == 0) {
-      sh.red[0][wave] = my_min;
-      sh.red[1][wave] = my_max;
+    for (int m = 0; m < kFSlots; ++m) {
+      const int i = lane + kWave * m;
+      if ((lane & (kFWaves - 1)) == wave && i < n) {
+        const int rank = my_rank[m];
+        sh.rank[i] = rank;
+        if (rank < kk) {
+          sh.page[rank] = page[m];
+          sh.ntok[rank] = ntok[m];
+          sh.tlo[rank] = lo[m];
+          sh.thi[rank] = hi[m];
+          sh.top[rank] = i;
+        }
+      }
     }
     __syncthreads();
-    bool flag = false;
-    if (i < n) {
-      float min_t_lo = INFINITY, max_o_hi = -INFINITY;
+    StampAt(a, sh, kRanked);
+    // 3. certification (every wave, same result)
+    float max_o_hi = -INFINITY;
+    bool member[kFSlots], outsider[kFSlots];
 #pragma unroll
-      for (int w = 0; w < kFWaves; ++w) {
-        min_t_lo = fminf(min_t_lo, sh.red[0][w]);
-        max_o_hi = fmaxf(max_o_hi, sh.red[1][w]);
-      }
+    for (int m = 0; m < kFSlots; ++m) {
+      const int i = lane + kWave * m;
       const int rank = sh.rank[i];
-      const float l = sh.lo[i];
-      const float h = sh.hi[i];
-      if (rank >= kk) {
-        flag = h >= min_t_lo;
-      } else {
-        // Overlap with any other member, or with the best outsider.  The
-        // members are in midpoint order, so a member ranked above overlaps
-        // iff its lo <= this hi, one ranked below iff its hi >= this lo.
-        float above_lo = INFINITY, below_hi = -INFINITY;
-#pragma unroll 4
-        for (int j = 0; j < kk; ++j) {
-          const float tl = sh.tlo[j];
-          const float th = sh.thi[j];
-          above_lo = j < rank ? fminf(above_lo, tl) : above_lo;
-          below_hi = j > rank ? fmaxf(below_hi, th) : below_hi;
-        }
-        flag = l <= max_o_hi || above_lo <= h || below_hi >= l;
-      }
+      member[m] = (i < n) & (rank < kk);
+      outsider[m] = (i < n) & (rank >= kk);
+      max_o_hi = fmaxf(max_o_hi, outsider[m] ? hi[m] : -INFINITY);
     }
-    if (__syncthreads_or(flag ? 1 : 0)) {
-      // Some order is not decided by the intervals: rescore those pages
+    max_o_hi = WaveMax(max_o_hi);
+    // The members in rank order: rank t = lane + 64m.
+    float tlo[kFSlots], thi[kFSlots], pmin[kFSlots], smax[kFSlots];
+#pragma unroll
+    for (int m = 0; m < kFSlots; ++m) {
+      const int t = lane + kWave * m;
+      const float l = sh.tlo[t], h = sh.thi[t];
+      tlo[m] = t < kk ? l : INFINITY;
+      thi[m] = t < kk ? h : -INFINITY;
+    }
+    float carry = INFINITY;  // min lo over the ranks of the slots before
+#pragma unroll
+    for (int m = 0; m < kFSlots; ++m) {
+      const float incl = fminf(WaveMinPrefix(tlo[m]), carry);
+      pmin[m] = DppOr<kWaveShr1>(incl, carry);  // every rank below t
+      carry = ReadLane(incl, kWave - 1);
+    }
+    const float min_t_lo = carry;
+    carry = -INFINITY;  // max hi over the ranks of the slots after
+#pragma unroll
+    for (int m = kFSlots - 1; m >= 0; --m) {
+      const float incl = fmaxf(WaveMaxSuffix(thi[m]), carry);
+      smax[m] = DppOr<kWaveShl1>(incl, carry);  // every rank above t
+      carry = ReadLane(incl, 0);
+    }
+    uint64_t oflag[kFSlots], mflag[kFSlots];
+    bool any = false;
+#pragma unroll
+    for (int m = 0; m < kFSlots; ++m) {
+      const int i = lane + kWave * m;  // candidate i, or rank i
+      oflag[m] = __ballot(outsider[m] & (hi[m] >= min_t_lo));
+      mflag[m] = __ballot((i < kk) & ((tlo[m] <= max_o_hi) | (pmin[m] <= thi[m]) |
+                                      (smax[m] >= tlo[m])));
+      any = any || oflag[m] != 0 || mflag[m] != 0;
+    }
+    if (any) {
+      // 4. Some order is not decided by the intervals: rescore those pages
       // with the exact chain, rank again and rewrite the members.
-      if (flag) sh.flag[atomicAdd(&sh.nflag, 1)] = i;
+      if (wave == 0) {
+        const uint64_t below = (1ull << lane) - 1ull;
+        int base = 0;
+#pragma unroll
+        for (int m = 0; m < kFSlots; ++m) {
+          const int i = lane + kWave * m;
+          if ((oflag[m] >> lane) & 1ull) sh.flag[base + Popc(oflag[m] & below)] = i;
+          base += Popc(oflag[m]);
+          if ((mflag[m] >> lane) & 1ull) sh.flag[base + Popc(mflag[m] & below)] = sh.top[i];
+          base += Popc(mflag[m]);
+          if (i < n) {
+            sh.key[i] = SelectKey(mid[m], page[m]);
+            sh.cpage[i] = page[m];
+            sh.cntok[i] = ntok[m];
+          }
+        }
+        if (lane == 0) sh.nflag = base;
+      }
       __syncthreads();
       const int nflag = sh.nflag;
       if (writer && threadIdx.x == 0 && a.exact_pages != nullptr) {
         atomicAdd(a.exact_pages, nflag);
       }
       RescoreExact(sh.flag, nflag, a.queries + static_cast<size_t>(r) * kFE, pool.summaries,
-                   pool.token_counts, a.cand_ids, begin, kFE, a.scale, sh.tile, sh.key);
+                   pool.token_counts, pool.capacity, a.cand_ids, begin, kFE, a.scale, sh.tile,
+                   sh.key);
       ParallelRanks(sh, n);
+      const int i = threadIdx.x;
       if (i < n && sh.rank[i] < kk) {
         sh.page[sh.rank[i]] = sh.cpage[i];
         sh.ntok[sh.rank[i]] = sh.cntok[i];
       }
       __syncthreads();
     }
-    // Every member slot holds a candidate's page id; one outside the pool
-    // would be a selection bug: drop it (no K/V access) and report it.
-    if (i < kk && (sh.page[i] < 0 || sh.page[i] >= pool.capacity)) {
-      sh.ntok[i] = 0;
-      ReportFailure(a, 3);
+    if (writer && static_cast<int>(threadIdx.x) < kk) {
+      a.selected[static_cast<size_t>(r) * a.sel_stride + threadIdx.x] = sh.page[threadIdx.x];
     }
-    __syncthreads();
-    if (writer && i < kk) a.selected[static_cast<size_t>(r) * a.sel_stride + i] = sh.page[i];
   }
   if (writer && threadIdx.x == 0) a.counts[r] = kk;
   return kk;
@@ -498,7 +595,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
 // waves 0-7 take head h0 and waves 8-15 head h0+1, each as
 // AttentionFastKernel<128, 16, 8, 4>.
 __device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, int begin, int n,
-                              int group, int groups, FusedShared& sh) {
+                              int group, FusedShared& sh) {
   const int h0 = group * kFHeadsPerItem;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -518,7 +615,7 @@ __device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, i
       acc[i] = 0.0f;
     }
   }
-  const int kk = SelectForRequest(pool, a, r, begin, n, groups, group == 0, sh);
+  const int kk = SelectForRequest(pool, a, r, begin, n, group == 0, sh);
   StampAt(a, sh, kSelected);
   if (kk == 0) {
     // Nothing selected: zeros (src/cuda/sparse_batched_attention.cu:621-627).
@@ -631,11 +728,6 @@ __global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, Fuse
   const int groups = pool.num_heads / kFHeadsPerItem;
   const int r = blockIdx.x / groups;
   const int g = blockIdx.x - r * groups;
-  if (blockIdx.x == 0 && static_cast<int>(threadIdx.x) < a.max_batch) {
-    // Clear the arrival counters the next launch uses.
-    __hip_atomic_store(ArrivalCounter(a, a.epoch + 1, threadIdx.x), 0, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  }
   const int begin = a.cand_offsets[r];
   const int n = a.cand_offsets[r + 1] - begin;
   // A request beyond kFMaxCand selects nothing (reported by the selection):
@@ -644,7 +736,7 @@ __global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, Fuse
     ScoreSlice(pool, a, r, begin + (g * n) / groups, begin + ((g + 1) * n) / groups, sh);
   }
   StampAt(a, sh, kScored);
-  AttentionItem(pool, a, r, begin, n, g, groups, sh);
+  AttentionItem(pool, a, r, begin, n, g, sh);
   StampAt(a, sh, kEnd);
   if (a.stamps != nullptr && threadIdx.x == 0) {
     // HW_ID (wave slot, SIMD, CU, shader array, shader engine) and XCC_ID.

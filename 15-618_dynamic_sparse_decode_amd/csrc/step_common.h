@@ -176,13 +176,14 @@ constexpr int kChainPages = 8;
 // candidate indices in flagged[]), written as select keys into keys[].  All
 // threads form the fp32 products of up to kChainPages pages per tile in LDS;
 // one lane per page then runs the dependent adds, so the cost is one chain's
-// latency per group of pages.  Must be called by the whole workgroup.
+// latency per group of pages.  An id outside [0, capacity) reads as an empty
+// page.  Must be called by the whole workgroup.
 constexpr int kRankTile = 1024;
 constexpr int kRankTileStride = kRankTile + 4;
 
 __device__ void RescoreExact(const int* flagged, int nflag, const float* __restrict__ q,
                              const float* __restrict__ summaries,
-                             const int* __restrict__ token_counts,
+                             const int* __restrict__ token_counts, int capacity,
                              const int* __restrict__ cand_ids, int begin, int E, float scale,
                              float* tile, uint64_t* keys) {
   for (int g0 = 0; g0 < nflag; g0 += kChainPages) {
@@ -194,7 +195,8 @@ __device__ void RescoreExact(const int* flagged, int nflag, const float* __restr
         const int f = x / len;
         const int e = x - f * len;
         const int page = cand_ids[begin + flagged[g0 + f]];
-        const float sv = token_counts[page] == 0
+        const bool in_pool = page >= 0 && page < capacity;
+        const float sv = !in_pool || token_counts[page] == 0
                              ? 0.0f
                              : summaries[static_cast<size_t>(page) * E + t0 + e];
         tile[f * kRankTileStride + e] = __fmul_rn(q[t0 + e], sv);

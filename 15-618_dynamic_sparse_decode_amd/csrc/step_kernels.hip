@@ -343,7 +343,7 @@ constexpr int kSelectLdsBytes = 64 * 1024;
 __global__ __launch_bounds__(256) void SelectCertifiedKernel(
     const float* __restrict__ mid, const float* __restrict__ lo,
     const float* __restrict__ hi, const float* __restrict__ queries,
-    const float* __restrict__ summaries, const int* __restrict__ token_counts,
+    const float* __restrict__ summaries, const int* __restrict__ token_counts, int capacity,
     const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int E,
     float scale, int top_k, int chain_floats, int* __restrict__ selected,
     int* __restrict__ counts, int* __restrict__ exact_pages) {
@@ -444,7 +444,7 @@ __global__ __launch_bounds__(256) void SelectCertifiedKernel(
           const int f = x / len;
           const int e = x - f * len;
           const int page = cand_ids[begin + idx[flagged[g0 + f]]];
-          const float sv = token_counts[page] == 0
+          const float sv = page < 0 || page >= capacity || token_counts[page] == 0
                                ? 0.0f
                                : summaries[static_cast<size_t>(page) * E + t0 + e];
           tile[f * stride + e] = __fmul_rn(q[t0 + e], sv);
@@ -485,7 +485,7 @@ constexpr int kRankMax = 256;
 __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
     const float* __restrict__ mid, const float* __restrict__ lo,
     const float* __restrict__ hi, const float* __restrict__ queries,
-    const float* __restrict__ summaries, const int* __restrict__ token_counts,
+    const float* __restrict__ summaries, const int* __restrict__ token_counts, int capacity,
     const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int E,
     float scale, int top_k, int* __restrict__ selected, int* __restrict__ counts,
     int* __restrict__ exact_pages) {
@@ -575,7 +575,7 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
   if (nflag > 0) {
     if (threadIdx.x == 0 && exact_pages != nullptr) atomicAdd(exact_pages, nflag);
     RescoreExact(s_flag, nflag, queries + static_cast<size_t>(r) * E, summaries,
-                 token_counts, cand_ids, begin, E, scale, tile, s_key);
+                 token_counts, capacity, cand_ids, begin, E, scale, tile, s_key);
     rank = active ? rank_of(i) : n;
   }
   if (active && rank < kk) selected[static_cast<size_t>(r) * top_k + rank] = cand_ids[begin + i];
@@ -974,7 +974,8 @@ void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float
     if (threads < kWave) threads = kWave;
     hipLaunchKernelGGL(SelectCertifiedRankKernel, dim3(batch), dim3(threads), 0, stream,
                        d_mid, d_lo, d_hi, d_queries, pool.summaries, pool.token_counts,
-                       d_cand_offsets, d_cand_ids, pool.elements, scale, top_k, d_selected,
+                       pool.capacity, d_cand_offsets, d_cand_ids, pool.elements, scale, top_k,
+                       d_selected,
                        d_counts, d_exact_pages);
     DSD_HIP_CHECK(hipGetLastError());
     return;
@@ -994,8 +995,9 @@ void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float
   const int chain_floats = static_cast<int>((kSelectLdsBytes - 256 - list_bytes) / sizeof(float));
   const size_t lds = list_bytes + sizeof(float) * static_cast<size_t>(chain_floats);
   hipLaunchKernelGGL(SelectCertifiedKernel, dim3(batch), dim3(threads), lds, stream, d_mid,
-                     d_lo, d_hi, d_queries, pool.summaries, pool.token_counts, d_cand_offsets,
-                     d_cand_ids, pool.elements, scale, top_k, chain_floats, d_selected,
+                     d_lo, d_hi, d_queries, pool.summaries, pool.token_counts, pool.capacity,
+                     d_cand_offsets, d_cand_ids, pool.elements, scale, top_k, chain_floats,
+                     d_selected,
                      d_counts, d_exact_pages);
   DSD_HIP_CHECK(hipGetLastError());
 }

@@ -151,3 +151,49 @@ def test_fused_device_path_reports_understated_max_candidates(gpu):
         torch.cuda.synchronize()
         assert ctx.exact_rescored_pages() >= 0
     pool.close()
+
+
+def test_fused_duplicate_candidate_ids_are_both_kept(gpu):
+    # A request that lists a page twice: the reference comparator sees two
+    # equal (score, id) keys and gathers the page twice; the ranks must stay
+    # a permutation (equal keys by position) so every member slot is written.
+    lengths = [600, 300, 900]
+    batch = gpu.SyntheticBatch(H, D, PS, lengths, seed=17)
+    pool = gpu.DevicePagePool(H, D, PS, batch.capacity)
+    batch.upload(pool)
+    offs = batch.cand_offsets.copy()
+    ids = [list(batch.cand_ids[offs[r]:offs[r + 1]]) for r in range(batch.batch)]
+    summ = np.zeros((batch.capacity, E), np.float32)
+    live = batch.live_page_ids()
+    summ[live] = orc.pool_summaries(batch.key_pool, batch.token_counts, E, live)
+    q = batch.queries
+    # duplicate request 0's best page and request 2's third best page
+    for r, pick in ((0, 0), (2, 2)):
+        sc = summ[ids[r]] @ q[r]
+        best = ids[r][int(np.argsort(-sc, kind="stable")[pick])]
+        ids[r].insert(len(ids[r]) // 2, best)
+    new_offs = np.zeros(batch.batch + 1, np.int32)
+    new_offs[1:] = np.cumsum([len(x) for x in ids])
+    new_ids = np.concatenate([np.asarray(x, np.int32) for x in ids])
+    k = 6
+    sel_total = int(sum(min(k, len(x)) for x in ids))
+    _, selected, outs = orc.sparse_batch(q, batch.key_pool, batch.value_pool, summ,
+                                         batch.token_counts, new_offs, new_ids, H, D, PS, k)
+    assert sum(list(selected[r]).count(ids[r][len(ids[r]) // 2]) for r in (0, 2)) >= 2
+    for fused in (True, False):
+        old = os.environ.get("DSD_FUSED_STEP")
+        os.environ["DSD_FUSED_STEP"] = "1" if fused else "0"
+        try:
+            ctx = gpu.SparseContext(pool, k, batch.batch, int(new_offs[-1]), sel_total)
+        finally:
+            if old is None:
+                del os.environ["DSD_FUSED_STEP"]
+            else:
+                os.environ["DSD_FUSED_STEP"] = old
+        with ctx:
+            res = ctx.run_batch(q, new_offs, new_ids, output_mode=gpu.OUTPUT_OUTPUTS,
+                                want_ids=True)
+        for r in range(batch.batch):
+            assert res["selected"][r].tolist() == selected[r].tolist(), (fused, r)
+        assert orc.max_abs_diff(res["outputs"], outs) <= 1e-4, fused
+    pool.close()
