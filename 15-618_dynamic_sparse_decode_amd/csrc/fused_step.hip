@@ -437,13 +437,21 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     kk = 0;
   }
   if (kk > 0) {
+    // Slots past n (candidates) or past kk (ranks) hold identities and are
+    // skipped by uniform branches.
+    const int cslots = (n + kWave - 1) / kWave;
+    const int rslots = (kk + kWave - 1) / kWave;
     float mid[kFSlots], lo[kFSlots], hi[kFSlots];
 #pragma unroll
     for (int m = 0; m < kFSlots; ++m) {
+      // Midpoints are finite; -inf marks the empty slots.
+      mid[m] = -INFINITY;
+      lo[m] = INFINITY;
+      hi[m] = -INFINITY;
+      if (m >= cslots) continue;
       const int i = lane + kWave * m;  // < kFMaxCand: the LDS reads stay in bounds
       const bool in = i < n;
       const float x = sh.mid[i], l = sh.lo[i], h = sh.hi[i];
-      // Midpoints are finite; -inf marks the empty slots.
       mid[m] = in ? x : -INFINITY;
       lo[m] = in ? l : INFINITY;
       hi[m] = in ? h : -INFINITY;
@@ -454,7 +462,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
 #pragma unroll
     for (int m = 0; m < kFSlots; ++m) {
       my_rank[m] = n;
-      if (kWave * m >= n) continue;
+      if (m >= cslots) continue;
 #pragma unroll
       for (int q = 0; q < kWave / kFWaves; ++q) {
         const int l = wave + kFWaves * q;
@@ -463,7 +471,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
         int above = 0, equal = 0;
 #pragma unroll
         for (int m2 = 0; m2 < kFSlots; ++m2) {
-          if (kWave * m2 >= n) continue;
+          if (m2 >= cslots) continue;
           above += Popc(__ballot(mid[m2] > s_mid));
           equal += Popc(__ballot(mid[m2] == s_mid));
         }
@@ -472,7 +480,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
           const int s_page = __builtin_amdgcn_readlane(page[m], l);
 #pragma unroll
           for (int m2 = 0; m2 < kFSlots; ++m2) {
-            if (kWave * m2 >= n) continue;
+            if (m2 >= cslots) continue;
             const int j = kWave * m2 + lane;
             const bool tie_before = (mid[m2] == s_mid) &
                                     ((page[m2] < s_page) | ((page[m2] == s_page) & (j < i)));
@@ -485,7 +493,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
 #pragma unroll
     for (int m = 0; m < kFSlots; ++m) {
       const int i = lane + kWave * m;
-      if ((lane & (kFWaves - 1)) == wave && i < n) {
+      if (m < cslots && (lane & (kFWaves - 1)) == wave && i < n) {
         const int rank = my_rank[m];
         sh.rank[i] = rank;
         if (rank < kk) {
@@ -504,6 +512,8 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     bool member[kFSlots], outsider[kFSlots];
 #pragma unroll
     for (int m = 0; m < kFSlots; ++m) {
+      member[m] = outsider[m] = false;
+      if (m >= cslots) continue;
       const int i = lane + kWave * m;
       const int rank = sh.rank[i];
       member[m] = (i < n) & (rank < kk);
@@ -515,6 +525,9 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     float tlo[kFSlots], thi[kFSlots], pmin[kFSlots], smax[kFSlots];
 #pragma unroll
     for (int m = 0; m < kFSlots; ++m) {
+      tlo[m] = pmin[m] = INFINITY;
+      thi[m] = smax[m] = -INFINITY;
+      if (m >= rslots) continue;
       const int t = lane + kWave * m;
       const float l = sh.tlo[t], h = sh.thi[t];
       tlo[m] = t < kk ? l : INFINITY;
@@ -523,6 +536,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     float carry = INFINITY;  // min lo over the ranks of the slots before
 #pragma unroll
     for (int m = 0; m < kFSlots; ++m) {
+      if (m >= rslots) continue;
       const float incl = fminf(WaveMinPrefix(tlo[m]), carry);
       pmin[m] = DppOr<kWaveShr1>(incl, carry);  // every rank below t
       carry = ReadLane(incl, kWave - 1);
@@ -531,6 +545,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     carry = -INFINITY;  // max hi over the ranks of the slots after
 #pragma unroll
     for (int m = kFSlots - 1; m >= 0; --m) {
+      if (m >= rslots) continue;
       const float incl = fmaxf(WaveMaxSuffix(thi[m]), carry);
       smax[m] = DppOr<kWaveShl1>(incl, carry);  // every rank above t
       carry = ReadLane(incl, 0);
@@ -539,6 +554,8 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     bool any = false;
 #pragma unroll
     for (int m = 0; m < kFSlots; ++m) {
+      oflag[m] = mflag[m] = 0;
+      if (m >= cslots) continue;  // rslots <= cslots
       const int i = lane + kWave * m;  // candidate i, or rank i
       oflag[m] = __ballot(outsider[m] & (hi[m] >= min_t_lo));
       mflag[m] = __ballot((i < kk) & ((tlo[m] <= max_o_hi) | (pmin[m] <= thi[m]) |
