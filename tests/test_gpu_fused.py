@@ -197,3 +197,47 @@ def test_fused_duplicate_candidate_ids_are_both_kept(gpu):
             assert res["selected"][r].tolist() == selected[r].tolist(), (fused, r)
         assert orc.max_abs_diff(res["outputs"], outs) <= 1e-4, fused
     pool.close()
+
+
+def test_fused_large_batch_of_small_requests(gpu):
+    # 300 small requests, some empty: 16 workgroups each (4800 in all, many
+    # dispatch waves), every request group waiting only on its own slices.
+    rng = np.random.default_rng(23)
+    lengths = [int(x) for x in rng.integers(0, 70, size=300)]
+    batch = gpu.SyntheticBatch(H, D, PS, lengths, seed=23)
+    pool = gpu.DevicePagePool(H, D, PS, batch.capacity)
+    batch.upload(pool)
+    k = 2
+    with make_ctx(gpu, pool, k, batch, True) as f, make_ctx(gpu, pool, k, batch, False) as u:
+        rf = f.run_batch(batch.queries, batch.cand_offsets, batch.cand_ids,
+                         output_mode=gpu.OUTPUT_OUTPUTS, want_ids=True)
+        ru = u.run_batch(batch.queries, batch.cand_offsets, batch.cand_ids,
+                         output_mode=gpu.OUTPUT_OUTPUTS, want_ids=True)
+    _, selected, outs = oracle_step(batch, batch.queries, k)
+    for r in range(batch.batch):
+        assert rf["selected"][r].tolist() == selected[r].tolist(), r
+        assert ru["selected"][r].tolist() == selected[r].tolist(), r
+    assert np.array_equal(rf["outputs"].view(np.uint32), ru["outputs"].view(np.uint32))
+    assert orc.max_abs_diff(rf["outputs"], outs) <= 1e-4
+    pool.close()
+
+
+@pytest.mark.parametrize("seed", [31, 32])
+def test_fused_skewed_lengths(gpu, seed):
+    # Very uneven requests (1 to 256 candidates, empty ones, equal sizes in
+    # several places), two launches in a row.
+    rng = np.random.default_rng(seed)
+    lengths = [int(x) for x in rng.choice([0, 5, 16, 200, 1000, 4096, 4096, 2500], size=24)]
+    batch = gpu.SyntheticBatch(H, D, PS, lengths, seed=seed)
+    pool = gpu.DevicePagePool(H, D, PS, batch.capacity)
+    batch.upload(pool)
+    k = 8
+    with make_ctx(gpu, pool, k, batch, True) as f:
+        for _ in range(2):
+            rf = f.run_batch(batch.queries, batch.cand_offsets, batch.cand_ids,
+                             output_mode=gpu.OUTPUT_OUTPUTS, want_ids=True)
+    _, selected, outs = oracle_step(batch, batch.queries, k)
+    for r in range(batch.batch):
+        assert rf["selected"][r].tolist() == selected[r].tolist(), r
+    assert orc.max_abs_diff(rf["outputs"], outs) <= 1e-4
+    pool.close()
