@@ -183,8 +183,8 @@ __device__ void ParallelRanks(FusedShared& sh, int n) {
 // into the page sum is at most 3 local + 6 scan + 8 rows of wave 2p + 8 rows
 // of wave 2p+1 + 1 = 26 (40 is used in the bound).  Called by the whole
 // workgroup.
-__device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int r, int first, int end,
-                          FusedShared& sh) {
+__device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int first, int end,
+                          int prefetched_page, const float4* q_lds, FusedShared& sh) {
   constexpr int kRows = kFPerLane / 4;  // 8
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -196,7 +196,7 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int r, int f
   float loc_abs = 0.0f;   // sum of |loc| over this lane's groups
   float p_abs = 0.0f;
   if (active) {
-    int page = a.cand_ids[c];
+    int page = prefetched_page >= 0 ? prefetched_page : a.cand_ids[c];
     int count = 0;
     if (page >= 0 && page < pool.capacity) {
       count = pool.token_counts[page];
@@ -205,8 +205,7 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int r, int f
       if (half == 0 && lane == 0) ReportFailure(a, 3);
       page = 0;
     }
-    const float4* q4 = reinterpret_cast<const float4*>(a.queries + static_cast<size_t>(r) * kFE) +
-                       half * 512 + lane;
+    const float4* q4 = q_lds + half * 512 + lane;
     const float4* s4 =
         reinterpret_cast<const float4*>(pool.summaries + static_cast<size_t>(page) * kFE) +
         half * 512 + lane;
@@ -271,7 +270,7 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int r, int f
     const float tsum = __fadd_rn(sh.abs_prefix[wave], sh.abs_prefix[wave + 1]);
     const float ap = __fadd_rn(sh.abs_p[wave], sh.abs_p[wave + 1]);
     float mid, lo, hi;
-    WriteBoundsFloat(s_hat, tsum, ap, kFE, 4, 40, a.scale, &mid, &lo, &hi);
+    WriteBoundsFloat<kFE, 4, 40>(s_hat, tsum, ap, a.scale, &mid, &lo, &hi);
     a.mid[c] = mid;
     a.lo[c] = lo;
     a.hi[c] = hi;
@@ -282,11 +281,22 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int r, int f
   }
 }
 
-// The candidates [c0, c1) of request r, eight per pass.
+// The candidates [c0, c1) of request r, eight per pass.  The query is
+// staged once in LDS (in the rescoring tile, idle until the selection); the
+// first pass's page ids load alongside it.
 __device__ void ScoreSlice(const PoolView& pool, const FusedArgs& a, int r, int c0, int c1,
                            FusedShared& sh) {
+  if (c0 >= c1) return;
+  static_assert(kFE / 4 == kFThreads, "one float4 of the query per thread");
+  static_assert(sizeof(sh.tile) >= kFE * sizeof(float), "the query fits the tile");
+  const int c = c0 + static_cast<int>(threadIdx.x) / (2 * kWave);
+  const int page0 = c < c1 ? a.cand_ids[c] : -1;
+  float4* q_lds = reinterpret_cast<float4*>(sh.tile);
+  q_lds[threadIdx.x] =
+      reinterpret_cast<const float4*>(a.queries + static_cast<size_t>(r) * kFE)[threadIdx.x];
+  __syncthreads();
   for (int first = c0; first < c1; first += kFPagesPerPass) {
-    ScorePass(pool, a, r, first, c1, sh);
+    ScorePass(pool, a, first, c1, first == c0 ? page0 : -1, q_lds, sh);
   }
 }
 

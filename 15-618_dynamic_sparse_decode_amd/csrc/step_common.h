@@ -99,18 +99,24 @@ __device__ __forceinline__ void WriteBounds(double s_hat, double abs_prefix, dou
 // the reference chain.  Float additions are exact in the subnormal range and
 // the products are the reference's own, so no subnormal term is needed;
 // 4*n*2^-149 is kept as slack, and 1.001 covers this function's own double
-// arithmetic.
-__device__ __forceinline__ void WriteBoundsFloat(float s_hat, float tsum, float abs_p, int n,
-                                                 int L, int depth, float scale, float* mid,
-                                                 float* lo, float* hi) {
-  const double dn = static_cast<double>(n);
-  const double u = 0x1p-24;
-  const double gl = static_cast<double>(L) * u / (1.0 - static_cast<double>(L) * u);
-  const double gd = static_cast<double>(depth) * u / (1.0 - static_cast<double>(depth) * u);
-  const double ap = static_cast<double>(abs_p) * (1.0 + 0x1p-16);
-  const double t_up = static_cast<double>(tsum) * (1.0 + 0x1p-16) + dn * (gd + gl) * ap;
-  double err = u * t_up / (1.0 - dn * u) + gd * ap + 4.0 * dn * 0x1p-149;
-  err *= 1.001;
+// arithmetic (here only two products and two sums; the constants are
+// computed at compile time).
+// The constant factors are folded at compile time:
+//   err = 1.001 * (c_t*tsum + c_p*abs_p + 4*n*2^-149)
+// with c_t = u(1 + 2^-16)/(1 - n*u) and
+//      c_p = (1 + 2^-16)(u*n*(g_depth + g_L)/(1 - n*u) + g_depth).
+template <int kN, int kL, int kDepth>
+__device__ __forceinline__ void WriteBoundsFloat(float s_hat, float tsum, float abs_p,
+                                                 float scale, float* mid, float* lo,
+                                                 float* hi) {
+  constexpr double u = 0x1p-24;
+  constexpr double dn = static_cast<double>(kN);
+  constexpr double gl = kL * u / (1.0 - kL * u);
+  constexpr double gd = kDepth * u / (1.0 - kDepth * u);
+  constexpr double c_t = 1.001 * (1.0 + 0x1p-16) * u / (1.0 - dn * u);
+  constexpr double c_p = 1.001 * (1.0 + 0x1p-16) * (u * dn * (gd + gl) / (1.0 - dn * u) + gd);
+  constexpr double c_0 = 1.001 * 4.0 * dn * 0x1p-149;
+  const double err = c_t * static_cast<double>(tsum) + c_p * static_cast<double>(abs_p) + c_0;
   WriteInterval(static_cast<double>(s_hat), err, scale, mid, lo, hi, 0);
 }
 
