@@ -164,4 +164,11 @@ int FusedStepGrid(const PoolView& pool, int batch);
 int FusedStepStampsPerGroup();
 void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t stream);
 
+// Certified intervals for E = 4096 with the fused step's score passes
+// (float, query staged in LDS, 8..64 pages per 1024-thread workgroup).
+void LaunchScorePages(const PoolView& pool, const float* d_queries, const int* d_cand_offsets,
+                      const int* d_cand_ids, int batch, int total_candidates,
+                      int max_candidates, float scale, float* d_mid, float* d_lo, float* d_hi,
+                      hipStream_t stream);
+
 }  // namespace dsdk

@@ -124,6 +124,7 @@ __device__ __forceinline__ bool Current(unsigned long long w, unsigned epoch) {
 }
 
 __device__ __forceinline__ void ReportFailure(const FusedArgs& a, int code) {
+  if (a.fail_flag == nullptr) return;
   __hip_atomic_store(a.fail_flag, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
@@ -183,8 +184,9 @@ __device__ void ParallelRanks(FusedShared& sh, int n) {
 // into the page sum is at most 3 local + 6 scan + 8 rows of wave 2p + 8 rows
 // of wave 2p+1 + 1 = 26 (40 is used in the bound).  Called by the whole
 // workgroup.
+template <class Shared>
 __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int first, int end,
-                          int prefetched_page, const float4* q_lds, FusedShared& sh) {
+                          int prefetched_page, const float4* q_lds, Shared& sh) {
   constexpr int kRows = kFPerLane / 4;  // 8
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -274,18 +276,21 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int first, i
     a.mid[c] = mid;
     a.lo[c] = lo;
     a.hi[c] = hi;
-    unsigned long long* rec = a.rec + 3 * static_cast<size_t>(c);
-    PutTagged(rec + 0, a.epoch, __float_as_uint(mid));
-    PutTagged(rec + 1, a.epoch, __float_as_uint(lo));
-    PutTagged(rec + 2, a.epoch, __float_as_uint(hi));
+    if (a.rec != nullptr) {
+      unsigned long long* rec = a.rec + 3 * static_cast<size_t>(c);
+      PutTagged(rec + 0, a.epoch, __float_as_uint(mid));
+      PutTagged(rec + 1, a.epoch, __float_as_uint(lo));
+      PutTagged(rec + 2, a.epoch, __float_as_uint(hi));
+    }
   }
 }
 
 // The candidates [c0, c1) of request r, eight per pass.  The query is
 // staged once in LDS (in the rescoring tile, idle until the selection); the
 // first pass's page ids load alongside it.
+template <class Shared>
 __device__ void ScoreSlice(const PoolView& pool, const FusedArgs& a, int r, int c0, int c1,
-                           FusedShared& sh) {
+                           Shared& sh) {
   if (c0 >= c1) return;
   static_assert(kFE / 4 == kFThreads, "one float4 of the query per thread");
   static_assert(sizeof(sh.tile) >= kFE * sizeof(float), "the query fits the tile");
@@ -776,7 +781,57 @@ __global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, Fuse
   }
 }
 
+// ---- stand-alone score kernel (the three-kernel step at E = 4096) ----------
+// Workgroup (x, r) scores candidates [P*x, P*x + P) of request r, P =
+// pages_per_group (a multiple of 8), with the score passes above: the query
+// staged once per workgroup, eight pages per pass.  Intervals go to
+// mid/lo/hi[c] only.
+struct ScoreShared {
+  float wave_total[kFWaves];
+  float abs_prefix[kFWaves];
+  float abs_p[kFWaves];
+  alignas(16) float tile[kFE];  // the query
+};
+
+__global__ __launch_bounds__(kFThreads) void ScorePagesKernel(PoolView pool, FusedArgs a,
+                                                              int pages_per_group) {
+  __shared__ ScoreShared sh;
+  const int r = blockIdx.y;
+  const int begin = a.cand_offsets[r];
+  const int n = a.cand_offsets[r + 1] - begin;
+  const int c0 = static_cast<int>(blockIdx.x) * pages_per_group;
+  if (c0 >= n) return;
+  const int c1 = n - c0 < pages_per_group ? n : c0 + pages_per_group;
+  ScoreSlice(pool, a, r, begin + c0, begin + c1, sh);
+}
+
 }  // namespace
+
+void LaunchScorePages(const PoolView& pool, const float* d_queries, const int* d_cand_offsets,
+                      const int* d_cand_ids, int batch, int total_candidates,
+                      int max_candidates, float scale, float* d_mid, float* d_lo, float* d_hi,
+                      hipStream_t stream) {
+  if (batch <= 0 || max_candidates <= 0 || total_candidates <= 0) return;
+  if (pool.elements != kFE) throw std::invalid_argument("ScorePages needs E = 4096");
+  // About two workgroups per CU in all, 8..64 pages each.
+  int per = (total_candidates + 511) / 512;
+  per = ((per + kFPagesPerPass - 1) / kFPagesPerPass) * kFPagesPerPass;
+  if (per < kFPagesPerPass) per = kFPagesPerPass;
+  if (per > 64) per = 64;
+  FusedArgs a;
+  a.queries = d_queries;
+  a.cand_offsets = d_cand_offsets;
+  a.cand_ids = d_cand_ids;
+  a.batch = batch;
+  a.total = total_candidates;
+  a.scale = scale;
+  a.mid = d_mid;
+  a.lo = d_lo;
+  a.hi = d_hi;
+  const dim3 grid((max_candidates + per - 1) / per, batch);
+  hipLaunchKernelGGL(ScorePagesKernel, grid, dim3(kFThreads), 0, stream, pool, a, per);
+  DSD_HIP_CHECK(hipGetLastError());
+}
 
 bool FusedStepSupported(const PoolView& pool, int max_candidates, int top_k) {
   return pool.elements == kFE && pool.head_dim == kFD && pool.page_size > 0 &&

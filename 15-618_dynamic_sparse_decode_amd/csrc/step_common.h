@@ -178,6 +178,40 @@ __device__ __forceinline__ int KeyPage(uint64_t key) {
 // ---- exact rescoring --------------------------------------------------------
 constexpr int kChainPages = 8;
 
+// acc + row[0] + row[1] + ... + row[len-1], one rounding per element in
+// order (the reference chain); len % 64 == 0, row 16-byte aligned.  The LDS
+// reads run 32 floats ahead of the adds.
+__device__ __forceinline__ float ChainAdd(const float* row, int len, float acc) {
+  const float4* r4 = reinterpret_cast<const float4*>(row);
+  const int n4 = len / 4;
+  float4 a[8], b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = r4[i];
+  for (int base = 0; base < n4; base += 16) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = r4[base + 8 + i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      acc = __fadd_rn(acc, a[i].x);
+      acc = __fadd_rn(acc, a[i].y);
+      acc = __fadd_rn(acc, a[i].z);
+      acc = __fadd_rn(acc, a[i].w);
+    }
+    if (base + 16 < n4) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = r4[base + 16 + i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      acc = __fadd_rn(acc, b[i].x);
+      acc = __fadd_rn(acc, b[i].y);
+      acc = __fadd_rn(acc, b[i].z);
+      acc = __fadd_rn(acc, b[i].w);
+    }
+  }
+  return acc;
+}
+
 // Exact sequential-chain scores for `nflag` candidates of request r (their
 // candidate indices in flagged[]), written as select keys into keys[].  All
 // threads form the fp32 products of up to kChainPages pages per tile in LDS;

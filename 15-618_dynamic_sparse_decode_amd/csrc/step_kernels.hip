@@ -81,122 +81,10 @@ __global__ __launch_bounds__(kWave) void ScoreExactKernel(
 // covered by generous slack terms.  The page's score interval
 // [fl(lo*scale), fl(hi*scale)] (lo/hi rounded outward to float) provably
 // contains the reference score, because fl(x*scale) is monotone in x.
+// At E = 4096 the fused step's float score passes (ScorePagesKernel in
+// fused_step.hip) take this role; the kernel below serves the other E.
 // ---------------------------------------------------------------------------
 constexpr int kBoundWaves = 4;
-
-// E = 4096, one 256-thread workgroup per candidate page (grid = candidates):
-// wave w covers elements [1024w, 1024w + 1024), lane l the contiguous block
-// [1024w + 16l, +16).  Rows are loaded coalesced and transposed through LDS
-// as above; the waves' partial sums meet in LDS for the carries.
-constexpr int kPageThreads = 256;
-constexpr int kPageWaves = kPageThreads / kWave;
-constexpr int kPageBlock = 4096 / kPageThreads;  // 16 products per lane
-constexpr int kPageStride = kPageBlock + 4;
-
-__device__ __forceinline__ int RequestOf(const int* __restrict__ cand_offsets, int batch,
-                                         int c) {
-  int lo = 0, hi = batch;  // cand_offsets[lo] <= c < cand_offsets[hi]
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (cand_offsets[mid] <= c) lo = mid;
-    else hi = mid;
-  }
-  return lo;
-}
-
-__global__ __launch_bounds__(kPageThreads) void ScoreBoundPageKernel(
-    const float* __restrict__ queries, const float* __restrict__ summaries,
-    const int* __restrict__ token_counts, const int* __restrict__ cand_offsets,
-    const int* __restrict__ cand_ids, int batch, float scale, float* __restrict__ mid_out,
-    float* __restrict__ lo_out, float* __restrict__ hi_out) {
-  constexpr int E = 4096;
-  __shared__ __align__(16) float lds[kPageWaves][kWave * kPageStride];
-  __shared__ double s_total[kPageWaves];
-  __shared__ double s_abs[kPageWaves];
-  __shared__ float s_absp[kPageWaves];
-  const int c = blockIdx.x;
-  const int r = RequestOf(cand_offsets, batch, c);
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int page = cand_ids[c];
-  const bool zero = token_counts[page] == 0;
-  const float4* __restrict__ q4 =
-      reinterpret_cast<const float4*>(queries + static_cast<size_t>(r) * E) + wave * 256;
-  const float4* __restrict__ s4 =
-      reinterpret_cast<const float4*>(summaries + static_cast<size_t>(page) * E) + wave * 256;
-  float* my = lds[wave];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {  // 4 rows of 256 elements
-    const float4 qv = q4[j * kWave + lane];
-    const float4 sv = zero ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : s4[j * kWave + lane];
-    float4 pv;
-    pv.x = __fmul_rn(qv.x, sv.x);
-    pv.y = __fmul_rn(qv.y, sv.y);
-    pv.z = __fmul_rn(qv.z, sv.z);
-    pv.w = __fmul_rn(qv.w, sv.w);
-    const int e = j * 4 * kWave + 4 * lane;
-    const int owner = e / kPageBlock;
-    *reinterpret_cast<float4*>(my + owner * kPageStride + (e - owner * kPageBlock)) = pv;
-  }
-  WaveSync();
-  float p[kPageBlock];
-#pragma unroll
-  for (int i = 0; i < kPageBlock; i += 4) {
-    const float4 pv = *reinterpret_cast<const float4*>(my + lane * kPageStride + i);
-    p[i + 0] = pv.x;
-    p[i + 1] = pv.y;
-    p[i + 2] = pv.z;
-    p[i + 3] = pv.w;
-  }
-  double block = 0.0;
-  float abs_p = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kPageBlock; ++i) {
-    block += static_cast<double>(p[i]);
-    abs_p += fabsf(p[i]);
-  }
-  double incl = block;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const double t = __shfl_up(incl, o, kWave);
-    if (lane >= o) incl += t;
-  }
-  if (lane == kWave - 1) s_total[wave] = incl;
-  __syncthreads();
-  double carry = 0.0;
-  for (int w = 0; w < wave; ++w) carry += s_total[w];
-  double prefix = __shfl_up(incl, 1, kWave);
-  if (lane == 0) prefix = 0.0;
-  prefix += carry;
-  double abs_prefix = 0.0;
-#pragma unroll
-  for (int i = 0; i < kPageBlock; ++i) {
-    prefix += static_cast<double>(p[i]);
-    abs_prefix += fabs(prefix);
-  }
-  double absp = static_cast<double>(abs_p);
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {  // both wave sums in one shuffle sequence
-    abs_prefix += __shfl_xor(abs_prefix, o, kWave);
-    absp += __shfl_xor(absp, o, kWave);
-  }
-  if (lane == 0) {
-    s_abs[wave] = abs_prefix;
-    s_absp[wave] = static_cast<float>(absp);
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    double s_hat = 0.0, at = 0.0, ap = 0.0;
-    for (int w = 0; w < kPageWaves; ++w) {
-      s_hat += s_total[w];
-      at += s_abs[w];
-      ap += s_absp[w];
-    }
-    // |p| sums carry float rounding (< 2^-17 relative); doubled to stay an
-    // upper bound for the slack terms they feed.
-    WriteBounds(s_hat, at, 2.0 * ap, E, scale, mid_out, lo_out, hi_out, c);
-  }
-}
 
 // Any E that is a multiple of 64: runtime block length, products re-formed
 // from the (cache-resident) operands in pass 2.
@@ -338,17 +226,25 @@ __device__ void BitonicSortDesc(uint64_t* keys, int* idx, int m, int log_m) {
 // pages into LDS, then one lane per page runs the dependent adds.
 // ---------------------------------------------------------------------------
 constexpr int kCertMaxKeys = 2048;   // next-pow2 candidates per request
-constexpr int kSelectLdsBytes = 64 * 1024;
+constexpr int kSelThreads = 1024;    // one compare-exchange per thread per stage at 2048 keys
+constexpr int kSelChain = 32;        // exact chains per group (lanes of wave 0)
+constexpr int kSelTile = 256;        // products per page per stretch of a chain
+constexpr int kSelStride = kSelTile + 4;
 
-__global__ __launch_bounds__(256) void SelectCertifiedKernel(
+__global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
     const float* __restrict__ mid, const float* __restrict__ lo,
     const float* __restrict__ hi, const float* __restrict__ queries,
     const float* __restrict__ summaries, const int* __restrict__ token_counts, int capacity,
     const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int E,
-    float scale, int top_k, int chain_floats, int* __restrict__ selected,
-    int* __restrict__ counts, int* __restrict__ exact_pages) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  __shared__ float s_red[2][4];
+    float scale, int top_k, int* __restrict__ selected, int* __restrict__ counts,
+    int* __restrict__ exact_pages) {
+  __shared__ uint64_t keys[kCertMaxKeys];
+  __shared__ int idx[kCertMaxKeys];
+  __shared__ int flagged[kCertMaxKeys];
+  __shared__ float s_lo[kCertMaxKeys];
+  __shared__ float s_hi[kCertMaxKeys];
+  __shared__ __align__(16) float tile[2][kSelChain * kSelStride];
+  __shared__ float s_red[2][kSelThreads / kWave];
   __shared__ int s_nflag;
   const int r = blockIdx.x;
   const int begin = cand_offsets[r];
@@ -363,14 +259,6 @@ __global__ __launch_bounds__(256) void SelectCertifiedKernel(
     m <<= 1;
     ++log_m;
   }
-  uint64_t* keys = reinterpret_cast<uint64_t*>(smem_raw);
-  int* idx = reinterpret_cast<int*>(keys + m);
-  int* flagged = idx + m;
-  float* s_lo = reinterpret_cast<float*>(flagged + m);
-  float* s_hi = s_lo + m;
-  float* tile = reinterpret_cast<float*>(
-      smem_raw + ((static_cast<size_t>(m) * 24 + 15) & ~static_cast<size_t>(15)));
-
   for (int i = threadIdx.x; i < m; i += blockDim.x) {
     if (i < n) {
       keys[i] = SelectKey(mid[begin + i], cand_ids[begin + i]);
@@ -431,41 +319,43 @@ __global__ __launch_bounds__(256) void SelectCertifiedKernel(
   const int nflag = s_nflag;
   if (nflag > 0) {
     if (threadIdx.x == 0 && exact_pages != nullptr) atomicAdd(exact_pages, nflag);
+    // Exact chains, kSelChain pages at a time: lane f of wave 0 adds page f's
+    // products of stretch t while waves 1.. form stretch t+1 in the other
+    // buffer.
     const float* __restrict__ q = queries + static_cast<size_t>(r) * E;
-    for (int g0 = 0; g0 < nflag; g0 += kChainPages) {
-      const int G = nflag - g0 < kChainPages ? nflag - g0 : kChainPages;
-      int tile_len = (chain_floats / G - 4) & ~3;
-      if (tile_len > E) tile_len = E;
-      const int stride = tile_len + 4;  // padded rows: conflict-free b128 reads
-      float acc = 0.0f;
-      for (int t0 = 0; t0 < E; t0 += tile_len) {
-        const int len = E - t0 < tile_len ? E - t0 : tile_len;
-        for (int x = threadIdx.x; x < G * len; x += blockDim.x) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int ntiles = (E + kSelTile - 1) / kSelTile;
+    for (int g0 = 0; g0 < nflag; g0 += kSelChain) {
+      const int G = nflag - g0 < kSelChain ? nflag - g0 : kSelChain;
+      auto fill = [&](int buf, int t0, int who, int count) {
+        const int len = E - t0 < kSelTile ? E - t0 : kSelTile;
+        for (int x = who; x < G * len; x += count) {
           const int f = x / len;
           const int e = x - f * len;
           const int page = cand_ids[begin + idx[flagged[g0 + f]]];
           const float sv = page < 0 || page >= capacity || token_counts[page] == 0
                                ? 0.0f
                                : summaries[static_cast<size_t>(page) * E + t0 + e];
-          tile[f * stride + e] = __fmul_rn(q[t0 + e], sv);
+          tile[buf][f * kSelStride + e] = __fmul_rn(q[t0 + e], sv);
         }
-        __syncthreads();
-        if (static_cast<int>(threadIdx.x) < G) {
-          const float* row = tile + threadIdx.x * stride;
-          int e = 0;
-          for (; e + 4 <= len; e += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(row + e);
-            acc = __fadd_rn(acc, v.x);
-            acc = __fadd_rn(acc, v.y);
-            acc = __fadd_rn(acc, v.z);
-            acc = __fadd_rn(acc, v.w);
-          }
-          for (; e < len; ++e) acc = __fadd_rn(acc, row[e]);
+      };
+      fill(0, 0, threadIdx.x, blockDim.x);
+      __syncthreads();
+      float acc = 0.0f;
+      for (int ti = 0; ti < ntiles; ++ti) {
+        const int cur = ti & 1;
+        const int t0 = ti * kSelTile;
+        const int len = E - t0 < kSelTile ? E - t0 : kSelTile;
+        if (wave == 0) {
+          if (lane < G) acc = ChainAdd(&tile[cur][lane * kSelStride], len, acc);
+        } else if (ti + 1 < ntiles) {
+          fill(1 - cur, t0 + kSelTile, static_cast<int>(threadIdx.x) - kWave,
+               static_cast<int>(blockDim.x) - kWave);
         }
         __syncthreads();
       }
-      if (static_cast<int>(threadIdx.x) < G) {
-        const int pos = flagged[g0 + threadIdx.x];
+      if (wave == 0 && lane < G) {
+        const int pos = flagged[g0 + lane];
         keys[pos] = SelectKey(__fmul_rn(acc, scale), cand_ids[begin + idx[pos]]);
       }
       __syncthreads();
@@ -949,11 +839,10 @@ void LaunchScoreBounds(const PoolView& pool, const float* d_queries,
   if (batch <= 0 || max_candidates <= 0) return;
   const dim3 grid((max_candidates + kBoundWaves - 1) / kBoundWaves, batch);
   const dim3 block(kBoundWaves * kWave);
-  if (pool.elements == 4096 && total_candidates > 0) {
-    hipLaunchKernelGGL(ScoreBoundPageKernel, dim3(total_candidates), dim3(kPageThreads), 0,
-                       stream, d_queries, pool.summaries, pool.token_counts, d_cand_offsets,
-                       d_cand_ids, batch, scale, d_mid, d_lo, d_hi);
-  } else if (pool.elements == 4096) {
+  if (pool.elements == 4096) {
+    // The fused step's float score passes, 8..64 pages per workgroup.
+    LaunchScorePages(pool, d_queries, d_cand_offsets, d_cand_ids, batch, total_candidates,
+                     max_candidates, scale, d_mid, d_lo, d_hi, stream);
     return;
   } else {
     hipLaunchKernelGGL(ScoreBoundGenericKernel, grid, block, 0, stream, d_queries,
@@ -986,18 +875,12 @@ void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float
     throw std::invalid_argument("certified select supports up to " +
                                 std::to_string(kCertMaxKeys) + " candidates per request");
   }
-  int threads = m / 2;
-  if (threads < kWave) threads = kWave;
-  if (threads > 256) threads = 256;
-  // keys/idx/flag lists and staged bounds, then the rest of 64 KiB for
-  // product tiles.
-  const size_t list_bytes = (static_cast<size_t>(m) * 24 + 15) & ~static_cast<size_t>(15);
-  const int chain_floats = static_cast<int>((kSelectLdsBytes - 256 - list_bytes) / sizeof(float));
-  const size_t lds = list_bytes + sizeof(float) * static_cast<size_t>(chain_floats);
-  hipLaunchKernelGGL(SelectCertifiedKernel, dim3(batch), dim3(threads), lds, stream, d_mid,
+  if (pool.elements % kWave != 0) {
+    throw std::invalid_argument("certified select needs E % 64 == 0");
+  }
+  hipLaunchKernelGGL(SelectCertifiedKernel, dim3(batch), dim3(kSelThreads), 0, stream, d_mid,
                      d_lo, d_hi, d_queries, pool.summaries, pool.token_counts, pool.capacity,
-                     d_cand_offsets, d_cand_ids, pool.elements, scale, top_k, chain_floats,
-                     d_selected,
+                     d_cand_offsets, d_cand_ids, pool.elements, scale, top_k, d_selected,
                      d_counts, d_exact_pages);
   DSD_HIP_CHECK(hipGetLastError());
 }

@@ -140,3 +140,52 @@ def test_certified_all_zero_query_ties_resolve_by_page_id(gpu):
         res = ctx.run_batch(np.zeros((1, 4096), np.float32), np.array([0, cap], np.int32), cand,
                             output_mode=gpu.OUTPUT_OUTPUTS, want_ids=True)
     assert res["selected"][0].tolist() == [0, 1, 2, 3]
+
+
+def test_certified_large_requests_match_oracle(gpu):
+    # More than 256 candidates per request: the bitonic certified select
+    # (up to 2048 candidates), random data, k = 64.
+    lengths = [5000, 32768]                       # 313 and 2048 pages of 16
+    batch = gpu.SyntheticBatch(32, 128, 16, lengths, seed=41)
+    pool = gpu.DevicePagePool(32, 128, 16, batch.capacity)
+    batch.upload(pool)
+    k = 64
+    cert, (mid, lo, hi), _, exact = run_both_paths(gpu, pool, batch.queries, batch.cand_offsets,
+                                                   batch.cand_ids, k)
+    assert np.all(lo <= exact["scores"]) and np.all(exact["scores"] <= hi)
+    summ = np.zeros((batch.capacity, 4096), np.float32)
+    live = batch.live_page_ids()
+    summ[live] = orc.pool_summaries(batch.key_pool, batch.token_counts, 4096, live)
+    _, selected, outs = orc.sparse_batch(batch.queries, batch.key_pool, batch.value_pool, summ,
+                                         batch.token_counts, batch.cand_offsets, batch.cand_ids,
+                                         32, 128, 16, k)
+    for r in range(batch.batch):
+        assert cert["selected"][r].tolist() == selected[r].tolist(), r
+        assert exact["selected"][r].tolist() == selected[r].tolist(), r
+    assert orc.max_abs_diff(cert["outputs"], outs) <= 1e-4
+    pool.close()
+
+
+@pytest.mark.parametrize("k", [40, 100])
+def test_certified_large_request_many_flags(gpu, k):
+    # 320 candidates in one request built from permuted and duplicated rows,
+    # with a constant query: hundreds of overlapping intervals, so the exact
+    # chain runs in several groups of pages.
+    rng = np.random.default_rng(7 + k)
+    H, D, ps = 32, 128, 16
+    E = H * D
+    pool, keys, values = adversarial_pool(gpu, rng, groups=80, copies=4)
+    cap = keys.shape[0]
+    q = np.stack([np.full(E, 0.37, np.float32)])
+    ids = rng.permutation(cap).astype(np.int32)
+    offs = np.array([0, cap], np.int32)
+    cert, (mid, lo, hi), rescored, exact = run_both_paths(gpu, pool, q, offs, ids, k)
+    assert np.all(lo <= exact["scores"]) and np.all(exact["scores"] <= hi)
+    summ = orc.pool_summaries(keys, np.full(cap, ps, np.int32), E)
+    _, selected, outs = orc.sparse_batch(q, keys, values, summ, np.full(cap, ps, np.int32),
+                                         offs, ids, H, D, ps, k)
+    assert cert["selected"][0].tolist() == selected[0].tolist()
+    assert exact["selected"][0].tolist() == selected[0].tolist()
+    assert orc.max_abs_diff(cert["outputs"], outs) <= 1e-4
+    assert rescored > 32, "expected several chain groups"
+    pool.close()
