@@ -349,6 +349,144 @@ __device__ __forceinline__ float WaveMax(float x) { return ReadLane(WaveMaxSuffi
 
 __device__ __forceinline__ int Popc(uint64_t m) { return __popcll(m); }
 
+// Steps 2 and 3 of SelectForRequest for CS candidate slots and RS rank slots
+// (compile-time counts, so the slot loops are straight-line code).  Reads the
+// intervals from LDS, ranks, certifies; when some order is undecided, wave 0
+// also lists the flagged candidates and all keys for the exact path.
+// Returns whether anything is flagged (the same in every wave).
+template <int CS, int RS>
+__device__ bool RankAndCertify(const FusedArgs& a, int n, int kk, const int (&page)[kFSlots],
+                               const int (&ntok)[kFSlots], FusedShared& sh) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  float mid[CS], lo[CS], hi[CS];
+#pragma unroll
+  for (int m = 0; m < CS; ++m) {
+    const int i = lane + kWave * m;  // < kFMaxCand: the LDS reads stay in bounds
+    const bool in = i < n;
+    const float x = sh.mid[i], l = sh.lo[i], h = sh.hi[i];
+    // Midpoints are finite; -inf marks the empty slots.
+    mid[m] = in ? x : -INFINITY;
+    lo[m] = in ? l : INFINITY;
+    hi[m] = in ? h : -INFINITY;
+  }
+  // 2. ranks: wave w ranks candidate i = 64m + l for l = w + 16q and keeps
+  // the rank in lane l (a uniform loop: ballots need every lane).
+  int my_rank[CS];
+#pragma unroll
+  for (int m = 0; m < CS; ++m) {
+    my_rank[m] = n;
+#pragma unroll
+    for (int q = 0; q < kWave / kFWaves; ++q) {
+      const int l = wave + kFWaves * q;
+      const int i = kWave * m + l;
+      const float s_mid = ReadLane(mid[m], l);
+      int above = 0, equal = 0;
+#pragma unroll
+      for (int m2 = 0; m2 < CS; ++m2) {
+        above += Popc(__ballot(mid[m2] > s_mid));
+        equal += Popc(__ballot(mid[m2] == s_mid));
+      }
+      if (equal > 1) {
+        // Equal midpoints (rare): order them by (page id, position).
+        const int s_page = __builtin_amdgcn_readlane(page[m], l);
+#pragma unroll
+        for (int m2 = 0; m2 < CS; ++m2) {
+          const int j = kWave * m2 + lane;
+          const bool tie_before = (mid[m2] == s_mid) &
+                                  ((page[m2] < s_page) | ((page[m2] == s_page) & (j < i)));
+          above += Popc(__ballot(tie_before));
+        }
+      }
+      my_rank[m] = (lane == l && i < n) ? above : my_rank[m];
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < CS; ++m) {
+    const int i = lane + kWave * m;
+    if ((lane & (kFWaves - 1)) == wave && i < n) {
+      const int rank = my_rank[m];
+      sh.rank[i] = rank;
+      if (rank < kk) {
+        sh.page[rank] = page[m];
+        sh.ntok[rank] = ntok[m];
+        sh.tlo[rank] = lo[m];
+        sh.thi[rank] = hi[m];
+        sh.top[rank] = i;
+      }
+    }
+  }
+  __syncthreads();
+  StampAt(a, sh, kRanked);
+  // 3. certification (every wave, same result)
+  float max_o_hi = -INFINITY;
+  bool outsider[CS];
+#pragma unroll
+  for (int m = 0; m < CS; ++m) {
+    const int i = lane + kWave * m;
+    const int rank = sh.rank[i];
+    outsider[m] = (i < n) & (rank >= kk);
+    max_o_hi = fmaxf(max_o_hi, outsider[m] ? hi[m] : -INFINITY);
+  }
+  max_o_hi = WaveMax(max_o_hi);
+  // The members in rank order: rank t = lane + 64m.
+  float tlo[RS], thi[RS], pmin[RS], smax[RS];
+#pragma unroll
+  for (int m = 0; m < RS; ++m) {
+    const int t = lane + kWave * m;
+    const float l = sh.tlo[t], h = sh.thi[t];
+    tlo[m] = t < kk ? l : INFINITY;
+    thi[m] = t < kk ? h : -INFINITY;
+  }
+  float carry = INFINITY;  // min lo over the ranks of the slots before
+#pragma unroll
+  for (int m = 0; m < RS; ++m) {
+    const float incl = fminf(WaveMinPrefix(tlo[m]), carry);
+    pmin[m] = DppOr<kWaveShr1>(incl, carry);  // every rank below t
+    carry = ReadLane(incl, kWave - 1);
+  }
+  const float min_t_lo = carry;
+  carry = -INFINITY;  // max hi over the ranks of the slots after
+#pragma unroll
+  for (int m = RS - 1; m >= 0; --m) {
+    const float incl = fmaxf(WaveMaxSuffix(thi[m]), carry);
+    smax[m] = DppOr<kWaveShl1>(incl, carry);  // every rank above t
+    carry = ReadLane(incl, 0);
+  }
+  uint64_t oflag[CS], mflag[CS];
+  bool any = false;
+#pragma unroll
+  for (int m = 0; m < CS; ++m) {
+    oflag[m] = __ballot(outsider[m] & (hi[m] >= min_t_lo));
+    mflag[m] = 0;
+    if (m < RS) {
+      const int t = lane + kWave * m;
+      mflag[m] = __ballot((t < kk) & ((tlo[m] <= max_o_hi) | (pmin[m] <= thi[m]) |
+                                      (smax[m] >= tlo[m])));
+    }
+    any = any || oflag[m] != 0 || mflag[m] != 0;
+  }
+  if (any && wave == 0) {
+    const uint64_t below = (1ull << lane) - 1ull;
+    int base = 0;
+#pragma unroll
+    for (int m = 0; m < CS; ++m) {
+      const int i = lane + kWave * m;
+      if ((oflag[m] >> lane) & 1ull) sh.flag[base + Popc(oflag[m] & below)] = i;
+      base += Popc(oflag[m]);
+      if ((mflag[m] >> lane) & 1ull) sh.flag[base + Popc(mflag[m] & below)] = sh.top[i];
+      base += Popc(mflag[m]);
+      if (i < n) {
+        sh.key[i] = SelectKey(mid[m], page[m]);
+        sh.cpage[i] = page[m];
+        sh.cntok[i] = ntok[m];
+      }
+    }
+    if (lane == 0) sh.nflag = base;
+  }
+  return any;
+}
+
 // Top-k of request r (n candidates from `begin`) from the published
 // intervals into sh.page / sh.ntok (rank order); returns the count (0 on
 // failure).  The order is that of the (score desc, page id asc) key of the
@@ -452,152 +590,25 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     kk = 0;
   }
   if (kk > 0) {
-    // Slots past n (candidates) or past kk (ranks) hold identities and are
-    // skipped by uniform branches.
-    const int cslots = (n + kWave - 1) / kWave;
-    const int rslots = (kk + kWave - 1) / kWave;
-    float mid[kFSlots], lo[kFSlots], hi[kFSlots];
-#pragma unroll
-    for (int m = 0; m < kFSlots; ++m) {
-      // Midpoints are finite; -inf marks the empty slots.
-      mid[m] = -INFINITY;
-      lo[m] = INFINITY;
-      hi[m] = -INFINITY;
-      if (m >= cslots) continue;
-      const int i = lane + kWave * m;  // < kFMaxCand: the LDS reads stay in bounds
-      const bool in = i < n;
-      const float x = sh.mid[i], l = sh.lo[i], h = sh.hi[i];
-      mid[m] = in ? x : -INFINITY;
-      lo[m] = in ? l : INFINITY;
-      hi[m] = in ? h : -INFINITY;
-    }
-    // 2. ranks: wave w ranks candidate i = 64m + l for l = w + 16q and keeps
-    // the rank in lane l (a uniform loop: ballots need every lane).
-    int my_rank[kFSlots];
-#pragma unroll
-    for (int m = 0; m < kFSlots; ++m) {
-      my_rank[m] = n;
-      if (m >= cslots) continue;
-#pragma unroll
-      for (int q = 0; q < kWave / kFWaves; ++q) {
-        const int l = wave + kFWaves * q;
-        const int i = kWave * m + l;
-        const float s_mid = ReadLane(mid[m], l);
-        int above = 0, equal = 0;
-#pragma unroll
-        for (int m2 = 0; m2 < kFSlots; ++m2) {
-          if (m2 >= cslots) continue;
-          above += Popc(__ballot(mid[m2] > s_mid));
-          equal += Popc(__ballot(mid[m2] == s_mid));
-        }
-        if (equal > 1) {
-          // Equal midpoints (rare): order them by (page id, position).
-          const int s_page = __builtin_amdgcn_readlane(page[m], l);
-#pragma unroll
-          for (int m2 = 0; m2 < kFSlots; ++m2) {
-            if (m2 >= cslots) continue;
-            const int j = kWave * m2 + lane;
-            const bool tie_before = (mid[m2] == s_mid) &
-                                    ((page[m2] < s_page) | ((page[m2] == s_page) & (j < i)));
-            above += Popc(__ballot(tie_before));
-          }
-        }
-        my_rank[m] = (lane == l && i < n) ? above : my_rank[m];
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < kFSlots; ++m) {
-      const int i = lane + kWave * m;
-      if (m < cslots && (lane & (kFWaves - 1)) == wave && i < n) {
-        const int rank = my_rank[m];
-        sh.rank[i] = rank;
-        if (rank < kk) {
-          sh.page[rank] = page[m];
-          sh.ntok[rank] = ntok[m];
-          sh.tlo[rank] = lo[m];
-          sh.thi[rank] = hi[m];
-          sh.top[rank] = i;
-        }
-      }
-    }
-    __syncthreads();
-    StampAt(a, sh, kRanked);
-    // 3. certification (every wave, same result)
-    float max_o_hi = -INFINITY;
-    bool member[kFSlots], outsider[kFSlots];
-#pragma unroll
-    for (int m = 0; m < kFSlots; ++m) {
-      member[m] = outsider[m] = false;
-      if (m >= cslots) continue;
-      const int i = lane + kWave * m;
-      const int rank = sh.rank[i];
-      member[m] = (i < n) & (rank < kk);
-      outsider[m] = (i < n) & (rank >= kk);
-      max_o_hi = fmaxf(max_o_hi, outsider[m] ? hi[m] : -INFINITY);
-    }
-    max_o_hi = WaveMax(max_o_hi);
-    // The members in rank order: rank t = lane + 64m.
-    float tlo[kFSlots], thi[kFSlots], pmin[kFSlots], smax[kFSlots];
-#pragma unroll
-    for (int m = 0; m < kFSlots; ++m) {
-      tlo[m] = pmin[m] = INFINITY;
-      thi[m] = smax[m] = -INFINITY;
-      if (m >= rslots) continue;
-      const int t = lane + kWave * m;
-      const float l = sh.tlo[t], h = sh.thi[t];
-      tlo[m] = t < kk ? l : INFINITY;
-      thi[m] = t < kk ? h : -INFINITY;
-    }
-    float carry = INFINITY;  // min lo over the ranks of the slots before
-#pragma unroll
-    for (int m = 0; m < kFSlots; ++m) {
-      if (m >= rslots) continue;
-      const float incl = fminf(WaveMinPrefix(tlo[m]), carry);
-      pmin[m] = DppOr<kWaveShr1>(incl, carry);  // every rank below t
-      carry = ReadLane(incl, kWave - 1);
-    }
-    const float min_t_lo = carry;
-    carry = -INFINITY;  // max hi over the ranks of the slots after
-#pragma unroll
-    for (int m = kFSlots - 1; m >= 0; --m) {
-      if (m >= rslots) continue;
-      const float incl = fmaxf(WaveMaxSuffix(thi[m]), carry);
-      smax[m] = DppOr<kWaveShl1>(incl, carry);  // every rank above t
-      carry = ReadLane(incl, 0);
-    }
-    uint64_t oflag[kFSlots], mflag[kFSlots];
+    // 2-3 with the slot counts fixed at compile time (straight-line code).
+    const int cs = (n + kWave - 1) / kWave;    // candidate slots, 1..4
+    const int rs = (kk + kWave - 1) / kWave;   // rank slots, 1..cs
     bool any = false;
-#pragma unroll
-    for (int m = 0; m < kFSlots; ++m) {
-      oflag[m] = mflag[m] = 0;
-      if (m >= cslots) continue;  // rslots <= cslots
-      const int i = lane + kWave * m;  // candidate i, or rank i
-      oflag[m] = __ballot(outsider[m] & (hi[m] >= min_t_lo));
-      mflag[m] = __ballot((i < kk) & ((tlo[m] <= max_o_hi) | (pmin[m] <= thi[m]) |
-                                      (smax[m] >= tlo[m])));
-      any = any || oflag[m] != 0 || mflag[m] != 0;
+    switch (cs * 8 + rs) {
+      case 1 * 8 + 1: any = RankAndCertify<1, 1>(a, n, kk, page, ntok, sh); break;
+      case 2 * 8 + 1: any = RankAndCertify<2, 1>(a, n, kk, page, ntok, sh); break;
+      case 2 * 8 + 2: any = RankAndCertify<2, 2>(a, n, kk, page, ntok, sh); break;
+      case 3 * 8 + 1: any = RankAndCertify<3, 1>(a, n, kk, page, ntok, sh); break;
+      case 3 * 8 + 2: any = RankAndCertify<3, 2>(a, n, kk, page, ntok, sh); break;
+      case 3 * 8 + 3: any = RankAndCertify<3, 3>(a, n, kk, page, ntok, sh); break;
+      case 4 * 8 + 1: any = RankAndCertify<4, 1>(a, n, kk, page, ntok, sh); break;
+      case 4 * 8 + 2: any = RankAndCertify<4, 2>(a, n, kk, page, ntok, sh); break;
+      case 4 * 8 + 3: any = RankAndCertify<4, 3>(a, n, kk, page, ntok, sh); break;
+      default: any = RankAndCertify<4, 4>(a, n, kk, page, ntok, sh); break;
     }
     if (any) {
       // 4. Some order is not decided by the intervals: rescore those pages
       // with the exact chain, rank again and rewrite the members.
-      if (wave == 0) {
-        const uint64_t below = (1ull << lane) - 1ull;
-        int base = 0;
-#pragma unroll
-        for (int m = 0; m < kFSlots; ++m) {
-          const int i = lane + kWave * m;
-          if ((oflag[m] >> lane) & 1ull) sh.flag[base + Popc(oflag[m] & below)] = i;
-          base += Popc(oflag[m]);
-          if ((mflag[m] >> lane) & 1ull) sh.flag[base + Popc(mflag[m] & below)] = sh.top[i];
-          base += Popc(mflag[m]);
-          if (i < n) {
-            sh.key[i] = SelectKey(mid[m], page[m]);
-            sh.cpage[i] = page[m];
-            sh.cntok[i] = ntok[m];
-          }
-        }
-        if (lane == 0) sh.nflag = base;
-      }
       __syncthreads();
       const int nflag = sh.nflag;
       if (writer && threadIdx.x == 0 && a.exact_pages != nullptr) {
