@@ -645,6 +645,7 @@ struct dsd_sparse_ctx {
   DeviceBuffer<unsigned long long> d_rec, d_stamps;
   unsigned epoch = 0;
   double wall_khz = 0.0;  // wall_clock64() rate
+  int compute_units = 256;
   int score_mode = DSD_SCORE_CERTIFIED;
   bool fused_enabled = true;
   PinnedBuffer<float> h_queries, h_scores, h_outputs;
@@ -707,6 +708,7 @@ struct dsd_sparse_ctx {
     a.total = L.total;
     a.top_k = top_k;
     a.sel_stride = top_k > 0 ? top_k : 1;
+    a.heads_per_group = dsdk::FusedStepHeadsPerGroup(pool->view, L.batch, compute_units);
     a.scale = Scale();
     a.mid = L.scores;
     a.lo = d_lo.ptr;
@@ -720,7 +722,7 @@ struct dsd_sparse_ctx {
     a.exact_pages = d_exact_pages.ptr;
     a.fail_flag = h_fail.ptr;
     if (stamp) {
-      stamp_grid = dsdk::FusedStepGrid(pool->view, L.batch);
+      stamp_grid = dsdk::FusedStepGrid(pool->view, L.batch, a.heads_per_group);
       a.stamps = d_stamps.ptr;
     }
     dsdk::LaunchFusedStep(pool->view, a, s);
@@ -850,7 +852,7 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     {
       const size_t rec = 3 * P;
       const size_t stamps =
-          static_cast<size_t>(dsdk::FusedStepGrid(pool->view, static_cast<int>(B))) *
+          static_cast<size_t>(dsdk::FusedStepGrid(pool->view, static_cast<int>(B), 2)) *
           dsdk::FusedStepStampsPerGroup();
       ctx->d_rec.Reserve(rec);
       ctx->d_stamps.Reserve(stamps);
@@ -864,6 +866,10 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
       DSD_HIP_CHECK(hipGetDevice(&device));
       DSD_HIP_CHECK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device));
       ctx->wall_khz = static_cast<double>(khz);
+      int cus = 0;
+      DSD_HIP_CHECK(
+          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+      if (cus > 0) ctx->compute_units = cus;
     }
     if (const char* env = std::getenv("DSD_FUSED_STEP")) {
       ctx->fused_enabled = std::strcmp(env, "0") != 0;

@@ -139,6 +139,7 @@ struct FusedArgs {
   int total = 0;
   int top_k = 0;
   int sel_stride = 1;                 // row stride of selected
+  int heads_per_group = 2;            // heads per workgroup: 2, 4 or 8
   float scale = 0.0f;
   float* mid = nullptr;               // [total] certified intervals (caller copy)
   float* lo = nullptr;
@@ -159,8 +160,11 @@ struct FusedArgs {
 
 // E = 4096, head_dim = 128, max_candidates <= 256, top_k <= 256.
 bool FusedStepSupported(const PoolView& pool, int max_candidates, int top_k);
-// Workgroups of one launch: num_heads / 2 per request.
-int FusedStepGrid(const PoolView& pool, int batch);
+// Heads per workgroup for a batch: the fewest (2, 4, 8) that keep the grid
+// within `compute_units` workgroups, else 8.
+int FusedStepHeadsPerGroup(const PoolView& pool, int batch, int compute_units);
+// Workgroups of one launch: num_heads / heads_per_group per request.
+int FusedStepGrid(const PoolView& pool, int batch, int heads_per_group);
 int FusedStepStampsPerGroup();
 void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t stream);
 

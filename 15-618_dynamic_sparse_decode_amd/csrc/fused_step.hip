@@ -7,17 +7,20 @@
 // (GatherPagesCpu + SparseAttentionCpu, :109-194) -- run in one kernel, so the
 // step pays one launch and no kernel boundary between dependent stages.
 //
-// Work items.  Request r owns the G = H/2 consecutive workgroups
-// [r*G, r*G + G); workgroup (r, g) takes heads 2g and 2g+1.  Each does:
+// Work items.  Request r owns the G = H/hpw consecutive workgroups
+// [r*G, r*G + G); workgroup (r, g) takes heads hpw*g .. hpw*g + hpw - 1,
+// where hpw (2, 4 or 8 heads per workgroup) is the fewest that keeps the
+// grid within one dispatch wave (B*H/hpw <= CUs) when that is possible.
+// Each does:
 //   1. score: the certified intervals of its slice of the request's
 //      candidates, [n*g/G, n*(g+1)/G), eight pages per pass, two waves per
 //      page, published as tagged words (below);
 //   2. select: waits until every interval of its request is published,
 //      then computes the request's top-k from them (the G workgroups
 //      compute the same selection; g = 0 writes it out);
-//   3. attend: eight waves per head over the selected pages.
+//   3. attend: 16/hpw waves per head over the selected pages.
 // Workgroups have 1024 threads (one per CU at this kernel's register use),
-// so at B*H/2 <= 256 the whole step is one dispatch wave.
+// so the whole step is one dispatch wave whenever B*H/8 <= the CU count.
 //
 // Every wait ends.  A workgroup waits only for the workgroups of its own
 // request, which have adjacent ids.  Workgroup i goes to XCD i mod 8 and each
@@ -51,8 +54,7 @@ constexpr int kFWaves = kFThreads / kWave;  // 16
 constexpr int kFE = 4096;
 constexpr int kFD = 128;
 constexpr int kFPagesPerPass = 8;           // score pass = 8 pages, 2 waves each
-constexpr int kFHeadsPerItem = 2;           // workgroup = 2 heads, 8 waves each
-constexpr int kFHeadWaves = kFWaves / kFHeadsPerItem;
+constexpr int kFMaxHeadsPerGroup = 8;       // workgroup = 2, 4 or 8 heads (16/hpw waves each)
 constexpr int kFPageLanes = 2 * kWave;      // 128 lanes per page
 constexpr int kFPerLane = kFE / kFPageLanes;  // 32 consecutive products per lane
 constexpr int kFMaxCand = 256;
@@ -639,11 +641,13 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
 // AttentionFastKernel<128, 16, 8, 4>.
 __device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, int begin, int n,
                               int group, FusedShared& sh) {
-  const int h0 = group * kFHeadsPerItem;
+  const int hpw = a.heads_per_group;
+  const int wph = kFWaves / hpw;       // waves per head
+  const int h0 = group * hpw;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int hw = wave % kFHeadWaves;   // wave within its head
-  const int h = h0 + wave / kFHeadWaves;
+  const int hw = wave % wph;   // wave within its head
+  const int h = h0 + wave / wph;
   const int g = lane / kFLpt;
   const int j = lane % kFLpt;
   const int head_off = h * kFD + j * kFDq;
@@ -662,7 +666,7 @@ __device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, i
   StampAt(a, sh, kSelected);
   if (kk == 0) {
     // Nothing selected: zeros (src/cuda/sparse_batched_attention.cu:621-627).
-    if (threadIdx.x < kFHeadsPerItem * kFD) {
+    if (static_cast<int>(threadIdx.x) < hpw * kFD) {
       a.outputs[static_cast<size_t>(r) * kFE + static_cast<size_t>(h0) * kFD + threadIdx.x] =
           0.0f;
     }
@@ -675,7 +679,7 @@ __device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, i
   float m = -INFINITY;
   float l = 0.0f;
   for (int base = hw * kFTpc * kFUnroll; base < total;
-       base += kFHeadWaves * kFTpc * kFUnroll) {
+       base += wph * kFTpc * kFUnroll) {
     float kv[kFUnroll][kFDq];
     float vv[kFUnroll][kFDq];
     bool valid[kFUnroll];
@@ -715,7 +719,7 @@ __device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, i
       }
     }
   }
-  // Merge the 4 token-slot streams of this wave, then the 8 waves of each
+  // Merge the 4 token-slot streams of this wave, then the waves of each
   // head in LDS.
   float wm = m;
 #pragma unroll
@@ -739,18 +743,16 @@ __device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, i
     for (int i = 0; i < kFDq; ++i) sh.acc[wave][j * kFDq + i] = acc[i];
   }
   __syncthreads();
-  if (threadIdx.x < kFHeadsPerItem * kFD) {
-    const int hh = threadIdx.x / kFD;  // which of the two heads
+  if (static_cast<int>(threadIdx.x) < hpw * kFD) {
+    const int hh = threadIdx.x / kFD;  // which of the workgroup's heads
     const int d = threadIdx.x - hh * kFD;
-    const int w0 = hh * kFHeadWaves;
+    const int w0 = hh * wph;
     float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kFHeadWaves; ++w) mx = fmaxf(mx, sh.m[w0 + w]);
+    for (int w = 0; w < wph; ++w) mx = fmaxf(mx, sh.m[w0 + w]);
     float lt = 0.0f;
     float at = 0.0f;
     if (mx != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < kFHeadWaves; ++w) {
+      for (int w = 0; w < wph; ++w) {
         const float sw = (sh.m[w0 + w] == -INFINITY) ? 0.0f : Exp2(sh.m[w0 + w] - mx);
         lt = fmaf(sh.l[w0 + w], sw, lt);
         at = fmaf(sh.acc[w0 + w][d], sw, at);
@@ -768,7 +770,7 @@ __global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, Fuse
     for (int i = 0; i < kStampsPerGroup; ++i) sh.stamp[i] = 0;
   }
   StampAt(a, sh, kStart);
-  const int groups = pool.num_heads / kFHeadsPerItem;
+  const int groups = pool.num_heads / a.heads_per_group;
   const int r = blockIdx.x / groups;
   const int g = blockIdx.x - r * groups;
   const int begin = a.cand_offsets[r];
@@ -846,19 +848,31 @@ void LaunchScorePages(const PoolView& pool, const float* d_queries, const int* d
 
 bool FusedStepSupported(const PoolView& pool, int max_candidates, int top_k) {
   return pool.elements == kFE && pool.head_dim == kFD && pool.page_size > 0 &&
-         pool.num_heads % kFHeadsPerItem == 0 && max_candidates <= kFMaxCand &&
-         top_k <= kFMaxK;
+         pool.num_heads % 2 == 0 && max_candidates <= kFMaxCand && top_k <= kFMaxK;
 }
 
-int FusedStepGrid(const PoolView& pool, int batch) {
-  return batch * (pool.num_heads / kFHeadsPerItem);
+int FusedStepHeadsPerGroup(const PoolView& pool, int batch, int compute_units) {
+  // The fewest heads per workgroup (most waves per head) that keeps the
+  // grid within one dispatch wave; 8 when none does.
+  for (int hpw = 2; hpw < kFMaxHeadsPerGroup; hpw *= 2) {
+    if (pool.num_heads % (2 * hpw) != 0) return hpw;
+    if (static_cast<int64_t>(batch) * (pool.num_heads / hpw) <= compute_units) return hpw;
+  }
+  return kFMaxHeadsPerGroup;
+}
+
+int FusedStepGrid(const PoolView& pool, int batch, int heads_per_group) {
+  return batch * (pool.num_heads / heads_per_group);
 }
 
 int FusedStepStampsPerGroup() { return kStampsPerGroup; }
 
 void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t stream) {
   if (args.batch <= 0) return;
-  const int grid = FusedStepGrid(pool, args.batch);
+  const int hpw = args.heads_per_group;
+  if (hpw != 2 && hpw != 4 && hpw != 8) throw std::invalid_argument("heads per group must be 2, 4 or 8");
+  if (pool.num_heads % hpw != 0) throw std::invalid_argument("heads per group must divide num_heads");
+  const int grid = FusedStepGrid(pool, args.batch, hpw);
   hipLaunchKernelGGL(FusedStepKernel, dim3(grid), dim3(kFThreads), 0, stream, pool, args);
   DSD_HIP_CHECK(hipGetLastError());
 }

@@ -200,8 +200,9 @@ def test_fused_duplicate_candidate_ids_are_both_kept(gpu):
 
 
 def test_fused_large_batch_of_small_requests(gpu):
-    # 300 small requests, some empty: 16 workgroups each (4800 in all, many
-    # dispatch waves), every request group waiting only on its own slices.
+    # 300 small requests, some empty: 8 heads per workgroup, 4 workgroups per
+    # request (1200 in all, several dispatch waves), every request group
+    # waiting only on its own slices.
     rng = np.random.default_rng(23)
     lengths = [int(x) for x in rng.integers(0, 70, size=300)]
     batch = gpu.SyntheticBatch(H, D, PS, lengths, seed=23)
@@ -217,7 +218,9 @@ def test_fused_large_batch_of_small_requests(gpu):
     for r in range(batch.batch):
         assert rf["selected"][r].tolist() == selected[r].tolist(), r
         assert ru["selected"][r].tolist() == selected[r].tolist(), r
-    assert np.array_equal(rf["outputs"].view(np.uint32), ru["outputs"].view(np.uint32))
+    # 8 heads per workgroup here (2 waves per head): the same selection,
+    # the softmax merged in another order than the 8-wave attention kernel.
+    assert orc.max_abs_diff(rf["outputs"], ru["outputs"]) <= 1e-5
     assert orc.max_abs_diff(rf["outputs"], outs) <= 1e-4
     pool.close()
 
@@ -225,7 +228,8 @@ def test_fused_large_batch_of_small_requests(gpu):
 @pytest.mark.parametrize("seed", [31, 32])
 def test_fused_skewed_lengths(gpu, seed):
     # Very uneven requests (1 to 256 candidates, empty ones, equal sizes in
-    # several places), two launches in a row.
+    # several places), two launches in a row; 24 requests: 4 heads per
+    # workgroup.
     rng = np.random.default_rng(seed)
     lengths = [int(x) for x in rng.choice([0, 5, 16, 200, 1000, 4096, 4096, 2500], size=24)]
     batch = gpu.SyntheticBatch(H, D, PS, lengths, seed=seed)
