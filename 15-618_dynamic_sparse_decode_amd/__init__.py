@@ -118,6 +118,10 @@ _SIGNATURES = {
                                             _c_int_p, ctypes.c_int, ctypes.c_int, _c_float_p,
                                             _c_float_p, _c_int_p, _c_int_p,
                                             ctypes.POINTER(StepTimings)]),
+    "dsd_sparse_staging": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.POINTER(ctypes.c_void_p)] * 4),
+    "dsd_sparse_run_staged": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                             ctypes.c_int, _c_int_p, _c_int_p,
+                                             ctypes.POINTER(StepTimings)]),
     "dsd_sparse_run_batch_device": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_int] * 3
                                     + [ctypes.c_void_p] * 8),
     "dsd_sparse_replay_stage": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]),

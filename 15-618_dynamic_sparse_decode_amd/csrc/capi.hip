@@ -123,8 +123,16 @@ struct dsd_pool {
   hipEvent_t dense_start = nullptr, dense_stop = nullptr;
   uint64_t* k_offsets = nullptr;  // [capacity] element offset of each page
   uint64_t* v_offsets = nullptr;
+  // The synthetic append returns once enqueued: `done` marks its end, its
+  // metadata travels from pinned staging, and every other pool call (and
+  // every step on a context using the pool) is ordered after it.
+  hipEvent_t done = nullptr;
+  mutable bool pending = false;
+  PinnedBuffer<int> h_meta;
 
   ~dsd_pool() {
+    if (pending && done) (void)hipEventSynchronize(done);
+    if (done) (void)hipEventDestroy(done);
     if (k_offsets) (void)hipFree(k_offsets);
     if (v_offsets) (void)hipFree(v_offsets);
     if (view.keys) (void)hipFree(view.keys);
@@ -152,6 +160,17 @@ struct dsd_pool {
     if (bytes >= kLargeCopyBytes) ++stats.d2h_large_calls;
   }
   void Sync() const { DSD_HIP_CHECK(hipStreamSynchronize(stream)); }
+  // The host waits for an enqueued append (before reusing its staging).
+  void WaitPending() const {
+    if (pending) {
+      DSD_HIP_CHECK(hipEventSynchronize(done));
+      pending = false;
+    }
+  }
+  // Work enqueued on another stream starts after an enqueued append.
+  void OrderAfterPending(hipStream_t s) const {
+    if (pending) DSD_HIP_CHECK(hipStreamWaitEvent(s, done, 0));
+  }
 
   void ValidatePage(int page_id) const {
     if (page_id < 0 || page_id >= view.capacity) {
@@ -205,6 +224,7 @@ int dsd_pool_create(int num_heads, int head_dim, int page_size,
     v.capacity = capacity_pages;
     v.page_elems = static_cast<int64_t>(page_size) * v.elements;
     DSD_HIP_CHECK(hipStreamCreateWithFlags(&pool->stream, hipStreamNonBlocking));
+    DSD_HIP_CHECK(hipEventCreateWithFlags(&pool->done, hipEventDisableTiming));
     DSD_HIP_CHECK(hipEventCreate(&pool->dense_start));
     DSD_HIP_CHECK(hipEventCreate(&pool->dense_stop));
     pool->host_counts.assign(static_cast<size_t>(capacity_pages), 0);
@@ -246,6 +266,7 @@ int dsd_pool_destroy(dsd_pool* pool) {
   return Guard([&] {
     if (pool != nullptr) {
       (void)hipStreamSynchronize(pool->stream);
+      pool->pending = false;
       delete pool;
     }
   });
@@ -258,6 +279,7 @@ int dsd_pool_capacity(const dsd_pool* pool) {
 int dsd_pool_reset(dsd_pool* pool) {
   return Guard([&] {
     Require(pool != nullptr, "pool must be non-null");
+    pool->WaitPending();
     const PoolView& v = pool->view;
     std::fill(pool->host_counts.begin(), pool->host_counts.end(), 0);
     std::fill(pool->host_live.begin(), pool->host_live.end(), 0);
@@ -282,6 +304,7 @@ int dsd_pool_upload_pages(dsd_pool* pool, int n, const int* page_ids,
                           const float* summaries) {
   return Guard([&] {
     Require(pool != nullptr, "pool must be non-null");
+    pool->WaitPending();
     Require(n >= 0, "page count must be non-negative");
     if (n == 0) return;
     Require(page_ids != nullptr && token_counts != nullptr && src_offsets != nullptr,
@@ -368,6 +391,7 @@ int dsd_pool_upload_tokens(dsd_pool* pool, int n, const int* page_ids,
                            const float* values, const float* summaries) {
   return Guard([&] {
     Require(pool != nullptr, "pool must be non-null");
+    pool->WaitPending();
     Require(n >= 0, "token count must be non-negative");
     if (n == 0) return;
     Require(page_ids != nullptr && token_offsets != nullptr &&
@@ -448,6 +472,7 @@ int dsd_pool_upload_tokens(dsd_pool* pool, int n, const int* page_ids,
 int dsd_pool_mark_free(dsd_pool* pool, int n, const int* page_ids) {
   return Guard([&] {
     Require(pool != nullptr, "pool must be non-null");
+    pool->WaitPending();
     Require(n >= 0, "page count must be non-negative");
     if (n == 0) return;
     Require(page_ids != nullptr, "page ids must be non-null");
@@ -471,6 +496,7 @@ int dsd_pool_download_page(const dsd_pool* pool, int page_id, float* keys,
                            float* values, int* token_count) {
   return Guard([&] {
     Require(pool != nullptr, "pool must be non-null");
+    pool->WaitPending();
     Require(keys != nullptr && values != nullptr, "download outputs must be non-null");
     pool->ValidatePage(page_id);
     const int count = pool->host_counts[page_id];
@@ -491,6 +517,7 @@ int dsd_pool_download_meta(const dsd_pool* pool, int* token_counts,
                            uint8_t* live) {
   return Guard([&] {
     Require(pool != nullptr, "pool must be non-null");
+    pool->WaitPending();
     Require(token_counts != nullptr && live != nullptr,
             "metadata outputs must be non-null");
     const PoolView& v = pool->view;
@@ -504,6 +531,7 @@ int dsd_pool_download_summaries(const dsd_pool* pool, int n,
                                 const int* page_ids, float* out) {
   return Guard([&] {
     Require(pool != nullptr, "pool must be non-null");
+    pool->WaitPending();
     Require(n >= 0, "page count must be non-negative");
     if (n == 0) return;
     Require(page_ids != nullptr && out != nullptr, "pointers must be non-null");
@@ -521,6 +549,7 @@ int dsd_pool_download_summaries(const dsd_pool* pool, int n,
 int dsd_pool_device_arrays(const dsd_pool* pool, dsd_pool_arrays* out) {
   return Guard([&] {
     Require(pool != nullptr && out != nullptr, "pointers must be non-null");
+    pool->WaitPending();
     out->keys = pool->view.keys;
     out->values = pool->view.values;
     out->summaries = pool->view.summaries;
@@ -535,6 +564,7 @@ int dsd_pool_prefill_synthetic(dsd_pool* pool, int n, const int* page_ids,
                                const int* token_counts, int request_id) {
   return Guard([&] {
     Require(pool != nullptr, "pool must be non-null");
+    pool->WaitPending();
     Require(n >= 0, "page count must be non-negative");
     if (n == 0) return;
     Require(page_ids != nullptr && token_counts != nullptr, "pointers must be non-null");
@@ -561,6 +591,7 @@ int dsd_pool_append_synthetic(dsd_pool* pool, int n, const int* page_ids,
                               const int* request_ids, const int* decode_steps) {
   return Guard([&] {
     Require(pool != nullptr, "pool must be non-null");
+    pool->WaitPending();
     Require(n >= 0, "token count must be non-negative");
     if (n == 0) return;
     Require(page_ids != nullptr && token_offsets != nullptr && page_token_counts != nullptr &&
@@ -596,18 +627,32 @@ int dsd_pool_append_synthetic(dsd_pool* pool, int n, const int* page_ids,
     pool->stage_segs.Reserve(nseg + 1);
     pool->stage_req.Reserve(n);
     pool->stage_steps.Reserve(n);
-    pool->H2D(pool->stage_ids.ptr, page_ids, sizeof(int) * n);
-    pool->H2D(pool->stage_offsets.ptr, token_offsets, sizeof(int) * n);
-    pool->H2D(pool->stage_counts.ptr, page_token_counts, sizeof(int) * n);
-    pool->H2D(pool->stage_order.ptr, order.data(), sizeof(int) * n);
-    pool->H2D(pool->stage_segs.ptr, segs.data(), sizeof(int) * (nseg + 1));
-    pool->H2D(pool->stage_req.ptr, request_ids, sizeof(int) * n);
-    pool->H2D(pool->stage_steps.ptr, decode_steps, sizeof(int) * n);
+    // The metadata goes through pinned staging (the previous append's copies
+    // have finished: WaitPending above), and the call returns once the work
+    // is enqueued.
+    const size_t un = static_cast<size_t>(n);
+    pool->h_meta.Reserve(6 * un + static_cast<size_t>(nseg) + 1);
+    int* m = pool->h_meta.ptr;
+    std::memcpy(m + 0 * un, page_ids, sizeof(int) * un);
+    std::memcpy(m + 1 * un, token_offsets, sizeof(int) * un);
+    std::memcpy(m + 2 * un, page_token_counts, sizeof(int) * un);
+    std::memcpy(m + 3 * un, order.data(), sizeof(int) * un);
+    std::memcpy(m + 4 * un, request_ids, sizeof(int) * un);
+    std::memcpy(m + 5 * un, decode_steps, sizeof(int) * un);
+    std::memcpy(m + 6 * un, segs.data(), sizeof(int) * (static_cast<size_t>(nseg) + 1));
+    pool->H2D(pool->stage_ids.ptr, m + 0 * un, sizeof(int) * un);
+    pool->H2D(pool->stage_offsets.ptr, m + 1 * un, sizeof(int) * un);
+    pool->H2D(pool->stage_counts.ptr, m + 2 * un, sizeof(int) * un);
+    pool->H2D(pool->stage_order.ptr, m + 3 * un, sizeof(int) * un);
+    pool->H2D(pool->stage_req.ptr, m + 4 * un, sizeof(int) * un);
+    pool->H2D(pool->stage_steps.ptr, m + 5 * un, sizeof(int) * un);
+    pool->H2D(pool->stage_segs.ptr, m + 6 * un, sizeof(int) * (static_cast<size_t>(nseg) + 1));
     dsdk::LaunchAppendSynthetic(pool->view, pool->stage_segs.ptr, pool->stage_order.ptr,
                                 pool->stage_ids.ptr, pool->stage_offsets.ptr,
                                 pool->stage_counts.ptr, pool->stage_req.ptr,
                                 pool->stage_steps.ptr, nseg, pool->stream);
-    pool->Sync();
+    DSD_HIP_CHECK(hipEventRecord(pool->done, pool->stream));
+    pool->pending = true;
   });
 }
 
@@ -898,12 +943,15 @@ void* dsd_sparse_stream(dsd_sparse_ctx* ctx) {
   return ctx == nullptr ? nullptr : reinterpret_cast<void*>(ctx->stream);
 }
 
-int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
-                         const int* cand_offsets, const int* cand_ids,
-                         int output_mode, int timing_mode, float* outputs,
-                         float* scores, int* selected, int* selected_counts,
-                         dsd_step_timings* timings) {
-  return Guard([&] {
+namespace {
+
+// One host-buffer step.  Inputs are copied into the context's pinned
+// staging unless `staged` (the caller wrote them there); outputs land in the
+// pinned staging and are copied to `outputs` when it is non-null.
+void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
+              const int* cand_offsets, const int* cand_ids, int output_mode, int timing_mode,
+              float* outputs, float* scores, int* selected, int* selected_counts,
+              dsd_step_timings* timings) {
     Require(ctx != nullptr, "context must be non-null");
     Require(batch >= 0, "batch must be non-negative");
     Require(output_mode >= DSD_OUTPUT_NONE && output_mode <= DSD_OUTPUT_DEBUG,
@@ -918,7 +966,7 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
     const bool want_ids =
         debug || (want_outputs && selected != nullptr && selected_counts != nullptr);
     const bool timing = timing_mode == DSD_TIMING_EVENTS;
-    if (want_outputs) Require(outputs != nullptr, "outputs must be non-null");
+    if (want_outputs && !staged) Require(outputs != nullptr, "outputs must be non-null");
     if (debug) {
       Require(scores != nullptr && selected != nullptr && selected_counts != nullptr,
               "debug outputs must be non-null");
@@ -953,9 +1001,12 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
     // Host -> device through pinned staging.
     auto t0 = Clock::now();
     const size_t qn = static_cast<size_t>(batch) * E;
-    std::memcpy(ctx->h_queries.ptr, queries, sizeof(float) * qn);
-    std::memcpy(ctx->h_offsets.ptr, cand_offsets, sizeof(int) * (batch + 1));
-    if (total > 0) std::memcpy(ctx->h_ids.ptr, cand_ids, sizeof(int) * total);
+    if (!staged) {
+      std::memcpy(ctx->h_queries.ptr, queries, sizeof(float) * qn);
+      std::memcpy(ctx->h_offsets.ptr, cand_offsets, sizeof(int) * (batch + 1));
+      if (total > 0) std::memcpy(ctx->h_ids.ptr, cand_ids, sizeof(int) * total);
+    }
+    ctx->pool->OrderAfterPending(ctx->stream);
     DSD_HIP_CHECK(hipMemcpyAsync(ctx->d_queries.ptr, ctx->h_queries.ptr,
                                  sizeof(float) * qn, hipMemcpyHostToDevice, ctx->stream));
     DSD_HIP_CHECK(hipMemcpyAsync(ctx->d_offsets.ptr, ctx->h_offsets.ptr,
@@ -1027,7 +1078,7 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
       t.kernel_ms = static_cast<double>(a) + b + c;
     }
     if (want_outputs) {
-      std::memcpy(outputs, ctx->h_outputs.ptr, sizeof(float) * qn);
+      if (outputs != nullptr) std::memcpy(outputs, ctx->h_outputs.ptr, sizeof(float) * qn);
       if (debug && total > 0) std::memcpy(scores, ctx->h_scores.ptr, sizeof(float) * total);
       if (want_ids) {
         int w = 0;
@@ -1040,6 +1091,39 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
       }
     }
     if (timings != nullptr) *timings = t;
+}
+
+}  // namespace
+
+int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
+                         const int* cand_offsets, const int* cand_ids,
+                         int output_mode, int timing_mode, float* outputs,
+                         float* scores, int* selected, int* selected_counts,
+                         dsd_step_timings* timings) {
+  return Guard([&] {
+    HostStep(ctx, batch, false, queries, cand_offsets, cand_ids, output_mode, timing_mode,
+             outputs, scores, selected, selected_counts, timings);
+  });
+}
+
+int dsd_sparse_staging(dsd_sparse_ctx* ctx, float** queries, int** cand_offsets, int** cand_ids,
+                       float** outputs) {
+  return Guard([&] {
+    Require(ctx != nullptr, "context must be non-null");
+    if (queries != nullptr) *queries = ctx->h_queries.ptr;
+    if (cand_offsets != nullptr) *cand_offsets = ctx->h_offsets.ptr;
+    if (cand_ids != nullptr) *cand_ids = ctx->h_ids.ptr;
+    if (outputs != nullptr) *outputs = ctx->h_outputs.ptr;
+  });
+}
+
+int dsd_sparse_run_staged(dsd_sparse_ctx* ctx, int batch, int output_mode, int timing_mode,
+                          int* selected, int* selected_counts, dsd_step_timings* timings) {
+  return Guard([&] {
+    Require(ctx != nullptr, "context must be non-null");
+    Require(output_mode != DSD_OUTPUT_DEBUG, "the staged step has no debug mode");
+    HostStep(ctx, batch, true, ctx->h_queries.ptr, ctx->h_offsets.ptr, ctx->h_ids.ptr,
+             output_mode, timing_mode, nullptr, nullptr, selected, selected_counts, timings);
   });
 }
 
@@ -1079,6 +1163,7 @@ int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
     L.selected = d_selected != nullptr ? d_selected : ctx->d_selected.ptr;
     L.counts = d_selected_counts != nullptr ? d_selected_counts : ctx->d_counts.ptr;
     hipStream_t s = stream != nullptr ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
+    ctx->pool->OrderAfterPending(s);
     ctx->Enqueue(L, s, false);
     ctx->last = L;
   });
@@ -1089,6 +1174,7 @@ int dsd_sparse_replay_stage(dsd_sparse_ctx* ctx, int stage, void* stream) {
     Require(ctx != nullptr, "context must be non-null");
     Require(ctx->last.valid, "no previous step to replay");
     hipStream_t s = stream != nullptr ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
+    ctx->pool->OrderAfterPending(s);
     const auto& L = ctx->last;
     switch (stage) {
       case 0: ctx->EnqueueScore(L, s); break;
@@ -1143,6 +1229,7 @@ int dsd_dense_run_batch(dsd_pool* pool, int batch, const float* queries,
                         float* outputs, double* kernel_ms) {
   return Guard([&] {
     Require(pool != nullptr, "pool must be non-null");
+    pool->WaitPending();
     Require(batch >= 0, "batch must be non-negative");
     if (kernel_ms != nullptr) *kernel_ms = 0.0;
     if (batch == 0) return;
@@ -1200,6 +1287,7 @@ int dsd_dense_run_batch_device(dsd_pool* pool, int batch,
                                void* stream) {
   return Guard([&] {
     Require(pool != nullptr, "pool must be non-null");
+    pool->WaitPending();
     Require(batch >= 0, "batch must be non-negative");
     if (batch == 0) return;
     Require(d_queries != nullptr && d_cand_offsets != nullptr && d_outputs != nullptr,

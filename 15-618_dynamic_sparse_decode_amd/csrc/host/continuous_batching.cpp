@@ -10,6 +10,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdint>
+#include <cstring>
 #include <deque>
 #include <numeric>
 #include <random>
@@ -20,6 +21,8 @@
 #include "dsd/cuda_dense_attention.h"
 #include "dsd/paged_kv_cache.h"
 #include "dsd/reference_kernels.h"
+#include "dsd_hip.h"
+#include "status.h"
 
 namespace dsd {
 
@@ -232,6 +235,82 @@ const float* Row(const std::vector<float>& v, int step, int E) {
   return v.data() + static_cast<std::size_t>(step) * static_cast<std::size_t>(E);
 }
 
+// An active request of the sparse loop: the reference's state plus where
+// its next query lives (a payload-store row, or its own buffer), so a step
+// writes each query once, straight into the context's pinned staging.
+struct LiveRequest {
+  ActiveDecodeRequest a;
+  const float* query = nullptr;  // payload-store row when !own
+  std::vector<float> query_buf;  // the query when own
+  bool own = true;
+  const float* Query() const { return own ? query_buf.data() : query; }
+};
+
+// One RunBatch of the loop in the outputs / no-outputs modes, on the C ABI:
+// PackSparseBatchInto's checks and layout written into the pinned staging
+// (queries from their rows, candidate lists from the cache), the step, and
+// the same timings RunBatch reports.  Outputs stay in the staging.
+SparseBatchCudaResult StagedStep(SparseCudaContext& ctx, const PagedKvCache& cache,
+                                 const std::vector<LiveRequest>& active, int E, int top_k,
+                                 int max_batch, int max_candidates, int max_selected,
+                                 const SparseRunBatchOptions& run) {
+  using detail::ThrowOnError;
+  SparseBatchCudaResult result;
+  const auto t0 = Clock::now();
+  const int B = static_cast<int>(active.size());
+  int total = 0;
+  int total_selected = 0;
+  for (const auto& l : active) {
+    const int n = static_cast<int>(cache.GetRequestPages(l.a.state.request_id).size());
+    total += n;
+    total_selected += std::max(0, std::min(top_k, n));
+  }
+  if (B > max_batch) throw std::invalid_argument("request batch exceeds sparse context capacity");
+  if (total > max_candidates) {
+    throw std::invalid_argument("candidate page count exceeds sparse context capacity");
+  }
+  if (total_selected > max_selected) {
+    throw std::invalid_argument("selected page count exceeds sparse context capacity");
+  }
+  float* queries = nullptr;
+  int* offsets = nullptr;
+  int* ids = nullptr;
+  ThrowOnError(dsd_sparse_staging(ctx.handle(), &queries, &offsets, &ids, nullptr));
+  offsets[0] = 0;
+  int at = 0;
+  for (int b = 0; b < B; ++b) {
+    const LiveRequest& l = active[static_cast<std::size_t>(b)];
+    std::memcpy(queries + static_cast<std::size_t>(b) * E, l.Query(), sizeof(float) * E);
+    const auto& pages = cache.GetRequestPages(l.a.state.request_id);
+    const int n = static_cast<int>(pages.size());
+    if (n > 0) std::memcpy(ids + at, pages.data(), sizeof(int) * n);
+    at += n;
+    offsets[b + 1] = at;
+  }
+  const double layout_ms = Ms(t0, Clock::now());
+  const bool timing = run.timing_mode == SparseBatchTimingMode::kKernelEvents;
+  const bool outputs = run.output_mode != SparseBatchOutputMode::kNoOutputs;
+  dsd_step_timings t{};
+  ThrowOnError(dsd_sparse_run_staged(ctx.handle(), B,
+                                     outputs ? DSD_OUTPUT_OUTPUTS : DSD_OUTPUT_NONE,
+                                     timing ? DSD_TIMING_EVENTS : DSD_TIMING_NONE, nullptr,
+                                     nullptr, &t));
+  if (timing) {
+    result.aggregate_timings.page_scoring_ms = t.score_ms;
+    result.aggregate_timings.topk_ms = t.topk_ms;
+    result.aggregate_timings.attention_ms = t.attention_ms;
+    result.aggregate_timings.gather_ms = 0.0;  // fused into attention
+    result.aggregate_timings.total_ms = t.score_ms + t.topk_ms + t.attention_ms;
+    result.kernel_ms = result.aggregate_timings.total_ms;
+    result.runtime_overheads.time_prepare_sparse_layout_ms = layout_ms;
+    result.runtime_overheads.time_memcpy_h2d_ms = t.h2d_ms;
+    result.runtime_overheads.time_memcpy_d2h_ms = t.d2h_ms;
+    result.runtime_overheads.time_kernel_launch_ms = t.launch_ms;
+    result.runtime_overheads.time_sync_ms = t.sync_ms;
+  }
+  return result;
+}
+
 void FinishStats(ContinuousBatchStats* stats, Clock::time_point wall_start,
                  const std::vector<double>& step_ms, const StageTimings& timings,
                  const RuntimeOverheadTimings& overheads, int steps, int batch_sum) {
@@ -350,10 +429,11 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
   int steps_run = 0;
   int batch_sum = 0;
   std::deque<std::size_t> pending;
-  std::vector<ActiveDecodeRequest> active;
+  std::vector<LiveRequest> active;
   active.reserve(static_cast<std::size_t>(options.max_active_requests));
   std::vector<const RequestState*> batch;
   std::vector<std::uint8_t> admitted(specs.size(), 0);
+  const bool debug_outputs = options.run_batch_output_mode == SparseBatchOutputMode::kDebugTensors;
 
   if (options.preadmit_prompts) {
     for (std::size_t i = 0; i < specs.size(); ++i) {
@@ -390,11 +470,13 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
         admitted[i] = 1;
       }
       if (s.decode_steps > 0) {
-        ActiveDecodeRequest a;
-        a.state = MakeRequestState(s.request_id, s.initial_query, cache, s.prompt_tokens);
-        a.remaining_decode_steps = s.decode_steps;
-        a.spec_index = i;
-        active.push_back(std::move(a));
+        LiveRequest l;
+        l.a.state = MakeRequestState(s.request_id, std::vector<float>(), cache, s.prompt_tokens);
+        l.a.remaining_decode_steps = s.decode_steps;
+        l.a.spec_index = i;
+        l.query_buf = s.initial_query;
+        l.own = true;
+        active.push_back(std::move(l));
       } else {
         const auto freed = cache.ReleaseRequest(s.request_id);
         if (!options.lazy_release) ctx.SyncFreedPages(freed);
@@ -406,12 +488,23 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
     }
 
     const auto t_step = Clock::now();
-    batch.clear();
-    for (const auto& a : active) batch.push_back(&a.state);
     SparseRunBatchOptions run;
     run.output_mode = options.run_batch_output_mode;
     run.timing_mode = options.run_batch_timing_mode;
-    const auto result = ctx.RunBatch(batch, run);
+    SparseBatchCudaResult result;
+    if (debug_outputs) {
+      // Debug tensors come back per request through RunBatch.
+      batch.clear();
+      for (auto& l : active) {
+        l.a.state.query.assign(l.Query(), l.Query() + E);
+        l.a.state.candidate_page_ids = cache.GetRequestPages(l.a.state.request_id);
+        batch.push_back(&l.a.state);
+      }
+      result = ctx.RunBatch(batch, run);
+    } else {
+      result = StagedStep(ctx, cache, active, E, config.top_k_pages,
+                          options.max_active_requests, max_candidates, max_selected, run);
+    }
     const double ms = Ms(t_step, Clock::now());
     stats.run_batch_wall_ms += ms;
     step_ms.push_back(ms);
@@ -423,7 +516,8 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
     std::vector<AppendTokenResult> appended;
     std::vector<float> keys, values;
     std::vector<int> synth_requests, synth_steps;
-    for (auto& a : active) {
+    for (auto& l : active) {
+      auto& a = l.a;
       const int id = a.state.request_id;
       const int dstep = a.decode_step_index;
       std::vector<float> gk, gv;
@@ -458,13 +552,14 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
         }
       }
       ++a.state.context_tokens;
-      const auto& pages = cache.GetRequestPages(id);
-      a.state.candidate_page_ids.assign(pages.begin(), pages.end());
+      // The next step's query; its candidate list is the cache's page list,
+      // read when the step is staged.
       if (options.precompute_decode_payloads) {
-        const float* q = Row(payloads.next_queries[a.spec_index], dstep, E);
-        a.state.query.assign(q, q + E);
+        l.query = Row(payloads.next_queries[a.spec_index], dstep, E);
+        l.own = false;
       } else {
-        a.state.query = TokenVector(E, id, dstep + 1, 0);
+        l.query_buf = TokenVector(E, id, dstep + 1, 0);
+        l.own = true;
       }
       ++a.decode_step_index;
       --a.remaining_decode_steps;
@@ -482,7 +577,8 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
 
     std::vector<PageId> freed;
     active.erase(std::remove_if(active.begin(), active.end(),
-                                [&](const ActiveDecodeRequest& a) {
+                                [&](const LiveRequest& l) {
+                                  const ActiveDecodeRequest& a = l.a;
                                   if (a.remaining_decode_steps > 0) return false;
                                   const auto ids = cache.ReleaseRequest(a.state.request_id);
                                   freed.insert(freed.end(), ids.begin(), ids.end());

@@ -119,6 +119,7 @@ SparseBatchCudaResult SparseCudaContext::RunBatch(
   const bool debug = options.output_mode == SparseBatchOutputMode::kDebugTensors;
   const bool outputs = options.output_mode != SparseBatchOutputMode::kNoOutputs;
 
+  if (!debug) return RunBatchStaged(requests, timing, outputs);
   const auto t0 = Clock::now();
   Pack(requests, config_, &packed_scratch_);
   const double layout_ms = MsSince(t0);
@@ -182,6 +183,83 @@ SparseBatchCudaResult SparseCudaContext::RunBatch(
     }
     const auto begin = host_outputs_.begin() + static_cast<std::ptrdiff_t>(r) * elements_per_token_;
     one.output.output.assign(begin, begin + elements_per_token_);
+    result.per_request.push_back(std::move(one));
+  }
+  return result;
+}
+
+// The outputs / no-outputs modes: PackSparseBatchInto's checks, then the
+// queries and the CSR go straight into the context's pinned staging and the
+// outputs are read from it (one copy each way).
+SparseBatchCudaResult SparseCudaContext::RunBatchStaged(
+    const std::vector<const RequestState*>& requests, bool timing, bool outputs) {
+  SparseBatchCudaResult result;
+  const auto t0 = Clock::now();
+  if (config_.head_dim <= 0 || config_.head_dim > 128) {
+    throw std::invalid_argument("sparse decode supports head_dim in (0, 128]");
+  }
+  const int B = static_cast<int>(requests.size());
+  const int E = elements_per_token_;
+  int total = 0;
+  int total_selected = 0;
+  for (const RequestState* r : requests) {
+    if (r == nullptr) throw std::invalid_argument("request pointer must be non-null");
+    if (static_cast<int>(r->query.size()) != E) {
+      throw std::invalid_argument("query length does not match model config");
+    }
+    const int n = static_cast<int>(r->candidate_page_ids.size());
+    total += n;
+    total_selected += std::max(0, std::min(config_.top_k_pages, n));
+  }
+  if (B > max_batch_size_) {
+    throw std::invalid_argument("request batch exceeds sparse context capacity");
+  }
+  if (total > max_total_candidates_) {
+    throw std::invalid_argument("candidate page count exceeds sparse context capacity");
+  }
+  if (total_selected > max_total_selected_pages_) {
+    throw std::invalid_argument("selected page count exceeds sparse context capacity");
+  }
+  float* queries = nullptr;
+  int* offsets = nullptr;
+  int* ids = nullptr;
+  float* out = nullptr;
+  ThrowOnError(dsd_sparse_staging(ctx_, &queries, &offsets, &ids, &out));
+  offsets[0] = 0;
+  int at = 0;
+  for (int b = 0; b < B; ++b) {
+    const RequestState& r = *requests[static_cast<std::size_t>(b)];
+    std::memcpy(queries + static_cast<std::size_t>(b) * E, r.query.data(), sizeof(float) * E);
+    const int n = static_cast<int>(r.candidate_page_ids.size());
+    if (n > 0) std::memcpy(ids + at, r.candidate_page_ids.data(), sizeof(int) * n);
+    at += n;
+    offsets[b + 1] = at;
+  }
+  const double layout_ms = MsSince(t0);
+  dsd_step_timings t{};
+  ThrowOnError(dsd_sparse_run_staged(ctx_, B, outputs ? DSD_OUTPUT_OUTPUTS : DSD_OUTPUT_NONE,
+                                     timing ? DSD_TIMING_EVENTS : DSD_TIMING_NONE, nullptr,
+                                     nullptr, &t));
+  if (timing) {
+    result.aggregate_timings.page_scoring_ms = t.score_ms;
+    result.aggregate_timings.topk_ms = t.topk_ms;
+    result.aggregate_timings.attention_ms = t.attention_ms;
+    result.aggregate_timings.gather_ms = 0.0;  // fused into attention
+    result.aggregate_timings.total_ms = t.score_ms + t.topk_ms + t.attention_ms;
+    result.kernel_ms = result.aggregate_timings.total_ms;
+    result.runtime_overheads.time_prepare_sparse_layout_ms = layout_ms;
+    result.runtime_overheads.time_memcpy_h2d_ms = t.h2d_ms;
+    result.runtime_overheads.time_memcpy_d2h_ms = t.d2h_ms;
+    result.runtime_overheads.time_kernel_launch_ms = t.launch_ms;
+    result.runtime_overheads.time_sync_ms = t.sync_ms;
+  }
+  if (!outputs) return result;
+  result.per_request.reserve(requests.size());
+  for (int b = 0; b < B; ++b) {
+    SparseDecodeResult one;
+    one.request_id = requests[static_cast<std::size_t>(b)]->request_id;
+    const float* o = out + static_cast<std::size_t>(b) * E;
+    one.output.output.assign(o, o + E);
     result.per_request.push_back(std::move(one));
   }
   return result;

@@ -96,6 +96,9 @@ class SparseCudaContext {
   ::dsd_sparse_ctx* handle() const { return ctx_; }
 
  private:
+  SparseBatchCudaResult RunBatchStaged(const std::vector<const RequestState*>& requests,
+                                       bool timing, bool outputs);
+
   const PagedKvCache* cache_ = nullptr;
   ModelConfig config_{};
   int elements_per_token_ = 0;

@@ -146,7 +146,9 @@ int dsd_pool_prefill_synthetic(dsd_pool* pool, int n, const int* page_ids,
 
 /* AppendTokensSynthetic (device_page_pool.h:65-69): token i's K/V generated
  * from (request_ids[i], decode_steps[i]) (src/device_page_pool.cpp:122-138),
- * written at (page_ids[i], token_offsets[i]), running-mean summary. */
+ * written at (page_ids[i], token_offsets[i]), running-mean summary.  Returns
+ * once the work is enqueued: every later call on the pool, and every step on
+ * a context using the pool, is ordered after it. */
 int dsd_pool_append_synthetic(dsd_pool* pool, int n, const int* page_ids,
                               const int* token_offsets,
                               const int* page_token_counts,
@@ -210,6 +212,24 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
                          int output_mode, int timing_mode, float* outputs,
                          float* scores, int* selected, int* selected_counts,
                          dsd_step_timings* timings);
+
+/* The context's pinned host staging, for callers that assemble a step in
+ * place (no copy of the inputs): queries [max_batch][E], cand_offsets
+ * [max_batch + 1], cand_ids [max_total_candidates], and outputs
+ * [max_batch][E] where dsd_sparse_run_staged leaves a step's outputs.  Any
+ * pointer argument may be NULL.  The buffers live as long as the context.
+ * No reference counterpart: the reference's RunBatch packs into its own
+ * host vectors (src/cuda/sparse_batched_attention.cu:24-96, :807-828). */
+int dsd_sparse_staging(dsd_sparse_ctx* ctx, float** queries, int** cand_offsets,
+                       int** cand_ids, float** outputs);
+
+/* dsd_sparse_run_batch on inputs already written to the staging: the same
+ * checks, output modes DSD_OUTPUT_NONE / DSD_OUTPUT_OUTPUTS (outputs stay in
+ * the staging), ids into selected / selected_counts when both are non-NULL,
+ * and the same timings. */
+int dsd_sparse_run_staged(dsd_sparse_ctx* ctx, int batch, int output_mode,
+                          int timing_mode, int* selected, int* selected_counts,
+                          dsd_step_timings* timings);
 
 /* Device-resident step: every pointer is device memory and the call only
  * enqueues work on `stream` (a hipStream_t; NULL = the context's stream).
