@@ -93,7 +93,7 @@ struct FusedShared {
   float tlo[kFMaxK];    // intervals of the top-k members, in rank order
   float thi[kFMaxK];
   float red[2][kFWaves];
-  alignas(16) float tile[kChainPages * kRankTileStride];
+  alignas(16) float tile[kRescoreFloats];  // exact-rescore buffers; the staged query before
   // attention
   int page[kFMaxK];
   int ntok[kFMaxK];
@@ -616,9 +616,14 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
       if (writer && threadIdx.x == 0 && a.exact_pages != nullptr) {
         atomicAdd(a.exact_pages, nflag);
       }
-      RescoreExact(sh.flag, nflag, a.queries + static_cast<size_t>(r) * kFE, pool.summaries,
-                   pool.token_counts, pool.capacity, a.cand_ids, begin, kFE, a.scale, sh.tile,
-                   sh.key);
+      RescoreChains(
+          nflag, [&](int f) { return sh.cpage[sh.flag[f]]; },
+          [&](int f, float score) {
+            const int i = sh.flag[f];
+            sh.key[i] = SelectKey(score, sh.cpage[i]);
+          },
+          a.queries + static_cast<size_t>(r) * kFE, pool.summaries, pool.token_counts,
+          pool.capacity, kFE, a.scale, sh.tile);
       ParallelRanks(sh, n);
       const int i = threadIdx.x;
       if (i < n && sh.rank[i] < kk) {

@@ -176,91 +176,132 @@ __device__ __forceinline__ int KeyPage(uint64_t key) {
 }
 
 // ---- exact rescoring --------------------------------------------------------
-constexpr int kChainPages = 8;
+// Candidates whose order the score intervals leave open get the reference's
+// chain (src/reference_kernels.cpp:13-19, :59-80): acc = fl(acc + fl(q_i*s_i))
+// for i = 0 .. E-1 in order, then fl(acc * scale).  The adds of one page are
+// a dependent chain (about 4.5 cycles per v_add_f32 from registers, the
+// issue time of a wave64 op), so pages run side by side in the lanes of
+// wave 0 while the other
+// waves form the next stretch of products in a second LDS buffer: the loads
+// of stretch t+1 overlap the adds of stretch t.  A group takes 8, 16 or 32
+// pages (the fewest that cover what remains), with stretches of 1024, 512 or
+// 256 products per page.  Fed from LDS, an add costs about 7 cycles (the
+// read latency is not fully hidden), so a 1024-product stretch outlasts one
+// memory round trip even on a busy HBM.  Measured slower: one stretch of all
+// E products per page (its whole fill latency is exposed), and fills that
+// batch four units per thread.
+constexpr int kRescoreMaxGroup = 32;
+constexpr int kRescoreBuf = kRescoreMaxGroup * (256 + 4);  // floats per buffer:
+                                                           // 8x1028, 16x516, 32x260
+constexpr int kRescoreFloats = 2 * kRescoreBuf;
 
 // acc + row[0] + row[1] + ... + row[len-1], one rounding per element in
-// order (the reference chain); len % 64 == 0, row 16-byte aligned.  The LDS
-// reads run 32 floats ahead of the adds.
-__device__ __forceinline__ float ChainAdd(const float* row, int len, float acc) {
-  const float4* r4 = reinterpret_cast<const float4*>(row);
-  const int n4 = len / 4;
+// order (the reference chain); len % 64 == 0, row 16-byte aligned.  Blocks
+// of 64 floats are fully unrolled, the LDS reads of the second 32-float half
+// issued while the first is added; nothing is carried in registers across
+// blocks, so no register copies (a rolled loop with a carried prefetch
+// buffer compiles to one v_mov per element).  Larger unrolled blocks were
+// no faster and, inlined into the fused step, cost it 4 us at config 2.
+__device__ __forceinline__ void AddRow8(const float4 (&v)[8], float& acc) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    acc = __fadd_rn(acc, v[i].x);
+    acc = __fadd_rn(acc, v[i].y);
+    acc = __fadd_rn(acc, v[i].z);
+    acc = __fadd_rn(acc, v[i].w);
+  }
+}
+
+template <int kHalves>  // kHalves * 32 floats, kHalves even
+__device__ __forceinline__ float ChainBlock(const float4* r4, float acc) {
   float4 a[8], b[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) a[i] = r4[i];
-  for (int base = 0; base < n4; base += 16) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) b[i] = r4[base + 8 + i];
+  for (int h = 0; h < kHalves; h += 2) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      acc = __fadd_rn(acc, a[i].x);
-      acc = __fadd_rn(acc, a[i].y);
-      acc = __fadd_rn(acc, a[i].z);
-      acc = __fadd_rn(acc, a[i].w);
+    for (int i = 0; i < 8; ++i) b[i] = r4[(h + 1) * 8 + i];
+    AddRow8(a, acc);
+    if (h + 2 < kHalves) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = r4[(h + 2) * 8 + i];
     }
-    if (base + 16 < n4) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) a[i] = r4[base + 16 + i];
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      acc = __fadd_rn(acc, b[i].x);
-      acc = __fadd_rn(acc, b[i].y);
-      acc = __fadd_rn(acc, b[i].z);
-      acc = __fadd_rn(acc, b[i].w);
-    }
+    AddRow8(b, acc);
   }
   return acc;
 }
 
-// Exact sequential-chain scores for `nflag` candidates of request r (their
-// candidate indices in flagged[]), written as select keys into keys[].  All
-// threads form the fp32 products of up to kChainPages pages per tile in LDS;
-// one lane per page then runs the dependent adds, so the cost is one chain's
-// latency per group of pages.  An id outside [0, capacity) reads as an empty
-// page.  Must be called by the whole workgroup.
-constexpr int kRankTile = 1024;
-constexpr int kRankTileStride = kRankTile + 4;
+__device__ __forceinline__ float ChainAdd(const float* row, int len, float acc) {
+  const float4* r4 = reinterpret_cast<const float4*>(row);
+  for (int e = 0; e < len; e += 64) acc = ChainBlock<2>(r4 + e / 4, acc);
+  return acc;
+}
 
-__device__ void RescoreExact(const int* flagged, int nflag, const float* __restrict__ q,
-                             const float* __restrict__ summaries,
-                             const int* __restrict__ token_counts, int capacity,
-                             const int* __restrict__ cand_ids, int begin, int E, float scale,
-                             float* tile, uint64_t* keys) {
-  for (int g0 = 0; g0 < nflag; g0 += kChainPages) {
-    const int G = nflag - g0 < kChainPages ? nflag - g0 : kChainPages;
-    float acc = 0.0f;
-    for (int t0 = 0; t0 < E; t0 += kRankTile) {
-      const int len = E - t0 < kRankTile ? E - t0 : kRankTile;
-      for (int x = threadIdx.x; x < G * len; x += blockDim.x) {
-        const int f = x / len;
-        const int e = x - f * len;
-        const int page = cand_ids[begin + flagged[g0 + f]];
-        const bool in_pool = page >= 0 && page < capacity;
-        const float sv = !in_pool || token_counts[page] == 0
-                             ? 0.0f
-                             : summaries[static_cast<size_t>(page) * E + t0 + e];
-        tile[f * kRankTileStride + e] = __fmul_rn(q[t0 + e], sv);
+// Exact scores of `nflag` candidates: page_of(f) gives the page id of the
+// f-th (an id outside [0, capacity), or a page holding no tokens, reads as
+// an all-zero summary: src/paged_kv_cache.cpp:457-459), emit(f, score)
+// receives its exact score.  q is the request's query (E floats, 16-byte
+// aligned), E % 64 == 0, tile holds kRescoreFloats floats of LDS.  Must be
+// called by the whole workgroup; emit runs in lanes of wave 0 only.  A
+// one-wave workgroup fills each stretch itself after adding the previous one
+// (no overlap).
+template <class PageOf, class Emit>
+__device__ void RescoreChains(int nflag, PageOf page_of, Emit emit, const float* __restrict__ q,
+                              const float* __restrict__ summaries,
+                              const int* __restrict__ token_counts, int capacity, int E,
+                              float scale, float* tile) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const bool one_wave = blockDim.x <= kWave;
+  // Threads that form the stretch after the one being added.
+  const int fill_first = one_wave ? 0 : kWave;
+  const int fill_count = static_cast<int>(blockDim.x) - fill_first;
+  for (int g0 = 0; g0 < nflag; ) {
+    const int left = nflag - g0;
+    const int width = left <= 8 ? 8 : (left <= 16 ? 16 : kRescoreMaxGroup);
+    const int G = left < width ? left : width;
+    const int C = width == 8 ? 1024 : (width == 16 ? 512 : 256);  // products per stretch
+    const int stride = C + 4;
+    const int stretches = (E + C - 1) / C;
+    // Products of stretch t for the group into buffer b, by threads
+    // [first, first + count) of the workgroup, one float4 per unit.
+    auto fill = [&](int b, int t, int first, int count) {
+      const int t0 = t * C;
+      const int len4 = (E - t0 < C ? E - t0 : C) / 4;
+      float* buf = tile + b * kRescoreBuf;
+      for (int u = static_cast<int>(threadIdx.x) - first; u < G * len4; u += count) {
+        const int f = u / len4;
+        const int e4 = u - f * len4;
+        const int page = page_of(g0 + f);
+        const bool live = page >= 0 && page < capacity && token_counts[page] != 0;
+        const float4 qv = reinterpret_cast<const float4*>(q + t0)[e4];
+        const float4 sv = live ? reinterpret_cast<const float4*>(
+                                     summaries + static_cast<size_t>(page) * E + t0)[e4]
+                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float4 p;
+        p.x = __fmul_rn(qv.x, sv.x);
+        p.y = __fmul_rn(qv.y, sv.y);
+        p.z = __fmul_rn(qv.z, sv.z);
+        p.w = __fmul_rn(qv.w, sv.w);
+        reinterpret_cast<float4*>(buf + f * stride)[e4] = p;
       }
-      __syncthreads();
-      if (static_cast<int>(threadIdx.x) < G) {
-        const float* row = tile + threadIdx.x * kRankTileStride;
-        int e = 0;
-        for (; e + 4 <= len; e += 4) {
-          const float4 v = *reinterpret_cast<const float4*>(row + e);
-          acc = __fadd_rn(acc, v.x);
-          acc = __fadd_rn(acc, v.y);
-          acc = __fadd_rn(acc, v.z);
-          acc = __fadd_rn(acc, v.w);
-        }
-        for (; e < len; ++e) acc = __fadd_rn(acc, row[e]);
-      }
-      __syncthreads();
-    }
-    if (static_cast<int>(threadIdx.x) < G) {
-      const int i = flagged[g0 + threadIdx.x];
-      keys[i] = SelectKey(__fmul_rn(acc, scale), cand_ids[begin + i]);
-    }
+    };
+    fill(0, 0, 0, blockDim.x);
     __syncthreads();
+    float acc = 0.0f;
+    for (int t = 0; t < stretches; ++t) {
+      if (wave == 0) {
+        const int len = E - t * C < C ? E - t * C : C;
+        if (lane < G) acc = ChainAdd(tile + (t & 1) * kRescoreBuf + lane * stride, len, acc);
+      }
+      if ((wave != 0 || one_wave) && t + 1 < stretches) {
+        fill((t + 1) & 1, t + 1, fill_first, fill_count);
+      }
+      __syncthreads();
+    }
+    if (wave == 0 && lane < G) emit(g0 + lane, __fmul_rn(acc, scale));
+    __syncthreads();
+    g0 += G;
   }
 }
 

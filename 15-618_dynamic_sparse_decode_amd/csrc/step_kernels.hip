@@ -222,14 +222,11 @@ __device__ void BitonicSortDesc(uint64_t* keys, int* idx, int m, int log_m) {
 // other comparison is already decided by disjoint intervals, so replacing the
 // flagged candidates' keys by their exact scores and sorting again yields the
 // reference order exactly.  Exact scores come from the reference's sequential
-// chain: all threads form the fp32 products of up to kChainPages flagged
-// pages into LDS, then one lane per page runs the dependent adds.
+// chain (RescoreChains: the lanes of wave 0 run the dependent adds of up to
+// 32 pages while the other waves form the next stretch of products).
 // ---------------------------------------------------------------------------
 constexpr int kCertMaxKeys = 2048;   // next-pow2 candidates per request
 constexpr int kSelThreads = 1024;    // one compare-exchange per thread per stage at 2048 keys
-constexpr int kSelChain = 32;        // exact chains per group (lanes of wave 0)
-constexpr int kSelTile = 256;        // products per page per stretch of a chain
-constexpr int kSelStride = kSelTile + 4;
 
 __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
     const float* __restrict__ mid, const float* __restrict__ lo,
@@ -243,7 +240,7 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
   __shared__ int flagged[kCertMaxKeys];
   __shared__ float s_lo[kCertMaxKeys];
   __shared__ float s_hi[kCertMaxKeys];
-  __shared__ __align__(16) float tile[2][kSelChain * kSelStride];
+  __shared__ __align__(16) float tile[kRescoreFloats];
   __shared__ float s_red[2][kSelThreads / kWave];
   __shared__ int s_nflag;
   const int r = blockIdx.x;
@@ -319,47 +316,14 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
   const int nflag = s_nflag;
   if (nflag > 0) {
     if (threadIdx.x == 0 && exact_pages != nullptr) atomicAdd(exact_pages, nflag);
-    // Exact chains, kSelChain pages at a time: lane f of wave 0 adds page f's
-    // products of stretch t while waves 1.. form stretch t+1 in the other
-    // buffer.
-    const float* __restrict__ q = queries + static_cast<size_t>(r) * E;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int ntiles = (E + kSelTile - 1) / kSelTile;
-    for (int g0 = 0; g0 < nflag; g0 += kSelChain) {
-      const int G = nflag - g0 < kSelChain ? nflag - g0 : kSelChain;
-      auto fill = [&](int buf, int t0, int who, int count) {
-        const int len = E - t0 < kSelTile ? E - t0 : kSelTile;
-        for (int x = who; x < G * len; x += count) {
-          const int f = x / len;
-          const int e = x - f * len;
-          const int page = cand_ids[begin + idx[flagged[g0 + f]]];
-          const float sv = page < 0 || page >= capacity || token_counts[page] == 0
-                               ? 0.0f
-                               : summaries[static_cast<size_t>(page) * E + t0 + e];
-          tile[buf][f * kSelStride + e] = __fmul_rn(q[t0 + e], sv);
-        }
-      };
-      fill(0, 0, threadIdx.x, blockDim.x);
-      __syncthreads();
-      float acc = 0.0f;
-      for (int ti = 0; ti < ntiles; ++ti) {
-        const int cur = ti & 1;
-        const int t0 = ti * kSelTile;
-        const int len = E - t0 < kSelTile ? E - t0 : kSelTile;
-        if (wave == 0) {
-          if (lane < G) acc = ChainAdd(&tile[cur][lane * kSelStride], len, acc);
-        } else if (ti + 1 < ntiles) {
-          fill(1 - cur, t0 + kSelTile, static_cast<int>(threadIdx.x) - kWave,
-               static_cast<int>(blockDim.x) - kWave);
-        }
-        __syncthreads();
-      }
-      if (wave == 0 && lane < G) {
-        const int pos = flagged[g0 + lane];
-        keys[pos] = SelectKey(__fmul_rn(acc, scale), cand_ids[begin + idx[pos]]);
-      }
-      __syncthreads();
-    }
+    const int* cand = cand_ids + begin;
+    RescoreChains(
+        nflag, [&](int f) { return cand[idx[flagged[f]]]; },
+        [&](int f, float score) {
+          const int pos = flagged[f];
+          keys[pos] = SelectKey(score, cand[idx[pos]]);
+        },
+        queries + static_cast<size_t>(r) * E, summaries, token_counts, capacity, E, scale, tile);
     BitonicSortDesc(keys, idx, m, log_m);
   }
   int* out = selected + static_cast<size_t>(r) * top_k;
@@ -386,7 +350,7 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
   __shared__ int s_flag[kRankMax];
   __shared__ float s_red[2][kRankMax / kWave];
   __shared__ int s_nflag;
-  __shared__ __align__(16) float tile[kChainPages * kRankTileStride];
+  __shared__ __align__(16) float tile[kRescoreFloats];
   const int r = blockIdx.x;
   const int begin = cand_offsets[r];
   const int n = cand_offsets[r + 1] - begin;
@@ -464,8 +428,14 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
   const int nflag = s_nflag;
   if (nflag > 0) {
     if (threadIdx.x == 0 && exact_pages != nullptr) atomicAdd(exact_pages, nflag);
-    RescoreExact(s_flag, nflag, queries + static_cast<size_t>(r) * E, summaries,
-                 token_counts, capacity, cand_ids, begin, E, scale, tile, s_key);
+    const int* cand = cand_ids + begin;
+    RescoreChains(
+        nflag, [&](int f) { return cand[s_flag[f]]; },
+        [&](int f, float score) {
+          const int c = s_flag[f];
+          s_key[c] = SelectKey(score, cand[c]);
+        },
+        queries + static_cast<size_t>(r) * E, summaries, token_counts, capacity, E, scale, tile);
     rank = active ? rank_of(i) : n;
   }
   if (active && rank < kk) selected[static_cast<size_t>(r) * top_k + rank] = cand_ids[begin + i];
@@ -859,9 +829,9 @@ void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float
                            int* d_counts, int* d_exact_pages, hipStream_t stream) {
   if (batch <= 0) return;
   if (max_candidates <= kRankMax) {
-    int threads = ((max_candidates + kWave - 1) / kWave) * kWave;
-    if (threads < kWave) threads = kWave;
-    hipLaunchKernelGGL(SelectCertifiedRankKernel, dim3(batch), dim3(threads), 0, stream,
+    // Always four waves: three of them form products while wave 0 runs the
+    // exact chains.
+    hipLaunchKernelGGL(SelectCertifiedRankKernel, dim3(batch), dim3(kRankMax), 0, stream,
                        d_mid, d_lo, d_hi, d_queries, pool.summaries, pool.token_counts,
                        pool.capacity, d_cand_offsets, d_cand_ids, pool.elements, scale, top_k,
                        d_selected,
