@@ -65,6 +65,7 @@ constexpr int kFTpc = kWave / kFLpt;      // 4 token rows per wave per chunk
 constexpr int kFUnroll = 4;               // chunks in flight per wave
 constexpr unsigned kSpinLimit = 1u << 22;  // polls (about 1 us each) before a timeout
 constexpr int kFSlots = kFMaxCand / kWave;  // candidates (or ranks) per lane: l + 64m
+constexpr int kFRescoreGroup = 16;            // exact chains per rescore group
 static_assert(kFMaxK <= kFMaxCand, "rank slots cover the candidate slots");
 // Timing mode: per-workgroup wall clocks at start, slice scored, counter
 // ready, records read, ranked, selected, end; then the hardware ids.
@@ -93,7 +94,7 @@ struct FusedShared {
   float tlo[kFMaxK];    // intervals of the top-k members, in rank order
   float thi[kFMaxK];
   float red[2][kFWaves];
-  alignas(16) float tile[kRescoreFloats];  // exact-rescore buffers; the staged query before
+  alignas(16) float tile[RescoreFloats<kFRescoreGroup>()];  // exact rescore; the staged query before
   // attention
   int page[kFMaxK];
   int ntok[kFMaxK];
@@ -616,7 +617,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
       if (writer && threadIdx.x == 0 && a.exact_pages != nullptr) {
         atomicAdd(a.exact_pages, nflag);
       }
-      RescoreChains(
+      RescoreChains<kFRescoreGroup>(
           nflag, [&](int f) { return sh.cpage[sh.flag[f]]; },
           [&](int f, float score) {
             const int i = sh.flag[f];

@@ -183,17 +183,21 @@ __device__ __forceinline__ int KeyPage(uint64_t key) {
 // issue time of a wave64 op), so pages run side by side in the lanes of
 // wave 0 while the other
 // waves form the next stretch of products in a second LDS buffer: the loads
-// of stretch t+1 overlap the adds of stretch t.  A group takes 8, 16 or 32
-// pages (the fewest that cover what remains), with stretches of 1024, 512 or
-// 256 products per page.  Fed from LDS, an add costs about 7 cycles (the
+// of stretch t+1 overlap the adds of stretch t.  With M = the largest group
+// the buffers hold (32 for the select kernels, 16 for the fused step, whose
+// LDS stays near its score-and-select footprint), a group takes M/4, M/2 or
+// M pages (the fewest that cover what remains), with stretches of 1024, 512
+// or 256 products per page.  Fed from LDS, an add costs about 7 cycles (the
 // read latency is not fully hidden), so a 1024-product stretch outlasts one
 // memory round trip even on a busy HBM.  Measured slower: one stretch of all
 // E products per page (its whole fill latency is exposed), and fills that
 // batch four units per thread.
-constexpr int kRescoreMaxGroup = 32;
-constexpr int kRescoreBuf = kRescoreMaxGroup * (256 + 4);  // floats per buffer:
-                                                           // 8x1028, 16x516, 32x260
-constexpr int kRescoreFloats = 2 * kRescoreBuf;
+// LDS floats of the two buffers for groups of up to kMaxGroup pages
+// (kMaxGroup/4 x 1028, kMaxGroup/2 x 516 or kMaxGroup x 260 per buffer).
+template <int kMaxGroup>
+constexpr int RescoreFloats() {
+  return 2 * kMaxGroup * (256 + 4);
+}
 
 // acc + row[0] + row[1] + ... + row[len-1], one rounding per element in
 // order (the reference chain); len % 64 == 0, row 16-byte aligned.  Blocks
@@ -241,15 +245,18 @@ __device__ __forceinline__ float ChainAdd(const float* row, int len, float acc) 
 // f-th (an id outside [0, capacity), or a page holding no tokens, reads as
 // an all-zero summary: src/paged_kv_cache.cpp:457-459), emit(f, score)
 // receives its exact score.  q is the request's query (E floats, 16-byte
-// aligned), E % 64 == 0, tile holds kRescoreFloats floats of LDS.  Must be
+// aligned), E % 64 == 0, tile holds RescoreFloats<kMaxGroup>() floats of
+// LDS (kMaxGroup a multiple of 4).  Must be
 // called by the whole workgroup; emit runs in lanes of wave 0 only.  A
 // one-wave workgroup fills each stretch itself after adding the previous one
 // (no overlap).
-template <class PageOf, class Emit>
+template <int kMaxGroup, class PageOf, class Emit>
 __device__ void RescoreChains(int nflag, PageOf page_of, Emit emit, const float* __restrict__ q,
                               const float* __restrict__ summaries,
                               const int* __restrict__ token_counts, int capacity, int E,
                               float scale, float* tile) {
+  static_assert(kMaxGroup % 4 == 0, "groups of kMaxGroup / 4 pages");
+  constexpr int kBuf = RescoreFloats<kMaxGroup>() / 2;  // floats per buffer
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const bool one_wave = blockDim.x <= kWave;
@@ -258,9 +265,10 @@ __device__ void RescoreChains(int nflag, PageOf page_of, Emit emit, const float*
   const int fill_count = static_cast<int>(blockDim.x) - fill_first;
   for (int g0 = 0; g0 < nflag; ) {
     const int left = nflag - g0;
-    const int width = left <= 8 ? 8 : (left <= 16 ? 16 : kRescoreMaxGroup);
+    const int width = left <= kMaxGroup / 4 ? kMaxGroup / 4
+                                            : (left <= kMaxGroup / 2 ? kMaxGroup / 2 : kMaxGroup);
     const int G = left < width ? left : width;
-    const int C = width == 8 ? 1024 : (width == 16 ? 512 : 256);  // products per stretch
+    const int C = width == kMaxGroup / 4 ? 1024 : (width == kMaxGroup / 2 ? 512 : 256);
     const int stride = C + 4;
     const int stretches = (E + C - 1) / C;
     // Products of stretch t for the group into buffer b, by threads
@@ -268,7 +276,7 @@ __device__ void RescoreChains(int nflag, PageOf page_of, Emit emit, const float*
     auto fill = [&](int b, int t, int first, int count) {
       const int t0 = t * C;
       const int len4 = (E - t0 < C ? E - t0 : C) / 4;
-      float* buf = tile + b * kRescoreBuf;
+      float* buf = tile + b * kBuf;
       for (int u = static_cast<int>(threadIdx.x) - first; u < G * len4; u += count) {
         const int f = u / len4;
         const int e4 = u - f * len4;
@@ -292,7 +300,7 @@ __device__ void RescoreChains(int nflag, PageOf page_of, Emit emit, const float*
     for (int t = 0; t < stretches; ++t) {
       if (wave == 0) {
         const int len = E - t * C < C ? E - t * C : C;
-        if (lane < G) acc = ChainAdd(tile + (t & 1) * kRescoreBuf + lane * stride, len, acc);
+        if (lane < G) acc = ChainAdd(tile + (t & 1) * kBuf + lane * stride, len, acc);
       }
       if ((wave != 0 || one_wave) && t + 1 < stretches) {
         fill((t + 1) & 1, t + 1, fill_first, fill_count);

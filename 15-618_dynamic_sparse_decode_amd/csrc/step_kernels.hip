@@ -226,6 +226,7 @@ __device__ void BitonicSortDesc(uint64_t* keys, int* idx, int m, int log_m) {
 // 32 pages while the other waves form the next stretch of products).
 // ---------------------------------------------------------------------------
 constexpr int kCertMaxKeys = 2048;   // next-pow2 candidates per request
+constexpr int kSelRescoreGroup = 32;  // exact chains per rescore group (lanes of wave 0)
 constexpr int kSelThreads = 1024;    // one compare-exchange per thread per stage at 2048 keys
 
 __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
@@ -240,7 +241,7 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
   __shared__ int flagged[kCertMaxKeys];
   __shared__ float s_lo[kCertMaxKeys];
   __shared__ float s_hi[kCertMaxKeys];
-  __shared__ __align__(16) float tile[kRescoreFloats];
+  __shared__ __align__(16) float tile[RescoreFloats<kSelRescoreGroup>()];
   __shared__ float s_red[2][kSelThreads / kWave];
   __shared__ int s_nflag;
   const int r = blockIdx.x;
@@ -317,7 +318,7 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
   if (nflag > 0) {
     if (threadIdx.x == 0 && exact_pages != nullptr) atomicAdd(exact_pages, nflag);
     const int* cand = cand_ids + begin;
-    RescoreChains(
+    RescoreChains<kSelRescoreGroup>(
         nflag, [&](int f) { return cand[idx[flagged[f]]]; },
         [&](int f, float score) {
           const int pos = flagged[f];
@@ -350,7 +351,7 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
   __shared__ int s_flag[kRankMax];
   __shared__ float s_red[2][kRankMax / kWave];
   __shared__ int s_nflag;
-  __shared__ __align__(16) float tile[kRescoreFloats];
+  __shared__ __align__(16) float tile[RescoreFloats<kSelRescoreGroup>()];
   const int r = blockIdx.x;
   const int begin = cand_offsets[r];
   const int n = cand_offsets[r + 1] - begin;
@@ -429,7 +430,7 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
   if (nflag > 0) {
     if (threadIdx.x == 0 && exact_pages != nullptr) atomicAdd(exact_pages, nflag);
     const int* cand = cand_ids + begin;
-    RescoreChains(
+    RescoreChains<kSelRescoreGroup>(
         nflag, [&](int f) { return cand[s_flag[f]]; },
         [&](int f, float score) {
           const int c = s_flag[f];
