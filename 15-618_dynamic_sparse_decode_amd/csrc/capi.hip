@@ -15,6 +15,7 @@
 
 #include "dsd_hip.h"
 #include "dsd_internal.h"
+#include "host_workers.h"
 
 using dsdk::PoolView;
 
@@ -102,6 +103,35 @@ struct PinnedBuffer {
 
 constexpr uint64_t kLargeCopyBytes = 1ull << 20;  // src/device_page_pool.cpp:13
 
+// Uploads from pageable memory of at least kStageMinBytes go through pinned
+// staging: the host threads copy one chunk while the DMA engine moves the
+// previous one (the runtime's own pageable path copies at about 27 GB/s on
+// the MI355X boxes, bound by one host thread).
+constexpr size_t kStageMinBytes = 4u << 20;
+constexpr size_t kStageChunkBytes = 16u << 20;
+constexpr int kStageBuffers = 3;
+constexpr size_t kStagePieceBytes = 1u << 20;  // per host thread task
+
+// True for memory the device reads directly (hipHostMalloc'd or registered).
+bool IsPinnedHost(const void* p) {
+  hipPointerAttribute_t attr{};
+  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();  // pageable memory may report an error: clear it
+    return false;
+  }
+  return attr.type == hipMemoryTypeHost;
+}
+
+// memcpy on the host threads, in pieces of kStagePieceBytes.
+void ParallelCopy(void* dst, const void* src, size_t bytes) {
+  const int pieces = static_cast<int>((bytes + kStagePieceBytes - 1) / kStagePieceBytes);
+  dsd_host::Workers::Get().ParallelFor(pieces, [&](int i) {
+    const size_t off = static_cast<size_t>(i) * kStagePieceBytes;
+    const size_t n = std::min(kStagePieceBytes, bytes - off);
+    std::memcpy(static_cast<char*>(dst) + off, static_cast<const char*>(src) + off, n);
+  });
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -129,10 +159,22 @@ struct dsd_pool {
   hipEvent_t done = nullptr;
   mutable bool pending = false;
   PinnedBuffer<int> h_meta;
+  // Pinned chunks for large pageable uploads; stage_ev[b] marks the end of
+  // the last DMA out of chunk b.
+  PinnedBuffer<char> stage_host[kStageBuffers];
+  hipEvent_t stage_ev[kStageBuffers] = {};
+  bool stage_busy[kStageBuffers] = {};
+  int stage_next = 0;
 
   ~dsd_pool() {
     if (pending && done) (void)hipEventSynchronize(done);
     if (done) (void)hipEventDestroy(done);
+    for (int b = 0; b < kStageBuffers; ++b) {
+      if (stage_ev[b]) {
+        if (stage_busy[b]) (void)hipEventSynchronize(stage_ev[b]);
+        (void)hipEventDestroy(stage_ev[b]);
+      }
+    }
     if (k_offsets) (void)hipFree(k_offsets);
     if (v_offsets) (void)hipFree(v_offsets);
     if (view.keys) (void)hipFree(view.keys);
@@ -147,7 +189,11 @@ struct dsd_pool {
 
   void H2D(void* dst, const void* src, size_t bytes) {
     if (bytes == 0) return;
-    DSD_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream));
+    if (bytes >= kStageMinBytes && !IsPinnedHost(src)) {
+      StagedH2D(dst, src, bytes);
+    } else {
+      DSD_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream));
+    }
     stats.h2d_bytes += bytes;
     ++stats.h2d_calls;
     if (bytes >= kLargeCopyBytes) ++stats.h2d_large_calls;
@@ -158,6 +204,28 @@ struct dsd_pool {
     stats.d2h_bytes += bytes;
     ++stats.d2h_calls;
     if (bytes >= kLargeCopyBytes) ++stats.d2h_large_calls;
+  }
+  // A pageable upload in chunks through the pinned staging ring.  The
+  // caller's buffer may be reused as soon as this returns (every byte has
+  // been copied out of it); the DMA of the last chunks may still run.
+  void StagedH2D(void* dst, const void* src, size_t bytes) {
+    for (int b = 0; b < kStageBuffers; ++b) {
+      if (stage_host[b].ptr == nullptr) {
+        stage_host[b].Reserve(kStageChunkBytes);
+        DSD_HIP_CHECK(hipEventCreateWithFlags(&stage_ev[b], hipEventDisableTiming));
+      }
+    }
+    for (size_t off = 0; off < bytes; off += kStageChunkBytes) {
+      const size_t n = std::min(kStageChunkBytes, bytes - off);
+      const int b = stage_next;
+      stage_next = (b + 1) % kStageBuffers;
+      if (stage_busy[b]) DSD_HIP_CHECK(hipEventSynchronize(stage_ev[b]));
+      ParallelCopy(stage_host[b].ptr, static_cast<const char*>(src) + off, n);
+      DSD_HIP_CHECK(hipMemcpyAsync(static_cast<char*>(dst) + off, stage_host[b].ptr, n,
+                                   hipMemcpyHostToDevice, stream));
+      DSD_HIP_CHECK(hipEventRecord(stage_ev[b], stream));
+      stage_busy[b] = true;
+    }
   }
   void Sync() const { DSD_HIP_CHECK(hipStreamSynchronize(stream)); }
   // The host waits for an enqueued append (before reusing its staging).

@@ -22,6 +22,7 @@
 #include "dsd/paged_kv_cache.h"
 #include "dsd/reference_kernels.h"
 #include "dsd_hip.h"
+#include "host_workers.h"
 #include "status.h"
 
 namespace dsd {
@@ -513,14 +514,40 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
     ++steps_run;
     batch_sum += static_cast<int>(active.size());
 
+    // Payloads generated during the loop (not precomputed): every vector has
+    // its own seed, so the host threads form them in any order with the
+    // same values as the reference's in-loop generation (:596-633).
+    const bool gen_kv =
+        !options.gpu_synthetic_decode_append && !options.precompute_decode_payloads;
+    const bool gen_q = !options.precompute_decode_payloads;
+    std::vector<std::vector<float>> gen_k(gen_kv ? active.size() : 0);
+    std::vector<std::vector<float>> gen_v(gen_kv ? active.size() : 0);
+    if (gen_kv || gen_q) {
+      const int per = (gen_kv ? 2 : 0) + (gen_q ? 1 : 0);
+      dsd_host::Workers::Get().ParallelFor(
+          static_cast<int>(active.size()) * per, [&](int t) {
+            const int i = t / per;
+            const int which = t - i * per;
+            LiveRequest& l = active[static_cast<std::size_t>(i)];
+            const int id = l.a.state.request_id;
+            const int dstep = l.a.decode_step_index;
+            if (gen_kv && which == 0) {
+              gen_k[static_cast<std::size_t>(i)] = TokenVector(E, id, dstep, 1);
+            } else if (gen_kv && which == 1) {
+              gen_v[static_cast<std::size_t>(i)] = TokenVector(E, id, dstep, 2);
+            } else {
+              l.query_buf = TokenVector(E, id, dstep + 1, 0);  // the next step's query
+            }
+          });
+    }
     std::vector<AppendTokenResult> appended;
     std::vector<float> keys, values;
     std::vector<int> synth_requests, synth_steps;
-    for (auto& l : active) {
+    for (std::size_t li = 0; li < active.size(); ++li) {
+      LiveRequest& l = active[li];
       auto& a = l.a;
       const int id = a.state.request_id;
       const int dstep = a.decode_step_index;
-      std::vector<float> gk, gv;
       const float* k = nullptr;
       const float* v = nullptr;
       if (!options.gpu_synthetic_decode_append) {
@@ -528,10 +555,8 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
           k = Row(payloads.keys[a.spec_index], dstep, E);
           v = Row(payloads.values[a.spec_index], dstep, E);
         } else {
-          gk = TokenVector(E, id, dstep, 1);
-          gv = TokenVector(E, id, dstep, 2);
-          k = gk.data();
-          v = gv.data();
+          k = gen_k[li].data();
+          v = gen_v[li].data();
         }
       }
       // Decode tokens of GPU-admitted prompts start a fresh page (:614-616).
@@ -558,8 +583,7 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
         l.query = Row(payloads.next_queries[a.spec_index], dstep, E);
         l.own = false;
       } else {
-        l.query_buf = TokenVector(E, id, dstep + 1, 0);
-        l.own = true;
+        l.own = true;  // query_buf already holds it (generated above)
       }
       ++a.decode_step_index;
       --a.remaining_decode_steps;
@@ -685,21 +709,36 @@ ContinuousBatchStats RunContinuousDenseGpuDecode(
     ++steps_run;
     batch_sum += static_cast<int>(active.size());
 
+    // In-loop payloads on the host threads, as in the sparse loop.
+    const bool gen = !options.precompute_decode_payloads;
+    std::vector<std::vector<float>> gen_k(gen ? active.size() : 0);
+    std::vector<std::vector<float>> gen_v(gen ? active.size() : 0);
+    std::vector<std::vector<float>> gen_q(gen ? active.size() : 0);
+    if (gen) {
+      dsd_host::Workers::Get().ParallelFor(static_cast<int>(active.size()) * 3, [&](int t) {
+        const std::size_t i = static_cast<std::size_t>(t / 3);
+        const int id = active[i].state.request_id;
+        const int dstep = active[i].decode_step_index;
+        switch (t % 3) {
+          case 0: gen_k[i] = TokenVector(E, id, dstep, 1); break;
+          case 1: gen_v[i] = TokenVector(E, id, dstep, 2); break;
+          default: gen_q[i] = TokenVector(E, id, dstep + 1, 0); break;
+        }
+      });
+    }
     std::vector<AppendTokenResult> appended;
-    for (auto& a : active) {
+    for (std::size_t ai = 0; ai < active.size(); ++ai) {
+      auto& a = active[ai];
       const int id = a.state.request_id;
       const int dstep = a.decode_step_index;
-      std::vector<float> gk, gv;
       const float* k;
       const float* v;
       if (options.precompute_decode_payloads) {
         k = Row(payloads.keys[a.spec_index], dstep, E);
         v = Row(payloads.values[a.spec_index], dstep, E);
       } else {
-        gk = TokenVector(E, id, dstep, 1);
-        gv = TokenVector(E, id, dstep, 2);
-        k = gk.data();
-        v = gv.data();
+        k = gen_k[ai].data();
+        v = gen_v[ai].data();
       }
       const auto r = cache.AppendToken(id, k, v, false);
       if (a.remaining_decode_steps > 1) appended.push_back(r);
@@ -710,7 +749,7 @@ ContinuousBatchStats RunContinuousDenseGpuDecode(
         const float* q = Row(payloads.next_queries[a.spec_index], dstep, E);
         a.state.query.assign(q, q + E);
       } else {
-        a.state.query = TokenVector(E, id, dstep + 1, 0);
+        a.state.query = std::move(gen_q[ai]);
       }
       ++a.decode_step_index;
       --a.remaining_decode_steps;
