@@ -92,11 +92,12 @@ struct PinnedBuffer {
     ptr = nullptr;
     count = 0;
   }
-  void Reserve(size_t n) {
+  // hipHostMallocCoherent for buffers that kernels read or write directly
+  // (no GPU caching of host lines, so no stale data across steps).
+  void Reserve(size_t n, unsigned flags = hipHostMallocDefault) {
     if (n <= count) return;
     Release();
-    DSD_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&ptr), n * sizeof(T),
-                                hipHostMallocDefault));
+    DSD_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&ptr), n * sizeof(T), flags));
     count = n;
   }
 };
@@ -751,11 +752,11 @@ struct dsd_sparse_ctx {
   int max_sel = 0;
   hipStream_t stream = nullptr;
   hipEvent_t ev[6] = {};
-  DeviceBuffer<float> d_queries, d_scores, d_outputs, d_lo, d_hi;
+  DeviceBuffer<float> d_queries, d_scores, d_lo, d_hi;
   DeviceBuffer<int> d_offsets, d_ids, d_selected, d_counts, d_exact_pages;
   // fused-step publication words (see fused_step.hip) and per-workgroup
   // clock stamps for the timing mode
-  DeviceBuffer<unsigned long long> d_rec, d_stamps;
+  DeviceBuffer<unsigned long long> d_rec;
   unsigned epoch = 0;
   double wall_khz = 0.0;  // wall_clock64() rate
   int compute_units = 256;
@@ -835,18 +836,12 @@ struct dsd_sparse_ctx {
     a.exact_pages = d_exact_pages.ptr;
     a.fail_flag = h_fail.ptr;
     if (stamp) {
+      // The kernel writes its stamps straight into pinned host memory.
       stamp_grid = dsdk::FusedStepGrid(pool->view, L.batch, a.heads_per_group);
-      a.stamps = d_stamps.ptr;
+      a.stamps = h_stamps.ptr;
     }
     dsdk::LaunchFusedStep(pool->view, a, s);
-    if (stamp) {
-      // The kernel's own end, before the stamps travel back.
-      DSD_HIP_CHECK(hipEventRecord(ev[3], s));
-      DSD_HIP_CHECK(hipMemcpyAsync(h_stamps.ptr, d_stamps.ptr,
-                                   sizeof(unsigned long long) * stamp_grid *
-                                       dsdk::FusedStepStampsPerGroup(),
-                                   hipMemcpyDeviceToHost, s));
-    }
+    if (stamp) DSD_HIP_CHECK(hipEventRecord(ev[3], s));
   }
   // Phase split of the last timed fused launch from its workgroup stamps
   // (start, slice scored, counter ready, records read, ranked, selected,
@@ -952,7 +947,6 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     const size_t P = static_cast<size_t>(std::max(1, max_total_candidates));
     const size_t K = static_cast<size_t>(std::max(1, top_k));
     ctx->d_queries.Reserve(B * E);
-    ctx->d_outputs.Reserve(B * E);
     ctx->d_scores.Reserve(P);
     ctx->d_offsets.Reserve(B + 1);
     ctx->d_ids.Reserve(P);
@@ -968,8 +962,7 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
           static_cast<size_t>(dsdk::FusedStepGrid(pool->view, static_cast<int>(B), 2)) *
           dsdk::FusedStepStampsPerGroup();
       ctx->d_rec.Reserve(rec);
-      ctx->d_stamps.Reserve(stamps);
-      ctx->h_stamps.Reserve(stamps);
+      ctx->h_stamps.Reserve(stamps, hipHostMallocCoherent);
       DSD_HIP_CHECK(hipMemset(ctx->d_rec.ptr, 0, rec * sizeof(unsigned long long)));
     }
     ctx->h_fail.Reserve(1);
@@ -987,11 +980,13 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     if (const char* env = std::getenv("DSD_FUSED_STEP")) {
       ctx->fused_enabled = std::strcmp(env, "0") != 0;
     }
-    ctx->h_queries.Reserve(B * E);
-    ctx->h_outputs.Reserve(B * E);
+    // The host step's staging: the step's kernels read the inputs from here
+    // and write the outputs here directly (no DMA copies).
+    ctx->h_queries.Reserve(B * E, hipHostMallocCoherent);
+    ctx->h_outputs.Reserve(B * E, hipHostMallocCoherent);
     ctx->h_scores.Reserve(P);
-    ctx->h_offsets.Reserve(B + 1);
-    ctx->h_ids.Reserve(P);
+    ctx->h_offsets.Reserve(B + 1, hipHostMallocCoherent);
+    ctx->h_ids.Reserve(P, hipHostMallocCoherent);
     ctx->h_selected.Reserve(B * K);
     ctx->h_counts.Reserve(B);
     *out_ctx = ctx.release();
@@ -1075,14 +1070,21 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
       if (total > 0) std::memcpy(ctx->h_ids.ptr, cand_ids, sizeof(int) * total);
     }
     ctx->pool->OrderAfterPending(ctx->stream);
-    DSD_HIP_CHECK(hipMemcpyAsync(ctx->d_queries.ptr, ctx->h_queries.ptr,
-                                 sizeof(float) * qn, hipMemcpyHostToDevice, ctx->stream));
-    DSD_HIP_CHECK(hipMemcpyAsync(ctx->d_offsets.ptr, ctx->h_offsets.ptr,
-                                 sizeof(int) * (batch + 1), hipMemcpyHostToDevice,
-                                 ctx->stream));
-    if (total > 0) {
-      DSD_HIP_CHECK(hipMemcpyAsync(ctx->d_ids.ptr, ctx->h_ids.ptr, sizeof(int) * total,
-                                   hipMemcpyHostToDevice, ctx->stream));
+    {
+      // One kernel on the step's stream copies the staged inputs to the
+      // device: DMA copies would each cost a copy-engine hand-off.
+      dsdk::StageSegments seg;
+      seg.src[0] = reinterpret_cast<const uint32_t*>(ctx->h_queries.ptr);
+      seg.dst[0] = reinterpret_cast<uint32_t*>(ctx->d_queries.ptr);
+      seg.words[0] = static_cast<int>(qn);
+      seg.src[1] = reinterpret_cast<const uint32_t*>(ctx->h_offsets.ptr);
+      seg.dst[1] = reinterpret_cast<uint32_t*>(ctx->d_offsets.ptr);
+      seg.words[1] = batch + 1;
+      seg.src[2] = reinterpret_cast<const uint32_t*>(ctx->h_ids.ptr);
+      seg.dst[2] = reinterpret_cast<uint32_t*>(ctx->d_ids.ptr);
+      seg.words[2] = total;
+      seg.count = 3;
+      dsdk::LaunchStageIn(seg, ctx->stream);
     }
     t.h2d_ms = MsSince(t0);
 
@@ -1096,7 +1098,8 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
     L.queries = ctx->d_queries.ptr;
     L.offsets = ctx->d_offsets.ptr;
     L.ids = ctx->d_ids.ptr;
-    L.outputs = ctx->d_outputs.ptr;
+    // The attention writes the outputs straight into the pinned staging.
+    L.outputs = ctx->h_outputs.ptr;
     L.scores = ctx->d_scores.ptr;
     L.selected = ctx->d_selected.ptr;
     L.counts = ctx->d_counts.ptr;
@@ -1107,8 +1110,6 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
 
     if (want_outputs) {
       t0 = Clock::now();
-      DSD_HIP_CHECK(hipMemcpyAsync(ctx->h_outputs.ptr, ctx->d_outputs.ptr,
-                                   sizeof(float) * qn, hipMemcpyDeviceToHost, ctx->stream));
       if (debug && total > 0) {
         DSD_HIP_CHECK(hipMemcpyAsync(ctx->h_scores.ptr, ctx->d_scores.ptr,
                                      sizeof(float) * total, hipMemcpyDeviceToHost,

@@ -72,6 +72,17 @@ void LaunchAppendSynthetic(const PoolView& pool, const int* d_seg_start, const i
 void LaunchMarkFree(const PoolView& pool, const int* d_page_ids, int n,
                     hipStream_t stream);
 
+// Up to four segments of 4-byte words, each 16-byte aligned at both ends of
+// the copy: src in pinned host memory the device reads directly, dst in
+// device memory.
+struct StageSegments {
+  const uint32_t* src[4] = {};
+  uint32_t* dst[4] = {};
+  int words[4] = {};
+  int count = 0;
+};
+void LaunchStageIn(const StageSegments& s, hipStream_t stream);
+
 // ---- decode-step kernels (step_kernels.hip) --------------------------------
 
 // Exact-order page scores: scores[c] = fl(sum_seq q*s) * scale, bit-equal to

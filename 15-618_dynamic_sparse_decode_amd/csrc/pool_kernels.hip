@@ -6,6 +6,8 @@
 // (src/paged_kv_cache.cpp:231-238).  The reference's device kernel instead
 // divides by the count (src/device_page_pool.cpp:89-99), which can differ by
 // an ulp; this pool reproduces the host cache bit for bit.
+#include <algorithm>
+
 #include "dsd_internal.h"
 
 namespace dsdk {
@@ -252,6 +254,39 @@ void LaunchAppendSynthetic(const PoolView& pool, const int* d_seg_start, const i
   hipLaunchKernelGGL(AppendSyntheticKernel, dim3(num_segments), dim3(kPoolThreads), 0, stream,
                      pool, d_seg_start, d_order, d_page_ids, d_offsets, d_counts,
                      d_request_ids, d_decode_steps, num_segments);
+  DSD_HIP_CHECK(hipGetLastError());
+}
+
+// The host step's inputs, from the context's pinned (device-visible,
+// coherent) staging into device buffers, on the step's stream: one small
+// kernel instead of DMA copies, each of which costs a hand-off between the
+// copy engine and the compute queue (tens of microseconds per step).
+__global__ __launch_bounds__(kPoolThreads) void StageInKernel(StageSegments s) {
+  const int tid = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
+  const int stride = static_cast<int>(gridDim.x * blockDim.x);
+  for (int k = 0; k < s.count; ++k) {
+    const int words = s.words[k];
+    const int n4 = words / 4;
+    const uint4* src4 = reinterpret_cast<const uint4*>(s.src[k]);
+    uint4* dst4 = reinterpret_cast<uint4*>(s.dst[k]);
+    for (int i = tid; i < n4; i += stride) dst4[i] = src4[i];
+    for (int i = 4 * n4 + tid; i < words; i += stride) s.dst[k][i] = s.src[k][i];
+  }
+}
+
+void LaunchStageIn(const StageSegments& s, hipStream_t stream) {
+  size_t words = 0;
+  for (int k = 0; k < s.count; ++k) {
+    if (s.words[k] < 0) throw std::invalid_argument("negative staging segment");
+    if ((reinterpret_cast<uintptr_t>(s.src[k]) | reinterpret_cast<uintptr_t>(s.dst[k])) % 16 != 0) {
+      throw std::invalid_argument("staging segments must be 16-byte aligned");
+    }
+    words += static_cast<size_t>(s.words[k]);
+  }
+  if (words == 0) return;
+  const size_t groups = std::min<size_t>((words / 4 + kPoolThreads - 1) / kPoolThreads + 1, 256);
+  hipLaunchKernelGGL(StageInKernel, dim3(static_cast<unsigned>(groups)), dim3(kPoolThreads), 0,
+                     stream, s);
   DSD_HIP_CHECK(hipGetLastError());
 }
 
