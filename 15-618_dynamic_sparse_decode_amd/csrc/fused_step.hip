@@ -76,9 +76,9 @@ struct FusedShared {
   uint64_t stamp[kStampsPerGroup];  // timing mode: thread 0's clocks
   // score pass (per wave): float total (the carry into wave 2p+1) and the
   // bound sums
-  float wave_total[kFWaves];
-  float abs_prefix[kFWaves];
-  float abs_p[kFWaves];
+  float wave_total[2][kFWaves];  // [pass parity]: a pass's leader reads its
+  float abs_prefix[2][kFWaves];  // sums after the pass's last barrier, while
+  float abs_p[2][kFWaves];       // the next pass may already write its own
   int fail;
   int nflag;
   // selection (attention item)
@@ -187,10 +187,48 @@ __device__ void ParallelRanks(FusedShared& sh, int n) {
 // into the page sum is at most 3 local + 6 scan + 8 rows of wave 2p + 8 rows
 // of wave 2p+1 + 1 = 26 (40 is used in the bound).  Called by the whole
 // workgroup.
+constexpr int kFRows = kFPerLane / 4;  // rows of float4 per lane and pass
+
+// A workgroup barrier that orders LDS only.  __syncthreads() also orders
+// global memory: with a global store outstanding (the previous pass's
+// intervals) it waits on vmcnt(0), which on gfx950 counts loads too, and so
+// would wait for the rows prefetched for the next pass.
+__device__ __forceinline__ void LdsBarrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// This wave's half of page `page`'s summary (kFRows float4 per lane) and its
+// token count, issued without waiting.  An id outside the pool loads page 0
+// with a count of 0 (the pass reports it).
+__device__ __forceinline__ void LoadPassRows(const PoolView& pool, int page,
+                                             float4 (&sv)[kFRows], int& count) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int half = (threadIdx.x / kWave) & 1;
+  count = 0;
+  if (page >= 0 && page < pool.capacity) {
+    count = pool.token_counts[page];
+  } else {
+    page = 0;
+  }
+  const float4* s4 =
+      reinterpret_cast<const float4*>(pool.summaries + static_cast<size_t>(page) * kFE) +
+      half * 512 + lane;
+#pragma unroll
+  for (int j = 0; j < kFRows; ++j) sv[j] = s4[j * kWave];
+}
+
+// One pass over rows already loaded (sv, count for this wave's candidate
+// first + wave/2, page id `page`).  Once the products are formed, the rows
+// of the next pass's candidate (page id `next`, when next_active) load into
+// the same registers, so their latency overlaps this pass's reductions and
+// publication.
 template <class Shared>
 __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int first, int end,
-                          int prefetched_page, const float4* q_lds, Shared& sh) {
-  constexpr int kRows = kFPerLane / 4;  // 8
+                          int page, float4 (&sv)[kFRows], int& count, bool next_active,
+                          int next, int parity, const float4* q_lds, Shared& sh) {
+  constexpr int kRows = kFRows;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int half = wave & 1;
@@ -201,26 +239,12 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int first, i
   float loc_abs = 0.0f;   // sum of |loc| over this lane's groups
   float p_abs = 0.0f;
   if (active) {
-    int page = prefetched_page >= 0 ? prefetched_page : a.cand_ids[c];
-    int count = 0;
-    if (page >= 0 && page < pool.capacity) {
-      count = pool.token_counts[page];
-    } else {
-      // An id outside the pool scores as an empty page and is reported.
-      if (half == 0 && lane == 0) ReportFailure(a, 3);
-      page = 0;
-    }
+    // An id outside the pool scores as an empty page and is reported.
+    if ((page < 0 || page >= pool.capacity) && half == 0 && lane == 0) ReportFailure(a, 3);
     const float4* q4 = q_lds + half * 512 + lane;
-    const float4* s4 =
-        reinterpret_cast<const float4*>(pool.summaries + static_cast<size_t>(page) * kFE) +
-        half * 512 + lane;
     float4 qv[kRows];
-    float4 sv[kRows];
 #pragma unroll
-    for (int j = 0; j < kRows; ++j) {
-      qv[j] = q4[j * kWave];
-      sv[j] = s4[j * kWave];
-    }
+    for (int j = 0; j < kRows; ++j) qv[j] = q4[j * kWave];
     // A page holding no tokens reads as an all-zero summary
     // (src/paged_kv_cache.cpp:457-459); the products q*0 are still formed.
     if (count == 0) {
@@ -248,13 +272,14 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int first, i
       float total = 0.0f;
 #pragma unroll
       for (int j = 0; j < kRows; ++j) total = __fadd_rn(total, row_sum[j]);
-      sh.wave_total[wave] = total;
+      sh.wave_total[parity][wave] = total;
     }
   }
-  __syncthreads();
+  if (next_active) LoadPassRows(pool, next, sv, count);
+  LdsBarrier();
   if (active) {
     // Starting prefix of each of this lane's groups, and the bound sums.
-    float base = half ? sh.wave_total[wave - 1] : 0.0f;
+    float base = half ? sh.wave_total[parity][wave - 1] : 0.0f;
     float tl = 0.0f;
 #pragma unroll
     for (int j = 0; j < kRows; ++j) {
@@ -265,15 +290,17 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int first, i
     const float tsum = WaveTotal(__fadd_rn(tl, loc_abs));
     const float absp = WaveTotal(p_abs);
     if (lane == 0) {
-      sh.abs_prefix[wave] = tsum;
-      sh.abs_p[wave] = absp;
+      sh.abs_prefix[parity][wave] = tsum;
+      sh.abs_p[parity][wave] = absp;
     }
   }
-  __syncthreads();
+  LdsBarrier();
   if (active && half == 0 && lane == 0) {
-    const float s_hat = __fadd_rn(sh.wave_total[wave], sh.wave_total[wave + 1]);
-    const float tsum = __fadd_rn(sh.abs_prefix[wave], sh.abs_prefix[wave + 1]);
-    const float ap = __fadd_rn(sh.abs_p[wave], sh.abs_p[wave + 1]);
+    const float s_hat =
+        __fadd_rn(sh.wave_total[parity][wave], sh.wave_total[parity][wave + 1]);
+    const float tsum =
+        __fadd_rn(sh.abs_prefix[parity][wave], sh.abs_prefix[parity][wave + 1]);
+    const float ap = __fadd_rn(sh.abs_p[parity][wave], sh.abs_p[parity][wave + 1]);
     float mid, lo, hi;
     WriteBoundsFloat<kFE, 4, 40>(s_hat, tsum, ap, a.scale, &mid, &lo, &hi);
     a.mid[c] = mid;
@@ -289,22 +316,44 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int first, i
 }
 
 // The candidates [c0, c1) of request r, eight per pass.  The query is
-// staged once in LDS (in the rescoring tile, idle until the selection); the
-// first pass's page ids load alongside it.
-template <class Shared>
+// staged once in LDS (in the rescoring tile, idle until the selection).
+// kPipeline: the first pass's rows load alongside the query, and each later
+// pass's id at the start of the pass before, its rows once that pass's
+// products are formed (the stand-alone score kernel, up to 8 passes).
+// Otherwise each pass loads its own rows first (the single-launch step,
+// where slices are mostly one pass: the pipelined form measured 0.5 us
+// slower at config 2 and 0.6 % faster at config 4).
+template <bool kPipeline, class Shared>
 __device__ void ScoreSlice(const PoolView& pool, const FusedArgs& a, int r, int c0, int c1,
                            Shared& sh) {
   if (c0 >= c1) return;
   static_assert(kFE / 4 == kFThreads, "one float4 of the query per thread");
   static_assert(sizeof(sh.tile) >= kFE * sizeof(float), "the query fits the tile");
   const int c = c0 + static_cast<int>(threadIdx.x) / (2 * kWave);
-  const int page0 = c < c1 ? a.cand_ids[c] : -1;
-  float4* q_lds = reinterpret_cast<float4*>(sh.tile);
-  q_lds[threadIdx.x] =
+  // The query and the first ids load together.
+  const float4 qv =
       reinterpret_cast<const float4*>(a.queries + static_cast<size_t>(r) * kFE)[threadIdx.x];
-  __syncthreads();
+  int page = c < c1 ? a.cand_ids[c] : -1;
+  float4 sv[kFRows];
+  int count = 0;
+  if (kPipeline && c < c1) LoadPassRows(pool, page, sv, count);
+  float4* q_lds = reinterpret_cast<float4*>(sh.tile);
+  q_lds[threadIdx.x] = qv;
+  LdsBarrier();
   for (int first = c0; first < c1; first += kFPagesPerPass) {
-    ScorePass(pool, a, first, c1, first == c0 ? page0 : -1, q_lds, sh);
+    const int parity = ((first - c0) / kFPagesPerPass) & 1;
+    if constexpr (kPipeline) {
+      const int cn = c + (first - c0) + kFPagesPerPass;  // this wave's next candidate
+      const bool next_active = cn < c1;
+      const int next = next_active ? a.cand_ids[cn] : -1;
+      ScorePass(pool, a, first, c1, page, sv, count, next_active, next, parity, q_lds, sh);
+      page = next;
+    } else {
+      const int cp = c + (first - c0);
+      if (first != c0) page = cp < c1 ? a.cand_ids[cp] : -1;
+      if (cp < c1) LoadPassRows(pool, page, sv, count);
+      ScorePass(pool, a, first, c1, page, sv, count, false, -1, parity, q_lds, sh);
+    }
   }
 }
 
@@ -784,7 +833,7 @@ __global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, Fuse
   // A request beyond kFMaxCand selects nothing (reported by the selection):
   // its slices are not scored.
   if (n <= kFMaxCand) {
-    ScoreSlice(pool, a, r, begin + (g * n) / groups, begin + ((g + 1) * n) / groups, sh);
+    ScoreSlice<false>(pool, a, r, begin + (g * n) / groups, begin + ((g + 1) * n) / groups, sh);
   }
   StampAt(a, sh, kScored);
   AttentionItem(pool, a, r, begin, n, g, sh);
@@ -806,9 +855,9 @@ __global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, Fuse
 // staged once per workgroup, eight pages per pass.  Intervals go to
 // mid/lo/hi[c] only.
 struct ScoreShared {
-  float wave_total[kFWaves];
-  float abs_prefix[kFWaves];
-  float abs_p[kFWaves];
+  float wave_total[2][kFWaves];  // [pass parity]: a pass's leader reads its
+  float abs_prefix[2][kFWaves];  // sums after the pass's last barrier, while
+  float abs_p[2][kFWaves];       // the next pass may already write its own
   alignas(16) float tile[kFE];  // the query
 };
 
@@ -821,7 +870,7 @@ __global__ __launch_bounds__(kFThreads) void ScorePagesKernel(PoolView pool, Fus
   const int c0 = static_cast<int>(blockIdx.x) * pages_per_group;
   if (c0 >= n) return;
   const int c1 = n - c0 < pages_per_group ? n : c0 + pages_per_group;
-  ScoreSlice(pool, a, r, begin + c0, begin + c1, sh);
+  ScoreSlice<true>(pool, a, r, begin + c0, begin + c1, sh);
 }
 
 }  // namespace
