@@ -216,3 +216,40 @@ def test_summary_rows_copied_verbatim_when_given(gpu):
     assert pool.download_summaries([1])[0].tolist() == [0.5] * E
     pool.upload_tokens([0], [0], [1], seq(E, 3.0), seq(E, 4.0), np.full((1, E), -2.0, np.float32))
     assert pool.download_summaries([0])[0].tolist() == [-2.0] * E
+
+
+@pytest.mark.parametrize("pinned", [False, True])
+def test_large_uploads_round_trip(gpu, pinned):
+    # Copies of 4 MB and more from pageable memory go through the pool's
+    # pinned staging ring (16 MB chunks, 1 MB host-thread tasks); from pinned
+    # memory they go straight to the DMA engine.  Either way every byte must
+    # land: a 200-page run (50 MB, a partial last chunk), a 77-page run
+    # (19.25 MB) and a lone partial page.
+    import torch
+    h, d, ps = 32, 128, 16
+    e = h * d
+    pool = gpu.DevicePagePool(h, d, ps, 300)
+    page_ids = list(range(10, 210)) + list(range(220, 297)) + [299]
+    counts = [ps] * 277 + [7]
+    src_offsets = [i * ps * e for i in range(len(page_ids))]
+    total = len(page_ids) * ps * e
+    rng = np.random.default_rng(5)
+    keys = rng.standard_normal(total, dtype=np.float32)
+    values = rng.standard_normal(total, dtype=np.float32)
+    if pinned:
+        tk = torch.empty(total, dtype=torch.float32, pin_memory=True)
+        tv = torch.empty(total, dtype=torch.float32, pin_memory=True)
+        tk.numpy()[:] = keys
+        tv.numpy()[:] = values
+        src_k, src_v = tk.numpy(), tv.numpy()
+    else:
+        src_k, src_v = keys, values
+    pool.upload_pages(page_ids, counts, src_offsets, src_k, src_v)
+    for i in sorted(set(range(0, len(page_ids), 13)) | {63, 64, 199, 200, 276, 277}):
+        k, v = pool.download_page(page_ids[i])
+        n = counts[i] * e
+        assert k.size == n and v.size == n, (pinned, i)
+        np.testing.assert_array_equal(k, keys[src_offsets[i]:src_offsets[i] + n])
+        np.testing.assert_array_equal(v, values[src_offsets[i]:src_offsets[i] + n])
+    st = pool.transfer_stats()
+    assert st["h2d_bytes"] >= 2 * 4 * e * sum(counts)  # keys and values, valid tokens
