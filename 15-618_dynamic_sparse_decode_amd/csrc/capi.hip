@@ -148,9 +148,12 @@ struct dsd_pool {
   DeviceBuffer<int> stage_ids, stage_counts, stage_offsets, stage_order, stage_segs;
   DeviceBuffer<int> stage_req, stage_steps;
   DeviceBuffer<float> stage_rows, stage_keys, stage_values;
-  // dense-path scratch
-  DeviceBuffer<float> dense_q, dense_out;
+  // dense-path scratch: device inputs, and coherent pinned staging that the
+  // stage-in kernel reads and the attention writes its outputs into
+  DeviceBuffer<float> dense_q;
   DeviceBuffer<int> dense_offsets, dense_ids;
+  PinnedBuffer<float> h_dense_q, h_dense_out;
+  PinnedBuffer<int> h_dense_offsets, h_dense_ids;
   hipEvent_t dense_start = nullptr, dense_stop = nullptr;
   uint64_t* k_offsets = nullptr;  // [capacity] element offset of each page
   uint64_t* v_offsets = nullptr;
@@ -1315,17 +1318,31 @@ int dsd_dense_run_batch(dsd_pool* pool, int batch, const float* queries,
     for (int c = 0; c < total; ++c) pool->ValidatePage(cand_ids[c]);
     const size_t qn = static_cast<size_t>(batch) * pool->view.elements;
     pool->dense_q.Reserve(qn);
-    pool->dense_out.Reserve(qn);
     pool->dense_offsets.Reserve(batch + 1);
     pool->dense_ids.Reserve(std::max(1, total));
-    DSD_HIP_CHECK(hipMemcpyAsync(pool->dense_q.ptr, queries, sizeof(float) * qn,
-                                 hipMemcpyHostToDevice, pool->stream));
-    DSD_HIP_CHECK(hipMemcpyAsync(pool->dense_offsets.ptr, cand_offsets,
-                                 sizeof(int) * (batch + 1), hipMemcpyHostToDevice,
-                                 pool->stream));
-    if (total > 0) {
-      DSD_HIP_CHECK(hipMemcpyAsync(pool->dense_ids.ptr, cand_ids, sizeof(int) * total,
-                                   hipMemcpyHostToDevice, pool->stream));
+    pool->h_dense_q.Reserve(qn, hipHostMallocCoherent);
+    pool->h_dense_out.Reserve(qn, hipHostMallocCoherent);
+    pool->h_dense_offsets.Reserve(batch + 1, hipHostMallocCoherent);
+    pool->h_dense_ids.Reserve(std::max(1, total), hipHostMallocCoherent);
+    // As the sparse host step: inputs through pinned staging and one
+    // stage-in kernel, outputs written by the attention into pinned memory
+    // (no DMA copies, so no copy-engine hand-offs).
+    std::memcpy(pool->h_dense_q.ptr, queries, sizeof(float) * qn);
+    std::memcpy(pool->h_dense_offsets.ptr, cand_offsets, sizeof(int) * (batch + 1));
+    if (total > 0) std::memcpy(pool->h_dense_ids.ptr, cand_ids, sizeof(int) * total);
+    {
+      dsdk::StageSegments seg;
+      seg.src[0] = reinterpret_cast<const uint32_t*>(pool->h_dense_q.ptr);
+      seg.dst[0] = reinterpret_cast<uint32_t*>(pool->dense_q.ptr);
+      seg.words[0] = static_cast<int>(qn);
+      seg.src[1] = reinterpret_cast<const uint32_t*>(pool->h_dense_offsets.ptr);
+      seg.dst[1] = reinterpret_cast<uint32_t*>(pool->dense_offsets.ptr);
+      seg.words[1] = batch + 1;
+      seg.src[2] = reinterpret_cast<const uint32_t*>(pool->h_dense_ids.ptr);
+      seg.dst[2] = reinterpret_cast<uint32_t*>(pool->dense_ids.ptr);
+      seg.words[2] = total;
+      seg.count = 3;
+      dsdk::LaunchStageIn(seg, pool->stream);
     }
     dsdk::AttentionArgs a;
     a.queries = pool->dense_q.ptr;
@@ -1334,13 +1351,12 @@ int dsd_dense_run_batch(dsd_pool* pool, int batch, const float* queries,
     a.list_stride = 0;
     a.batch = batch;
     a.scale = 1.0f / std::sqrt(static_cast<float>(pool->view.head_dim));
-    a.outputs = pool->dense_out.ptr;
+    a.outputs = pool->h_dense_out.ptr;
     DSD_HIP_CHECK(hipEventRecord(pool->dense_start, pool->stream));
     dsdk::LaunchAttention(pool->view, a, pool->stream);
     DSD_HIP_CHECK(hipEventRecord(pool->dense_stop, pool->stream));
-    DSD_HIP_CHECK(hipMemcpyAsync(outputs, pool->dense_out.ptr, sizeof(float) * qn,
-                                 hipMemcpyDeviceToHost, pool->stream));
     pool->Sync();
+    std::memcpy(outputs, pool->h_dense_out.ptr, sizeof(float) * qn);
     if (kernel_ms != nullptr) {
       float ms = 0.f;
       DSD_HIP_CHECK(hipEventElapsedTime(&ms, pool->dense_start, pool->dense_stop));
