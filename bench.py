@@ -258,6 +258,15 @@ def main() -> int:
                                        "(FETCH_SIZE/WRITE_SIZE per launch, copy-calibrated)",
                      "kernel": roof_kernel, "bytes_per_launch": roof_bytes,
                      "us_per_launch": roof_ms * 1e3},
+        # The BASELINE target is phrased for the fused gather + attention
+        # stage (>= 60 % of 8 TB/s at config 2): that stage alone, replayed
+        # back to back (AttentionFastKernel, the three-kernel step's third
+        # kernel; inside the single launch it shares the launch with scoring
+        # and selection, which the roofline above covers).
+        "attention_roofline": {"bound": "hbm", "achieved": attn_gbps, "peak": HBM_PEAK_GBPS,
+                               "unit": "GB/s", "frac": attn_gbps / HBM_PEAK_GBPS,
+                               "target_frac": 0.6, "bytes_per_launch": attn_bytes,
+                               "us_per_launch": stage_ms[2] * 1e3},
         "step_phases_us": {k[:-3]: phases[k] * 1e3
                            for k in ("score_ms", "topk_ms", "attention_ms", "kernel_ms")},
         "host_path": {"us_per_step": host_ms * 1e3, "tokens_per_s": B / (host_ms * 1e-3),
