@@ -189,3 +189,60 @@ def test_certified_large_request_many_flags(gpu, k):
     assert orc.max_abs_diff(cert["outputs"], outs) <= 1e-4
     assert rescored > 32, "expected several chain groups"
     pool.close()
+
+
+def extreme_summaries(kind, rng, cap, E):
+    """Summary rows that strain the float error bound of the certified score."""
+    if kind == "cancel":        # partial sums swing by 1e4, scores end near 0
+        sign = np.where(np.arange(E) % 2 == 0, 1.0, -1.0)
+        rows = 1e4 * sign + 1e-3 * rng.standard_normal((cap, E))
+    elif kind == "grow_cancel":  # the first half climbs, the second half cancels it
+        sign = np.where(np.arange(E) < E // 2, 1.0, -1.0)
+        rows = 3e3 * sign * (1.0 + 1e-4 * rng.standard_normal((cap, E)))
+    elif kind == "wide_range":   # magnitudes 1e-22 .. 1e16, random signs
+        rows = 10.0 ** rng.uniform(-22, 16, (cap, E)) * rng.choice([-1.0, 1.0], (cap, E))
+    elif kind == "subnormal":    # products in the subnormal range (|q s| ~ 1e-44 .. 1e-40)
+        rows = 10.0 ** rng.uniform(-23, -21, (cap, E)) * rng.choice([-1.0, 1.0], (cap, E))
+    else:
+        raise ValueError(kind)
+    return rows.astype(np.float32)
+
+
+@pytest.mark.parametrize("kind", ["cancel", "grow_cancel", "wide_range", "subnormal"])
+def test_certified_intervals_hold_on_extreme_summaries(gpu, kind):
+    # Summary rows are uploaded verbatim (not key means), so scores can be
+    # dominated by cancellation, span 38 orders of magnitude, or be built
+    # from subnormal products.  Every interval must still contain the exact
+    # sequential score, and the selection must equal sparse_cpu's.
+    rng = np.random.default_rng({"cancel": 1, "grow_cancel": 2, "wide_range": 3,
+                                 "subnormal": 4}[kind])
+    H, D, ps, cap = 32, 128, 16, 96
+    E = H * D
+    summ = extreme_summaries(kind, rng, cap, E)
+    keys = rng.standard_normal((cap, ps, E)).astype(np.float32)
+    values = rng.standard_normal((cap, ps, E)).astype(np.float32)
+    pool = gpu.DevicePagePool(H, D, ps, cap)
+    page_ids = np.arange(cap, dtype=np.int32)
+    pool.upload_pages(page_ids, np.full(cap, ps, np.int32), page_ids.astype(np.int64) * ps * E,
+                      keys, values, summ)
+    if kind == "wide_range":
+        q = (10.0 ** rng.uniform(-22, 16, (2, E)) * rng.choice([-1.0, 1.0], (2, E)))
+    elif kind == "subnormal":
+        q = 10.0 ** rng.uniform(-23, -21, (2, E)) * rng.choice([-1.0, 1.0], (2, E))
+    else:
+        q = 1.0 + 1e-3 * rng.standard_normal((2, E))
+    q = q.astype(np.float32)
+    cand = rng.permutation(cap).astype(np.int32)
+    offs = np.array([0, cap, 2 * cap], np.int32)
+    ids = np.concatenate([cand, cand[::-1]]).astype(np.int32)
+    counts = np.full(cap, ps, np.int32)
+    for k in (1, 4, 8):
+        cert, (mid, lo, hi), rescored, exact = run_both_paths(gpu, pool, q, offs, ids, k)
+        ex = exact["scores"]
+        assert np.all(np.isfinite(ex))
+        assert np.all(lo <= ex) and np.all(ex <= hi), (kind, k, "an interval misses the exact score")
+        _, selected, outs = orc.sparse_batch(q, keys, values, summ, counts, offs, ids, H, D, ps, k)
+        for r in range(2):
+            assert cert["selected"][r].tolist() == selected[r].tolist(), (kind, k, r)
+        assert orc.max_abs_diff(cert["outputs"], outs) <= 1e-4
+    pool.close()
