@@ -187,12 +187,22 @@ __global__ __launch_bounds__(256) void SelectTopKKernel(
 }
 
 // Bitonic sort of (key, idx) pairs, descending, over m = 2^log_m entries.
+// Thread i handles pair i of each stage; for strides up to 64 the pairs of
+// wave w lie in keys [128w, 128w + 128), touched by no other wave, so those
+// stages need only a wave-level sync (m <= 2 * blockDim).  A workgroup
+// barrier follows every stage that crosses waves or precedes one that does
+// (about 18 barriers at m = 2048 instead of 66).
 __device__ void BitonicSortDesc(uint64_t* keys, int* idx, int m, int log_m) {
   const int half = m >> 1;
+  const bool pairs_in_one_pass = half <= static_cast<int>(blockDim.x);
+  auto wave_local = [&](int log_stride) { return pairs_in_one_pass && log_stride <= 6; };
   for (int log_size = 1; log_size <= log_m; ++log_size) {
     const int size = 1 << log_size;
     for (int log_stride = log_size - 1; log_stride >= 0; --log_stride) {
       const int stride = 1 << log_stride;
+      // The stage after this one (none after the last: a full barrier).
+      const bool next_local = log_stride > 0 ? wave_local(log_stride - 1)
+                                             : (log_size < log_m && wave_local(log_size));
       for (int i = threadIdx.x; i < half; i += blockDim.x) {
         const int lo = ((i >> log_stride) << (log_stride + 1)) | (i & (stride - 1));
         const int hi = lo + stride;
@@ -207,7 +217,11 @@ __device__ void BitonicSortDesc(uint64_t* keys, int* idx, int m, int log_m) {
           idx[hi] = t;
         }
       }
-      __syncthreads();
+      if (wave_local(log_stride) && next_local) {
+        WaveSync();
+      } else {
+        __syncthreads();
+      }
     }
   }
 }
@@ -229,6 +243,70 @@ constexpr int kCertMaxKeys = 2048;   // next-pow2 candidates per request
 constexpr int kSelRescoreGroup = 32;  // exact chains per rescore group (lanes of wave 0)
 constexpr int kSelThreads = 1024;    // one compare-exchange per thread per stage at 2048 keys
 
+// Radix select of the kk-th largest 64-bit key among keys[0, n): 8 bits a
+// round from the top, stopping as soon as the boundary bucket holds exactly
+// the members still needed.  On return *shift is the last round's shift,
+// *prefix the kept bucket's key bits above it, *need how many keys of that
+// bucket are members and *all whether they all are (need == bucket size).
+// Keys above the bucket (key >> shift > prefix) are members.  Whole
+// workgroup; hist is 256 ints of LDS.
+__device__ void RadixSelectKth(const uint64_t* keys, int n, int kk, int* hist,
+                               unsigned long long* s_prefix, int* s_need, int* s_all,
+                               int* shift_out, uint64_t* prefix_out, int* need_out,
+                               bool* all_out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  uint64_t prefix = 0;
+  int need = kk;
+  int shift = 56;
+  bool all = false;
+  for (int round = 0; round < 8; ++round) {
+    shift = 56 - 8 * round;
+    for (int b = threadIdx.x; b < 256; b += blockDim.x) hist[b] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const uint64_t key = keys[i];
+      if (round == 0 || (key >> (shift + 8)) == prefix) {
+        atomicAdd(&hist[static_cast<int>((key >> shift) & 255u)], 1);
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      // Lane l holds bins 4l .. 4l+3; suffix sums from the top bin down find
+      // the bucket b with sum(bins > b) < need <= sum(bins >= b).
+      const int b0 = 4 * lane;
+      const int c3 = hist[b0 + 3], c2 = hist[b0 + 2], c1 = hist[b0 + 1], c0 = hist[b0];
+      int suffix = c0 + c1 + c2 + c3;  // becomes the sum over lanes >= l
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int other = __shfl_down(suffix, o, kWave);
+        if (lane + o < kWave) suffix += other;
+      }
+      int above = __shfl_down(suffix, 1, kWave);  // sum over lanes > l
+      if (lane == kWave - 1) above = 0;
+      if (suffix >= need && above < need) {
+        int b = b0 + 3;
+        int count = c3;
+        if (above + c3 < need) { above += c3; b = b0 + 2; count = c2;
+          if (above + c2 < need) { above += c2; b = b0 + 1; count = c1;
+            if (above + c1 < need) { above += c1; b = b0; count = c0; } } }
+        *s_prefix = (static_cast<unsigned long long>(prefix) << 8) | static_cast<unsigned>(b);
+        *s_need = need - above;
+        *s_all = count == need - above;
+      }
+    }
+    __syncthreads();
+    prefix = *s_prefix;
+    need = *s_need;
+    all = *s_all != 0;
+    __syncthreads();  // the next round rewrites hist and the shared words
+    if (all) break;
+  }
+  *shift_out = shift;
+  *prefix_out = prefix;
+  *need_out = need;
+  *all_out = all;
+}
+
 __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
     const float* __restrict__ mid, const float* __restrict__ lo,
     const float* __restrict__ hi, const float* __restrict__ queries,
@@ -236,14 +314,18 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
     const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int E,
     float scale, int top_k, int* __restrict__ selected, int* __restrict__ counts,
     int* __restrict__ exact_pages) {
-  __shared__ uint64_t keys[kCertMaxKeys];
-  __shared__ int idx[kCertMaxKeys];
-  __shared__ int flagged[kCertMaxKeys];
+  __shared__ uint64_t keys[kCertMaxKeys];   // by candidate
   __shared__ float s_lo[kCertMaxKeys];
   __shared__ float s_hi[kCertMaxKeys];
+  __shared__ uint8_t member[kCertMaxKeys];  // by candidate
+  __shared__ uint64_t skeys[kCertMaxKeys];  // the members, then the final set, sorted
+  __shared__ int sidx[kCertMaxKeys];
+  __shared__ int flagged[kCertMaxKeys];
+  __shared__ int hist[256];
   __shared__ __align__(16) float tile[RescoreFloats<kSelRescoreGroup>()];
   __shared__ float s_red[2][kSelThreads / kWave];
-  __shared__ int s_nflag;
+  __shared__ unsigned long long s_prefix;
+  __shared__ int s_need, s_all, s_count, s_tie, s_nflag;
   const int r = blockIdx.x;
   const int begin = cand_offsets[r];
   const int n = cand_offsets[r + 1] - begin;
@@ -252,32 +334,63 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
     if (threadIdx.x == 0) counts[r] = 0;
     return;
   }
+  const int* cand = cand_ids + begin;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    keys[i] = SelectKey(mid[begin + i], cand[i]);
+    s_lo[i] = lo[begin + i];
+    s_hi[i] = hi[begin + i];
+  }
+  if (threadIdx.x == 0) {
+    s_count = 0;
+    s_tie = 0;
+    s_nflag = 0;
+  }
+  __syncthreads();
+
+  // 1. The members: the kk largest keys (equal keys are the same page listed
+  //    twice, so which of them counts is immaterial).
+  int shift;
+  uint64_t prefix;
+  int need;
+  bool all;
+  RadixSelectKth(keys, n, kk, hist, &s_prefix, &s_need, &s_all, &shift, &prefix, &need, &all);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const uint64_t top = keys[i] >> shift;
+    bool in = top > prefix;
+    if (top == prefix) in = all || atomicAdd(&s_tie, 1) < need;
+    member[i] = in ? 1 : 0;
+    if (in) {
+      const int pos = atomicAdd(&s_count, 1);
+      skeys[pos] = keys[i];
+      sidx[pos] = i;
+    }
+  }
+  __syncthreads();
   int m = 1, log_m = 0;
-  while (m < n) {
+  while (m < kk) {
     m <<= 1;
     ++log_m;
   }
-  for (int i = threadIdx.x; i < m; i += blockDim.x) {
-    if (i < n) {
-      keys[i] = SelectKey(mid[begin + i], cand_ids[begin + i]);
-      idx[i] = i;
-      s_lo[i] = lo[begin + i];
-      s_hi[i] = hi[begin + i];
-    } else {
-      keys[i] = 0ull;
-      idx[i] = -1;
-    }
+  for (int t = kk + threadIdx.x; t < m; t += blockDim.x) {
+    skeys[t] = 0ull;
+    sidx[t] = -1;
   }
-  if (threadIdx.x == 0) s_nflag = 0;
   __syncthreads();
-  BitonicSortDesc(keys, idx, m, log_m);
+  BitonicSortDesc(skeys, sidx, m, log_m);
 
-  // min lo over T and max hi over the outsiders.
+  // 2. Certification.  Member intervals in rank order go to the rescoring
+  //    tile (idle until step 3): mlo = tile[0, kk), mhi = tile[kk, 2kk).
+  float* mlo = tile;
+  float* mhi = tile + kCertMaxKeys;
   float my_min = INFINITY, my_max = -INFINITY;
+  for (int t = threadIdx.x; t < kk; t += blockDim.x) {
+    const int c = sidx[t];
+    mlo[t] = s_lo[c];
+    mhi[t] = s_hi[c];
+    my_min = fminf(my_min, s_lo[c]);
+  }
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const int cnd = idx[i];
-    if (i < kk) my_min = fminf(my_min, s_lo[cnd]);
-    else my_max = fmaxf(my_max, s_hi[cnd]);
+    if (!member[i]) my_max = fmaxf(my_max, s_hi[i]);
   }
   for (int o = 1; o < kWave; o <<= 1) {
     my_min = fminf(my_min, __shfl_xor(my_min, o, kWave));
@@ -295,40 +408,62 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
     min_t_lo = fminf(min_t_lo, s_red[0][w]);
     max_o_hi = fmaxf(max_o_hi, s_red[1][w]);
   }
-
+  // An outsider is flagged when its hi reaches the members' smallest lo; a
+  // member when its lo reaches the outsiders' largest hi or its interval
+  // meets another member's.
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const int cnd = idx[i];
-    const float l = s_lo[cnd];
-    const float h = s_hi[cnd];
-    bool flag;
-    if (i >= kk) {
-      flag = h >= min_t_lo;
-    } else {
-      flag = l <= max_o_hi;
-      for (int j = 0; j < kk && !flag; ++j) {
-        if (j == i) continue;
-        const int c2 = idx[j];
-        flag = l <= s_hi[c2] && s_lo[c2] <= h;
-      }
+    if (!member[i] && s_hi[i] >= min_t_lo) flagged[atomicAdd(&s_nflag, 1)] = i;
+  }
+  for (int t = threadIdx.x; t < kk; t += blockDim.x) {
+    const float l = mlo[t];
+    const float h = mhi[t];
+    bool flag = l <= max_o_hi;
+    for (int u = 0; u < kk && !flag; ++u) {
+      flag = (u != t) & (l <= mhi[u]) & (mlo[u] <= h);
     }
-    if (flag) flagged[atomicAdd(&s_nflag, 1)] = i;
+    if (flag) flagged[atomicAdd(&s_nflag, 1)] = sidx[t];
   }
   __syncthreads();
   const int nflag = s_nflag;
   if (nflag > 0) {
+    // 3. Exact chains for the flagged candidates, then the final order over
+    //    the members and the flagged outsiders: every other outsider's hi
+    //    is below every member's lo, so it cannot enter the top kk.
     if (threadIdx.x == 0 && exact_pages != nullptr) atomicAdd(exact_pages, nflag);
-    const int* cand = cand_ids + begin;
     RescoreChains<kSelRescoreGroup>(
-        nflag, [&](int f) { return cand[idx[flagged[f]]]; },
+        nflag, [&](int f) { return cand[flagged[f]]; },
         [&](int f, float score) {
-          const int pos = flagged[f];
-          keys[pos] = SelectKey(score, cand[idx[pos]]);
+          const int c = flagged[f];
+          keys[c] = SelectKey(score, cand[c]);
         },
         queries + static_cast<size_t>(r) * E, summaries, token_counts, capacity, E, scale, tile);
-    BitonicSortDesc(keys, idx, m, log_m);
+    if (threadIdx.x == 0) s_count = kk;
+    __syncthreads();
+    for (int t = threadIdx.x; t < kk; t += blockDim.x) skeys[t] = keys[sidx[t]];
+    for (int f = threadIdx.x; f < nflag; f += blockDim.x) {
+      const int c = flagged[f];
+      if (!member[c]) {
+        const int pos = atomicAdd(&s_count, 1);
+        skeys[pos] = keys[c];
+        sidx[pos] = c;
+      }
+    }
+    __syncthreads();
+    const int total = s_count;
+    int m2 = 1, log_m2 = 0;
+    while (m2 < total) {
+      m2 <<= 1;
+      ++log_m2;
+    }
+    for (int t = total + threadIdx.x; t < m2; t += blockDim.x) {
+      skeys[t] = 0ull;
+      sidx[t] = -1;
+    }
+    __syncthreads();
+    BitonicSortDesc(skeys, sidx, m2, log_m2);
   }
   int* out = selected + static_cast<size_t>(r) * top_k;
-  for (int i = threadIdx.x; i < kk; i += blockDim.x) out[i] = KeyPage(keys[i]);
+  for (int i = threadIdx.x; i < kk; i += blockDim.x) out[i] = KeyPage(skeys[i]);
   if (threadIdx.x == 0) counts[r] = kk;
 }
 

@@ -246,3 +246,31 @@ def test_certified_intervals_hold_on_extreme_summaries(gpu, kind):
             assert cert["selected"][r].tolist() == selected[r].tolist(), (kind, k, r)
         assert orc.max_abs_diff(cert["outputs"], outs) <= 1e-4
     pool.close()
+
+
+@pytest.mark.parametrize("query", ["zero", "random"])
+def test_certified_large_request_ties_and_duplicates(gpu, query):
+    # 700 candidates (the selection kernel for more than 256): 350 pages each
+    # listed twice.  With a zero query every score is +0, so the radix select
+    # runs down to the id bits and every interval overlaps (all rescored); with
+    # a random query the duplicates are exact ties of the same page.
+    rng = np.random.default_rng(11 if query == "zero" else 12)
+    H, D, ps, cap = 32, 128, 16, 350
+    E = H * D
+    keys = rng.standard_normal((cap, ps, E)).astype(np.float32)
+    values = rng.standard_normal((cap, ps, E)).astype(np.float32)
+    pool = gpu.DevicePagePool(H, D, ps, cap)
+    page_ids = np.arange(cap, dtype=np.int32)
+    counts = np.full(cap, ps, np.int32)
+    pool.upload_pages(page_ids, counts, page_ids.astype(np.int64) * ps * E, keys, values)
+    ids = np.concatenate([rng.permutation(cap), rng.permutation(cap)]).astype(np.int32)
+    offs = np.array([0, ids.size], np.int32)
+    q = (np.zeros((1, E)) if query == "zero" else rng.standard_normal((1, E))).astype(np.float32)
+    summ = orc.pool_summaries(keys, counts, E)
+    for k in (1, 64, 200):
+        with gpu.SparseContext(pool, k, 1, ids.size, k) as ctx:
+            res = ctx.run_batch(q, offs, ids, output_mode=gpu.OUTPUT_OUTPUTS, want_ids=True)
+        _, selected, outs = orc.sparse_batch(q, keys, values, summ, counts, offs, ids, H, D, ps, k)
+        assert res["selected"][0].tolist() == selected[0].tolist(), (query, k)
+        assert orc.max_abs_diff(res["outputs"], outs) <= 1e-4
+    pool.close()
