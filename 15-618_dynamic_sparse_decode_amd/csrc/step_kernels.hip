@@ -186,46 +186,6 @@ __global__ __launch_bounds__(256) void SelectTopKKernel(
   if (threadIdx.x == 0) counts[r] = kk;
 }
 
-// Bitonic sort of (key, idx) pairs, descending, over m = 2^log_m entries.
-// Thread i handles pair i of each stage; for strides up to 64 the pairs of
-// wave w lie in keys [128w, 128w + 128), touched by no other wave, so those
-// stages need only a wave-level sync (m <= 2 * blockDim).  A workgroup
-// barrier follows every stage that crosses waves or precedes one that does
-// (about 18 barriers at m = 2048 instead of 66).
-__device__ void BitonicSortDesc(uint64_t* keys, int* idx, int m, int log_m) {
-  const int half = m >> 1;
-  const bool pairs_in_one_pass = half <= static_cast<int>(blockDim.x);
-  auto wave_local = [&](int log_stride) { return pairs_in_one_pass && log_stride <= 6; };
-  for (int log_size = 1; log_size <= log_m; ++log_size) {
-    const int size = 1 << log_size;
-    for (int log_stride = log_size - 1; log_stride >= 0; --log_stride) {
-      const int stride = 1 << log_stride;
-      // The stage after this one (none after the last: a full barrier).
-      const bool next_local = log_stride > 0 ? wave_local(log_stride - 1)
-                                             : (log_size < log_m && wave_local(log_size));
-      for (int i = threadIdx.x; i < half; i += blockDim.x) {
-        const int lo = ((i >> log_stride) << (log_stride + 1)) | (i & (stride - 1));
-        const int hi = lo + stride;
-        const bool descending = (lo & size) == 0;
-        const uint64_t a = keys[lo];
-        const uint64_t b = keys[hi];
-        if ((a < b) == descending) {
-          keys[lo] = b;
-          keys[hi] = a;
-          const int t = idx[lo];
-          idx[lo] = idx[hi];
-          idx[hi] = t;
-        }
-      }
-      if (wave_local(log_stride) && next_local) {
-        WaveSync();
-      } else {
-        __syncthreads();
-      }
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // 2b. Certified top-k select.
 //
@@ -307,6 +267,34 @@ __device__ void RadixSelectKth(const uint64_t* keys, int n, int kk, int* hist,
   *all_out = all;
 }
 
+// (key, idx) pairs [0, count) into out_keys / out_idx in descending key
+// order, by counting: rank(i) = #{j : key_j > key_i} + #{j < i : key_j ==
+// key_i} (a permutation even with equal keys).  Cheaper than a bitonic sort
+// for the few dozen members (no stage chain); O(count^2) work in all.  Whole
+// workgroup; the outputs are complete after the closing barrier.
+__device__ void RankSortDesc(const uint64_t* keys, const int* idx, int count,
+                             uint64_t* out_keys, int* out_idx) {
+  for (int i = threadIdx.x; i < count; i += blockDim.x) {
+    const uint64_t key = keys[i];
+    int rank = 0;
+    int j = 0;
+    for (; j + 8 <= count; j += 8) {
+      uint64_t kj[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) kj[u] = keys[j + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) rank += (kj[u] > key) | ((kj[u] == key) & (j + u < i));
+    }
+    for (; j < count; ++j) {
+      const uint64_t kj = keys[j];
+      rank += (kj > key) | ((kj == key) & (j < i));
+    }
+    out_keys[rank] = key;
+    out_idx[rank] = idx[i];
+  }
+  __syncthreads();
+}
+
 __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
     const float* __restrict__ mid, const float* __restrict__ lo,
     const float* __restrict__ hi, const float* __restrict__ queries,
@@ -354,6 +342,10 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
   int need;
   bool all;
   RadixSelectKth(keys, n, kk, hist, &s_prefix, &s_need, &s_all, &shift, &prefix, &need, &all);
+  // The members, unordered, into the rescoring tile (idle until step 3),
+  // then in key order into skeys / sidx.
+  uint64_t* tkeys = reinterpret_cast<uint64_t*>(tile);
+  int* tidx = reinterpret_cast<int*>(tile + 2 * kCertMaxKeys);
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
     const uint64_t top = keys[i] >> shift;
     bool in = top > prefix;
@@ -361,22 +353,12 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
     member[i] = in ? 1 : 0;
     if (in) {
       const int pos = atomicAdd(&s_count, 1);
-      skeys[pos] = keys[i];
-      sidx[pos] = i;
+      tkeys[pos] = keys[i];
+      tidx[pos] = i;
     }
   }
   __syncthreads();
-  int m = 1, log_m = 0;
-  while (m < kk) {
-    m <<= 1;
-    ++log_m;
-  }
-  for (int t = kk + threadIdx.x; t < m; t += blockDim.x) {
-    skeys[t] = 0ull;
-    sidx[t] = -1;
-  }
-  __syncthreads();
-  BitonicSortDesc(skeys, sidx, m, log_m);
+  RankSortDesc(tkeys, tidx, kk, skeys, sidx);
 
   // 2. Certification.  Member intervals in rank order go to the rescoring
   //    tile (idle until step 3): mlo = tile[0, kk), mhi = tile[kk, 2kk).
@@ -418,8 +400,16 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
     const float l = mlo[t];
     const float h = mhi[t];
     bool flag = l <= max_o_hi;
-    for (int u = 0; u < kk && !flag; ++u) {
-      flag = (u != t) & (l <= mhi[u]) & (mlo[u] <= h);
+    // Eight independent reads per round (an early exit would serialise them).
+    for (int u0 = 0; u0 < kk && !flag; u0 += 8) {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const int u = u0 + v;
+        const bool in = u < kk;
+        const float lu = in ? mlo[u] : INFINITY;
+        const float hu = in ? mhi[u] : -INFINITY;
+        flag |= (u != t) & (l <= hu) & (lu <= h);
+      }
     }
     if (flag) flagged[atomicAdd(&s_nflag, 1)] = sidx[t];
   }
@@ -449,21 +439,11 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
       }
     }
     __syncthreads();
-    const int total = s_count;
-    int m2 = 1, log_m2 = 0;
-    while (m2 < total) {
-      m2 <<= 1;
-      ++log_m2;
-    }
-    for (int t = total + threadIdx.x; t < m2; t += blockDim.x) {
-      skeys[t] = 0ull;
-      sidx[t] = -1;
-    }
-    __syncthreads();
-    BitonicSortDesc(skeys, sidx, m2, log_m2);
+    RankSortDesc(skeys, sidx, s_count, tkeys, tidx);
   }
+  const uint64_t* final_keys = nflag > 0 ? tkeys : skeys;
   int* out = selected + static_cast<size_t>(r) * top_k;
-  for (int i = threadIdx.x; i < kk; i += blockDim.x) out[i] = KeyPage(skeys[i]);
+  for (int i = threadIdx.x; i < kk; i += blockDim.x) out[i] = KeyPage(final_keys[i]);
   if (threadIdx.x == 0) counts[r] = kk;
 }
 
