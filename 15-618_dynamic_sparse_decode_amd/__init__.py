@@ -122,6 +122,12 @@ _SIGNATURES = {
     "dsd_sparse_run_staged": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                              ctypes.c_int, _c_int_p, _c_int_p,
                                              ctypes.POINTER(StepTimings)]),
+    "dsd_sparse_run_staged_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int,
+                                                  ctypes.POINTER(ctypes.c_void_p), ctypes.c_int,
+                                                  ctypes.c_int, _c_int_p, _c_int_p,
+                                                  ctypes.POINTER(StepTimings)]),
+    "dsd_host_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
+    "dsd_host_free": (ctypes.c_int, [ctypes.c_void_p]),
     "dsd_sparse_run_batch_device": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_int] * 3
                                     + [ctypes.c_void_p] * 8),
     "dsd_sparse_replay_stage": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]),
@@ -370,6 +376,45 @@ class SparseContext:
             result["selected"] = selected
         return result
 
+    def run_staged_rows(self, query_rows, cand_offsets, cand_ids, want_ids=False,
+                        timing_mode=TIMING_NONE):
+        """Host step whose queries are read in place: query_rows[r] is the
+        address of request r's E floats inside a HostBlock (or the staging's
+        own row r).  The candidate CSR is written into the context's staging
+        first.  Returns outputs [B][E] (copied out of the staging) and, with
+        want_ids, the selected ids."""
+        offs = _i32(cand_offsets)
+        ids = _i32(cand_ids)
+        batch = len(offs) - 1
+        total = int(offs[-1]) if batch > 0 else 0
+        E = self.pool.elements
+        q_st, off_st, ids_st, out_st = (ctypes.c_void_p() for _ in range(4))
+        _check(self._lib.dsd_sparse_staging(self.handle, ctypes.byref(q_st), ctypes.byref(off_st),
+                                            ctypes.byref(ids_st), ctypes.byref(out_st)))
+        ctypes.memmove(off_st.value, offs.ctypes.data, 4 * (batch + 1))
+        if total > 0:
+            ctypes.memmove(ids_st.value, ids.ctypes.data, 4 * total)
+        rows = (ctypes.c_void_p * max(batch, 1))(*[int(p) for p in query_rows])
+        sel = np.zeros(max(1, batch * max(1, self.top_k)), np.int32)
+        counts = np.zeros(max(batch, 1), np.int32)
+        t = StepTimings()
+        _check(self._lib.dsd_sparse_run_staged_rows(
+            self.handle, batch, rows, OUTPUT_OUTPUTS, timing_mode,
+            _ptr(sel, ctypes.c_int) if want_ids else None,
+            _ptr(counts, ctypes.c_int) if want_ids else None, ctypes.byref(t)))
+        out = np.zeros((batch, E), np.float32)
+        if batch > 0:
+            ctypes.memmove(out.ctypes.data, out_st.value, 4 * batch * E)
+        result = {"outputs": out, "timings": t.as_dict(), "staging_queries": q_st.value}
+        if want_ids:
+            selected, w = [], 0
+            for r in range(batch):
+                c = int(counts[r])
+                selected.append(sel[w:w + c].copy())
+                w += c
+            result["selected"] = selected
+        return result
+
     def run_batch_device(self, batch, total_candidates, max_candidates, d_queries,
                          d_cand_offsets, d_cand_ids, d_outputs, d_scores=0, d_selected=0,
                          d_counts=0, stream=0) -> None:
@@ -398,6 +443,30 @@ class SparseContext:
 
     def replay_stage(self, stage: int, stream=0) -> None:
         _check(self._lib.dsd_sparse_replay_stage(self.handle, stage, stream or None))
+
+
+class HostBlock:
+    """Pinned host memory from dsd_host_alloc, viewed as a float32 array;
+    rows inside it may be passed to SparseContext.run_staged_rows."""
+
+    def __init__(self, count: int):
+        self._lib = load_library()
+        p = ctypes.c_void_p()
+        _check(self._lib.dsd_host_alloc(4 * count, ctypes.byref(p)))
+        self.address = p.value
+        self.array = np.ctypeslib.as_array((ctypes.c_float * count).from_address(p.value))
+
+    def close(self) -> None:
+        if self.address:
+            self.array = None
+            _check(self._lib.dsd_host_free(ctypes.c_void_p(self.address)))
+            self.address = 0
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
 
 def dense_run_batch(pool: DevicePagePool, queries, cand_offsets, cand_ids):

@@ -8,7 +8,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <memory>
+#include <mutex>
 #include <numeric>
 #include <string>
 #include <vector>
@@ -122,6 +124,43 @@ bool IsPinnedHost(const void* p) {
   }
   return attr.type == hipMemoryTypeHost;
 }
+
+// The pinned blocks handed out by dsd_host_alloc (start -> bytes), so a step
+// that reads query rows straight from host memory can check that every row
+// lies inside memory the device may read.
+class HostBlocks {
+ public:
+  static HostBlocks& Get() {
+    static HostBlocks blocks;
+    return blocks;
+  }
+  void Add(void* p, size_t bytes) {
+    std::lock_guard<std::mutex> lock(mu_);
+    blocks_[reinterpret_cast<uintptr_t>(p)] = bytes;
+  }
+  bool Remove(void* p) {
+    std::lock_guard<std::mutex> lock(mu_);
+    return blocks_.erase(reinterpret_cast<uintptr_t>(p)) == 1;
+  }
+  // Index of the first of rows[0..n) that does not lie whole inside one
+  // block, or -1 when all do.
+  int FirstOutside(const float* const* rows, int n, size_t row_bytes) {
+    std::lock_guard<std::mutex> lock(mu_);
+    for (int r = 0; r < n; ++r) {
+      const uintptr_t a = reinterpret_cast<uintptr_t>(rows[r]);
+      auto it = blocks_.upper_bound(a);
+      if (it == blocks_.begin()) return r;
+      --it;
+      const uintptr_t off = a - it->first;
+      if (off > it->second || row_bytes > it->second - off) return r;
+    }
+    return -1;
+  }
+
+ private:
+  std::mutex mu_;
+  std::map<uintptr_t, size_t> blocks_;
+};
 
 // memcpy on the host threads, in pieces of kStagePieceBytes.
 void ParallelCopy(void* dst, const void* src, size_t bytes) {
@@ -768,6 +807,7 @@ struct dsd_sparse_ctx {
   PinnedBuffer<float> h_queries, h_scores, h_outputs;
   PinnedBuffer<int> h_offsets, h_ids, h_selected, h_counts, h_fail;
   PinnedBuffer<unsigned long long> h_stamps;
+  PinnedBuffer<const float*> h_rows;  // row pointers of a row-gather step
   int stamp_grid = 0;  // workgroups stamped by the last timed fused launch
 
   struct Launch {
@@ -986,6 +1026,7 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     // The host step's staging: the step's kernels read the inputs from here
     // and write the outputs here directly (no DMA copies).
     ctx->h_queries.Reserve(B * E, hipHostMallocCoherent);
+    ctx->h_rows.Reserve(B, hipHostMallocCoherent);
     ctx->h_outputs.Reserve(B * E, hipHostMallocCoherent);
     ctx->h_scores.Reserve(P);
     ctx->h_offsets.Reserve(B + 1, hipHostMallocCoherent);
@@ -1013,11 +1054,13 @@ namespace {
 
 // One host-buffer step.  Inputs are copied into the context's pinned
 // staging unless `staged` (the caller wrote them there); outputs land in the
-// pinned staging and are copied to `outputs` when it is non-null.
+// pinned staging and are copied to `outputs` when it is non-null.  With
+// `rows`, request r's query is read from rows[r] (pinned memory the device
+// reads directly) instead of from `queries`.
 void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
-              const int* cand_offsets, const int* cand_ids, int output_mode, int timing_mode,
-              float* outputs, float* scores, int* selected, int* selected_counts,
-              dsd_step_timings* timings) {
+              const float* const* rows, const int* cand_offsets, const int* cand_ids,
+              int output_mode, int timing_mode, float* outputs, float* scores, int* selected,
+              int* selected_counts, dsd_step_timings* timings) {
     Require(ctx != nullptr, "context must be non-null");
     Require(batch >= 0, "batch must be non-negative");
     Require(output_mode >= DSD_OUTPUT_NONE && output_mode <= DSD_OUTPUT_DEBUG,
@@ -1025,7 +1068,8 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
     dsd_step_timings t{};
     if (timings != nullptr) *timings = t;
     if (batch == 0) return;
-    Require(queries != nullptr && cand_offsets != nullptr, "inputs must be non-null");
+    Require((queries != nullptr || rows != nullptr) && cand_offsets != nullptr,
+            "inputs must be non-null");
     const bool want_outputs = output_mode != DSD_OUTPUT_NONE;
     const bool debug = output_mode == DSD_OUTPUT_DEBUG;
     // Ids are returned in debug mode, or in outputs mode when buffers are given.
@@ -1063,12 +1107,37 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
     }
     if (total > 0) Require(cand_ids != nullptr, "cand_ids must be non-null");
     for (int c = 0; c < total; ++c) ctx->pool->ValidatePage(cand_ids[c]);
+    if (rows != nullptr) {
+      // Each row: non-null, 16-byte aligned, and inside a dsd_host_alloc
+      // block or the context's own query staging (its row r).
+      Require(E % 4 == 0, "query rows need a multiple of 4 elements");
+      const size_t row_bytes = sizeof(float) * static_cast<size_t>(E);
+      for (int r = 0; r < batch; ++r) {
+        Require(rows[r] != nullptr, "query rows must be non-null");
+        Require(reinterpret_cast<uintptr_t>(rows[r]) % 16 == 0,
+                "query rows must be 16-byte aligned");
+      }
+      std::vector<const float*> foreign;
+      std::vector<int> foreign_at;
+      for (int r = 0; r < batch; ++r) {
+        if (rows[r] != ctx->h_queries.ptr + static_cast<size_t>(r) * E) {
+          foreign.push_back(rows[r]);
+          foreign_at.push_back(r);
+        }
+      }
+      const int bad = HostBlocks::Get().FirstOutside(foreign.data(),
+                                                     static_cast<int>(foreign.size()), row_bytes);
+      if (bad >= 0) {
+        throw std::invalid_argument("query row " + std::to_string(foreign_at[bad]) +
+                                    " is not in dsd_host_alloc memory");
+      }
+    }
 
     // Host -> device through pinned staging.
     auto t0 = Clock::now();
     const size_t qn = static_cast<size_t>(batch) * E;
     if (!staged) {
-      std::memcpy(ctx->h_queries.ptr, queries, sizeof(float) * qn);
+      if (rows == nullptr) std::memcpy(ctx->h_queries.ptr, queries, sizeof(float) * qn);
       std::memcpy(ctx->h_offsets.ptr, cand_offsets, sizeof(int) * (batch + 1));
       if (total > 0) std::memcpy(ctx->h_ids.ptr, cand_ids, sizeof(int) * total);
     }
@@ -1077,16 +1146,25 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
       // One kernel on the step's stream copies the staged inputs to the
       // device: DMA copies would each cost a copy-engine hand-off.
       dsdk::StageSegments seg;
-      seg.src[0] = reinterpret_cast<const uint32_t*>(ctx->h_queries.ptr);
-      seg.dst[0] = reinterpret_cast<uint32_t*>(ctx->d_queries.ptr);
-      seg.words[0] = static_cast<int>(qn);
-      seg.src[1] = reinterpret_cast<const uint32_t*>(ctx->h_offsets.ptr);
-      seg.dst[1] = reinterpret_cast<uint32_t*>(ctx->d_offsets.ptr);
-      seg.words[1] = batch + 1;
-      seg.src[2] = reinterpret_cast<const uint32_t*>(ctx->h_ids.ptr);
-      seg.dst[2] = reinterpret_cast<uint32_t*>(ctx->d_ids.ptr);
-      seg.words[2] = total;
-      seg.count = 3;
+      seg.src[0] = reinterpret_cast<const uint32_t*>(ctx->h_offsets.ptr);
+      seg.dst[0] = reinterpret_cast<uint32_t*>(ctx->d_offsets.ptr);
+      seg.words[0] = batch + 1;
+      seg.src[1] = reinterpret_cast<const uint32_t*>(ctx->h_ids.ptr);
+      seg.dst[1] = reinterpret_cast<uint32_t*>(ctx->d_ids.ptr);
+      seg.words[1] = total;
+      seg.count = 2;
+      if (rows != nullptr) {
+        std::memcpy(ctx->h_rows.ptr, rows, sizeof(const float*) * batch);
+        seg.rows = ctx->h_rows.ptr;
+        seg.rows_dst = ctx->d_queries.ptr;
+        seg.nrows = batch;
+        seg.row_words = E;
+      } else {
+        seg.src[2] = reinterpret_cast<const uint32_t*>(ctx->h_queries.ptr);
+        seg.dst[2] = reinterpret_cast<uint32_t*>(ctx->d_queries.ptr);
+        seg.words[2] = static_cast<int>(qn);
+        seg.count = 3;
+      }
       dsdk::LaunchStageIn(seg, ctx->stream);
     }
     t.h2d_ms = MsSince(t0);
@@ -1173,8 +1251,8 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
                          float* scores, int* selected, int* selected_counts,
                          dsd_step_timings* timings) {
   return Guard([&] {
-    HostStep(ctx, batch, false, queries, cand_offsets, cand_ids, output_mode, timing_mode,
-             outputs, scores, selected, selected_counts, timings);
+    HostStep(ctx, batch, false, queries, nullptr, cand_offsets, cand_ids, output_mode,
+             timing_mode, outputs, scores, selected, selected_counts, timings);
   });
 }
 
@@ -1194,8 +1272,42 @@ int dsd_sparse_run_staged(dsd_sparse_ctx* ctx, int batch, int output_mode, int t
   return Guard([&] {
     Require(ctx != nullptr, "context must be non-null");
     Require(output_mode != DSD_OUTPUT_DEBUG, "the staged step has no debug mode");
-    HostStep(ctx, batch, true, ctx->h_queries.ptr, ctx->h_offsets.ptr, ctx->h_ids.ptr,
+    HostStep(ctx, batch, true, ctx->h_queries.ptr, nullptr, ctx->h_offsets.ptr,
+             ctx->h_ids.ptr, output_mode, timing_mode, nullptr, nullptr, selected,
+             selected_counts, timings);
+  });
+}
+
+int dsd_sparse_run_staged_rows(dsd_sparse_ctx* ctx, int batch, const float* const* query_rows,
+                               int output_mode, int timing_mode, int* selected,
+                               int* selected_counts, dsd_step_timings* timings) {
+  return Guard([&] {
+    Require(ctx != nullptr, "context must be non-null");
+    Require(output_mode != DSD_OUTPUT_DEBUG, "the staged step has no debug mode");
+    if (batch > 0) Require(query_rows != nullptr, "query_rows must be non-null");
+    Require(batch <= ctx->max_batch, "request batch exceeds sparse context capacity");
+    HostStep(ctx, batch, true, nullptr, query_rows, ctx->h_offsets.ptr, ctx->h_ids.ptr,
              output_mode, timing_mode, nullptr, nullptr, selected, selected_counts, timings);
+  });
+}
+
+int dsd_host_alloc(size_t bytes, void** out) {
+  return Guard([&] {
+    Require(out != nullptr, "out must be non-null");
+    Require(bytes > 0, "bytes must be positive");
+    *out = nullptr;
+    void* p = nullptr;
+    DSD_HIP_CHECK(hipHostMalloc(&p, bytes, hipHostMallocCoherent));
+    HostBlocks::Get().Add(p, bytes);
+    *out = p;
+  });
+}
+
+int dsd_host_free(void* p) {
+  return Guard([&] {
+    if (p == nullptr) return;
+    Require(HostBlocks::Get().Remove(p), "pointer was not returned by dsd_host_alloc");
+    DSD_HIP_CHECK(hipHostFree(p));
   });
 }
 

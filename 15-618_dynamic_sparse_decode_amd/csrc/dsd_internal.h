@@ -74,12 +74,18 @@ void LaunchMarkFree(const PoolView& pool, const int* d_page_ids, int n,
 
 // Up to four segments of 4-byte words, each 16-byte aligned at both ends of
 // the copy: src in pinned host memory the device reads directly, dst in
-// device memory.
+// device memory.  Optionally also a row gather: nrows rows of row_words
+// words (a multiple of 4), row r from rows[r] (a device-visible table of
+// device-visible, 16-byte aligned pointers) to rows_dst + r * row_words.
 struct StageSegments {
   const uint32_t* src[4] = {};
   uint32_t* dst[4] = {};
   int words[4] = {};
   int count = 0;
+  const float* const* rows = nullptr;
+  float* rows_dst = nullptr;
+  int nrows = 0;
+  int row_words = 0;
 };
 void LaunchStageIn(const StageSegments& s, hipStream_t stream);
 

@@ -203,32 +203,84 @@ std::vector<PageId> AdmitPrompt(const ModelConfig& c, const ContinuousRequestSpe
   throw std::invalid_argument("unknown prompt admission mode");
 }
 
-struct DecodePayloads {
-  std::vector<std::vector<float>> next_queries, keys, values;
+// Pinned host memory from dsd_host_alloc: the device reads rows in it
+// directly, so a step can take its queries in place.
+class PinnedFloats {
+ public:
+  PinnedFloats() = default;
+  explicit PinnedFloats(std::size_t count) {
+    if (count == 0) return;
+    void* p = nullptr;
+    detail::ThrowOnError(dsd_host_alloc(sizeof(float) * count, &p));
+    ptr_ = static_cast<float*>(p);
+  }
+  PinnedFloats(PinnedFloats&& o) noexcept : ptr_(o.ptr_) { o.ptr_ = nullptr; }
+  PinnedFloats& operator=(PinnedFloats&& o) noexcept {
+    std::swap(ptr_, o.ptr_);
+    return *this;
+  }
+  PinnedFloats(const PinnedFloats&) = delete;
+  PinnedFloats& operator=(const PinnedFloats&) = delete;
+  ~PinnedFloats() {
+    if (ptr_ != nullptr) (void)dsd_host_free(ptr_);
+  }
+  float* data() const { return ptr_; }
+
+ private:
+  float* ptr_ = nullptr;
 };
 
+// The precomputed payloads (src/continuous_batching.cpp:272-300, :444-454): every
+// request's next-step queries in one pinned block, request i's rows from
+// query_row0[i] on, and the appended keys / values per request.
+struct DecodePayloads {
+  PinnedFloats queries;
+  std::vector<std::size_t> query_row0;
+  std::vector<std::vector<float>> keys, values;
+  const float* NextQuery(std::size_t spec, int step, int E) const {
+    return queries.data() + (query_row0[spec] + static_cast<std::size_t>(step)) *
+                                static_cast<std::size_t>(E);
+  }
+};
+
+// Every vector has its own seed, so the host threads form the requests'
+// payloads in any order with the reference's values.
 DecodePayloads BuildPayloads(const ModelConfig& c,
                              const std::vector<ContinuousRequestSpec>& specs, bool kv) {
   const int E = Ept(c);
   DecodePayloads p;
-  p.next_queries.resize(specs.size());
+  p.query_row0.resize(specs.size());
+  std::size_t rows = 0;
+  for (std::size_t i = 0; i < specs.size(); ++i) {
+    p.query_row0[i] = rows;
+    rows += static_cast<std::size_t>(std::max(0, specs[i].decode_steps));
+  }
+  p.queries = PinnedFloats(rows * static_cast<std::size_t>(E));
   if (kv) {
     p.keys.resize(specs.size());
     p.values.resize(specs.size());
   }
-  for (std::size_t i = 0; i < specs.size(); ++i) {
-    const auto& s = specs[i];
+  const std::size_t row_bytes = sizeof(float) * static_cast<std::size_t>(E);
+  dsd_host::Workers::Get().ParallelFor(static_cast<int>(specs.size()), [&](int i) {
+    const auto& s = specs[static_cast<std::size_t>(i)];
+    const std::size_t steps = static_cast<std::size_t>(std::max(0, s.decode_steps));
+    if (kv) {
+      p.keys[static_cast<std::size_t>(i)].resize(steps * static_cast<std::size_t>(E));
+      p.values[static_cast<std::size_t>(i)].resize(steps * static_cast<std::size_t>(E));
+    }
     for (int step = 0; step < s.decode_steps; ++step) {
-      auto q = TokenVector(E, s.request_id, step + 1, 0);
-      p.next_queries[i].insert(p.next_queries[i].end(), q.begin(), q.end());
+      const auto q = TokenVector(E, s.request_id, step + 1, 0);
+      std::memcpy(const_cast<float*>(p.NextQuery(static_cast<std::size_t>(i), step, E)),
+                  q.data(), row_bytes);
       if (kv) {
-        auto k = TokenVector(E, s.request_id, step, 1);
-        auto v = TokenVector(E, s.request_id, step, 2);
-        p.keys[i].insert(p.keys[i].end(), k.begin(), k.end());
-        p.values[i].insert(p.values[i].end(), v.begin(), v.end());
+        const std::size_t at = static_cast<std::size_t>(step) * static_cast<std::size_t>(E);
+        const auto k = TokenVector(E, s.request_id, step, 1);
+        const auto v = TokenVector(E, s.request_id, step, 2);
+        std::memcpy(p.keys[static_cast<std::size_t>(i)].data() + at, k.data(), row_bytes);
+        std::memcpy(p.values[static_cast<std::size_t>(i)].data() + at, v.data(), row_bytes);
       }
     }
-  }
+  });
   return p;
 }
 
@@ -237,8 +289,9 @@ const float* Row(const std::vector<float>& v, int step, int E) {
 }
 
 // An active request of the sparse loop: the reference's state plus where
-// its next query lives (a payload-store row, or its own buffer), so a step
-// writes each query once, straight into the context's pinned staging.
+// its next query lives: a row of the pinned payload store, which the step
+// reads in place, or its own buffer, which the step copies into the
+// context's pinned staging.
 struct LiveRequest {
   ActiveDecodeRequest a;
   const float* query = nullptr;  // payload-store row when !own
@@ -249,12 +302,14 @@ struct LiveRequest {
 
 // One RunBatch of the loop in the outputs / no-outputs modes, on the C ABI:
 // PackSparseBatchInto's checks and layout written into the pinned staging
-// (queries from their rows, candidate lists from the cache), the step, and
-// the same timings RunBatch reports.  Outputs stay in the staging.
+// (candidate lists from the cache; queries that live in the pinned payload
+// store are read in place, the others copied into the staging), the step,
+// and the same timings RunBatch reports.  Outputs stay in the staging.
 SparseBatchCudaResult StagedStep(SparseCudaContext& ctx, const PagedKvCache& cache,
                                  const std::vector<LiveRequest>& active, int E, int top_k,
                                  int max_batch, int max_candidates, int max_selected,
-                                 const SparseRunBatchOptions& run) {
+                                 const SparseRunBatchOptions& run,
+                                 std::vector<const float*>* rows) {
   using detail::ThrowOnError;
   SparseBatchCudaResult result;
   const auto t0 = Clock::now();
@@ -279,9 +334,18 @@ SparseBatchCudaResult StagedStep(SparseCudaContext& ctx, const PagedKvCache& cac
   ThrowOnError(dsd_sparse_staging(ctx.handle(), &queries, &offsets, &ids, nullptr));
   offsets[0] = 0;
   int at = 0;
+  bool in_place = false;
+  rows->resize(static_cast<std::size_t>(B));
   for (int b = 0; b < B; ++b) {
     const LiveRequest& l = active[static_cast<std::size_t>(b)];
-    std::memcpy(queries + static_cast<std::size_t>(b) * E, l.Query(), sizeof(float) * E);
+    float* row = queries + static_cast<std::size_t>(b) * E;
+    if (l.own) {
+      std::memcpy(row, l.query_buf.data(), sizeof(float) * E);
+      (*rows)[static_cast<std::size_t>(b)] = row;
+    } else {
+      (*rows)[static_cast<std::size_t>(b)] = l.query;
+      in_place = true;
+    }
     const auto& pages = cache.GetRequestPages(l.a.state.request_id);
     const int n = static_cast<int>(pages.size());
     if (n > 0) std::memcpy(ids + at, pages.data(), sizeof(int) * n);
@@ -292,10 +356,15 @@ SparseBatchCudaResult StagedStep(SparseCudaContext& ctx, const PagedKvCache& cac
   const bool timing = run.timing_mode == SparseBatchTimingMode::kKernelEvents;
   const bool outputs = run.output_mode != SparseBatchOutputMode::kNoOutputs;
   dsd_step_timings t{};
-  ThrowOnError(dsd_sparse_run_staged(ctx.handle(), B,
-                                     outputs ? DSD_OUTPUT_OUTPUTS : DSD_OUTPUT_NONE,
-                                     timing ? DSD_TIMING_EVENTS : DSD_TIMING_NONE, nullptr,
-                                     nullptr, &t));
+  const int out_mode = outputs ? DSD_OUTPUT_OUTPUTS : DSD_OUTPUT_NONE;
+  const int time_mode = timing ? DSD_TIMING_EVENTS : DSD_TIMING_NONE;
+  if (in_place) {
+    ThrowOnError(dsd_sparse_run_staged_rows(ctx.handle(), B, rows->data(), out_mode, time_mode,
+                                            nullptr, nullptr, &t));
+  } else {
+    ThrowOnError(dsd_sparse_run_staged(ctx.handle(), B, out_mode, time_mode, nullptr, nullptr,
+                                       &t));
+  }
   if (timing) {
     result.aggregate_timings.page_scoring_ms = t.score_ms;
     result.aggregate_timings.topk_ms = t.topk_ms;
@@ -432,6 +501,7 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
   std::deque<std::size_t> pending;
   std::vector<LiveRequest> active;
   active.reserve(static_cast<std::size_t>(options.max_active_requests));
+  std::vector<const float*> step_rows;
   std::vector<const RequestState*> batch;
   std::vector<std::uint8_t> admitted(specs.size(), 0);
   const bool debug_outputs = options.run_batch_output_mode == SparseBatchOutputMode::kDebugTensors;
@@ -504,7 +574,8 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
       result = ctx.RunBatch(batch, run);
     } else {
       result = StagedStep(ctx, cache, active, E, config.top_k_pages,
-                          options.max_active_requests, max_candidates, max_selected, run);
+                          options.max_active_requests, max_candidates, max_selected, run,
+                          &step_rows);
     }
     const double ms = Ms(t_step, Clock::now());
     stats.run_batch_wall_ms += ms;
@@ -580,7 +651,7 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
       // The next step's query; its candidate list is the cache's page list,
       // read when the step is staged.
       if (options.precompute_decode_payloads) {
-        l.query = Row(payloads.next_queries[a.spec_index], dstep, E);
+        l.query = payloads.NextQuery(a.spec_index, dstep, E);
         l.own = false;
       } else {
         l.own = true;  // query_buf already holds it (generated above)
@@ -746,7 +817,7 @@ ContinuousBatchStats RunContinuousDenseGpuDecode(
       const auto& pages = cache.GetRequestPages(id);
       a.state.candidate_page_ids.assign(pages.begin(), pages.end());
       if (options.precompute_decode_payloads) {
-        const float* q = Row(payloads.next_queries[a.spec_index], dstep, E);
+        const float* q = payloads.NextQuery(a.spec_index, dstep, E);
         a.state.query.assign(q, q + E);
       } else {
         a.state.query = std::move(gen_q[ai]);

@@ -272,6 +272,23 @@ __global__ __launch_bounds__(kPoolThreads) void StageInKernel(StageSegments s) {
     for (int i = tid; i < n4; i += stride) dst4[i] = src4[i];
     for (int i = 4 * n4 + tid; i < words; i += stride) s.dst[k][i] = s.src[k][i];
   }
+  if (s.nrows > 0) {
+    // One chunk of blockDim.x float4s per workgroup turn, so each workgroup
+    // reads its row pointer once (a uniform load) and the rows stream
+    // straight from host memory.
+    const int per_row = s.row_words / 4;
+    const int chunks = (per_row + kPoolThreads - 1) / kPoolThreads;
+    const int items = s.nrows * chunks;
+    for (int item = static_cast<int>(blockIdx.x); item < items;
+         item += static_cast<int>(gridDim.x)) {
+      const int row = item / chunks;
+      const int i = (item - row * chunks) * kPoolThreads + static_cast<int>(threadIdx.x);
+      if (i < per_row) {
+        const float4* src = reinterpret_cast<const float4*>(s.rows[row]);
+        reinterpret_cast<float4*>(s.rows_dst)[static_cast<size_t>(row) * per_row + i] = src[i];
+      }
+    }
+  }
 }
 
 void LaunchStageIn(const StageSegments& s, hipStream_t stream) {
@@ -283,8 +300,21 @@ void LaunchStageIn(const StageSegments& s, hipStream_t stream) {
     }
     words += static_cast<size_t>(s.words[k]);
   }
+  if (s.nrows > 0) {
+    if (s.rows == nullptr || s.rows_dst == nullptr || s.row_words % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(s.rows_dst) % 16 != 0) {
+      throw std::invalid_argument("row gather needs 16-byte aligned rows of 4k words");
+    }
+    words += static_cast<size_t>(s.nrows) * static_cast<size_t>(s.row_words);
+  }
   if (words == 0) return;
-  const size_t groups = std::min<size_t>((words / 4 + kPoolThreads - 1) / kPoolThreads + 1, 256);
+  size_t groups = (words / 4 + kPoolThreads - 1) / kPoolThreads + 1;
+  if (s.nrows > 0) {
+    const size_t per_row = static_cast<size_t>(s.row_words) / 4;
+    groups = std::max(groups, static_cast<size_t>(s.nrows) *
+                                  ((per_row + kPoolThreads - 1) / kPoolThreads));
+  }
+  groups = std::min<size_t>(groups, 256);
   hipLaunchKernelGGL(StageInKernel, dim3(static_cast<unsigned>(groups)), dim3(kPoolThreads), 0,
                      stream, s);
   DSD_HIP_CHECK(hipGetLastError());

@@ -231,6 +231,28 @@ int dsd_sparse_run_staged(dsd_sparse_ctx* ctx, int batch, int output_mode,
                           int timing_mode, int* selected, int* selected_counts,
                           dsd_step_timings* timings);
 
+/* dsd_sparse_run_staged with request r's query read from query_rows[r]
+ * (E floats) instead of the staging's queries; the candidate lists come
+ * from the staging as before.  Every row must be 16-byte aligned and lie
+ * inside a dsd_host_alloc block, or be the staging's own row r; anything
+ * else fails with DSD_ERR_INVALID_ARGUMENT before any work.  The rows are
+ * read by the device directly (no host copy), and the call returns after
+ * the step, so they may change once it has returned.
+ * No reference counterpart: lets a serving loop that keeps its queries in
+ * pinned memory skip the per-step packing copy (the reference packs into
+ * host vectors, src/cuda/sparse_batched_attention.cu:24-96). */
+int dsd_sparse_run_staged_rows(dsd_sparse_ctx* ctx, int batch,
+                               const float* const* query_rows, int output_mode,
+                               int timing_mode, int* selected, int* selected_counts,
+                               dsd_step_timings* timings);
+
+/* Pinned host memory the device reads directly (coherent, so rows written
+ * by the host between steps are seen by the next step).  dsd_host_free
+ * takes only pointers from dsd_host_alloc (NULL is a no-op).  No reference
+ * counterpart: the memory behind dsd_sparse_run_staged_rows. */
+int dsd_host_alloc(size_t bytes, void** out);
+int dsd_host_free(void* p);
+
 /* Device-resident step: every pointer is device memory and the call only
  * enqueues work on `stream` (a hipStream_t; NULL = the context's stream).
  * total_candidates and max_candidates (largest n_r) must describe the CSR.

@@ -64,6 +64,18 @@ def test_invalid_arguments_are_checked_before_the_device(dsd):
         dsd.DevicePagePool(0, 4, 4, 4)
 
 
+def test_host_free_takes_only_its_own_blocks(dsd):
+    import ctypes
+    lib = dsd.load_library()
+    assert lib.dsd_host_free(None) == 0
+    buf = ctypes.create_string_buffer(64)
+    assert lib.dsd_host_free(ctypes.cast(buf, ctypes.c_void_p)) == 1  # invalid_argument
+    assert b"dsd_host_alloc" in lib.dsd_last_error()
+    out = ctypes.c_void_p()
+    assert lib.dsd_host_alloc(0, ctypes.byref(out)) == 1
+    assert lib.dsd_host_alloc(16, None) == 1
+
+
 CPP_LIB = ROOT / "15-618_dynamic_sparse_decode_amd" / "build" / "libdsd.so"
 
 

@@ -255,3 +255,71 @@ def test_device_resident_step_matches_host_step(gpu):
     got = sel.cpu().numpy()
     for r in range(batch.batch):
         assert got[r, :counts[r].item()].tolist() == host["selected"][r].tolist()
+
+
+def test_staged_rows_step_matches_host_step(gpu):
+    """Queries read in place from pinned rows (dsd_sparse_run_staged_rows)
+    give the host step's outputs and ids bit for bit: rows scattered over a
+    dsd_host_alloc block, one row taken from the staging itself, and a
+    second, smaller step after the first."""
+    import ctypes
+    lengths = gpu.reference_context_lengths(16, 512, 2048, 7)
+    batch = gpu.SyntheticBatch(32, 128, 16, lengths, seed=5)
+    pool = gpu.DevicePagePool(32, 128, 16, batch.capacity)
+    batch.upload(pool)
+    B, E = batch.batch, 32 * 128
+    q = batch.queries.reshape(B, E)
+    sel_total = selected_total(batch.cand_offsets, 8)
+    perm = np.random.default_rng(1).permutation(2 * B)[:B]
+    with gpu.SparseContext(pool, 8, B, batch.total_candidates, sel_total) as ctx, \
+            gpu.HostBlock(2 * B * E) as block:
+        host = ctx.run_batch(batch.queries, batch.cand_offsets, batch.cand_ids,
+                             output_mode=gpu.OUTPUT_OUTPUTS, want_ids=True)
+        rows = []
+        for r in range(B):
+            block.array[perm[r] * E:(perm[r] + 1) * E] = q[r]
+            rows.append(block.address + 4 * int(perm[r]) * E)
+        staging_q = ctx.run_staged_rows(rows[:1], batch.cand_offsets[:2],
+                                        batch.cand_ids[:batch.cand_offsets[1]])["staging_queries"]
+        ctypes.memmove(staging_q + 4 * 3 * E, q[3].ctypes.data, 4 * E)
+        rows[3] = staging_q + 4 * 3 * E
+        got = ctx.run_staged_rows(rows, batch.cand_offsets, batch.cand_ids, want_ids=True)
+        assert np.array_equal(got["outputs"].view(np.uint32),
+                              host["outputs"].reshape(B, E).view(np.uint32))
+        for r in range(B):
+            assert got["selected"][r].tolist() == host["selected"][r].tolist()
+        # a smaller step: the last five requests, rows in reverse block order
+        sub = slice(B - 5, B)
+        offs = batch.cand_offsets[B - 5:] - batch.cand_offsets[B - 5]
+        ids = batch.cand_ids[batch.cand_offsets[B - 5]:]
+        small = ctx.run_staged_rows(rows[sub], offs, ids, want_ids=True)
+        assert np.array_equal(small["outputs"].view(np.uint32),
+                              host["outputs"].reshape(B, E)[sub].view(np.uint32))
+        for i in range(5):
+            assert small["selected"][i].tolist() == host["selected"][B - 5 + i].tolist()
+
+
+def test_staged_rows_are_checked_before_the_device(gpu):
+    lengths = [64, 96]
+    batch = gpu.SyntheticBatch(2, 64, 16, lengths, seed=2)
+    pool = gpu.DevicePagePool(2, 64, 16, batch.capacity)
+    batch.upload(pool)
+    E = 2 * 64
+    with gpu.SparseContext(pool, 2, 2, batch.total_candidates, 4) as ctx, \
+            gpu.HostBlock(2 * E) as block:
+        base = block.address
+        cases = [
+            ([base, batch.queries.ctypes.data], "not in dsd_host_alloc"),   # pageable memory
+            ([base, base + 4], "aligned"),                                 # misaligned
+            ([base, base + 4 * (E + 4)], "not in dsd_host_alloc"),          # runs past the end
+            ([base, 0], "non-null"),
+        ]
+        for rows, msg in cases:
+            with pytest.raises(gpu.InvalidArgument, match=msg):
+                ctx.run_staged_rows(rows, batch.cand_offsets, batch.cand_ids)
+        block.array[:] = batch.queries.reshape(-1)
+        ok = ctx.run_staged_rows([base, base + 4 * E], batch.cand_offsets, batch.cand_ids)
+        ref = ctx.run_batch(batch.queries, batch.cand_offsets, batch.cand_ids,
+                            output_mode=gpu.OUTPUT_OUTPUTS)
+        assert np.array_equal(ok["outputs"].view(np.uint32),
+                              ref["outputs"].reshape(2, E).view(np.uint32))
