@@ -185,7 +185,6 @@ struct dsd_pool {
   hipStream_t stream = nullptr;
   // staging for metadata / token uploads
   DeviceBuffer<int> stage_ids, stage_counts, stage_offsets, stage_order, stage_segs;
-  DeviceBuffer<int> stage_req, stage_steps;
   DeviceBuffer<float> stage_rows, stage_keys, stage_values;
   // dense-path scratch: device inputs, and coherent pinned staging that the
   // stage-in kernel reads and the attention writes its outputs into
@@ -237,6 +236,11 @@ struct dsd_pool {
     } else {
       DSD_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream));
     }
+    CountH2D(bytes);
+  }
+  // One host -> device transfer of the reference's accounting
+  // (src/device_page_pool.cpp:1137-1150).
+  void CountH2D(size_t bytes) {
     stats.h2d_bytes += bytes;
     ++stats.h2d_calls;
     if (bytes >= kLargeCopyBytes) ++stats.h2d_large_calls;
@@ -278,9 +282,10 @@ struct dsd_pool {
       pending = false;
     }
   }
-  // Work enqueued on another stream starts after an enqueued append.
+  // Work enqueued on another stream starts after an enqueued append (on
+  // the pool's own stream, stream order does it).
   void OrderAfterPending(hipStream_t s) const {
-    if (pending) DSD_HIP_CHECK(hipStreamWaitEvent(s, done, 0));
+    if (pending && s != stream) DSD_HIP_CHECK(hipStreamWaitEvent(s, done, 0));
   }
 
   void ValidatePage(int page_id) const {
@@ -731,37 +736,26 @@ int dsd_pool_append_synthetic(dsd_pool* pool, int n, const int* page_ids,
       pool->host_counts[page_ids[q]] = page_token_counts[q];
       pool->host_live[page_ids[q]] = 1;
     }
-    pool->stage_ids.Reserve(n);
-    pool->stage_offsets.Reserve(n);
-    pool->stage_counts.Reserve(n);
-    pool->stage_order.Reserve(n);
-    pool->stage_segs.Reserve(nseg + 1);
-    pool->stage_req.Reserve(n);
-    pool->stage_steps.Reserve(n);
-    // The metadata goes through pinned staging (the previous append's copies
-    // have finished: WaitPending above), and the call returns once the work
-    // is enqueued.
+    // The metadata goes into coherent pinned staging that the kernel reads
+    // directly (the previous append has finished with it: WaitPending
+    // above): segment starts, then the tokens' five fields in page / offset
+    // order.  The call returns once the kernel is enqueued.  The transfer
+    // count is the reference's: five copies of n ints.
     const size_t un = static_cast<size_t>(n);
-    pool->h_meta.Reserve(6 * un + static_cast<size_t>(nseg) + 1);
+    pool->h_meta.Reserve(5 * un + static_cast<size_t>(nseg) + 1, hipHostMallocCoherent);
     int* m = pool->h_meta.ptr;
-    std::memcpy(m + 0 * un, page_ids, sizeof(int) * un);
-    std::memcpy(m + 1 * un, token_offsets, sizeof(int) * un);
-    std::memcpy(m + 2 * un, page_token_counts, sizeof(int) * un);
-    std::memcpy(m + 3 * un, order.data(), sizeof(int) * un);
-    std::memcpy(m + 4 * un, request_ids, sizeof(int) * un);
-    std::memcpy(m + 5 * un, decode_steps, sizeof(int) * un);
-    std::memcpy(m + 6 * un, segs.data(), sizeof(int) * (static_cast<size_t>(nseg) + 1));
-    pool->H2D(pool->stage_ids.ptr, m + 0 * un, sizeof(int) * un);
-    pool->H2D(pool->stage_offsets.ptr, m + 1 * un, sizeof(int) * un);
-    pool->H2D(pool->stage_counts.ptr, m + 2 * un, sizeof(int) * un);
-    pool->H2D(pool->stage_order.ptr, m + 3 * un, sizeof(int) * un);
-    pool->H2D(pool->stage_req.ptr, m + 4 * un, sizeof(int) * un);
-    pool->H2D(pool->stage_steps.ptr, m + 5 * un, sizeof(int) * un);
-    pool->H2D(pool->stage_segs.ptr, m + 6 * un, sizeof(int) * (static_cast<size_t>(nseg) + 1));
-    dsdk::LaunchAppendSynthetic(pool->view, pool->stage_segs.ptr, pool->stage_order.ptr,
-                                pool->stage_ids.ptr, pool->stage_offsets.ptr,
-                                pool->stage_counts.ptr, pool->stage_req.ptr,
-                                pool->stage_steps.ptr, nseg, pool->stream);
+    std::memcpy(m, segs.data(), sizeof(int) * (static_cast<size_t>(nseg) + 1));
+    int* f = m + nseg + 1;
+    for (int q = 0; q < n; ++q) {
+      const int t = order[q];
+      f[q] = page_ids[t];
+      f[un + q] = token_offsets[t];
+      f[2 * un + q] = page_token_counts[t];
+      f[3 * un + q] = request_ids[t];
+      f[4 * un + q] = decode_steps[t];
+    }
+    for (int c = 0; c < 5; ++c) pool->CountH2D(sizeof(int) * un);
+    dsdk::LaunchAppendSynthetic(pool->view, m, n, nseg, pool->stream);
     DSD_HIP_CHECK(hipEventRecord(pool->done, pool->stream));
     pool->pending = true;
   });
@@ -792,7 +786,7 @@ struct dsd_sparse_ctx {
   int max_batch = 0;
   int max_cand = 0;
   int max_sel = 0;
-  hipStream_t stream = nullptr;
+  hipStream_t stream = nullptr;  // the pool's stream (not owned)
   hipEvent_t ev[6] = {};
   DeviceBuffer<float> d_queries, d_scores, d_lo, d_hi;
   DeviceBuffer<int> d_offsets, d_ids, d_selected, d_counts, d_exact_pages;
@@ -828,7 +822,6 @@ struct dsd_sparse_ctx {
     for (hipEvent_t& e : ev) {
       if (e) (void)hipEventDestroy(e);
     }
-    if (stream) (void)hipStreamDestroy(stream);
   }
 
   float Scale() const {
@@ -983,7 +976,10 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     ctx->max_batch = max_batch;
     ctx->max_cand = max_total_candidates;
     ctx->max_sel = max_total_selected;
-    DSD_HIP_CHECK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+    // Steps run on the pool's stream: stream order then places them after
+    // an enqueued append and before any later pool work, with no cross-
+    // stream waits (each costs several microseconds of host time per step).
+    ctx->stream = pool->stream;
     for (hipEvent_t& e : ctx->ev) DSD_HIP_CHECK(hipEventCreate(&e));
     const size_t E = static_cast<size_t>(pool->view.elements);
     const size_t B = static_cast<size_t>(std::max(1, max_batch));

@@ -63,10 +63,11 @@ void LaunchAppendTokens(const PoolView& pool, const int* d_seg_start,
 void LaunchPrefillSynthetic(const PoolView& pool, const int* d_page_ids,
                             const int* d_token_counts, int n, int request_id,
                             hipStream_t stream);
-void LaunchAppendSynthetic(const PoolView& pool, const int* d_seg_start, const int* d_order,
-                           const int* d_page_ids, const int* d_offsets, const int* d_counts,
-                           const int* d_request_ids, const int* d_decode_steps,
-                           int num_segments, hipStream_t stream);
+// meta: device-readable (pinned, coherent) ints, seg_start[num_segments + 1]
+// then five arrays of n in page / offset order: page ids, token offsets, page
+// token counts, request ids, decode steps.
+void LaunchAppendSynthetic(const PoolView& pool, const int* meta, int n, int num_segments,
+                           hipStream_t stream);
 
 // Clears token count, live flag and summary row of n pages.
 void LaunchMarkFree(const PoolView& pool, const int* d_page_ids, int n,

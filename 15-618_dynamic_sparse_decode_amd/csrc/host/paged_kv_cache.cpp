@@ -24,6 +24,7 @@ PagedKvCache::PagedKvCache(ModelConfig config, int capacity_pages, bool allocate
                  0.0f) {
   pages_.reserve(static_cast<std::size_t>(capacity_pages));
   for (PageId id = 0; id < capacity_pages; ++id) pages_.push_back(FreeDescriptor(id));
+  summary_written_.assign(static_cast<std::size_t>(std::max(capacity_pages, 0)), 0);
 }
 
 PageId PagedKvCache::AppendPage(int request_id, const std::vector<float>& keys,
@@ -60,9 +61,10 @@ PageId PagedKvCache::AppendPage(int request_id, const float* keys, const float* 
   const int start = NextStartToken(request_id);
   std::copy(keys, keys + n, pool_.get_k_page_ptr(id));
   std::copy(values, values + n, pool_.get_v_page_ptr(id));
+  ClearSummary(id);
   float* s = SummaryRow(id);
-  std::fill(s, s + E, 0.0f);
   if (compute_summary) {
+    summary_written_[static_cast<std::size_t>(id)] = 1;
     for (int t = 0; t < token_count; ++t) {
       const float* row = keys + static_cast<std::size_t>(t) * E;
       for (int i = 0; i < E; ++i) s[i] += row[i];
@@ -95,7 +97,7 @@ std::vector<PageId> PagedKvCache::ReservePagesForRequest(int request_id,
   const int E = ElementsPerToken();
   for (std::size_t i = 0; i < ids.size(); ++i) {
     const PageId id = ids[i];
-    std::fill(SummaryRow(id), SummaryRow(id) + E, 0.0f);
+    ClearSummary(id);
     const std::size_t offset = static_cast<std::size_t>(id) * ElementsPerPage();
     pages_[static_cast<std::size_t>(id)] =
         PageDescriptor{id, request_id, start, token_counts[i], offset, offset};
@@ -117,7 +119,7 @@ PageDescriptor& PagedKvCache::TailForAppend(int request_id, bool force_new_page,
     const std::size_t offset = static_cast<std::size_t>(id) * ElementsPerPage();
     pages_[static_cast<std::size_t>(id)] =
         PageDescriptor{id, request_id, NextStartToken(request_id), 0, offset, offset};
-    std::fill(SummaryRow(id), SummaryRow(id) + ElementsPerToken(), 0.0f);
+    ClearSummary(id);
     list.push_back(id);
     ++live_pages_;
     *allocated = true;
@@ -160,6 +162,7 @@ AppendTokenResult PagedKvCache::AppendToken(int request_id, const float* key,
   std::copy(key, key + E, pool_.get_k_page_ptr(page.id) + row);
   std::copy(value, value + E, pool_.get_v_page_ptr(page.id) + row);
   float* s = SummaryRow(page.id);
+  summary_written_[static_cast<std::size_t>(page.id)] = 1;
   const float old_count = static_cast<float>(page.token_count);
   const float new_count = old_count + 1.0f;
   for (int i = 0; i < E; ++i) s[i] = (s[i] * old_count + key[i]) / new_count;
@@ -184,6 +187,7 @@ AppendTokenResult PagedKvCache::AppendTokenMetadataOnly(int request_id, const fl
   const int E = ElementsPerToken();
   const int offset = page.token_count;
   float* s = SummaryRow(page.id);
+  summary_written_[static_cast<std::size_t>(page.id)] = 1;
   const float old_count = static_cast<float>(page.token_count);
   const float new_count = old_count + 1.0f;
   for (int i = 0; i < E; ++i) s[i] = (s[i] * old_count + key[i]) / new_count;
@@ -203,12 +207,11 @@ std::vector<PageId> PagedKvCache::ReleaseRequest(int request_id) {
   const auto it = request_pages_.find(request_id);
   if (it == request_pages_.end()) return {};
   std::vector<PageId> released = it->second;
-  const int E = ElementsPerToken();
   for (PageId id : released) {
     if (pages_[static_cast<std::size_t>(id)].request_id != request_id) {
       throw std::runtime_error("request page mapping is inconsistent");
     }
-    std::fill(SummaryRow(id), SummaryRow(id) + E, 0.0f);
+    ClearSummary(id);
     pages_[static_cast<std::size_t>(id)] = FreeDescriptor(id);
     pool_.free_page(id);
     --live_pages_;
@@ -222,6 +225,7 @@ void PagedKvCache::Reset() {
   live_pages_ = 0;
   pool_.reset_pool();
   std::fill(summaries_.begin(), summaries_.end(), 0.0f);
+  std::fill(summary_written_.begin(), summary_written_.end(), 0);
   for (PageId id = 0; id < static_cast<PageId>(pages_.size()); ++id) {
     pages_[static_cast<std::size_t>(id)] = FreeDescriptor(id);
   }
@@ -303,6 +307,16 @@ int PagedKvCache::NextStartToken(int request_id) const {
   if (it == request_pages_.end() || it->second.empty()) return 0;
   const auto& last = GetPage(it->second.back());
   return last.start_token + last.token_count;
+}
+
+// A summary row holds nonzero values only once written; rows never written
+// since their last clear are zero already, so clearing them is skipped (a
+// request released from GPU-side admission owns hundreds of such rows).
+void PagedKvCache::ClearSummary(PageId page_id) {
+  float* s = SummaryRow(page_id);
+  std::uint8_t& written = summary_written_[static_cast<std::size_t>(page_id)];
+  if (written) std::fill(s, s + ElementsPerToken(), 0.0f);
+  written = 0;
 }
 
 float* PagedKvCache::SummaryRow(PageId page_id) {

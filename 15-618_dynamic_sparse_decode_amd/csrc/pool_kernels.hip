@@ -177,37 +177,43 @@ __global__ __launch_bounds__(kPoolThreads) void PrefillSyntheticKernel(
   }
 }
 
-// One workgroup per page segment (tokens in offset order), running mean.
-__global__ __launch_bounds__(kPoolThreads) void AppendSyntheticKernel(
-    PoolView pool, const int* __restrict__ seg_start, const int* __restrict__ order,
-    const int* __restrict__ page_ids, const int* __restrict__ offsets,
-    const int* __restrict__ counts, const int* __restrict__ request_ids,
-    const int* __restrict__ decode_steps, int num_segments) {
+// One workgroup per (page segment, kPoolThreads elements of the token row):
+// the segment's tokens in offset order, summary by the running mean.  The
+// metadata is read straight from the caller's pinned staging (layout at
+// LaunchAppendSynthetic), so the append is one launch with no copies.
+__global__ __launch_bounds__(kPoolThreads) void AppendSyntheticKernel(PoolView pool,
+                                                                      const int* __restrict__ meta,
+                                                                      int n, int num_segments) {
   const int seg = blockIdx.x;
   if (seg >= num_segments) return;
-  const int begin = seg_start[seg];
-  const int end = seg_start[seg + 1];
+  const int* page_ids = meta + num_segments + 1;
+  const int* offsets = page_ids + n;
+  const int* counts = offsets + n;
+  const int* request_ids = counts + n;
+  const int* decode_steps = request_ids + n;
+  const int begin = meta[seg];
+  const int end = meta[seg + 1];
   const int E = pool.elements;
-  const int page = page_ids[order[begin]];
+  const int page = page_ids[begin];
   const size_t base = static_cast<size_t>(page) * pool.page_elems;
   float* summary = pool.summaries + static_cast<size_t>(page) * E;
-  const bool fresh = offsets[order[begin]] == 0;
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    float s = fresh ? 0.0f : summary[e];
+  const int e = static_cast<int>(blockIdx.y * kPoolThreads + threadIdx.x);
+  if (e < E) {
+    float s = offsets[begin] == 0 ? 0.0f : summary[e];
     for (int q = begin; q < end; ++q) {
-      const int tok = order[q];
-      const float k = DecodeValue(request_ids[tok], decode_steps[tok], e, 1);
-      const float v = DecodeValue(request_ids[tok], decode_steps[tok], e, 2);
-      const size_t dst = base + static_cast<size_t>(offsets[tok]) * E + e;
+      const int off = offsets[q];
+      const float k = DecodeValue(request_ids[q], decode_steps[q], e, 1);
+      const float v = DecodeValue(request_ids[q], decode_steps[q], e, 2);
+      const size_t dst = base + static_cast<size_t>(off) * E + e;
       pool.keys[dst] = k;
       pool.values[dst] = v;
-      const float old_count = static_cast<float>(offsets[tok]);
+      const float old_count = static_cast<float>(off);
       s = __fdiv_rn(__fadd_rn(__fmul_rn(s, old_count), k), __fadd_rn(old_count, 1.0f));
     }
     summary[e] = s;
   }
-  if (threadIdx.x == 0) {
-    pool.token_counts[page] = counts[order[end - 1]];
+  if (blockIdx.y == 0 && threadIdx.x == 0) {
+    pool.token_counts[page] = counts[end - 1];
     pool.live[page] = 1;
   }
 }
@@ -246,14 +252,12 @@ void LaunchPrefillSynthetic(const PoolView& pool, const int* d_page_ids,
   DSD_HIP_CHECK(hipGetLastError());
 }
 
-void LaunchAppendSynthetic(const PoolView& pool, const int* d_seg_start, const int* d_order,
-                           const int* d_page_ids, const int* d_offsets, const int* d_counts,
-                           const int* d_request_ids, const int* d_decode_steps,
-                           int num_segments, hipStream_t stream) {
+void LaunchAppendSynthetic(const PoolView& pool, const int* meta, int n, int num_segments,
+                           hipStream_t stream) {
   if (num_segments <= 0) return;
-  hipLaunchKernelGGL(AppendSyntheticKernel, dim3(num_segments), dim3(kPoolThreads), 0, stream,
-                     pool, d_seg_start, d_order, d_page_ids, d_offsets, d_counts,
-                     d_request_ids, d_decode_steps, num_segments);
+  const unsigned slices = static_cast<unsigned>((pool.elements + kPoolThreads - 1) / kPoolThreads);
+  hipLaunchKernelGGL(AppendSyntheticKernel, dim3(static_cast<unsigned>(num_segments), slices),
+                     dim3(kPoolThreads), 0, stream, pool, meta, n, num_segments);
   DSD_HIP_CHECK(hipGetLastError());
 }
 

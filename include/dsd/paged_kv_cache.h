@@ -7,6 +7,7 @@
 #pragma once
 
 #include <cstddef>
+#include <cstdint>
 #include <unordered_map>
 #include <vector>
 
@@ -84,11 +85,13 @@ class PagedKvCache {
   int NextStartToken(int request_id) const;
   float* SummaryRow(PageId page_id);
   const float* SummaryRow(PageId page_id) const;
+  void ClearSummary(PageId page_id);
 
   ModelConfig config_;
   PagePool pool_;
   std::vector<PageDescriptor> pages_;
   std::vector<float> summaries_;
+  std::vector<std::uint8_t> summary_written_;  // per page: summary row nonzero
   std::unordered_map<int, std::vector<PageId>> request_pages_;
   int live_pages_ = 0;
 };

@@ -272,7 +272,8 @@ int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
  * For per-kernel timing of the hot loop. */
 int dsd_sparse_replay_stage(dsd_sparse_ctx* ctx, int stage, void* stream);
 
-/* The context's own stream (hipStream_t). */
+/* The stream the context's host-buffer steps run on (hipStream_t): the
+ * pool's stream, so steps and pool work are ordered by the stream. */
 void* dsd_sparse_stream(dsd_sparse_ctx* ctx);
 
 /* Scoring mode (no counterpart in the reference, whose GPU scores are a

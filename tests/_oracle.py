@@ -73,6 +73,13 @@ def pool_summaries(key_pool, token_counts, elements: int, page_ids=None):
     return out
 
 
+def synthetic_decode_row(request_id: int, decode_step: int, stream: int, elements: int):
+    out = np.empty(elements, np.float32)
+    lib().oracle_synthetic_decode_row(int(request_id), int(decode_step), int(stream),
+                                      int(elements), P(out))
+    return out
+
+
 def append_summary(summary, key, old_count: int):
     s = f32(summary).copy()
     k = f32(key)

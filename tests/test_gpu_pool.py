@@ -253,3 +253,44 @@ def test_large_uploads_round_trip(gpu, pinned):
         np.testing.assert_array_equal(v, values[src_offsets[i]:src_offsets[i] + n])
     st = pool.transfer_stats()
     assert st["h2d_bytes"] >= 2 * 4 * e * sum(counts)  # keys and values, valid tokens
+
+
+@pytest.mark.parametrize("heads,head_dim", [(2, 64), (4, 96)])
+def test_synthetic_append_matches_oracle(gpu, heads, head_dim):
+    """dsd_pool_append_synthetic: K/V rows from the reference's decode hash,
+    running-mean summaries in offset order (several tokens of one page in one
+    call, given out of order, and a second call continuing the pages), page
+    counts and live flags, and the reference's transfer accounting (five
+    copies of n ints per call)."""
+    ps = 4
+    E = heads * head_dim
+    pool = gpu.DevicePagePool(heads, head_dim, ps, 8)
+    pool.reset_transfer_stats()
+    calls = [
+        # page, offset, page count after the call, request, decode step
+        [(3, 2, 3, 11, 2), (5, 0, 1, 12, 0), (3, 0, 3, 11, 0), (3, 1, 3, 11, 1)],
+        [(5, 1, 2, 12, 1), (3, 3, 4, 11, 3)],
+    ]
+    keys = {p: np.zeros((ps, E), np.float32) for p in (3, 5)}
+    vals = {p: np.zeros((ps, E), np.float32) for p in (3, 5)}
+    summ = {p: np.zeros(E, np.float32) for p in (3, 5)}
+    for toks in calls:
+        cols = list(zip(*toks))
+        pool.append_synthetic(*[np.array(c, np.int32) for c in cols])
+        for page, off, _, req, step in sorted(toks, key=lambda t: (t[0], t[1])):
+            k = orc.synthetic_decode_row(req, step, 1, E)
+            keys[page][off] = k
+            vals[page][off] = orc.synthetic_decode_row(req, step, 2, E)
+            summ[page] = orc.append_summary(summ[page], k, off)
+    st = pool.transfer_stats()
+    assert st["h2d_calls"] == 10 and st["h2d_bytes"] == 5 * 4 * (4 + 2)
+    counts, live = pool.download_meta()
+    assert counts[3] == 4 and counts[5] == 2 and live[3] == 1 and live[5] == 1
+    assert counts[[0, 1, 2, 4, 6, 7]].tolist() == [0] * 6
+    got = pool.download_summaries([3, 5])
+    for i, p in enumerate((3, 5)):
+        k, v = pool.download_page(p)
+        n = int(counts[p])
+        assert np.array_equal(k.reshape(-1, E).view(np.uint32), keys[p][:n].view(np.uint32))
+        assert np.array_equal(v.reshape(-1, E).view(np.uint32), vals[p][:n].view(np.uint32))
+        assert np.array_equal(got[i].view(np.uint32), summ[p].view(np.uint32))

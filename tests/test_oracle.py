@@ -281,3 +281,31 @@ def test_planted_mistakes_are_caught():
                                    c["token_counts"], c["cand_offsets"], c["cand_ids"],
                                    H, D, ps, k)
     assert orc.max_abs_diff(o_bad, c["ref_sparse_out"]) > 1e-2
+
+
+def test_synthetic_decode_rows_lie_on_the_grid_and_are_uniform():
+    """The synthetic decode generator (reference src/device_page_pool.cpp:
+    122-138) maps a hash onto k/1000, k in [-1000, 1000]: every value is on
+    that grid, the 2001 values are near-uniform (mean near 0), and the key
+    and value streams and the elements differ.  A wrong modulus, a missing
+    shift or an ignored argument fails here; the hash constants themselves
+    have no vectors in the reference."""
+    E = 4096
+    rows = np.stack([orc.synthetic_decode_row(r, s, st, E)
+                     for r in (0, 7, 123) for s in (0, 1, 63) for st in (1, 2)])
+    k = np.rint(rows.astype(np.float64) * 1000.0).astype(np.int64)
+    assert np.array_equal(rows, (k.astype(np.float32) / np.float32(1000.0)))
+    assert k.min() >= -1000 and k.max() <= 1000
+    # each row is near-uniform over the 2001 values: chi-square(2000) within
+    # 6 sigma (rows of different steps share structure, so rows are tested
+    # one at a time, not pooled)
+    for row in k:
+        counts = np.bincount(row + 1000, minlength=2001)
+        expected = E / 2001.0
+        chi2 = float(((counts - expected) ** 2 / expected).sum())
+        assert abs(chi2 - 2000) < 6 * np.sqrt(2 * 2000)
+    assert abs(float(rows.astype(np.float64).mean())) < 0.01
+    assert not np.array_equal(rows[0], rows[1])              # key vs value stream
+    assert len(np.unique(rows[0])) > 1500                     # element enters the hash
+    assert not np.array_equal(orc.synthetic_decode_row(7, 1, 1, E),
+                              orc.synthetic_decode_row(7, 2, 1, E))
