@@ -859,6 +859,7 @@ struct dsd_sparse_ctx {
     a.top_k = top_k;
     a.sel_stride = top_k > 0 ? top_k : 1;
     a.heads_per_group = dsdk::FusedStepHeadsPerGroup(pool->view, L.batch, compute_units);
+    a.max_candidates = L.max_n;
     a.scale = Scale();
     a.mid = L.scores;
     a.lo = d_lo.ptr;

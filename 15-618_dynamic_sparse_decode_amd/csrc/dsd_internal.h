@@ -158,6 +158,7 @@ struct FusedArgs {
   int top_k = 0;
   int sel_stride = 1;                 // row stride of selected
   int heads_per_group = 2;            // heads per workgroup: 2, 4 or 8
+  int max_candidates = 0;             // the largest request's candidate count
   float scale = 0.0f;
   float* mid = nullptr;               // [total] certified intervals (caller copy)
   float* lo = nullptr;

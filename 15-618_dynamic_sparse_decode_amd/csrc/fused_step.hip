@@ -319,10 +319,11 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int first, i
 // staged once in LDS (in the rescoring tile, idle until the selection).
 // kPipeline: the first pass's rows load alongside the query, and each later
 // pass's id at the start of the pass before, its rows once that pass's
-// products are formed (the stand-alone score kernel, up to 8 passes).
-// Otherwise each pass loads its own rows first (the single-launch step,
-// where slices are mostly one pass: the pipelined form measured 0.5 us
-// slower at config 2 and 0.6 % faster at config 4).
+// products are formed (the stand-alone score kernel, and single-launch steps
+// whose slices span several passes: 4 us off the score phase at B = 32 with
+// 1024-4096-token contexts).  Otherwise each pass loads its own rows first
+// (single-launch steps of one pass per slice, where the pipelined form
+// measured 0.2-0.5 us slower at BASELINE config 2).
 template <bool kPipeline, class Shared>
 __device__ void ScoreSlice(const PoolView& pool, const FusedArgs& a, int r, int c0, int c1,
                            Shared& sh) {
@@ -694,7 +695,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
 // head softmax(q_h K^T * scale) V over the selected pages' valid tokens;
 // waves 0-7 take head h0 and waves 8-15 head h0+1, each as
 // AttentionFastKernel<128, 16, 8, 4>.
-__device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, int begin, int n,
+__device__ __forceinline__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, int begin, int n,
                               int group, FusedShared& sh) {
   const int hpw = a.heads_per_group;
   const int wph = kFWaves / hpw;       // waves per head
@@ -819,6 +820,11 @@ __device__ void AttentionItem(const PoolView& pool, const FusedArgs& a, int r, i
   }
 }
 
+// kMultiPass: some workgroup's slice spans several score passes; those
+// slices pipeline their passes (each pass's rows load while the previous
+// pass reduces).  Single-pass launches keep the plain form, which measured
+// faster there.
+template <bool kMultiPass>
 __global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, FusedArgs a) {
   __shared__ FusedShared sh;
   if (a.stamps != nullptr && threadIdx.x == 0) {
@@ -833,7 +839,8 @@ __global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, Fuse
   // A request beyond kFMaxCand selects nothing (reported by the selection):
   // its slices are not scored.
   if (n <= kFMaxCand) {
-    ScoreSlice<false>(pool, a, r, begin + (g * n) / groups, begin + ((g + 1) * n) / groups, sh);
+    ScoreSlice<kMultiPass>(pool, a, r, begin + (g * n) / groups,
+                           begin + ((g + 1) * n) / groups, sh);
   }
   StampAt(a, sh, kScored);
   AttentionItem(pool, a, r, begin, n, g, sh);
@@ -928,7 +935,14 @@ void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t st
   if (hpw != 2 && hpw != 4 && hpw != 8) throw std::invalid_argument("heads per group must be 2, 4 or 8");
   if (pool.num_heads % hpw != 0) throw std::invalid_argument("heads per group must divide num_heads");
   const int grid = FusedStepGrid(pool, args.batch, hpw);
-  hipLaunchKernelGGL(FusedStepKernel, dim3(grid), dim3(kFThreads), 0, stream, pool, args);
+  // Slices of a request split its candidates evenly over its workgroups.
+  const int groups = pool.num_heads / hpw;
+  const bool multi_pass = (args.max_candidates + groups - 1) / groups > kFPagesPerPass;
+  if (multi_pass) {
+    hipLaunchKernelGGL(FusedStepKernel<true>, dim3(grid), dim3(kFThreads), 0, stream, pool, args);
+  } else {
+    hipLaunchKernelGGL(FusedStepKernel<false>, dim3(grid), dim3(kFThreads), 0, stream, pool, args);
+  }
   DSD_HIP_CHECK(hipGetLastError());
 }
 

@@ -229,7 +229,8 @@ def test_fused_large_batch_of_small_requests(gpu):
 def test_fused_skewed_lengths(gpu, seed):
     # Very uneven requests (1 to 256 candidates, empty ones, equal sizes in
     # several places), two launches in a row; 24 requests: 4 heads per
-    # workgroup.
+    # workgroup, so 8 slices per request and up to 32 candidates per slice
+    # (the launch form whose slices pipeline several score passes).
     rng = np.random.default_rng(seed)
     lengths = [int(x) for x in rng.choice([0, 5, 16, 200, 1000, 4096, 4096, 2500], size=24)]
     batch = gpu.SyntheticBatch(H, D, PS, lengths, seed=seed)
