@@ -323,3 +323,18 @@ def test_staged_rows_are_checked_before_the_device(gpu):
                             output_mode=gpu.OUTPUT_OUTPUTS)
         assert np.array_equal(ok["outputs"].view(np.uint32),
                               ref["outputs"].reshape(2, E).view(np.uint32))
+        # an empty step needs no rows; a freed block no longer qualifies
+        lib = gpu.load_library()
+        assert lib.dsd_sparse_run_staged_rows(ctx.handle, 0, None, gpu.OUTPUT_OUTPUTS,
+                                              gpu.TIMING_NONE, None, None, None) == 0
+        other = gpu.HostBlock(E)
+        rows = [base, other.address]
+        other.array[:] = batch.queries.reshape(-1)[E:]
+        again = ctx.run_staged_rows(rows, batch.cand_offsets, batch.cand_ids)
+        assert np.array_equal(again["outputs"].view(np.uint32), ok["outputs"].view(np.uint32))
+        addr = other.address
+        other.close()
+        with pytest.raises(gpu.InvalidArgument, match="not in dsd_host_alloc"):
+            ctx.run_staged_rows(rows, batch.cand_offsets, batch.cand_ids)
+        import ctypes
+        assert lib.dsd_host_free(ctypes.c_void_p(addr)) == 1  # freed twice
