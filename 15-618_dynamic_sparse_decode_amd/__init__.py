@@ -313,6 +313,8 @@ class SparseContext:
         self._lib = load_library()
         self.pool = pool
         self.top_k = top_k
+        self.max_batch = max_batch
+        self.max_total_candidates = max_total_candidates
         handle = ctypes.c_void_p()
         _check(self._lib.dsd_sparse_create(pool.handle, top_k, max_batch, max_total_candidates,
                                            max_total_selected, ctypes.byref(handle)))
@@ -388,6 +390,13 @@ class SparseContext:
         batch = len(offs) - 1
         total = int(offs[-1]) if batch > 0 else 0
         E = self.pool.elements
+        # the staging holds max_batch + 1 offsets and max_total_candidates ids
+        if batch > self.max_batch:
+            raise InvalidArgument(1, "request batch exceeds sparse context capacity")
+        if total > self.max_total_candidates or len(ids) < total:
+            raise InvalidArgument(1, "candidate page count exceeds sparse context capacity")
+        if len(query_rows) != batch:
+            raise InvalidArgument(1, "one query row per request")
         q_st, off_st, ids_st, out_st = (ctypes.c_void_p() for _ in range(4))
         _check(self._lib.dsd_sparse_staging(self.handle, ctypes.byref(q_st), ctypes.byref(off_st),
                                             ctypes.byref(ids_st), ctypes.byref(out_st)))

@@ -1269,6 +1269,8 @@ int dsd_sparse_run_staged(dsd_sparse_ctx* ctx, int batch, int output_mode, int t
   return Guard([&] {
     Require(ctx != nullptr, "context must be non-null");
     Require(output_mode != DSD_OUTPUT_DEBUG, "the staged step has no debug mode");
+    // Before the staging's offsets are read: it holds max_batch + 1 of them.
+    Require(batch <= ctx->max_batch, "request batch exceeds sparse context capacity");
     HostStep(ctx, batch, true, ctx->h_queries.ptr, nullptr, ctx->h_offsets.ptr,
              ctx->h_ids.ptr, output_mode, timing_mode, nullptr, nullptr, selected,
              selected_counts, timings);
@@ -1282,6 +1284,7 @@ int dsd_sparse_run_staged_rows(dsd_sparse_ctx* ctx, int batch, const float* cons
     Require(ctx != nullptr, "context must be non-null");
     Require(output_mode != DSD_OUTPUT_DEBUG, "the staged step has no debug mode");
     if (batch > 0) Require(query_rows != nullptr, "query_rows must be non-null");
+    // Before the staging's offsets are read: it holds max_batch + 1 of them.
     Require(batch <= ctx->max_batch, "request batch exceeds sparse context capacity");
     HostStep(ctx, batch, true, nullptr, query_rows, ctx->h_offsets.ptr, ctx->h_ids.ptr,
              output_mode, timing_mode, nullptr, nullptr, selected, selected_counts, timings);
