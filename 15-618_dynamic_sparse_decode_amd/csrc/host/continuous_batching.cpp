@@ -10,11 +10,14 @@
 #include <chrono>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <deque>
 #include <numeric>
 #include <random>
 #include <stdexcept>
+#include <string>
 #include <unordered_set>
 #include <utility>
 
@@ -300,6 +303,53 @@ struct LiveRequest {
   const float* Query() const { return own ? query_buf.data() : query; }
 };
 
+// DSD_VERIFY_STAGED=1 (a self-check for tests; the loop's step outputs are
+// not otherwise observable): each staged step is run again through
+// SparseCudaContext::RunBatch, whose packing copies every query and page
+// list, and the two steps' outputs must agree bit for bit.
+bool VerifyStagedSteps() {
+  static const bool on = [] {
+    const char* e = std::getenv("DSD_VERIFY_STAGED");
+    return e != nullptr && std::strcmp(e, "0") != 0;
+  }();
+  return on;
+}
+
+long long g_verified_steps = 0;  // staged steps checked in this process
+
+void VerifyStagedStep(SparseCudaContext& ctx, const PagedKvCache& cache,
+                      const std::vector<LiveRequest>& active, int E) {
+  using detail::ThrowOnError;
+  float* staged_out = nullptr;
+  ThrowOnError(dsd_sparse_staging(ctx.handle(), nullptr, nullptr, nullptr, &staged_out));
+  const std::size_t B = active.size();
+  const std::vector<float> staged(staged_out, staged_out + B * static_cast<std::size_t>(E));
+  std::vector<RequestState> states(B);
+  std::vector<const RequestState*> ptrs;
+  for (std::size_t b = 0; b < B; ++b) {
+    const LiveRequest& l = active[b];
+    states[b].request_id = l.a.state.request_id;
+    states[b].query.assign(l.Query(), l.Query() + E);
+    states[b].candidate_page_ids = cache.GetRequestPages(l.a.state.request_id);
+    states[b].context_tokens = l.a.state.context_tokens;
+    ptrs.push_back(&states[b]);
+  }
+  SparseRunBatchOptions o;
+  o.output_mode = SparseBatchOutputMode::kOutputsOnly;
+  o.timing_mode = SparseBatchTimingMode::kNone;
+  const auto check = ctx.RunBatch(ptrs, o);
+  for (std::size_t b = 0; b < B; ++b) {
+    const auto& out = check.per_request[b].output.output;
+    if (out.size() != static_cast<std::size_t>(E) ||
+        std::memcmp(out.data(), staged.data() + b * static_cast<std::size_t>(E),
+                    sizeof(float) * static_cast<std::size_t>(E)) != 0) {
+      throw std::runtime_error("staged step differs from RunBatch for request " +
+                               std::to_string(states[b].request_id));
+    }
+  }
+  ++g_verified_steps;
+}
+
 // One RunBatch of the loop in the outputs / no-outputs modes, on the C ABI:
 // PackSparseBatchInto's checks and layout written into the pinned staging
 // (candidate lists from the cache; queries that live in the pinned payload
@@ -365,6 +415,7 @@ SparseBatchCudaResult StagedStep(SparseCudaContext& ctx, const PagedKvCache& cac
     ThrowOnError(dsd_sparse_run_staged(ctx.handle(), B, out_mode, time_mode, nullptr, nullptr,
                                        &t));
   }
+  if (VerifyStagedSteps()) VerifyStagedStep(ctx, cache, active, E);
   if (timing) {
     result.aggregate_timings.page_scoring_ms = t.score_ms;
     result.aggregate_timings.topk_ms = t.topk_ms;
@@ -687,6 +738,9 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
   }
   FinishStats(&stats, wall_start, step_ms, timings, overheads, steps_run, batch_sum);
   Add(&stats.device_transfer_stats, ctx.DeviceTransfers());
+  if (VerifyStagedSteps()) {
+    std::fprintf(stderr, "dsd: %lld staged steps verified against RunBatch\n", g_verified_steps);
+  }
   return stats;
 }
 

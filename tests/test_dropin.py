@@ -76,3 +76,34 @@ def test_reference_bench_decode_accuracy_lines(args):
     assert float(diffs["avg_max_abs_diff_sparse_gpu_vs_sparse_cpu"]) <= 1e-4
     if "avg_max_abs_diff_dense_gpu_vs_dense_cpu" in diffs:
         assert float(diffs["avg_max_abs_diff_dense_gpu_vs_dense_cpu"]) <= 1e-4
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("args", [
+    # requests, max active, window, prompt min/max, decode min/max, seed, heads,
+    # head_dim, page size, top-k, then admission mode, preadmit, precompute,
+    # GPU synthetic append, lazy release, output mode, timing mode (argv order)
+    ("8", "4", "4", "64", "512", "2", "6", "7", "32", "128", "16", "4",
+     "1", "1", "1", "1", "1", "1", "1"),                       # published flags, fused step
+    ("8", "4", "4", "64", "512", "2", "6", "7", "32", "128", "16", "4"),  # driver defaults
+    ("8", "4", "4", "64", "512", "2", "6", "7", "32", "64", "16", "4",
+     "1", "1", "1", "1", "1", "0", "0"),                       # three-kernel step, no outputs
+])
+def test_reference_continuous_driver_staged_steps_verified(args):
+    """The reference's continuous driver against libdsd.so with
+    DSD_VERIFY_STAGED=1: every step the loop stages in place (queries read
+    from the pinned payload rows or the staging, page lists from the cache)
+    is run again through RunBatch's packing path and must match it bit for
+    bit, or the run fails."""
+    import os
+    exe = DROPIN / "bench_continuous_decode"
+    if not exe.exists():
+        pytest.skip(f"{exe} not built (needs the reference tree: make -C oracle dropin)")
+    print(f"[dropin] bench_continuous_decode {' '.join(args)} (verified)", flush=True)
+    env = dict(os.environ, DSD_VERIFY_STAGED="1")
+    proc = subprocess.run([str(exe), *args], capture_output=True, text=True, timeout=300, env=env)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    assert "continuous_sparse_tokens_per_second=" in proc.stdout, proc.stdout
+    # the continuous and the serial run each report their running total
+    counts = [int(n) for n in re.findall(r"dsd: (\d+) staged steps verified", proc.stderr)]
+    assert len(counts) >= 2 and counts[0] > 0 and counts[-1] > counts[0], proc.stderr
