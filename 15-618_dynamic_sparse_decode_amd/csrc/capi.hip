@@ -875,6 +875,9 @@ struct dsd_sparse_ctx {
     if (stamp) {
       // The kernel writes its stamps straight into pinned host memory.
       stamp_grid = dsdk::FusedStepGrid(pool->view, L.batch, a.heads_per_group);
+      if (static_cast<size_t>(stamp_grid) * dsdk::FusedStepStampsPerGroup() > h_stamps.count) {
+        throw std::runtime_error("fused step stamps exceed their buffer");
+      }
       a.stamps = h_stamps.ptr;
     }
     dsdk::LaunchFusedStep(pool->view, a, s);
@@ -998,8 +1001,9 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     DSD_HIP_CHECK(hipMemset(ctx->d_exact_pages.ptr, 0, sizeof(int)));
     {
       const size_t rec = 3 * P;
+      // The largest fused grid: one head per workgroup.
       const size_t stamps =
-          static_cast<size_t>(dsdk::FusedStepGrid(pool->view, static_cast<int>(B), 2)) *
+          static_cast<size_t>(dsdk::FusedStepGrid(pool->view, static_cast<int>(B), 1)) *
           dsdk::FusedStepStampsPerGroup();
       ctx->d_rec.Reserve(rec);
       ctx->h_stamps.Reserve(stamps, hipHostMallocCoherent);

@@ -157,7 +157,7 @@ struct FusedArgs {
   int total = 0;
   int top_k = 0;
   int sel_stride = 1;                 // row stride of selected
-  int heads_per_group = 2;            // heads per workgroup: 2, 4 or 8
+  int heads_per_group = 2;            // heads per workgroup: 1, 2, 4 or 8
   int max_candidates = 0;             // the largest request's candidate count
   float scale = 0.0f;
   float* mid = nullptr;               // [total] certified intervals (caller copy)
@@ -179,7 +179,7 @@ struct FusedArgs {
 
 // E = 4096, head_dim = 128, max_candidates <= 256, top_k <= 256.
 bool FusedStepSupported(const PoolView& pool, int max_candidates, int top_k);
-// Heads per workgroup for a batch: the fewest (2, 4, 8) that keep the grid
+// Heads per workgroup for a batch: the fewest (1, 2, 4, 8) that keep the grid
 // within `compute_units` workgroups, else 8.
 int FusedStepHeadsPerGroup(const PoolView& pool, int batch, int compute_units);
 // Workgroups of one launch: num_heads / heads_per_group per request.

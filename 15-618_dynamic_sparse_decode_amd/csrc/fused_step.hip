@@ -9,7 +9,7 @@
 //
 // Work items.  Request r owns the G = H/hpw consecutive workgroups
 // [r*G, r*G + G); workgroup (r, g) takes heads hpw*g .. hpw*g + hpw - 1,
-// where hpw (2, 4 or 8 heads per workgroup) is the fewest that keeps the
+// where hpw (1, 2, 4 or 8 heads per workgroup) is the fewest that keeps the
 // grid within one dispatch wave (B*H/hpw <= CUs) when that is possible.
 // Each does:
 //   1. score: the certified intervals of its slice of the request's
@@ -54,7 +54,7 @@ constexpr int kFWaves = kFThreads / kWave;  // 16
 constexpr int kFE = 4096;
 constexpr int kFD = 128;
 constexpr int kFPagesPerPass = 8;           // score pass = 8 pages, 2 waves each
-constexpr int kFMaxHeadsPerGroup = 8;       // workgroup = 2, 4 or 8 heads (16/hpw waves each)
+constexpr int kFMaxHeadsPerGroup = 8;       // workgroup = 1, 2, 4 or 8 heads (16/hpw waves each)
 constexpr int kFPageLanes = 2 * kWave;      // 128 lanes per page
 constexpr int kFPerLane = kFE / kFPageLanes;  // 32 consecutive products per lane
 constexpr int kFMaxCand = 256;
@@ -918,7 +918,7 @@ bool FusedStepSupported(const PoolView& pool, int max_candidates, int top_k) {
 int FusedStepHeadsPerGroup(const PoolView& pool, int batch, int compute_units) {
   // The fewest heads per workgroup (most waves per head) that keeps the
   // grid within one dispatch wave; 8 when none does.
-  for (int hpw = 2; hpw < kFMaxHeadsPerGroup; hpw *= 2) {
+  for (int hpw = 1; hpw < kFMaxHeadsPerGroup; hpw *= 2) {
     if (pool.num_heads % (2 * hpw) != 0) return hpw;
     if (static_cast<int64_t>(batch) * (pool.num_heads / hpw) <= compute_units) return hpw;
   }
@@ -934,7 +934,9 @@ int FusedStepStampsPerGroup() { return kStampsPerGroup; }
 void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t stream) {
   if (args.batch <= 0) return;
   const int hpw = args.heads_per_group;
-  if (hpw != 2 && hpw != 4 && hpw != 8) throw std::invalid_argument("heads per group must be 2, 4 or 8");
+  if (hpw != 1 && hpw != 2 && hpw != 4 && hpw != 8) {
+    throw std::invalid_argument("heads per group must be 1, 2, 4 or 8");
+  }
   if (pool.num_heads % hpw != 0) throw std::invalid_argument("heads per group must divide num_heads");
   const int grid = FusedStepGrid(pool, args.batch, hpw);
   // Slices of a request split its candidates evenly over its workgroups.
