@@ -14,7 +14,9 @@
 // Each does:
 //   1. score: the certified intervals of its slice of the request's
 //      candidates, [n*g/G, n*(g+1)/G), eight pages per pass, two waves per
-//      page, published as tagged words (below);
+//      page, published as tagged words (below); when some slice spans
+//      several passes the launch uses FusedStepKernel<true>, whose passes
+//      load the next pass's rows while they reduce;
 //   2. select: waits until every interval of its request is published,
 //      then computes the request's top-k from them (the G workgroups
 //      compute the same selection; g = 0 writes it out);
