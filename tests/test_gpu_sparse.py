@@ -338,3 +338,13 @@ def test_staged_rows_are_checked_before_the_device(gpu):
             ctx.run_staged_rows(rows, batch.cand_offsets, batch.cand_ids)
         import ctypes
         assert lib.dsd_host_free(ctypes.c_void_p(addr)) == 1  # freed twice
+        # a batch beyond the staging's capacity fails before the staging is read
+        assert lib.dsd_sparse_run_staged(ctx.handle, 3, gpu.OUTPUT_OUTPUTS, gpu.TIMING_NONE,
+                                         None, None, None) == 1
+        assert b"capacity" in lib.dsd_last_error()
+        rows3 = (ctypes.c_void_p * 3)(base, base, base)
+        assert lib.dsd_sparse_run_staged_rows(ctx.handle, 3, rows3, gpu.OUTPUT_OUTPUTS,
+                                              gpu.TIMING_NONE, None, None, None) == 1
+        with pytest.raises(gpu.InvalidArgument, match="capacity"):
+            ctx.run_staged_rows([base] * 3, np.array([0, 1, 2, 3], np.int32),
+                                batch.cand_ids[:3])
