@@ -77,6 +77,15 @@ class PoolArrays(ctypes.Structure):
                 ("v_offsets", ctypes.c_void_p)]
 
 
+class LaunchInfo(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "fused", "certified", "multi_pass", "heads_per_group", "grid",
+        "score_pages_per_group")]
+
+    def as_dict(self):
+        return {n: int(getattr(self, n)) for n, _ in self._fields_}
+
+
 class StepTimings(ctypes.Structure):
     _fields_ = [(n, ctypes.c_double) for n in (
         "score_ms", "topk_ms", "attention_ms", "kernel_ms",
@@ -136,6 +145,9 @@ _SIGNATURES = {
     "dsd_sparse_score_bounds": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_float_p,
                                                _c_float_p, _c_float_p]),
     "dsd_sparse_exact_rescored_pages": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p]),
+    "dsd_sparse_device_status": (ctypes.c_int, [ctypes.c_void_p]),
+    "dsd_sparse_last_launch": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(LaunchInfo)]),
+    "dsd_sparse_set_wait_limit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint, ctypes.c_int]),
     "dsd_dense_run_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_float_p, _c_int_p,
                                            _c_int_p, _c_float_p, _c_double_p]),
     "dsd_dense_run_batch_device": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int] + [ctypes.c_void_p] * 5),
@@ -450,6 +462,21 @@ class SparseContext:
                                                          ctypes.byref(out)))
         return out.value
 
+    def last_launch(self) -> dict:
+        """Launch form of the last step: fused, certified, multi_pass,
+        heads_per_group, grid, score_pages_per_group."""
+        info = LaunchInfo()
+        _check(self._lib.dsd_sparse_last_launch(self.handle, ctypes.byref(info)))
+        return info.as_dict()
+
+    def device_status(self) -> None:
+        """Synchronize; raise the last unreported input failure of a step."""
+        _check(self._lib.dsd_sparse_device_status(self.handle))
+
+    def set_wait_limit(self, spin_limit: int, never_ready: bool = False) -> None:
+        _check(self._lib.dsd_sparse_set_wait_limit(self.handle, int(spin_limit),
+                                                   int(bool(never_ready))))
+
     def replay_stage(self, stage: int, stream=0) -> None:
         _check(self._lib.dsd_sparse_replay_stage(self.handle, stage, stream or None))
 
@@ -529,34 +556,40 @@ class SyntheticBatch:
     """A ragged batch laid out like the reference's BuildSyntheticBatch
     (src/synthetic_data.cpp:23-68): capacity = total pages, LIFO page ids
     (the first page allocated is capacity-1, src/page_pool.cpp:36-45), each
-    request's candidates in logical page order.  Values are i.i.d. N(0,1)
-    float32 from numpy's PCG64 stream seeded with `seed` (keys, values, then
-    queries)."""
+    request's candidates in logical page order.
+
+    Values are i.i.d. N(0,1) float32 from numpy's PCG64.  Each request has
+    its own stream, child r of numpy.random.SeedSequence(seed) spawned into
+    B + 1 children: its pages' keys ([n_r][page_size][E]), then their values.
+    Child B gives the queries ([B][E]).  Streams are independent, so requests
+    are generated in parallel (host threads) or one at a time
+    (request_pages), and anyone with numpy regenerates the same batch."""
 
     def __init__(self, num_heads, head_dim, page_size, context_lengths, seed,
                  capacity=None, dtype=np.float32):
         self.num_heads, self.head_dim, self.page_size = num_heads, head_dim, page_size
         self.elements = E = num_heads * head_dim
+        self.dtype = dtype
         self.context_lengths = [int(c) for c in context_lengths]
-        pages_per = [(c + page_size - 1) // page_size for c in self.context_lengths]
-        total_pages = sum(pages_per)
+        self.pages_per = [(c + page_size - 1) // page_size for c in self.context_lengths]
+        total_pages = sum(self.pages_per)
         self.capacity = capacity if capacity is not None else total_pages
         B = len(self.context_lengths)
         self.cand_offsets = np.zeros(B + 1, np.int32)
-        self.cand_offsets[1:] = np.cumsum(pages_per)
+        self.cand_offsets[1:] = np.cumsum(self.pages_per)
         ids = np.arange(total_pages, dtype=np.int32)
         self.cand_ids = (self.capacity - 1 - ids).astype(np.int32)
         self.token_counts = np.zeros(self.capacity, np.int32)
         g = 0
         for r, c in enumerate(self.context_lengths):
-            for j in range(pages_per[r]):
+            for j in range(self.pages_per[r]):
                 self.token_counts[self.cand_ids[g]] = min(page_size, c - j * page_size)
                 g += 1
-        rng = np.random.default_rng(seed)
-        shape = (self.capacity, page_size, E)
-        self.key_pool = rng.standard_normal(shape, dtype=dtype)
-        self.value_pool = rng.standard_normal(shape, dtype=dtype)
-        self.queries = rng.standard_normal((B, E), dtype=dtype)
+        self._streams = np.random.SeedSequence(seed).spawn(B + 1)
+        self.queries = np.random.default_rng(self._streams[B]).standard_normal(
+            (B, E), dtype=dtype)
+        self._key_pool = None
+        self._value_pool = None
 
     @property
     def batch(self):
@@ -570,6 +603,56 @@ class SyntheticBatch:
     def max_candidates(self):
         return int(np.max(np.diff(self.cand_offsets))) if self.batch else 0
 
+    def request_ids(self, r: int):
+        """Page ids of request r, in logical order."""
+        return self.cand_ids[self.cand_offsets[r]:self.cand_offsets[r + 1]]
+
+    def request_pages(self, r: int, out_keys=None, out_values=None):
+        """Keys and values of request r's pages, [n_r][page_size][E] each
+        (written into out_keys / out_values when given)."""
+        n = self.pages_per[r]
+        shape = (n, self.page_size, self.elements)
+        k = np.empty(shape, self.dtype) if out_keys is None else out_keys
+        v = np.empty(shape, self.dtype) if out_values is None else out_values
+        rng = np.random.default_rng(self._streams[r])
+        rng.standard_normal(out=k.reshape(-1), dtype=self.dtype)
+        rng.standard_normal(out=v.reshape(-1), dtype=self.dtype)
+        return k, v
+
+    def _materialize(self):
+        import concurrent.futures as cf
+        shape = (self.capacity, self.page_size, self.elements)
+        kp = np.zeros(shape, self.dtype)
+        vp = np.zeros(shape, self.dtype)
+
+        def fill(r):
+            n = self.pages_per[r]
+            if n == 0:
+                return
+            # a request's ids are consecutive and descending: rows lo..hi
+            hi = int(self.cand_ids[self.cand_offsets[r]])
+            lo = hi - n + 1
+            k, v = self.request_pages(r)
+            kp[lo:hi + 1] = k[::-1]
+            vp[lo:hi + 1] = v[::-1]
+
+        with cf.ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
+            list(ex.map(fill, range(self.batch)))
+        self._key_pool, self._value_pool = kp, vp
+
+    @property
+    def key_pool(self):
+        """[capacity][page_size][E] keys (built on first use)."""
+        if self._key_pool is None:
+            self._materialize()
+        return self._key_pool
+
+    @property
+    def value_pool(self):
+        if self._value_pool is None:
+            self._materialize()
+        return self._value_pool
+
     def live_page_ids(self):
         return self.cand_ids.copy()
 
@@ -580,3 +663,14 @@ class SyntheticBatch:
         offs = ids.astype(np.int64) * self.page_size * self.elements
         pool.upload_pages(ids, counts, offs, self.key_pool.reshape(-1),
                           self.value_pool.reshape(-1), summaries)
+
+    def upload_request(self, pool: DevicePagePool, r: int, keys, values):
+        """Upload request r's pages from request_pages(r)'s arrays (device
+        summaries)."""
+        ids = self.request_ids(r)
+        n = len(ids)
+        if n == 0:
+            return
+        offs = np.arange(n, dtype=np.int64) * self.page_size * self.elements
+        pool.upload_pages(ids, self.token_counts[ids], offs, keys.reshape(-1),
+                          values.reshape(-1))

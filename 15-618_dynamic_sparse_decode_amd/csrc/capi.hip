@@ -106,6 +106,13 @@ struct PinnedBuffer {
 
 constexpr uint64_t kLargeCopyBytes = 1ull << 20;  // src/device_page_pool.cpp:13
 
+// Polls of a cross-workgroup wait of the single-launch step before it gives
+// up (each poll is a sleep plus a coherent read, about 1-2 us).  A wait
+// normally ends within microseconds; the limit, about 0.1-0.3 s, only
+// bounds a step whose workgroups cannot all get a compute unit (another
+// process holding them), which then fails instead of hanging.
+constexpr unsigned kDefaultSpinLimit = 1u << 17;
+
 // Uploads from pageable memory of at least kStageMinBytes go through pinned
 // staging: the host threads copy one chunk while the DMA engine moves the
 // previous one (the runtime's own pageable path copies at about 27 GB/s on
@@ -793,13 +800,23 @@ struct dsd_sparse_ctx {
   // fused-step publication words (see fused_step.hip) and per-workgroup
   // clock stamps for the timing mode
   DeviceBuffer<unsigned long long> d_rec;
+  // The epoch of the step being enqueued: it tags the fused step's
+  // publication words and every failure report of the step's kernels.
   unsigned epoch = 0;
+  unsigned spin_limit = kDefaultSpinLimit;
+  bool never_ready = false;  // test hook: every fused-step wait gives up
+  // The stream of the last launch that used the context's scratch, and the
+  // event that orders a launch on another stream after it.
+  hipStream_t last_stream = nullptr;
+  hipEvent_t ev_switch = nullptr;
   double wall_khz = 0.0;  // wall_clock64() rate
   int compute_units = 256;
   int score_mode = DSD_SCORE_CERTIFIED;
   bool fused_enabled = true;
   PinnedBuffer<float> h_queries, h_scores, h_outputs;
-  PinnedBuffer<int> h_offsets, h_ids, h_selected, h_counts, h_fail;
+  PinnedBuffer<int> h_offsets, h_ids, h_selected, h_counts;
+  // The step kernels' failure word: (epoch << 32) | code, pinned, coherent.
+  PinnedBuffer<unsigned long long> h_fail;
   PinnedBuffer<unsigned long long> h_stamps;
   PinnedBuffer<const float*> h_rows;  // row pointers of a row-gather step
   int stamp_grid = 0;  // workgroups stamped by the last timed fused launch
@@ -822,6 +839,48 @@ struct dsd_sparse_ctx {
     for (hipEvent_t& e : ev) {
       if (e) (void)hipEventDestroy(e);
     }
+    if (ev_switch) (void)hipEventDestroy(ev_switch);
+  }
+
+  // A fresh epoch for the next step (never 0: the words start at 0).
+  void NextEpoch() {
+    if (++epoch == 0) epoch = 1;
+  }
+  dsdk::FailReport Fail() const {
+    dsdk::FailReport f;
+    f.word = h_fail.ptr;
+    f.epoch = epoch;
+    return f;
+  }
+  // Every launch shares the context's scratch (intervals, publication words,
+  // ids).  Launches on one stream are ordered by it; a launch on another
+  // stream first waits for everything enqueued on the previous one.
+  void OrderOn(hipStream_t s) {
+    if (last_stream != nullptr && last_stream != s) {
+      DSD_HIP_CHECK(hipEventRecord(ev_switch, last_stream));
+      DSD_HIP_CHECK(hipStreamWaitEvent(s, ev_switch, 0));
+    }
+    last_stream = s;
+  }
+  // After the launches of interest have finished: throws the failure a step
+  // reported, if any -- only one of `only_epoch`'s when that is non-zero --
+  // and clears the word.  A failure of another epoch is left in place.
+  void CheckFailure(unsigned only_epoch) {
+    const unsigned long long w =
+        __hip_atomic_load(h_fail.ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const int code = static_cast<int>(w & 0xffffffffull);
+    const unsigned at = static_cast<unsigned>(w >> 32);
+    if (code == 0 || (only_epoch != 0 && at != only_epoch)) return;
+    h_fail.ptr[0] = 0;
+    if (code == dsdk::kFailShape) {
+      throw std::invalid_argument(
+          "a request's candidate list does not fit the step's max_candidates / "
+          "total_candidates (or its offsets are malformed): nothing was selected for it");
+    }
+    if (code == dsdk::kFailPageId) {
+      throw std::out_of_range("a candidate page id of the step is outside the pool");
+    }
+    throw std::runtime_error("fused decode step: wait for page selection timed out");
   }
 
   float Scale() const {
@@ -838,10 +897,10 @@ struct dsd_sparse_ctx {
     if (L.total <= 0) return;
     if (L.certified) {
       dsdk::LaunchScoreBounds(pool->view, L.queries, L.offsets, L.ids, L.batch, L.total,
-                              L.max_n, Scale(), L.scores, d_lo.ptr, d_hi.ptr, s);
+                              L.max_n, Scale(), L.scores, d_lo.ptr, d_hi.ptr, Fail(), s);
     } else {
-      dsdk::LaunchScoreExact(pool->view, L.queries, L.offsets, L.ids, L.batch, L.max_n,
-                             Scale(), L.scores, s);
+      dsdk::LaunchScoreExact(pool->view, L.queries, L.offsets, L.ids, L.batch, L.total,
+                             L.max_n, Scale(), L.scores, Fail(), s);
     }
   }
   // The single-launch step covers certified selection on the hot shape.
@@ -868,10 +927,11 @@ struct dsd_sparse_ctx {
     a.counts = L.counts;
     a.outputs = L.outputs;
     a.rec = d_rec.ptr;
-    if (++epoch == 0) epoch = 1;  // words start at 0: never tag with epoch 0
     a.epoch = epoch;
+    a.wait_tag = never_ready ? (epoch ^ 0x80000000u) : epoch;
+    a.spin_limit = spin_limit;
     a.exact_pages = d_exact_pages.ptr;
-    a.fail_flag = h_fail.ptr;
+    a.fail = Fail();
     if (stamp) {
       // The kernel writes its stamps straight into pinned host memory.
       stamp_grid = dsdk::FusedStepGrid(pool->view, L.batch, a.heads_per_group);
@@ -906,6 +966,7 @@ struct dsd_sparse_ctx {
     *attention_ms = static_cast<double>(t_end - t_select) / wall_khz;
   }
   void Enqueue(const Launch& L, hipStream_t s, bool timing) {
+    NextEpoch();
     if (L.fused) {
       if (timing) DSD_HIP_CHECK(hipEventRecord(ev[0], s));
       EnqueueFused(L, s, timing);  // records ev[3] at the kernel's end
@@ -919,30 +980,14 @@ struct dsd_sparse_ctx {
     EnqueueAttention(L, s);
     if (timing) DSD_HIP_CHECK(hipEventRecord(ev[3], s));
   }
-  // After the stream has synchronised: a fused step that reported a failure
-  // (a timed-out wait, or a request beyond max_candidates) left zeros.
-  void CheckTimeout() {
-    if (h_fail.ptr != nullptr && h_fail.ptr[0] != 0) {
-      const int code = h_fail.ptr[0];
-      h_fail.ptr[0] = 0;
-      if (code == 2) {
-        throw std::invalid_argument(
-            "a request has more candidates than the max_candidates the step was given");
-      }
-      if (code == 3) {
-        throw std::runtime_error("fused decode step: a selected page id was out of range");
-      }
-      throw std::runtime_error("fused decode step: wait for page selection timed out");
-    }
-  }
   void EnqueueSelect(const Launch& L, hipStream_t s) {
     if (L.certified) {
       dsdk::LaunchSelectCertified(pool->view, L.scores, d_lo.ptr, d_hi.ptr, L.queries,
-                                  L.offsets, L.ids, L.batch, L.max_n, Scale(), top_k,
-                                  L.selected, L.counts, d_exact_pages.ptr, s);
+                                  L.offsets, L.ids, L.batch, L.total, L.max_n, Scale(), top_k,
+                                  L.selected, L.counts, d_exact_pages.ptr, Fail(), s);
     } else {
-      dsdk::LaunchSelectTopK(L.scores, L.offsets, L.ids, L.batch, L.max_n, top_k,
-                             L.selected, L.counts, s);
+      dsdk::LaunchSelectTopK(L.scores, L.offsets, L.ids, L.batch, L.total, L.max_n, top_k,
+                             L.selected, L.counts, Fail(), s);
     }
   }
   void EnqueueAttention(const Launch& L, hipStream_t s) {
@@ -985,6 +1030,7 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     // stream waits (each costs several microseconds of host time per step).
     ctx->stream = pool->stream;
     for (hipEvent_t& e : ctx->ev) DSD_HIP_CHECK(hipEventCreate(&e));
+    DSD_HIP_CHECK(hipEventCreateWithFlags(&ctx->ev_switch, hipEventDisableTiming));
     const size_t E = static_cast<size_t>(pool->view.elements);
     const size_t B = static_cast<size_t>(std::max(1, max_batch));
     const size_t P = static_cast<size_t>(std::max(1, max_total_candidates));
@@ -1009,7 +1055,7 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
       ctx->h_stamps.Reserve(stamps, hipHostMallocCoherent);
       DSD_HIP_CHECK(hipMemset(ctx->d_rec.ptr, 0, rec * sizeof(unsigned long long)));
     }
-    ctx->h_fail.Reserve(1);
+    ctx->h_fail.Reserve(1, hipHostMallocCoherent);
     ctx->h_fail.ptr[0] = 0;
     {
       int device = 0, khz = 0;
@@ -1041,7 +1087,9 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
 int dsd_sparse_destroy(dsd_sparse_ctx* ctx) {
   return Guard([&] {
     if (ctx != nullptr) {
-      (void)hipStreamSynchronize(ctx->stream);
+      // A device-buffer step may still run on a caller's stream: wait for
+      // every stream before the scratch it uses is freed.
+      (void)hipDeviceSynchronize();
       delete ctx;
     }
   });
@@ -1143,6 +1191,7 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
       if (total > 0) std::memcpy(ctx->h_ids.ptr, cand_ids, sizeof(int) * total);
     }
     ctx->pool->OrderAfterPending(ctx->stream);
+    ctx->OrderOn(ctx->stream);
     {
       // One kernel on the step's stream copies the staged inputs to the
       // device: DMA copies would each cost a copy-engine hand-off.
@@ -1211,7 +1260,10 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
     t0 = Clock::now();
     DSD_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     t.sync_ms = MsSince(t0);
-    if (L.fused) ctx->CheckTimeout();
+    // A failure this step reported (its outputs are then zeros for the
+    // request concerned); failures of earlier device-buffer steps are left
+    // for dsd_sparse_device_status.
+    ctx->CheckFailure(ctx->epoch);
     if (timing && L.fused) {
       // One kernel: its event time, split at the workgroup clock stamps.
       float k = 0.f;
@@ -1352,6 +1404,7 @@ int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
     L.counts = d_selected_counts != nullptr ? d_selected_counts : ctx->d_counts.ptr;
     hipStream_t s = stream != nullptr ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
     ctx->pool->OrderAfterPending(s);
+    ctx->OrderOn(s);
     ctx->Enqueue(L, s, false);
     ctx->last = L;
   });
@@ -1363,6 +1416,8 @@ int dsd_sparse_replay_stage(dsd_sparse_ctx* ctx, int stage, void* stream) {
     Require(ctx->last.valid, "no previous step to replay");
     hipStream_t s = stream != nullptr ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
     ctx->pool->OrderAfterPending(s);
+    ctx->OrderOn(s);
+    ctx->NextEpoch();
     const auto& L = ctx->last;
     switch (stage) {
       case 0: ctx->EnqueueScore(L, s); break;
@@ -1403,9 +1458,48 @@ int dsd_sparse_exact_rescored_pages(dsd_sparse_ctx* ctx, int reset, int* out) {
   return Guard([&] {
     Require(ctx != nullptr && out != nullptr, "pointers must be non-null");
     DSD_HIP_CHECK(hipDeviceSynchronize());
-    ctx->CheckTimeout();
+    ctx->CheckFailure(0);
     DSD_HIP_CHECK(hipMemcpy(out, ctx->d_exact_pages.ptr, sizeof(int), hipMemcpyDeviceToHost));
     if (reset) DSD_HIP_CHECK(hipMemset(ctx->d_exact_pages.ptr, 0, sizeof(int)));
+  });
+}
+
+int dsd_sparse_last_launch(const dsd_sparse_ctx* ctx, dsd_launch_info* out) {
+  return Guard([&] {
+    Require(ctx != nullptr && out != nullptr, "pointers must be non-null");
+    Require(ctx->last.valid, "no step has been launched on this context");
+    const auto& L = ctx->last;
+    const dsdk::PoolView& v = ctx->pool->view;
+    *out = dsd_launch_info{};
+    out->fused = L.fused ? 1 : 0;
+    out->certified = L.certified ? 1 : 0;
+    if (L.fused) {
+      const int hpw = dsdk::FusedStepHeadsPerGroup(v, L.batch, ctx->compute_units);
+      out->heads_per_group = hpw;
+      out->multi_pass = dsdk::FusedStepMultiPass(v, L.max_n, hpw) ? 1 : 0;
+      out->grid = dsdk::FusedStepGrid(v, L.batch, hpw);
+    } else if (L.certified && v.elements == 4096) {
+      const int per = dsdk::ScorePagesPerGroup(L.total);
+      out->score_pages_per_group = per;
+      out->grid = L.batch * ((L.max_n + per - 1) / per);
+    }
+  });
+}
+
+int dsd_sparse_device_status(dsd_sparse_ctx* ctx) {
+  return Guard([&] {
+    Require(ctx != nullptr, "context must be non-null");
+    DSD_HIP_CHECK(hipDeviceSynchronize());
+    ctx->CheckFailure(0);
+  });
+}
+
+int dsd_sparse_set_wait_limit(dsd_sparse_ctx* ctx, unsigned spin_limit, int never_ready) {
+  return Guard([&] {
+    Require(ctx != nullptr, "context must be non-null");
+    Require(spin_limit > 0, "spin_limit must be positive");
+    ctx->spin_limit = spin_limit;
+    ctx->never_ready = never_ready != 0;
   });
 }
 

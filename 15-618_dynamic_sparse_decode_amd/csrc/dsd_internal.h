@@ -38,6 +38,19 @@ inline void CheckHip(hipError_t status, const char* expr) {
 
 #define DSD_HIP_CHECK(expr) ::dsdk::CheckHip((expr), #expr)
 
+// Where a step's kernels report an input they cannot use: they store
+// (epoch << 32) | code into *word, a host-visible pinned word, so the host
+// can tell which launch failed.  Codes: 1 a cross-workgroup wait of the
+// single-launch step gave up, 2 a request's candidate list does not fit what
+// the launch was told (max_candidates, total_candidates, or a malformed CSR),
+// 3 a candidate page id outside the pool.  The request is then skipped
+// (nothing selected, zero outputs); every kernel still exits normally.
+struct FailReport {
+  unsigned long long* word = nullptr;  // null: failures are not reported
+  unsigned epoch = 0;
+};
+enum FailCode { kFailWait = 1, kFailShape = 2, kFailPageId = 3 };
+
 // ---- pool kernels (pool_kernels.hip) --------------------------------------
 
 // For each of n pages: token count and live flag, then the summary row --
@@ -96,8 +109,8 @@ void LaunchStageIn(const StageSegments& s, hipStream_t stream);
 // the reference's sequential CPU loop.
 void LaunchScoreExact(const PoolView& pool, const float* d_queries,
                       const int* d_cand_offsets, const int* d_cand_ids,
-                      int batch, int max_candidates, float scale,
-                      float* d_scores, hipStream_t stream);
+                      int batch, int total_candidates, int max_candidates, float scale,
+                      float* d_scores, FailReport fail, hipStream_t stream);
 
 // Certified scoring: per candidate an interval [lo, hi] that provably holds
 // the reference's sequential-fp32 score, and its midpoint.  Needs E % 64 == 0
@@ -106,16 +119,20 @@ bool CertifiedScoringSupported(int elements, int max_candidates);
 void LaunchScoreBounds(const PoolView& pool, const float* d_queries,
                        const int* d_cand_offsets, const int* d_cand_ids, int batch,
                        int total_candidates, int max_candidates, float scale, float* d_mid,
-                       float* d_lo, float* d_hi, hipStream_t stream);
+                       float* d_lo, float* d_hi, FailReport fail, hipStream_t stream);
 
 // Top-k from certified intervals; candidates whose order is not decided by
 // disjoint intervals are rescored with the exact sequential chain.  Adds the
-// number of rescored pages to *d_exact_pages when non-null.
+// number of rescored pages to *d_exact_pages when non-null.  A request whose
+// candidate list is longer than max_candidates (the score kernels covered
+// only that many) or whose offsets leave [0, total_candidates] selects
+// nothing and is reported (kFailShape).
 void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float* d_lo,
                            const float* d_hi, const float* d_queries,
                            const int* d_cand_offsets, const int* d_cand_ids, int batch,
-                           int max_candidates, float scale, int top_k, int* d_selected,
-                           int* d_counts, int* d_exact_pages, hipStream_t stream);
+                           int total_candidates, int max_candidates, float scale, int top_k,
+                           int* d_selected, int* d_counts, int* d_exact_pages, FailReport fail,
+                           hipStream_t stream);
 
 // Largest next-pow2 candidate count the LDS select handles.
 int SelectMaxCandidates();
@@ -123,13 +140,14 @@ int SelectMaxCandidates();
 // Per-request top-k by (score desc, id asc): selected[r*top_k + j],
 // counts[r] = min(top_k, n_r).
 void LaunchSelectTopK(const float* d_scores, const int* d_cand_offsets,
-                      const int* d_cand_ids, int batch, int max_candidates,
-                      int top_k, int* d_selected, int* d_counts,
-                      hipStream_t stream);
+                      const int* d_cand_ids, int batch, int total_candidates,
+                      int max_candidates, int top_k, int* d_selected, int* d_counts,
+                      FailReport fail, hipStream_t stream);
 
 // Fused gather + softmax attention over page lists.  Request r attends over
 // list_ids[start_r .. start_r + count_r): with list_stride > 0, start_r =
 // r*list_stride and count_r = list_counts[r]; otherwise CSR list_offsets.
+// A list id outside the pool holds no tokens (never read).
 struct AttentionArgs {
   const float* queries = nullptr;  // [batch][E]
   const int* list_ids = nullptr;
@@ -169,8 +187,10 @@ struct FusedArgs {
   unsigned long long* rec = nullptr;
   unsigned epoch = 0;
   int* exact_pages = nullptr;         // may be null
-  int* fail_flag = nullptr;           // host-visible: 1 wait timed out, 2 CSR overflow,
-                                      // 3 page id outside the pool
+  FailReport fail;                    // kFailWait / kFailShape / kFailPageId
+  unsigned spin_limit = 0;            // polls of a cross-workgroup wait before it gives up
+  unsigned wait_tag = 0;              // the tag the waits look for: epoch (a test
+                                      // sets another, so every wait gives up)
   unsigned long long* stamps = nullptr;  // null, or [grid][FusedStepStampsPerGroup()]:
                                          // clocks at start, slice scored, counter
                                          // ready, records read, ranked, selected,
@@ -185,6 +205,11 @@ int FusedStepHeadsPerGroup(const PoolView& pool, int batch, int compute_units);
 // Workgroups of one launch: num_heads / heads_per_group per request.
 int FusedStepGrid(const PoolView& pool, int batch, int heads_per_group);
 int FusedStepStampsPerGroup();
+// Whether a launch takes FusedStepKernel<true> (a slice spans several score
+// passes of 8 pages, so each pass's rows load while the previous one reduces).
+bool FusedStepMultiPass(const PoolView& pool, int max_candidates, int heads_per_group);
+// Pages per workgroup of the stand-alone score kernel (E = 4096).
+int ScorePagesPerGroup(int total_candidates);
 void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t stream);
 
 // Certified intervals for E = 4096 with the fused step's score passes
@@ -192,6 +217,6 @@ void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t st
 void LaunchScorePages(const PoolView& pool, const float* d_queries, const int* d_cand_offsets,
                       const int* d_cand_ids, int batch, int total_candidates,
                       int max_candidates, float scale, float* d_mid, float* d_lo, float* d_hi,
-                      hipStream_t stream);
+                      FailReport fail, hipStream_t stream);
 
 }  // namespace dsdk

@@ -65,7 +65,6 @@ constexpr int kFLpt = 16;                 // lanes per token row (8 dims each)
 constexpr int kFDq = kFD / kFLpt;         // 8
 constexpr int kFTpc = kWave / kFLpt;      // 4 token rows per wave per chunk
 constexpr int kFUnroll = 4;               // chunks in flight per wave
-constexpr unsigned kSpinLimit = 1u << 22;  // polls (about 1 us each) before a timeout
 constexpr int kFSlots = kFMaxCand / kWave;  // candidates (or ranks) per lane: l + 64m
 constexpr int kFRescoreGroup = 16;            // exact chains per rescore group
 static_assert(kFMaxK <= kFMaxCand, "rank slots cover the candidate slots");
@@ -126,11 +125,6 @@ __device__ __forceinline__ unsigned long long LoadWord(unsigned long long* p) {
 
 __device__ __forceinline__ bool Current(unsigned long long w, unsigned epoch) {
   return static_cast<unsigned>(w >> 32) == epoch;
-}
-
-__device__ __forceinline__ void ReportFailure(const FusedArgs& a, int code) {
-  if (a.fail_flag == nullptr) return;
-  __hip_atomic_store(a.fail_flag, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // Ranks of the n <= 256 keys in sh.key (descending; equal keys by position):
@@ -242,7 +236,7 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int first, i
   float p_abs = 0.0f;
   if (active) {
     // An id outside the pool scores as an empty page and is reported.
-    if ((page < 0 || page >= pool.capacity) && half == 0 && lane == 0) ReportFailure(a, 3);
+    if (!InPool(page, pool.capacity) && half == 0 && lane == 0) ReportFailure(a.fail, kFailPageId);
     const float4* q4 = q_lds + half * 512 + lane;
     float4 qv[kRows];
 #pragma unroll
@@ -567,7 +561,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
   if (n > kFMaxCand) {
     // The caller's max_candidates understated the CSR: select nothing (the
     // outputs are zeros) and report it to the host.
-    if (writer && threadIdx.x == 0) ReportFailure(a, 2);
+    if (writer && threadIdx.x == 0) ReportFailure(a.fail, kFailShape);
     kk = 0;
   }
   const int lane = threadIdx.x & (kWave - 1);
@@ -595,19 +589,19 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
 #pragma unroll
     for (int m = 0; m < kFSlots; ++m) {
       const int i = lane + kWave * m;
-      w[m][0] = w[m][1] = w[m][2] = static_cast<unsigned long long>(a.epoch) << 32;
+      w[m][0] = w[m][1] = w[m][2] = static_cast<unsigned long long>(a.wait_tag) << 32;
       if (i < n) {
         const unsigned long long* rec = a.rec + 3 * static_cast<size_t>(begin + i);
         w[m][0] = rec[0];
         w[m][1] = rec[1];
         w[m][2] = rec[2];
-        ok = ok && Current(w[m][0], a.epoch) && Current(w[m][1], a.epoch) &&
-             Current(w[m][2], a.epoch);
+        ok = ok && Current(w[m][0], a.wait_tag) && Current(w[m][1], a.wait_tag) &&
+             Current(w[m][2], a.wait_tag);
       }
     }
     unsigned spins = 0;
     while (__ballot(!ok) != 0) {
-      if (++spins >= kSpinLimit) {
+      if (++spins >= a.spin_limit) {
         if (lane == 0) sh.fail = 1;
         break;
       }
@@ -620,10 +614,10 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
           unsigned long long* rec = a.rec + 3 * static_cast<size_t>(begin + i);
 #pragma unroll
           for (int x = 0; x < 3; ++x) {
-            if (!Current(w[m][x], a.epoch)) w[m][x] = LoadWord(rec + x);
+            if (!Current(w[m][x], a.wait_tag)) w[m][x] = LoadWord(rec + x);
           }
-          ok = ok && Current(w[m][0], a.epoch) && Current(w[m][1], a.epoch) &&
-               Current(w[m][2], a.epoch);
+          ok = ok && Current(w[m][0], a.wait_tag) && Current(w[m][1], a.wait_tag) &&
+               Current(w[m][2], a.wait_tag);
         }
       }
     }
@@ -641,7 +635,7 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
   __syncthreads();
   StampAt(a, sh, kRecords);
   if (sh.fail) {
-    if (threadIdx.x == 0) ReportFailure(a, 1);
+    if (threadIdx.x == 0) ReportFailure(a.fail, kFailWait);
     kk = 0;
   }
   if (kk > 0) {
@@ -836,8 +830,10 @@ __global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, Fuse
   const int groups = pool.num_heads / a.heads_per_group;
   const int r = blockIdx.x / groups;
   const int g = blockIdx.x - r * groups;
-  const int begin = a.cand_offsets[r];
-  const int n = a.cand_offsets[r + 1] - begin;
+  // A request whose offsets leave [0, total] is skipped (n = 0: nothing
+  // scored or selected, zero outputs) and reported.
+  int begin, n;
+  RequestRange(a.cand_offsets, r, a.total, g == 0 ? a.fail : FailReport{}, &begin, &n);
   // A request beyond kFMaxCand selects nothing (reported by the selection):
   // its slices are not scored.
   if (n <= kFMaxCand) {
@@ -874,8 +870,11 @@ __global__ __launch_bounds__(kFThreads) void ScorePagesKernel(PoolView pool, Fus
                                                               int pages_per_group) {
   __shared__ ScoreShared sh;
   const int r = blockIdx.y;
-  const int begin = a.cand_offsets[r];
-  const int n = a.cand_offsets[r + 1] - begin;
+  int begin, n;
+  if (!RequestRange(a.cand_offsets, r, a.total, blockIdx.x == 0 ? a.fail : FailReport{}, &begin,
+                    &n)) {
+    return;
+  }
   const int c0 = static_cast<int>(blockIdx.x) * pages_per_group;
   if (c0 >= n) return;
   const int c1 = n - c0 < pages_per_group ? n : c0 + pages_per_group;
@@ -887,16 +886,10 @@ __global__ __launch_bounds__(kFThreads) void ScorePagesKernel(PoolView pool, Fus
 void LaunchScorePages(const PoolView& pool, const float* d_queries, const int* d_cand_offsets,
                       const int* d_cand_ids, int batch, int total_candidates,
                       int max_candidates, float scale, float* d_mid, float* d_lo, float* d_hi,
-                      hipStream_t stream) {
+                      FailReport fail, hipStream_t stream) {
   if (batch <= 0 || max_candidates <= 0 || total_candidates <= 0) return;
   if (pool.elements != kFE) throw std::invalid_argument("ScorePages needs E = 4096");
-  // About two workgroups per CU in all, 8..128 pages each (config 3,
-  // 65,536 candidates: 128 pages per workgroup scored in 184.7 us, against
-  // 187.5 at 64, 191.4 at 256 and 188.6 at 32).
-  int per = (total_candidates + 511) / 512;
-  per = ((per + kFPagesPerPass - 1) / kFPagesPerPass) * kFPagesPerPass;
-  if (per < kFPagesPerPass) per = kFPagesPerPass;
-  if (per > 128) per = 128;
+  const int per = ScorePagesPerGroup(total_candidates);
   FusedArgs a;
   a.queries = d_queries;
   a.cand_offsets = d_cand_offsets;
@@ -907,9 +900,27 @@ void LaunchScorePages(const PoolView& pool, const float* d_queries, const int* d
   a.mid = d_mid;
   a.lo = d_lo;
   a.hi = d_hi;
+  a.fail = fail;
   const dim3 grid((max_candidates + per - 1) / per, batch);
   hipLaunchKernelGGL(ScorePagesKernel, grid, dim3(kFThreads), 0, stream, pool, a, per);
   DSD_HIP_CHECK(hipGetLastError());
+}
+
+int ScorePagesPerGroup(int total_candidates) {
+  // About two workgroups per CU in all, 8..128 pages each (config 3,
+  // 65,536 candidates: 128 pages per workgroup scored in 184.7 us, against
+  // 187.5 at 64, 191.4 at 256 and 188.6 at 32).
+  int per = (total_candidates + 511) / 512;
+  per = ((per + kFPagesPerPass - 1) / kFPagesPerPass) * kFPagesPerPass;
+  if (per < kFPagesPerPass) per = kFPagesPerPass;
+  if (per > 128) per = 128;
+  return per;
+}
+
+bool FusedStepMultiPass(const PoolView& pool, int max_candidates, int heads_per_group) {
+  // Slices of a request split its candidates evenly over its workgroups.
+  const int groups = pool.num_heads / heads_per_group;
+  return (max_candidates + groups - 1) / groups > kFPagesPerPass;
 }
 
 bool FusedStepSupported(const PoolView& pool, int max_candidates, int top_k) {
@@ -941,10 +952,7 @@ void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t st
   }
   if (pool.num_heads % hpw != 0) throw std::invalid_argument("heads per group must divide num_heads");
   const int grid = FusedStepGrid(pool, args.batch, hpw);
-  // Slices of a request split its candidates evenly over its workgroups.
-  const int groups = pool.num_heads / hpw;
-  const bool multi_pass = (args.max_candidates + groups - 1) / groups > kFPagesPerPass;
-  if (multi_pass) {
+  if (FusedStepMultiPass(pool, args.max_candidates, hpw)) {
     hipLaunchKernelGGL(FusedStepKernel<true>, dim3(grid), dim3(kFThreads), 0, stream, pool, args);
   } else {
     hipLaunchKernelGGL(FusedStepKernel<false>, dim3(grid), dim3(kFThreads), 0, stream, pool, args);

@@ -94,7 +94,6 @@ std::vector<PageId> PagedKvCache::ReservePagesForRequest(int request_id,
   std::sort(ids.begin(), ids.end());
   int start = NextStartToken(request_id);
   auto& list = request_pages_[request_id];
-  const int E = ElementsPerToken();
   for (std::size_t i = 0; i < ids.size(); ++i) {
     const PageId id = ids[i];
     ClearSummary(id);

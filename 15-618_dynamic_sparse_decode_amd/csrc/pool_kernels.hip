@@ -177,10 +177,17 @@ __global__ __launch_bounds__(kPoolThreads) void PrefillSyntheticKernel(
   }
 }
 
-// One workgroup per (page segment, kPoolThreads elements of the token row):
-// the segment's tokens in offset order, summary by the running mean.  The
-// metadata is read straight from the caller's pinned staging (layout at
-// LaunchAppendSynthetic), so the append is one launch with no copies.
+// One workgroup per (page segment, kPoolThreads elements of the token row),
+// summary by the running mean s = (s*old + k)/new, each operation rounded
+// separately (the host rule).  A page's single token of the call uses the
+// reference's counts: old = the page's token count - 1, new = that count
+// (src/device_page_pool.cpp:219-231; the serving loop appends one token per
+// page per step, so this is every real call).  The reference runs one block
+// per token, so several tokens of one page in one call race there; here
+// they apply in offset order with old = offset, the host cache's sequence
+// (src/paged_kv_cache.cpp:231-238).  The metadata is read straight from the
+// caller's pinned staging (layout at LaunchAppendSynthetic), so the append
+// is one launch with no copies.
 __global__ __launch_bounds__(kPoolThreads) void AppendSyntheticKernel(PoolView pool,
                                                                       const int* __restrict__ meta,
                                                                       int n, int num_segments) {
@@ -199,7 +206,8 @@ __global__ __launch_bounds__(kPoolThreads) void AppendSyntheticKernel(PoolView p
   float* summary = pool.summaries + static_cast<size_t>(page) * E;
   const int e = static_cast<int>(blockIdx.y * kPoolThreads + threadIdx.x);
   if (e < E) {
-    float s = offsets[begin] == 0 ? 0.0f : summary[e];
+    float s = summary[e];
+    const bool single = end - begin == 1;
     for (int q = begin; q < end; ++q) {
       const int off = offsets[q];
       const float k = DecodeValue(request_ids[q], decode_steps[q], e, 1);
@@ -207,8 +215,12 @@ __global__ __launch_bounds__(kPoolThreads) void AppendSyntheticKernel(PoolView p
       const size_t dst = base + static_cast<size_t>(off) * E + e;
       pool.keys[dst] = k;
       pool.values[dst] = v;
-      const float old_count = static_cast<float>(off);
-      s = __fdiv_rn(__fadd_rn(__fmul_rn(s, old_count), k), __fadd_rn(old_count, 1.0f));
+      const int old = single ? counts[q] - 1 : off;
+      // A page's first token: whatever the row held before (a lazily freed
+      // page keeps its old summary) is multiplied by 0, i.e. dropped.
+      if (old == 0) s = 0.0f;
+      s = __fdiv_rn(__fadd_rn(__fmul_rn(s, static_cast<float>(old)), k),
+                    static_cast<float>(old + 1));
     }
     summary[e] = s;
   }

@@ -4,6 +4,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include "dsd_internal.h"
+
 #include <cmath>
 #include <cstdint>
 
@@ -11,6 +13,39 @@ namespace dsdk {
 namespace {
 
 constexpr int kWave = 64;
+
+// Stores (epoch << 32) | code into the launch's failure word (a system-scope
+// store: the word is pinned host memory the host reads after the step).
+__device__ __forceinline__ void ReportFailure(const FailReport& f, int code) {
+  if (f.word == nullptr) return;
+  __hip_atomic_store(f.word,
+                     (static_cast<unsigned long long>(f.epoch) << 32) |
+                         static_cast<unsigned>(code),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// The CSR bounds of request r: false (and kFailShape reported) when its
+// offsets leave [0, total] or decrease, so no candidate index outside the
+// launch's buffers is ever formed.
+__device__ __forceinline__ bool RequestRange(const int* cand_offsets, int r, int total,
+                                             const FailReport& f, int* begin, int* n) {
+  const int b = cand_offsets[r];
+  const int e = cand_offsets[r + 1];
+  if (b < 0 || e < b || e > total) {
+    ReportFailure(f, kFailShape);
+    *begin = 0;
+    *n = 0;
+    return false;
+  }
+  *begin = b;
+  *n = e - b;
+  return true;
+}
+
+// A candidate page id usable as an index into the pool arrays.
+__device__ __forceinline__ bool InPool(int page, int capacity) {
+  return page >= 0 && page < capacity;
+}
 
 // ---- certified score intervals ---------------------------------------------
 // The reference score is acc = fl(acc + fl(q_i*s_i)) over i = 0..E-1, then

@@ -28,20 +28,28 @@ namespace {
 template <bool kVec4>
 __global__ __launch_bounds__(kWave) void ScoreExactKernel(
     const float* __restrict__ queries, const float* __restrict__ summaries,
-    const int* __restrict__ token_counts, const int* __restrict__ cand_offsets,
-    const int* __restrict__ cand_ids, int E, float scale,
-    float* __restrict__ scores) {
+    const int* __restrict__ token_counts, int capacity, const int* __restrict__ cand_offsets,
+    const int* __restrict__ cand_ids, int total, int E, float scale,
+    float* __restrict__ scores, FailReport fail) {
   const int r = blockIdx.y;
-  const int begin = cand_offsets[r];
-  const int end = cand_offsets[r + 1];
+  int begin, n;
+  if (!RequestRange(cand_offsets, r, total, fail, &begin, &n)) return;
+  const int end = begin + n;
   const int first = begin + blockIdx.x * kWave;
   if (first >= end) return;
   const int c = first + static_cast<int>(threadIdx.x);
   const bool active = c < end;
-  const int page = active ? cand_ids[c] : cand_ids[first];
+  int page = active ? cand_ids[c] : cand_ids[first];
   // A page holding no tokens reads as an all-zero summary
-  // (src/paged_kv_cache.cpp:457-459); the products q*0 are still formed.
-  const bool zero = !active || token_counts[page] == 0;
+  // (src/paged_kv_cache.cpp:457-459); the products q*0 are still formed.  An
+  // id outside the pool scores as such a page and is reported.
+  bool zero = !active;
+  if (!InPool(page, capacity)) {
+    if (active) ReportFailure(fail, kFailPageId);
+    page = 0;
+    zero = true;
+  }
+  zero = zero || token_counts[page] == 0;
   const float* __restrict__ q = queries + static_cast<size_t>(r) * E;
   const float* __restrict__ s = summaries + static_cast<size_t>(page) * E;
 
@@ -90,18 +98,25 @@ constexpr int kBoundWaves = 4;
 // from the (cache-resident) operands in pass 2.
 __global__ __launch_bounds__(kBoundWaves * kWave) void ScoreBoundGenericKernel(
     const float* __restrict__ queries, const float* __restrict__ summaries,
-    const int* __restrict__ token_counts, const int* __restrict__ cand_offsets,
-    const int* __restrict__ cand_ids, int E, float scale, float* __restrict__ mid_out,
-    float* __restrict__ lo_out, float* __restrict__ hi_out) {
+    const int* __restrict__ token_counts, int capacity, const int* __restrict__ cand_offsets,
+    const int* __restrict__ cand_ids, int total, int E, float scale, float* __restrict__ mid_out,
+    float* __restrict__ lo_out, float* __restrict__ hi_out, FailReport fail) {
   const int BL = E / kWave;
   const int r = blockIdx.y;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int begin = cand_offsets[r];
+  int begin, n;
+  if (!RequestRange(cand_offsets, r, total, fail, &begin, &n)) return;
   const int c = begin + blockIdx.x * kBoundWaves + wave;
-  if (c >= cand_offsets[r + 1]) return;
-  const int page = cand_ids[c];
-  const bool zero = token_counts[page] == 0;
+  if (c >= begin + n) return;
+  int page = cand_ids[c];
+  bool zero = false;
+  if (!InPool(page, capacity)) {  // scores as an empty page, reported
+    if (lane == 0) ReportFailure(fail, kFailPageId);
+    page = 0;
+    zero = true;
+  }
+  zero = zero || token_counts[page] == 0;
   const float* __restrict__ q = queries + static_cast<size_t>(r) * E + lane * BL;
   const float* __restrict__ s = summaries + static_cast<size_t>(page) * E + lane * BL;
   double block = 0.0, abs_p = 0.0;
@@ -141,12 +156,17 @@ constexpr int kSelectMaxKeys = 8192;  // 64 KiB of LDS
 
 __global__ __launch_bounds__(256) void SelectTopKKernel(
     const float* __restrict__ scores, const int* __restrict__ cand_offsets,
-    const int* __restrict__ cand_ids, int top_k, int* __restrict__ selected,
-    int* __restrict__ counts) {
+    const int* __restrict__ cand_ids, int total, int max_candidates, int top_k,
+    int* __restrict__ selected, int* __restrict__ counts, FailReport fail) {
   extern __shared__ uint64_t keys[];
   const int r = blockIdx.x;
-  const int begin = cand_offsets[r];
-  const int n = cand_offsets[r + 1] - begin;
+  int begin, n;
+  RequestRange(cand_offsets, r, total, fail, &begin, &n);
+  if (n > max_candidates) {
+    // The launch (LDS, score grid) was sized for max_candidates.
+    if (threadIdx.x == 0) ReportFailure(fail, kFailShape);
+    n = 0;
+  }
   const int kk = top_k <= 0 ? 0 : (top_k < n ? top_k : n);
   if (kk == 0) {
     if (threadIdx.x == 0) counts[r] = 0;
@@ -299,9 +319,9 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
     const float* __restrict__ mid, const float* __restrict__ lo,
     const float* __restrict__ hi, const float* __restrict__ queries,
     const float* __restrict__ summaries, const int* __restrict__ token_counts, int capacity,
-    const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int E,
-    float scale, int top_k, int* __restrict__ selected, int* __restrict__ counts,
-    int* __restrict__ exact_pages) {
+    const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int total,
+    int max_candidates, int E, float scale, int top_k, int* __restrict__ selected,
+    int* __restrict__ counts, int* __restrict__ exact_pages, FailReport fail) {
   __shared__ uint64_t keys[kCertMaxKeys];   // by candidate
   __shared__ float s_lo[kCertMaxKeys];
   __shared__ float s_hi[kCertMaxKeys];
@@ -315,8 +335,14 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
   __shared__ unsigned long long s_prefix;
   __shared__ int s_need, s_all, s_count, s_tie, s_nflag;
   const int r = blockIdx.x;
-  const int begin = cand_offsets[r];
-  const int n = cand_offsets[r + 1] - begin;
+  int begin, n;
+  RequestRange(cand_offsets, r, total, fail, &begin, &n);
+  if (n > max_candidates || n > kCertMaxKeys) {
+    // Only max_candidates were scored (and this kernel holds kCertMaxKeys):
+    // select nothing and report it.
+    if (threadIdx.x == 0) ReportFailure(fail, kFailShape);
+    n = 0;
+  }
   const int kk = top_k <= 0 ? 0 : (top_k < n ? top_k : n);
   if (kk == 0) {
     if (threadIdx.x == 0) counts[r] = 0;
@@ -456,9 +482,9 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
     const float* __restrict__ mid, const float* __restrict__ lo,
     const float* __restrict__ hi, const float* __restrict__ queries,
     const float* __restrict__ summaries, const int* __restrict__ token_counts, int capacity,
-    const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int E,
-    float scale, int top_k, int* __restrict__ selected, int* __restrict__ counts,
-    int* __restrict__ exact_pages) {
+    const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int total,
+    int max_candidates, int E, float scale, int top_k, int* __restrict__ selected,
+    int* __restrict__ counts, int* __restrict__ exact_pages, FailReport fail) {
   __shared__ uint64_t s_key[kRankMax];
   __shared__ float s_lo[kRankMax];
   __shared__ float s_hi[kRankMax];
@@ -468,8 +494,14 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
   __shared__ int s_nflag;
   __shared__ __align__(16) float tile[RescoreFloats<kSelRescoreGroup>()];
   const int r = blockIdx.x;
-  const int begin = cand_offsets[r];
-  const int n = cand_offsets[r + 1] - begin;
+  int begin, n;
+  RequestRange(cand_offsets, r, total, fail, &begin, &n);
+  if (n > max_candidates || n > kRankMax) {
+    // Only max_candidates were scored (and this kernel holds kRankMax):
+    // select nothing and report it.
+    if (threadIdx.x == 0) ReportFailure(fail, kFailShape);
+    n = 0;
+  }
   const int kk = top_k <= 0 ? 0 : (top_k < n ? top_k : n);
   if (kk == 0) {
     if (threadIdx.x == 0) counts[r] = 0;
@@ -635,7 +667,7 @@ __global__ __launch_bounds__(kAttnThreads) void AttentionKernel(
       const int slot = f / ps;
       const int t = f - slot * ps;
       const int page = args.list_ids[start + slot];
-      valid = t < pool.token_counts[page];
+      valid = InPool(page, pool.capacity) && t < pool.token_counts[page];
       if (valid) {
         const size_t off = static_cast<size_t>(page) * pool.page_elems +
                            static_cast<size_t>(t) * E + head_off;
@@ -775,7 +807,7 @@ __global__ __launch_bounds__(WAVES * kWave) void AttentionFastKernel(
         const int slot = f / ps;
         const int t = f - slot * ps;
         const int page = args.list_ids[start + slot];
-        valid[u] = t < pool.token_counts[page];
+        valid[u] = InPool(page, pool.capacity) && t < pool.token_counts[page];
         if (valid[u]) {
           const size_t off = static_cast<size_t>(page) * pool.page_elems +
                              static_cast<size_t>(t) * E + head_off;
@@ -896,18 +928,20 @@ void LaunchAttentionT(const PoolView& pool, const AttentionArgs& args,
 
 void LaunchScoreExact(const PoolView& pool, const float* d_queries,
                       const int* d_cand_offsets, const int* d_cand_ids,
-                      int batch, int max_candidates, float scale,
-                      float* d_scores, hipStream_t stream) {
+                      int batch, int total_candidates, int max_candidates, float scale,
+                      float* d_scores, FailReport fail, hipStream_t stream) {
   if (batch <= 0 || max_candidates <= 0) return;
   const dim3 grid((max_candidates + kWave - 1) / kWave, batch);
   if (pool.elements % 4 == 0) {
     hipLaunchKernelGGL(ScoreExactKernel<true>, grid, dim3(kWave), 0, stream,
-                       d_queries, pool.summaries, pool.token_counts,
-                       d_cand_offsets, d_cand_ids, pool.elements, scale, d_scores);
+                       d_queries, pool.summaries, pool.token_counts, pool.capacity,
+                       d_cand_offsets, d_cand_ids, total_candidates, pool.elements, scale,
+                       d_scores, fail);
   } else {
     hipLaunchKernelGGL(ScoreExactKernel<false>, grid, dim3(kWave), 0, stream,
-                       d_queries, pool.summaries, pool.token_counts,
-                       d_cand_offsets, d_cand_ids, pool.elements, scale, d_scores);
+                       d_queries, pool.summaries, pool.token_counts, pool.capacity,
+                       d_cand_offsets, d_cand_ids, total_candidates, pool.elements, scale,
+                       d_scores, fail);
   }
   DSD_HIP_CHECK(hipGetLastError());
 }
@@ -921,19 +955,20 @@ bool CertifiedScoringSupported(int elements, int max_candidates) {
 void LaunchScoreBounds(const PoolView& pool, const float* d_queries,
                        const int* d_cand_offsets, const int* d_cand_ids, int batch,
                        int total_candidates, int max_candidates, float scale, float* d_mid,
-                       float* d_lo, float* d_hi, hipStream_t stream) {
+                       float* d_lo, float* d_hi, FailReport fail, hipStream_t stream) {
   if (batch <= 0 || max_candidates <= 0) return;
   const dim3 grid((max_candidates + kBoundWaves - 1) / kBoundWaves, batch);
   const dim3 block(kBoundWaves * kWave);
   if (pool.elements == 4096) {
-    // The fused step's float score passes, 8..64 pages per workgroup.
+    // The fused step's float score passes, 8..128 pages per workgroup.
     LaunchScorePages(pool, d_queries, d_cand_offsets, d_cand_ids, batch, total_candidates,
-                     max_candidates, scale, d_mid, d_lo, d_hi, stream);
+                     max_candidates, scale, d_mid, d_lo, d_hi, fail, stream);
     return;
   } else {
     hipLaunchKernelGGL(ScoreBoundGenericKernel, grid, block, 0, stream, d_queries,
-                       pool.summaries, pool.token_counts, d_cand_offsets, d_cand_ids,
-                       pool.elements, scale, d_mid, d_lo, d_hi);
+                       pool.summaries, pool.token_counts, pool.capacity, d_cand_offsets,
+                       d_cand_ids, total_candidates, pool.elements, scale, d_mid, d_lo, d_hi,
+                       fail);
   }
   DSD_HIP_CHECK(hipGetLastError());
 }
@@ -941,17 +976,18 @@ void LaunchScoreBounds(const PoolView& pool, const float* d_queries,
 void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float* d_lo,
                            const float* d_hi, const float* d_queries,
                            const int* d_cand_offsets, const int* d_cand_ids, int batch,
-                           int max_candidates, float scale, int top_k, int* d_selected,
-                           int* d_counts, int* d_exact_pages, hipStream_t stream) {
+                           int total_candidates, int max_candidates, float scale, int top_k,
+                           int* d_selected, int* d_counts, int* d_exact_pages, FailReport fail,
+                           hipStream_t stream) {
   if (batch <= 0) return;
   if (max_candidates <= kRankMax) {
     // Always four waves: three of them form products while wave 0 runs the
     // exact chains.
     hipLaunchKernelGGL(SelectCertifiedRankKernel, dim3(batch), dim3(kRankMax), 0, stream,
                        d_mid, d_lo, d_hi, d_queries, pool.summaries, pool.token_counts,
-                       pool.capacity, d_cand_offsets, d_cand_ids, pool.elements, scale, top_k,
-                       d_selected,
-                       d_counts, d_exact_pages);
+                       pool.capacity, d_cand_offsets, d_cand_ids, total_candidates,
+                       max_candidates, pool.elements, scale, top_k, d_selected, d_counts,
+                       d_exact_pages, fail);
     DSD_HIP_CHECK(hipGetLastError());
     return;
   }
@@ -966,17 +1002,17 @@ void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float
   }
   hipLaunchKernelGGL(SelectCertifiedKernel, dim3(batch), dim3(kSelThreads), 0, stream, d_mid,
                      d_lo, d_hi, d_queries, pool.summaries, pool.token_counts, pool.capacity,
-                     d_cand_offsets, d_cand_ids, pool.elements, scale, top_k, d_selected,
-                     d_counts, d_exact_pages);
+                     d_cand_offsets, d_cand_ids, total_candidates, max_candidates,
+                     pool.elements, scale, top_k, d_selected, d_counts, d_exact_pages, fail);
   DSD_HIP_CHECK(hipGetLastError());
 }
 
 int SelectMaxCandidates() { return kSelectMaxKeys; }
 
 void LaunchSelectTopK(const float* d_scores, const int* d_cand_offsets,
-                      const int* d_cand_ids, int batch, int max_candidates,
-                      int top_k, int* d_selected, int* d_counts,
-                      hipStream_t stream) {
+                      const int* d_cand_ids, int batch, int total_candidates,
+                      int max_candidates, int top_k, int* d_selected, int* d_counts,
+                      FailReport fail, hipStream_t stream) {
   if (batch <= 0) return;
   int m = 1;
   while (m < max_candidates) m <<= 1;
@@ -990,7 +1026,8 @@ void LaunchSelectTopK(const float* d_scores, const int* d_cand_offsets,
   if (threads > 256) threads = 256;
   hipLaunchKernelGGL(SelectTopKKernel, dim3(batch), dim3(threads),
                      sizeof(uint64_t) * static_cast<size_t>(m), stream, d_scores,
-                     d_cand_offsets, d_cand_ids, top_k, d_selected, d_counts);
+                     d_cand_offsets, d_cand_ids, total_candidates, max_candidates, top_k,
+                     d_selected, d_counts, fail);
   DSD_HIP_CHECK(hipGetLastError());
 }
 

@@ -257,7 +257,15 @@ int dsd_host_free(void* p);
  * enqueues work on `stream` (a hipStream_t; NULL = the context's stream).
  * total_candidates and max_candidates (largest n_r) must describe the CSR.
  * selected ([batch][top_k], unused slots untouched), selected_counts,
- * scores may be NULL (context scratch is used). */
+ * scores may be NULL (context scratch is used).
+ * The inputs are checked on the device, not the host: a request whose
+ * offsets leave [0, total_candidates] or whose list is longer than
+ * max_candidates selects nothing, and a candidate id outside the pool scores
+ * as an empty page; either way the step's kernels finish normally, the
+ * request's outputs are zeros, and dsd_sparse_device_status reports it.
+ * Steps on one context share its scratch: a step on a stream other than the
+ * previous step's first waits for the previous stream's work, so that
+ * stream must still be valid then (it is used for an event record). */
 int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
                                 int total_candidates, int max_candidates,
                                 const float* d_queries,
@@ -265,6 +273,39 @@ int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
                                 const int* d_cand_ids, float* d_outputs,
                                 float* d_scores, int* d_selected,
                                 int* d_selected_counts, void* stream);
+
+/* The launch form of the context's last step (for tests and benchmarks
+ * that must know which kernels ran).  No reference counterpart. */
+typedef struct dsd_launch_info {
+  int fused;                 /* 1: the single-launch step, 0: three kernels */
+  int certified;             /* 1: certified scoring, 0: exact chains */
+  int multi_pass;            /* fused: slices span several 8-page passes */
+  int heads_per_group;       /* fused: heads per 1024-thread workgroup */
+  int grid;                  /* fused: workgroups; three-kernel at E = 4096:
+                                score workgroups */
+  int score_pages_per_group; /* three-kernel at E = 4096: pages per score
+                                workgroup */
+} dsd_launch_info;
+int dsd_sparse_last_launch(const dsd_sparse_ctx* ctx, dsd_launch_info* out);
+
+/* Synchronizes the device, then reports (as its status, with the message in
+ * dsd_last_error) the last input failure any step of the context recorded
+ * and not yet reported -- e.g. from dsd_sparse_run_batch_device, which
+ * cannot report it itself -- and clears it: DSD_ERR_INVALID_ARGUMENT for a
+ * candidate list that does not fit the step's sizes, DSD_ERR_OUT_OF_RANGE
+ * for a page id outside the pool, DSD_ERR_RUNTIME for a timed-out wait.
+ * Host-buffer steps report their own failures when they return.  No
+ * reference counterpart (the reference's RunBatch checks on the host,
+ * src/cuda/sparse_batched_attention.cu:600-608). */
+int dsd_sparse_device_status(dsd_sparse_ctx* ctx);
+
+/* The single-launch step's cross-workgroup waits poll at most spin_limit
+ * times (default 2^17, about 0.1-0.3 s) before they give up: the step then
+ * selects nothing for the request, its outputs are zeros and the failure is
+ * reported (DSD_ERR_RUNTIME).  never_ready != 0 makes every wait look for a
+ * tag no workgroup writes, so every wait gives up: a test hook for that
+ * path, which never reaches a GPU hang.  No reference counterpart. */
+int dsd_sparse_set_wait_limit(dsd_sparse_ctx* ctx, unsigned spin_limit, int never_ready);
 
 /* Re-enqueue one stage of the last dsd_sparse_run_batch_device call on the
  * same buffers (stage 0 = score, 1 = select, 2 = attention, each as its own

@@ -50,31 +50,6 @@ void oracle_append_summary(float* summary, const float* key, int old_count,
   }
 }
 
-/* src/device_page_pool.cpp:122-138: four hash-combine rounds (request,
- * step, element, stream, each offset by its constant), then a 32-bit
- * finaliser, then x mod 2001 shifted to [-1000, 1000] and divided by 1000. */
-static uint32_t oracle_hash_combine(uint32_t x, int v, uint32_t c) {
-  return x ^ ((uint32_t)v + c + (x << 6) + (x >> 2));
-}
-
-void oracle_synthetic_decode_row(int request_id, int decode_step, int stream,
-                                 int elements, float* out) {
-  int e;
-  for (e = 0; e < elements; ++e) {
-    uint32_t x = 0x9e3779b9u;
-    x = oracle_hash_combine(x, request_id, 0x85ebca6bu);
-    x = oracle_hash_combine(x, decode_step, 0xc2b2ae35u);
-    x = oracle_hash_combine(x, e, 0x165667b1u);
-    x = oracle_hash_combine(x, stream, 0xd3a2646cu);
-    x ^= x >> 16;
-    x *= 0x7feb352du;
-    x ^= x >> 15;
-    x *= 0x846ca68bu;
-    x ^= x >> 16;
-    out[e] = (float)((int)(x % 2001u) - 1000) / 1000.0f;
-  }
-}
-
 /* src/reference_kernels.cpp:13-19 */
 float oracle_dot(const float* a, const float* b, int count) {
   float acc = 0.0f;

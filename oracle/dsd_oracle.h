@@ -38,16 +38,6 @@ void oracle_page_summary(const float* keys, int token_count, int elements,
 void oracle_append_summary(float* summary, const float* key, int old_count,
                            int elements);
 
-/* Synthetic decode-token payload row: out[e] for e < elements is the
- * reference's integer hash of (request_id, decode_step, e, stream) mapped
- * onto the grid k/1000, k in [-1000, 1000]; stream 1 = key, 2 = value
- * (src/device_page_pool.cpp:122-138, used at :223-224).  Parity unpinned
- * for the hash constants: the reference holds no vectors of this
- * device-only generator, so only the grid and the uniformity over the 2001
- * values are checked (tests/test_oracle.py). */
-void oracle_synthetic_decode_row(int request_id, int decode_step, int stream,
-                                 int elements, float* out);
-
 /* Sequential dot product, acc += a[i]*b[i] (src/reference_kernels.cpp:13-19). */
 float oracle_dot(const float* a, const float* b, int count);
 

@@ -73,13 +73,6 @@ def pool_summaries(key_pool, token_counts, elements: int, page_ids=None):
     return out
 
 
-def synthetic_decode_row(request_id: int, decode_step: int, stream: int, elements: int):
-    out = np.empty(elements, np.float32)
-    lib().oracle_synthetic_decode_row(int(request_id), int(decode_step), int(stream),
-                                      int(elements), P(out))
-    return out
-
-
 def append_summary(summary, key, old_count: int):
     s = f32(summary).copy()
     k = f32(key)
@@ -135,6 +128,34 @@ def sparse_batch(queries, key_pool, value_pool, summaries, token_counts, cand_of
         stage_ms += ms
     selected = [sel[r * kk: r * kk + counts[r]].copy() for r in range(B)]
     return scores[:total].copy(), selected, outs
+
+
+def request_step(query, keys, values, counts, page_ids, num_heads, head_dim, page_size, top_k,
+                 dense=False):
+    """sparse_cpu for one request whose pages are given in logical order:
+    keys / values [n][page_size][E], counts [n] and page_ids [n] (distinct).
+    Composes the oracle's own rows as oracle_sparse_step does: summaries
+    (oracle_page_summary), scores (oracle_score_pages), top-k by (score desc,
+    page id asc) over the real ids (oracle_select_topk), then gather +
+    attention over the selected pages in selected order (oracle_attention).
+    Returns (selected ids, sparse output [E], dense output [E] or None) --
+    dense is oracle_attention over every page in logical order (dense_cpu).
+    Lets a test stream a large batch one request at a time."""
+    E = num_heads * head_dim
+    ids = i32(page_ids)
+    n = len(ids)
+    cnt = i32(counts)
+    pos = np.arange(n, dtype=np.int32)
+    summ = pool_summaries(keys, cnt, E)
+    scores = score_pages(query, summ, cnt, pos, head_dim)
+    selected = select_topk(scores, ids, top_k) if n else np.zeros(0, np.int32)
+    where = {int(p): j for j, p in enumerate(ids)}
+    sel_pos = np.array([where[int(p)] for p in selected], np.int32)
+    out = attention(query, keys, values, cnt, sel_pos, num_heads, head_dim, page_size)
+    dense_out = None
+    if dense:
+        dense_out = attention(query, keys, values, cnt, pos, num_heads, head_dim, page_size)
+    return selected, out, dense_out
 
 
 def dense_batch(queries, key_pool, value_pool, token_counts, cand_offsets, cand_ids,

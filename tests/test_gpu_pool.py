@@ -256,12 +256,22 @@ def test_large_uploads_round_trip(gpu, pinned):
 
 
 @pytest.mark.parametrize("heads,head_dim", [(2, 64), (4, 96)])
-def test_synthetic_append_matches_oracle(gpu, heads, head_dim):
-    """dsd_pool_append_synthetic: K/V rows from the reference's decode hash,
-    running-mean summaries in offset order (several tokens of one page in one
-    call, given out of order, and a second call continuing the pages), page
-    counts and live flags, and the reference's transfer accounting (five
-    copies of n ints per call)."""
+def test_synthetic_append_summaries_follow_the_running_mean(gpu, heads, head_dim):
+    """dsd_pool_append_synthetic (reference AppendTokensSynthetic,
+    src/device_page_pool.cpp:904-983, kernel :190-237).  The generated K/V
+    values themselves have no reference vectors (the reference's generator
+    is device-only), so what is checked is everything around them:
+      * every value lies on the reference's grid k/1000, k in [-1000, 1000],
+        and rows differ between key and value streams, decode steps and
+        requests, and are a function of (request, step) only;
+      * each summary equals the oracle's running mean (oracle_append_summary,
+        the host rule of src/paged_kv_cache.cpp:231-238) applied to the K rows
+        the kernel wrote -- in offset order for several tokens of one page in
+        one call, and with the reference's counts (old = the page's token
+        count - 1) for a page's single token of a call, also when that token
+        is not the page's last;
+      * page counts, live flags and the reference's transfer accounting (five
+        copies of n ints per call)."""
     ps = 4
     E = heads * head_dim
     pool = gpu.DevicePagePool(heads, head_dim, ps, 8)
@@ -270,27 +280,46 @@ def test_synthetic_append_matches_oracle(gpu, heads, head_dim):
         # page, offset, page count after the call, request, decode step
         [(3, 2, 3, 11, 2), (5, 0, 1, 12, 0), (3, 0, 3, 11, 0), (3, 1, 3, 11, 1)],
         [(5, 1, 2, 12, 1), (3, 3, 4, 11, 3)],
+        # one token rewriting offset 0 of a 2-token page: old count = 1
+        [(5, 0, 2, 12, 5)],
+        # the same (request, step) as page 3's offset 0, into another page
+        [(6, 0, 1, 11, 0)],
     ]
-    keys = {p: np.zeros((ps, E), np.float32) for p in (3, 5)}
-    vals = {p: np.zeros((ps, E), np.float32) for p in (3, 5)}
-    summ = {p: np.zeros(E, np.float32) for p in (3, 5)}
+    summ = {p: np.zeros(E, np.float32) for p in (3, 5, 6)}
+    rows = {}
     for toks in calls:
         cols = list(zip(*toks))
         pool.append_synthetic(*[np.array(c, np.int32) for c in cols])
-        for page, off, _, req, step in sorted(toks, key=lambda t: (t[0], t[1])):
-            k = orc.synthetic_decode_row(req, step, 1, E)
-            keys[page][off] = k
-            vals[page][off] = orc.synthetic_decode_row(req, step, 2, E)
-            summ[page] = orc.append_summary(summ[page], k, off)
+        counts, _ = pool.download_meta()
+        pages = sorted({t[0] for t in toks})
+        written = {p: pool.download_page(p) for p in pages}
+        for p in pages:
+            seg = sorted((t for t in toks if t[0] == p), key=lambda t: t[1])
+            k_all = written[p][0].reshape(-1, E)
+            v_all = written[p][1].reshape(-1, E)
+            for page, off, cnt, req, step in seg:
+                k, v = k_all[off].copy(), v_all[off].copy()
+                rows.setdefault((req, step), (k, v))
+                old = cnt - 1 if len(seg) == 1 else off
+                summ[p] = orc.append_summary(summ[p], k, old)
     st = pool.transfer_stats()
-    assert st["h2d_calls"] == 10 and st["h2d_bytes"] == 5 * 4 * (4 + 2)
+    assert st["h2d_calls"] == 5 * len(calls)
+    assert st["h2d_bytes"] == 5 * 4 * sum(len(c) for c in calls)
     counts, live = pool.download_meta()
-    assert counts[3] == 4 and counts[5] == 2 and live[3] == 1 and live[5] == 1
-    assert counts[[0, 1, 2, 4, 6, 7]].tolist() == [0] * 6
-    got = pool.download_summaries([3, 5])
-    for i, p in enumerate((3, 5)):
-        k, v = pool.download_page(p)
-        n = int(counts[p])
-        assert np.array_equal(k.reshape(-1, E).view(np.uint32), keys[p][:n].view(np.uint32))
-        assert np.array_equal(v.reshape(-1, E).view(np.uint32), vals[p][:n].view(np.uint32))
-        assert np.array_equal(got[i].view(np.uint32), summ[p].view(np.uint32))
+    assert counts[[3, 5, 6]].tolist() == [4, 2, 1] and live[[3, 5, 6]].tolist() == [1, 1, 1]
+    assert counts[[0, 1, 2, 4, 7]].tolist() == [0] * 5
+    got = pool.download_summaries([3, 5, 6])
+    for i, p in enumerate((3, 5, 6)):
+        assert np.array_equal(got[i].view(np.uint32), summ[p].view(np.uint32)), p
+    # the grid, and what enters the generator
+    allv = np.concatenate([np.concatenate(kv) for kv in rows.values()])
+    grid = np.rint(allv.astype(np.float64) * 1000.0)
+    assert np.array_equal(allv, (grid / 1000.0).astype(np.float32))
+    assert grid.min() >= -1000 and grid.max() <= 1000
+    k0, v0 = rows[(11, 0)]
+    assert not np.array_equal(k0, v0)                        # stream enters
+    assert not np.array_equal(k0, rows[(11, 1)][0])          # decode step enters
+    assert not np.array_equal(rows[(12, 0)][0], k0)          # request enters
+    assert len(np.unique(k0)) > E // 2                       # element enters
+    k6, v6 = pool.download_page(6)
+    assert np.array_equal(k6, k0) and np.array_equal(v6, v0)  # page does not

@@ -283,29 +283,31 @@ def test_planted_mistakes_are_caught():
     assert orc.max_abs_diff(o_bad, c["ref_sparse_out"]) > 1e-2
 
 
-def test_synthetic_decode_rows_lie_on_the_grid_and_are_uniform():
-    """The synthetic decode generator (reference src/device_page_pool.cpp:
-    122-138) maps a hash onto k/1000, k in [-1000, 1000]: every value is on
-    that grid, the 2001 values are near-uniform (mean near 0), and the key
-    and value streams and the elements differ.  A wrong modulus, a missing
-    shift or an ignored argument fails here; the hash constants themselves
-    have no vectors in the reference."""
-    E = 4096
-    rows = np.stack([orc.synthetic_decode_row(r, s, st, E)
-                     for r in (0, 7, 123) for s in (0, 1, 63) for st in (1, 2)])
-    k = np.rint(rows.astype(np.float64) * 1000.0).astype(np.int64)
-    assert np.array_equal(rows, (k.astype(np.float32) / np.float32(1000.0)))
-    assert k.min() >= -1000 and k.max() <= 1000
-    # each row is near-uniform over the 2001 values: chi-square(2000) within
-    # 6 sigma (rows of different steps share structure, so rows are tested
-    # one at a time, not pooled)
-    for row in k:
-        counts = np.bincount(row + 1000, minlength=2001)
-        expected = E / 2001.0
-        chi2 = float(((counts - expected) ** 2 / expected).sum())
-        assert abs(chi2 - 2000) < 6 * np.sqrt(2 * 2000)
-    assert abs(float(rows.astype(np.float64).mean())) < 0.01
-    assert not np.array_equal(rows[0], rows[1])              # key vs value stream
-    assert len(np.unique(rows[0])) > 1500                     # element enters the hash
-    assert not np.array_equal(orc.synthetic_decode_row(7, 1, 1, E),
-                              orc.synthetic_decode_row(7, 2, 1, E))
+def test_request_step_equals_the_batched_oracle(dsd):
+    """_oracle.request_step (one request from its own page arrays, as the
+    full-size GPU tests stream them) selects and attends exactly as
+    oracle_sparse_batch over the pool -- including the tie-break on the
+    real page ids, which run opposite to the logical order here -- and its
+    dense output equals oracle_dense_step's."""
+    H, D, ps, k = 4, 16, 8, 3
+    E = H * D
+    batch = dsd.SyntheticBatch(H, D, ps, [70, 9, 33], seed=5)
+    # two requests get duplicated summaries so that scores tie exactly
+    kp = batch.key_pool
+    r0 = batch.request_ids(0)
+    kp[r0[1]] = kp[r0[4]]
+    batch.token_counts[r0[1]] = batch.token_counts[r0[4]]
+    summ = orc.pool_summaries(kp, batch.token_counts, E)
+    _, sel_b, out_b = orc.sparse_batch(batch.queries, kp, batch.value_pool, summ,
+                                       batch.token_counts, batch.cand_offsets,
+                                       batch.cand_ids, H, D, ps, k)
+    dense_b = orc.dense_batch(batch.queries, kp, batch.value_pool, batch.token_counts,
+                              batch.cand_offsets, batch.cand_ids, H, D, ps)
+    for r in range(batch.batch):
+        ids = batch.request_ids(r)
+        sel, out, dense = orc.request_step(batch.queries[r], kp[ids], batch.value_pool[ids],
+                                           batch.token_counts[ids], ids, H, D, ps, k,
+                                           dense=True)
+        assert sel.tolist() == sel_b[r].tolist(), r
+        assert np.array_equal(out.view(np.uint32), out_b[r].view(np.uint32)), r
+        assert np.array_equal(dense.view(np.uint32), dense_b[r].view(np.uint32)), r
