@@ -24,6 +24,7 @@
 #include "dsd/cuda_dense_attention.h"
 #include "dsd/paged_kv_cache.h"
 #include "dsd/reference_kernels.h"
+#include "dsd/step_observer.h"
 #include "dsd_hip.h"
 #include "host_workers.h"
 #include "status.h"
@@ -33,6 +34,9 @@ namespace dsd {
 namespace {
 
 using Clock = std::chrono::steady_clock;
+
+ContinuousStepObserver g_observer;
+int g_observe_every = 0;
 
 double Ms(Clock::time_point a, Clock::time_point b) {
   return std::chrono::duration<double, std::milli>(b - a).count();
@@ -359,7 +363,8 @@ SparseBatchCudaResult StagedStep(SparseCudaContext& ctx, const PagedKvCache& cac
                                  const std::vector<LiveRequest>& active, int E, int top_k,
                                  int max_batch, int max_candidates, int max_selected,
                                  const SparseRunBatchOptions& run,
-                                 std::vector<const float*>* rows) {
+                                 std::vector<const float*>* rows,
+                                 ObservedDecodeStep* observe) {
   using detail::ThrowOnError;
   SparseBatchCudaResult result;
   const auto t0 = Clock::now();
@@ -404,16 +409,38 @@ SparseBatchCudaResult StagedStep(SparseCudaContext& ctx, const PagedKvCache& cac
   }
   const double layout_ms = Ms(t0, Clock::now());
   const bool timing = run.timing_mode == SparseBatchTimingMode::kKernelEvents;
-  const bool outputs = run.output_mode != SparseBatchOutputMode::kNoOutputs;
+  const bool outputs = run.output_mode != SparseBatchOutputMode::kNoOutputs || observe;
   dsd_step_timings t{};
   const int out_mode = outputs ? DSD_OUTPUT_OUTPUTS : DSD_OUTPUT_NONE;
   const int time_mode = timing ? DSD_TIMING_EVENTS : DSD_TIMING_NONE;
+  int* sel = nullptr;
+  int* sel_counts = nullptr;
+  if (observe != nullptr) {
+    // The inputs as staged, before the step runs.
+    observe->cand_offsets.assign(offsets, offsets + B + 1);
+    observe->cand_ids.assign(ids, ids + at);
+    observe->queries.resize(static_cast<std::size_t>(B) * E);
+    for (int b = 0; b < B; ++b) {
+      std::memcpy(observe->queries.data() + static_cast<std::size_t>(b) * E,
+                  (*rows)[static_cast<std::size_t>(b)], sizeof(float) * E);
+    }
+    observe->selected.assign(static_cast<std::size_t>(std::max(1, total_selected)), 0);
+    observe->selected_counts.assign(static_cast<std::size_t>(B), 0);
+    sel = observe->selected.data();
+    sel_counts = observe->selected_counts.data();
+  }
   if (in_place) {
     ThrowOnError(dsd_sparse_run_staged_rows(ctx.handle(), B, rows->data(), out_mode, time_mode,
-                                            nullptr, nullptr, &t));
+                                            sel, sel_counts, &t));
   } else {
-    ThrowOnError(dsd_sparse_run_staged(ctx.handle(), B, out_mode, time_mode, nullptr, nullptr,
+    ThrowOnError(dsd_sparse_run_staged(ctx.handle(), B, out_mode, time_mode, sel, sel_counts,
                                        &t));
+  }
+  if (observe != nullptr) {
+    float* staged_out = nullptr;
+    ThrowOnError(dsd_sparse_staging(ctx.handle(), nullptr, nullptr, nullptr, &staged_out));
+    observe->outputs.assign(staged_out, staged_out + static_cast<std::size_t>(B) * E);
+    observe->selected.resize(static_cast<std::size_t>(total_selected));
   }
   if (VerifyStagedSteps()) VerifyStagedStep(ctx, cache, active, E);
   if (timing) {
@@ -463,6 +490,11 @@ void FinishStats(ContinuousBatchStats* stats, Clock::time_point wall_start,
 }
 
 }  // namespace
+
+void SetContinuousStepObserver(ContinuousStepObserver observer, int every) {
+  g_observer = std::move(observer);
+  g_observe_every = g_observer ? every : 0;
+}
 
 std::vector<ContinuousRequestSpec> BuildSyntheticContinuousWorkload(
     const ModelConfig& config, int num_requests, int arrival_window, int min_prompt_tokens,
@@ -614,6 +646,8 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
     run.output_mode = options.run_batch_output_mode;
     run.timing_mode = options.run_batch_timing_mode;
     SparseBatchCudaResult result;
+    const bool observe = g_observer && g_observe_every > 0 && steps_run % g_observe_every == 0;
+    ObservedDecodeStep seen;
     if (debug_outputs) {
       // Debug tensors come back per request through RunBatch.
       batch.clear();
@@ -623,10 +657,35 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
         batch.push_back(&l.a.state);
       }
       result = ctx.RunBatch(batch, run);
+      if (observe) {
+        seen.cand_offsets.push_back(0);
+        for (std::size_t b = 0; b < active.size(); ++b) {
+          const RequestState& st = active[b].a.state;
+          seen.cand_ids.insert(seen.cand_ids.end(), st.candidate_page_ids.begin(),
+                               st.candidate_page_ids.end());
+          seen.cand_offsets.push_back(static_cast<int>(seen.cand_ids.size()));
+          seen.queries.insert(seen.queries.end(), st.query.begin(), st.query.end());
+          const auto& pr = result.per_request[b];
+          seen.selected_counts.push_back(static_cast<int>(pr.selected_page_ids.size()));
+          seen.selected.insert(seen.selected.end(), pr.selected_page_ids.begin(),
+                               pr.selected_page_ids.end());
+          seen.outputs.insert(seen.outputs.end(), pr.output.output.begin(),
+                              pr.output.output.end());
+        }
+      }
     } else {
       result = StagedStep(ctx, cache, active, E, config.top_k_pages,
                           options.max_active_requests, max_candidates, max_selected, run,
-                          &step_rows);
+                          &step_rows, observe ? &seen : nullptr);
+    }
+    if (observe) {
+      seen.step = step;
+      seen.elements = E;
+      for (const auto& l : active) {
+        seen.request_ids.push_back(l.a.state.request_id);
+        seen.decode_steps.push_back(l.a.decode_step_index);
+        seen.context_tokens.push_back(l.a.state.context_tokens);
+      }
     }
     const double ms = Ms(t_step, Clock::now());
     stats.run_batch_wall_ms += ms;
@@ -635,6 +694,7 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
     Add(&overheads, result.runtime_overheads);
     ++steps_run;
     batch_sum += static_cast<int>(active.size());
+    if (observe) g_observer(seen);
 
     // Payloads generated during the loop (not precomputed): every vector has
     // its own seed, so the host threads form them in any order with the

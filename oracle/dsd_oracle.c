@@ -286,3 +286,75 @@ float oracle_max_abs_diff(const float* a, int64_t na, const float* b,
   }
   return diff;
 }
+
+/* ---- the serving loop's decode payloads --------------------------------- */
+
+/* MT19937 (Matsumoto and Nishimura, ACM TOMACS 8(1), 1998), the engine of
+ * std::mt19937: seeding by x_i = 1812433253 (x_{i-1} ^ (x_{i-1} >> 30)) + i,
+ * then the twist and tempering of the paper. */
+typedef struct {
+  uint32_t mt[624];
+  int next;
+} oracle_mt;
+
+static void oracle_mt_seed(oracle_mt* g, uint32_t seed) {
+  int i;
+  g->mt[0] = seed;
+  for (i = 1; i < 624; ++i) {
+    g->mt[i] = 1812433253u * (g->mt[i - 1] ^ (g->mt[i - 1] >> 30)) + (uint32_t)i;
+  }
+  g->next = 624;
+}
+
+static uint32_t oracle_mt_draw(oracle_mt* g) {
+  uint32_t y;
+  if (g->next >= 624) {
+    int k;
+    for (k = 0; k < 624; ++k) {
+      y = (g->mt[k] & 0x80000000u) | (g->mt[(k + 1) % 624] & 0x7fffffffu);
+      g->mt[k] = g->mt[(k + 397) % 624] ^ (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
+    }
+    g->next = 0;
+  }
+  y = g->mt[g->next++];
+  y ^= y >> 11;
+  y ^= (y << 7) & 0x9d2c5680u;
+  y ^= (y << 15) & 0xefc60000u;
+  y ^= y >> 18;
+  return y;
+}
+
+void oracle_mt19937_draws(uint32_t seed, int count, uint32_t* out) {
+  oracle_mt g;
+  int i;
+  oracle_mt_seed(&g, seed);
+  for (i = 0; i < count; ++i) out[i] = oracle_mt_draw(&g);
+}
+
+/* src/continuous_batching.cpp:44-51 (MixSeed). */
+uint32_t oracle_mix_seed(int request_id, int decode_step, int stream) {
+  uint32_t x = 0x9e3779b9u;
+  x ^= ((uint32_t)request_id + 0x85ebca6bu) + (x << 6) + (x >> 2);
+  x ^= ((uint32_t)decode_step + 0xc2b2ae35u) + (x << 6) + (x >> 2);
+  x ^= ((uint32_t)stream + 0x27d4eb2fu) + (x << 6) + (x >> 2);
+  return x;
+}
+
+/* std::uniform_real_distribution<float>(-1, 1) on std::mt19937 as libstdc++
+ * evaluates it: generate_canonical<float, 24> takes one 32-bit draw g and
+ * returns fl(fl(g) / 2^32) (clamped below 1), and the distribution returns
+ * fl(fl(u * 2) + -1) (src/continuous_batching.cpp:35-42 uses it). */
+static float oracle_uniform_pm1(oracle_mt* g) {
+  float u = (float)oracle_mt_draw(g) / 4294967296.0f;
+  if (u >= 1.0f) u = nextafterf(1.0f, 0.0f);
+  return u * 2.0f + -1.0f;
+}
+
+/* DeterministicTokenVector (src/continuous_batching.cpp:53-59). */
+void oracle_token_vector(int count, int request_id, int decode_step, int stream,
+                         float* out) {
+  oracle_mt g;
+  int i;
+  oracle_mt_seed(&g, oracle_mix_seed(request_id, decode_step, stream));
+  for (i = 0; i < count; ++i) out[i] = oracle_uniform_pm1(&g);
+}

@@ -98,6 +98,24 @@ void oracle_dense_step(const float* query, const float* key_pool,
 float oracle_max_abs_diff(const float* a, int64_t na, const float* b,
                           int64_t nb);
 
+/* ---- the serving loop's decode payloads (src/continuous_batching.cpp) -- */
+
+/* The first `count` outputs of std::mt19937 seeded with `seed` (MT19937,
+ * Matsumoto and Nishimura 1998). */
+void oracle_mt19937_draws(uint32_t seed, int count, uint32_t* out);
+
+/* MixSeed(request_id, decode_step, stream) (src/continuous_batching.cpp:44-51). */
+uint32_t oracle_mix_seed(int request_id, int decode_step, int stream);
+
+/* DeterministicTokenVector (src/continuous_batching.cpp:53-59): `count`
+ * draws of std::uniform_real_distribution<float>(-1, 1) (as libstdc++
+ * evaluates it) from std::mt19937(MixSeed(request_id, decode_step, stream)).
+ * Stream 0 = the next query (decode_step + 1 for the query after step
+ * decode_step), 1 = the appended key, 2 = the appended value
+ * (:294-306, :596-633). */
+void oracle_token_vector(int count, int request_id, int decode_step, int stream,
+                         float* out);
+
 #ifdef __cplusplus
 }
 #endif
