@@ -785,8 +785,134 @@ int dsd_pool_reset_transfer_stats(dsd_pool* pool) {
 }  // extern "C"
 
 // ---------------------------------------------------------------------------
-// Sparse decode context
+// Sparse decode step
 // ---------------------------------------------------------------------------
+namespace {
+
+// One decode step's launch: inputs and outputs, the scratch its kernels use
+// (score intervals, publication words, counters) and the launch parameters.
+// A context fills it with its own scratch; the allocation-free entry point
+// with the library's static scratch.
+struct StepLaunch {
+  bool valid = false;
+  bool certified = false;
+  bool fused = false;
+  int batch = 0, total = 0, max_n = 0;
+  int top_k = 0;
+  int compute_units = 256;
+  float scale = 0.0f;
+  const float* queries = nullptr;
+  const int* offsets = nullptr;
+  const int* ids = nullptr;
+  float* outputs = nullptr;
+  float* scores = nullptr;  // exact scores, or the certified midpoints
+  int* selected = nullptr;  // [batch][max(1, top_k)]
+  int* counts = nullptr;
+  float* lo = nullptr;
+  float* hi = nullptr;
+  unsigned long long* rec = nullptr;  // [3 * total] publication words
+  int* exact_pages = nullptr;         // may be null
+  unsigned long long* fail_word = nullptr;
+  unsigned epoch = 0;  // fresh (non-zero) for every launch
+  unsigned spin_limit = kDefaultSpinLimit;
+  bool never_ready = false;
+  dsdk::FailReport Fail() const {
+    dsdk::FailReport f;
+    f.word = fail_word;
+    f.epoch = epoch;
+    return f;
+  }
+};
+
+float StepScale(const PoolView& v) {
+  return 1.0f / std::sqrt(static_cast<float>(v.head_dim));
+}
+
+// Certified scoring unless exact scores are requested or the shape is
+// outside what the certified kernels handle; the single-launch step for
+// certified selection on the hot shape.
+bool StepCertified(const PoolView& v, int score_mode, int max_n, bool need_exact_scores) {
+  return score_mode == DSD_SCORE_CERTIFIED && !need_exact_scores &&
+         dsdk::CertifiedScoringSupported(v.elements, max_n);
+}
+bool StepFused(const PoolView& v, bool certified, bool enabled, int max_n, int top_k) {
+  return certified && enabled && dsdk::FusedStepSupported(v, max_n, top_k);
+}
+
+void EnqueueScoreStage(const PoolView& v, const StepLaunch& L, hipStream_t s) {
+  if (L.total <= 0) return;
+  if (L.certified) {
+    dsdk::LaunchScoreBounds(v, L.queries, L.offsets, L.ids, L.batch, L.total, L.max_n, L.scale,
+                            L.scores, L.lo, L.hi, L.Fail(), s);
+  } else {
+    dsdk::LaunchScoreExact(v, L.queries, L.offsets, L.ids, L.batch, L.total, L.max_n, L.scale,
+                           L.scores, L.Fail(), s);
+  }
+}
+
+void EnqueueSelectStage(const PoolView& v, const StepLaunch& L, hipStream_t s) {
+  if (L.certified) {
+    dsdk::LaunchSelectCertified(v, L.scores, L.lo, L.hi, L.queries, L.offsets, L.ids, L.batch,
+                                L.total, L.max_n, L.scale, L.top_k, L.selected, L.counts,
+                                L.exact_pages, L.Fail(), s);
+  } else {
+    dsdk::LaunchSelectTopK(L.scores, L.offsets, L.ids, L.batch, L.total, L.max_n, L.top_k,
+                           L.selected, L.counts, L.Fail(), s);
+  }
+}
+
+void EnqueueAttentionStage(const PoolView& v, const StepLaunch& L, hipStream_t s) {
+  dsdk::AttentionArgs a;
+  a.queries = L.queries;
+  a.list_ids = L.selected;
+  a.list_counts = L.counts;
+  a.list_stride = L.top_k > 0 ? L.top_k : 1;
+  a.batch = L.batch;
+  a.scale = L.scale;
+  a.outputs = L.outputs;
+  dsdk::LaunchAttention(v, a, s);
+}
+
+dsdk::FusedArgs FusedStepArgs(const PoolView& v, const StepLaunch& L) {
+  dsdk::FusedArgs a;
+  a.queries = L.queries;
+  a.cand_offsets = L.offsets;
+  a.cand_ids = L.ids;
+  a.batch = L.batch;
+  a.total = L.total;
+  a.top_k = L.top_k;
+  a.sel_stride = L.top_k > 0 ? L.top_k : 1;
+  a.heads_per_group = dsdk::FusedStepHeadsPerGroup(v, L.batch, L.compute_units);
+  a.max_candidates = L.max_n;
+  a.scale = L.scale;
+  a.mid = L.scores;
+  a.lo = L.lo;
+  a.hi = L.hi;
+  a.selected = L.selected;
+  a.counts = L.counts;
+  a.outputs = L.outputs;
+  a.rec = L.rec;
+  a.epoch = L.epoch;
+  a.wait_tag = L.never_ready ? (L.epoch ^ 0x80000000u) : L.epoch;
+  a.spin_limit = L.spin_limit;
+  a.exact_pages = L.exact_pages;
+  a.fail = L.Fail();
+  return a;
+}
+
+// The whole step: one launch (fused) or score, select and attention.
+void EnqueueStep(const PoolView& v, const StepLaunch& L, hipStream_t s) {
+  if (L.fused) {
+    dsdk::LaunchFusedStep(v, FusedStepArgs(v, L), s);
+    return;
+  }
+  EnqueueScoreStage(v, L, s);
+  EnqueueSelectStage(v, L, s);
+  EnqueueAttentionStage(v, L, s);
+}
+
+}  // namespace
+
 struct dsd_sparse_ctx {
   dsd_pool* pool = nullptr;
   int top_k = 0;
@@ -797,8 +923,7 @@ struct dsd_sparse_ctx {
   hipEvent_t ev[6] = {};
   DeviceBuffer<float> d_queries, d_scores, d_lo, d_hi;
   DeviceBuffer<int> d_offsets, d_ids, d_selected, d_counts, d_exact_pages;
-  // fused-step publication words (see fused_step.hip) and per-workgroup
-  // clock stamps for the timing mode
+  // fused-step publication words (see fused_step.hip)
   DeviceBuffer<unsigned long long> d_rec;
   // The epoch of the step being enqueued: it tags the fused step's
   // publication words and every failure report of the step's kernels.
@@ -817,23 +942,12 @@ struct dsd_sparse_ctx {
   PinnedBuffer<int> h_offsets, h_ids, h_selected, h_counts;
   // The step kernels' failure word: (epoch << 32) | code, pinned, coherent.
   PinnedBuffer<unsigned long long> h_fail;
+  // per-workgroup clock stamps of a timed fused launch
   PinnedBuffer<unsigned long long> h_stamps;
   PinnedBuffer<const float*> h_rows;  // row pointers of a row-gather step
   int stamp_grid = 0;  // workgroups stamped by the last timed fused launch
 
-  struct Launch {
-    bool valid = false;
-    bool certified = false;
-    bool fused = false;
-    int batch = 0, total = 0, max_n = 0;
-    const float* queries = nullptr;
-    const int* offsets = nullptr;
-    const int* ids = nullptr;
-    float* outputs = nullptr;
-    float* scores = nullptr;
-    int* selected = nullptr;
-    int* counts = nullptr;
-  } last;
+  StepLaunch last;  // the last step's launch (replays re-enqueue its stages)
 
   ~dsd_sparse_ctx() {
     for (hipEvent_t& e : ev) {
@@ -842,15 +956,9 @@ struct dsd_sparse_ctx {
     if (ev_switch) (void)hipEventDestroy(ev_switch);
   }
 
-  // A fresh epoch for the next step (never 0: the words start at 0).
+  // A fresh epoch for the next launch (never 0: the words start at 0).
   void NextEpoch() {
     if (++epoch == 0) epoch = 1;
-  }
-  dsdk::FailReport Fail() const {
-    dsdk::FailReport f;
-    f.word = h_fail.ptr;
-    f.epoch = epoch;
-    return f;
   }
   // Every launch shares the context's scratch (intervals, publication words,
   // ids).  Launches on one stream are ordered by it; a launch on another
@@ -883,65 +991,48 @@ struct dsd_sparse_ctx {
     throw std::runtime_error("fused decode step: wait for page selection timed out");
   }
 
-  float Scale() const {
-    return 1.0f / std::sqrt(static_cast<float>(pool->view.head_dim));
+  // A launch over the context's scratch; the caller fills inputs and
+  // outputs.
+  StepLaunch Plan(int batch, int total, int max_n, bool need_exact_scores) const {
+    StepLaunch L;
+    const PoolView& v = pool->view;
+    L.valid = true;
+    L.certified = StepCertified(v, score_mode, max_n, need_exact_scores);
+    L.fused = StepFused(v, L.certified, fused_enabled, max_n, top_k);
+    L.batch = batch;
+    L.total = total;
+    L.max_n = max_n;
+    L.top_k = top_k;
+    L.compute_units = compute_units;
+    L.scale = StepScale(v);
+    L.scores = d_scores.ptr;
+    L.selected = d_selected.ptr;
+    L.counts = d_counts.ptr;
+    L.lo = d_lo.ptr;
+    L.hi = d_hi.ptr;
+    L.rec = d_rec.ptr;
+    L.exact_pages = d_exact_pages.ptr;
+    L.fail_word = h_fail.ptr;
+    return L;
+  }
+  // Stamps the launch with a fresh epoch and the current wait settings.
+  void Fresh(StepLaunch* L) {
+    NextEpoch();
+    L->epoch = epoch;
+    L->spin_limit = spin_limit;
+    L->never_ready = never_ready;
   }
 
-  // Certified scoring unless exact scores are requested or the shape is
-  // outside what the certified kernels handle.
-  bool UseCertified(int max_n, bool need_exact_scores) const {
-    return score_mode == DSD_SCORE_CERTIFIED && !need_exact_scores &&
-           dsdk::CertifiedScoringSupported(pool->view.elements, max_n);
-  }
-  void EnqueueScore(const Launch& L, hipStream_t s) {
-    if (L.total <= 0) return;
-    if (L.certified) {
-      dsdk::LaunchScoreBounds(pool->view, L.queries, L.offsets, L.ids, L.batch, L.total,
-                              L.max_n, Scale(), L.scores, d_lo.ptr, d_hi.ptr, Fail(), s);
-    } else {
-      dsdk::LaunchScoreExact(pool->view, L.queries, L.offsets, L.ids, L.batch, L.total,
-                             L.max_n, Scale(), L.scores, Fail(), s);
+  // The single-launch step with per-workgroup clock stamps written straight
+  // into pinned host memory (timing mode).
+  void EnqueueFusedStamped(const StepLaunch& L, hipStream_t s) {
+    dsdk::FusedArgs a = FusedStepArgs(pool->view, L);
+    stamp_grid = dsdk::FusedStepGrid(pool->view, L.batch, a.heads_per_group);
+    if (static_cast<size_t>(stamp_grid) * dsdk::FusedStepStampsPerGroup() > h_stamps.count) {
+      throw std::runtime_error("fused step stamps exceed their buffer");
     }
-  }
-  // The single-launch step covers certified selection on the hot shape.
-  bool UseFused(bool certified, int max_n) const {
-    return certified && fused_enabled &&
-           dsdk::FusedStepSupported(pool->view, max_n, top_k);
-  }
-  void EnqueueFused(const Launch& L, hipStream_t s, bool stamp) {
-    dsdk::FusedArgs a;
-    a.queries = L.queries;
-    a.cand_offsets = L.offsets;
-    a.cand_ids = L.ids;
-    a.batch = L.batch;
-    a.total = L.total;
-    a.top_k = top_k;
-    a.sel_stride = top_k > 0 ? top_k : 1;
-    a.heads_per_group = dsdk::FusedStepHeadsPerGroup(pool->view, L.batch, compute_units);
-    a.max_candidates = L.max_n;
-    a.scale = Scale();
-    a.mid = L.scores;
-    a.lo = d_lo.ptr;
-    a.hi = d_hi.ptr;
-    a.selected = L.selected;
-    a.counts = L.counts;
-    a.outputs = L.outputs;
-    a.rec = d_rec.ptr;
-    a.epoch = epoch;
-    a.wait_tag = never_ready ? (epoch ^ 0x80000000u) : epoch;
-    a.spin_limit = spin_limit;
-    a.exact_pages = d_exact_pages.ptr;
-    a.fail = Fail();
-    if (stamp) {
-      // The kernel writes its stamps straight into pinned host memory.
-      stamp_grid = dsdk::FusedStepGrid(pool->view, L.batch, a.heads_per_group);
-      if (static_cast<size_t>(stamp_grid) * dsdk::FusedStepStampsPerGroup() > h_stamps.count) {
-        throw std::runtime_error("fused step stamps exceed their buffer");
-      }
-      a.stamps = h_stamps.ptr;
-    }
+    a.stamps = h_stamps.ptr;
     dsdk::LaunchFusedStep(pool->view, a, s);
-    if (stamp) DSD_HIP_CHECK(hipEventRecord(ev[3], s));
   }
   // Phase split of the last timed fused launch from its workgroup stamps
   // (start, slice scored, counter ready, records read, ranked, selected,
@@ -965,41 +1056,27 @@ struct dsd_sparse_ctx {
     *select_ms = static_cast<double>(t_select - t_score) / wall_khz;
     *attention_ms = static_cast<double>(t_end - t_select) / wall_khz;
   }
-  void Enqueue(const Launch& L, hipStream_t s, bool timing) {
-    NextEpoch();
-    if (L.fused) {
-      if (timing) DSD_HIP_CHECK(hipEventRecord(ev[0], s));
-      EnqueueFused(L, s, timing);  // records ev[3] at the kernel's end
+  // Enqueues a step (fresh epoch); with timing, events around the stages
+  // (ev[0] .. ev[3]) and, for the fused step, the workgroup stamps.
+  void Enqueue(StepLaunch* L, hipStream_t s, bool timing) {
+    Fresh(L);
+    const PoolView& v = pool->view;
+    if (!timing) {
+      EnqueueStep(v, *L, s);
       return;
     }
-    if (timing) DSD_HIP_CHECK(hipEventRecord(ev[0], s));
-    EnqueueScore(L, s);
-    if (timing) DSD_HIP_CHECK(hipEventRecord(ev[1], s));
-    EnqueueSelect(L, s);
-    if (timing) DSD_HIP_CHECK(hipEventRecord(ev[2], s));
-    EnqueueAttention(L, s);
-    if (timing) DSD_HIP_CHECK(hipEventRecord(ev[3], s));
-  }
-  void EnqueueSelect(const Launch& L, hipStream_t s) {
-    if (L.certified) {
-      dsdk::LaunchSelectCertified(pool->view, L.scores, d_lo.ptr, d_hi.ptr, L.queries,
-                                  L.offsets, L.ids, L.batch, L.total, L.max_n, Scale(), top_k,
-                                  L.selected, L.counts, d_exact_pages.ptr, Fail(), s);
-    } else {
-      dsdk::LaunchSelectTopK(L.scores, L.offsets, L.ids, L.batch, L.total, L.max_n, top_k,
-                             L.selected, L.counts, Fail(), s);
+    DSD_HIP_CHECK(hipEventRecord(ev[0], s));
+    if (L->fused) {
+      EnqueueFusedStamped(*L, s);
+      DSD_HIP_CHECK(hipEventRecord(ev[3], s));
+      return;
     }
-  }
-  void EnqueueAttention(const Launch& L, hipStream_t s) {
-    dsdk::AttentionArgs a;
-    a.queries = L.queries;
-    a.list_ids = L.selected;
-    a.list_counts = L.counts;
-    a.list_stride = top_k > 0 ? top_k : 1;
-    a.batch = L.batch;
-    a.scale = Scale();
-    a.outputs = L.outputs;
-    dsdk::LaunchAttention(pool->view, a, s);
+    EnqueueScoreStage(v, *L, s);
+    DSD_HIP_CHECK(hipEventRecord(ev[1], s));
+    EnqueueSelectStage(v, *L, s);
+    DSD_HIP_CHECK(hipEventRecord(ev[2], s));
+    EnqueueAttentionStage(v, *L, s);
+    DSD_HIP_CHECK(hipEventRecord(ev[3], s));
   }
 };
 
@@ -1219,23 +1296,14 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
     }
     t.h2d_ms = MsSince(t0);
 
-    dsd_sparse_ctx::Launch L;
-    L.valid = true;
-    L.certified = ctx->UseCertified(max_n, debug);
-    L.fused = ctx->UseFused(L.certified, max_n);
-    L.batch = batch;
-    L.total = total;
-    L.max_n = max_n;
+    StepLaunch L = ctx->Plan(batch, total, max_n, debug);
     L.queries = ctx->d_queries.ptr;
     L.offsets = ctx->d_offsets.ptr;
     L.ids = ctx->d_ids.ptr;
     // The attention writes the outputs straight into the pinned staging.
     L.outputs = ctx->h_outputs.ptr;
-    L.scores = ctx->d_scores.ptr;
-    L.selected = ctx->d_selected.ptr;
-    L.counts = ctx->d_counts.ptr;
     t0 = Clock::now();
-    ctx->Enqueue(L, ctx->stream, timing);
+    ctx->Enqueue(&L, ctx->stream, timing);
     ctx->last = L;
     t.launch_ms = MsSince(t0);
 
@@ -1388,24 +1456,18 @@ int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
     Require(d_queries != nullptr && d_cand_offsets != nullptr && d_outputs != nullptr,
             "device inputs must be non-null");
     if (total_candidates > 0) Require(d_cand_ids != nullptr, "cand_ids must be non-null");
-    dsd_sparse_ctx::Launch L;
-    L.valid = true;
-    L.certified = ctx->UseCertified(max_candidates, false);
-    L.fused = ctx->UseFused(L.certified, max_candidates);
-    L.batch = batch;
-    L.total = total_candidates;
-    L.max_n = max_candidates;
+    StepLaunch L = ctx->Plan(batch, total_candidates, max_candidates, false);
     L.queries = d_queries;
     L.offsets = d_cand_offsets;
     L.ids = d_cand_ids;
     L.outputs = d_outputs;
-    L.scores = d_scores != nullptr ? d_scores : ctx->d_scores.ptr;
-    L.selected = d_selected != nullptr ? d_selected : ctx->d_selected.ptr;
-    L.counts = d_selected_counts != nullptr ? d_selected_counts : ctx->d_counts.ptr;
+    if (d_scores != nullptr) L.scores = d_scores;
+    if (d_selected != nullptr) L.selected = d_selected;
+    if (d_selected_counts != nullptr) L.counts = d_selected_counts;
     hipStream_t s = stream != nullptr ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
     ctx->pool->OrderAfterPending(s);
     ctx->OrderOn(s);
-    ctx->Enqueue(L, s, false);
+    ctx->Enqueue(&L, s, false);
     ctx->last = L;
   });
 }
@@ -1415,19 +1477,18 @@ int dsd_sparse_replay_stage(dsd_sparse_ctx* ctx, int stage, void* stream) {
     Require(ctx != nullptr, "context must be non-null");
     Require(ctx->last.valid, "no previous step to replay");
     hipStream_t s = stream != nullptr ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
+    Require(stage >= 0 && stage <= 3, "stage must be 0, 1, 2 or 3");
+    if (stage == 3) Require(ctx->last.fused, "the last step did not use the single-launch kernel");
     ctx->pool->OrderAfterPending(s);
     ctx->OrderOn(s);
-    ctx->NextEpoch();
-    const auto& L = ctx->last;
+    StepLaunch L = ctx->last;
+    ctx->Fresh(&L);
+    const PoolView& v = ctx->pool->view;
     switch (stage) {
-      case 0: ctx->EnqueueScore(L, s); break;
-      case 1: ctx->EnqueueSelect(L, s); break;
-      case 2: ctx->EnqueueAttention(L, s); break;
-      case 3:
-        Require(L.fused, "the last step did not use the single-launch kernel");
-        ctx->EnqueueFused(L, s, false);
-        break;
-      default: throw std::invalid_argument("stage must be 0, 1, 2 or 3");
+      case 0: EnqueueScoreStage(v, L, s); break;
+      case 1: EnqueueSelectStage(v, L, s); break;
+      case 2: EnqueueAttentionStage(v, L, s); break;
+      default: EnqueueStep(v, L, s); break;
     }
   });
 }
