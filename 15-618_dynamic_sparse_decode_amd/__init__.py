@@ -139,6 +139,8 @@ _SIGNATURES = {
     "dsd_host_free": (ctypes.c_int, [ctypes.c_void_p]),
     "dsd_sparse_run_batch_device": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_int] * 3
                                     + [ctypes.c_void_p] * 8),
+    "dsd_sparse_run_batch_device_static": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_int] * 4
+                                           + [ctypes.c_void_p] * 9),
     "dsd_sparse_replay_stage": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]),
     "dsd_sparse_stream": (ctypes.c_void_p, [ctypes.c_void_p]),
     "dsd_sparse_set_score_mode": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
@@ -503,6 +505,18 @@ class HostBlock:
 
     def __exit__(self, *exc):
         self.close()
+
+
+def sparse_run_batch_device_static(pool: DevicePagePool, top_k, batch, total_candidates,
+                                   max_candidates, d_queries, d_cand_offsets, d_cand_ids,
+                                   d_outputs, d_scores=0, d_selected=0, d_counts=0, d_fail=0,
+                                   stream=0) -> None:
+    """The allocation-free device step (no context; the library's static
+    scratch): integer device addresses, async on `stream`."""
+    _check(load_library().dsd_sparse_run_batch_device_static(
+        pool.handle, top_k, batch, total_candidates, max_candidates, d_queries, d_cand_offsets,
+        d_cand_ids, d_outputs, d_scores or None, d_selected or None, d_counts or None,
+        d_fail or None, stream or None))
 
 
 def dense_run_batch(pool: DevicePagePool, queries, cand_offsets, cand_ids):

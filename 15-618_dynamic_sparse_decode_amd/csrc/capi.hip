@@ -1564,6 +1564,145 @@ int dsd_sparse_set_wait_limit(dsd_sparse_ctx* ctx, unsigned spin_limit, int neve
   });
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free device step
+// ---------------------------------------------------------------------------
+namespace {
+
+// Limits of one call of dsd_sparse_run_batch_device_static, set by the size
+// of the static scratch below.
+constexpr int kStaticMaxBatch = 1024;
+constexpr int kStaticMaxCandidates = 65536;  // total candidates per call
+constexpr int kStaticMaxSelected = 65536;    // batch * max(1, top_k) held for
+                                             // a caller that passes no ids
+constexpr size_t Align256(size_t bytes) { return (bytes + 255) / 256 * 256; }
+// Byte offsets of the scratch's parts: publication words (3 per candidate),
+// midpoints, lower and upper bounds, selected ids, selected counts.
+constexpr size_t kStaticRec = 0;
+constexpr size_t kStaticMid =
+    Align256(kStaticRec + sizeof(unsigned long long) * 3 * kStaticMaxCandidates);
+constexpr size_t kStaticLo = Align256(kStaticMid + sizeof(float) * kStaticMaxCandidates);
+constexpr size_t kStaticHi = Align256(kStaticLo + sizeof(float) * kStaticMaxCandidates);
+constexpr size_t kStaticSel = Align256(kStaticHi + sizeof(float) * kStaticMaxCandidates);
+constexpr size_t kStaticCounts = Align256(kStaticSel + sizeof(int) * kStaticMaxSelected);
+constexpr size_t kStaticBytes = Align256(kStaticCounts + sizeof(int) * kStaticMaxBatch);
+
+}  // namespace
+
+// The scratch of dsd_sparse_run_batch_device_static (2.5 MiB): one copy per
+// GPU, held until the process ends, shared by every call on that GPU.  Host
+// code never names it except to look up its device address.
+static __device__ __align__(256) unsigned char scratch[kStaticBytes];
+
+namespace {
+
+constexpr int kStaticMaxDevices = 64;
+
+// Per GPU: the device address of `scratch` (looked up once, with that GPU
+// current) and the epoch counter of the calls on it.
+struct StaticScratch {
+  std::once_flag once;
+  hipError_t status = hipSuccess;
+  unsigned char* ptr = nullptr;
+  int compute_units = 256;
+  unsigned epoch = 0;
+};
+StaticScratch g_static_scratch[kStaticMaxDevices];
+
+StaticScratch& StaticScratchOn(int device) {
+  StaticScratch& st = g_static_scratch[device];
+  std::call_once(st.once, [&] {
+    void* p = nullptr;
+    st.status = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (st.status != hipSuccess) return;
+    st.ptr = static_cast<unsigned char*>(p);
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) ==
+            hipSuccess &&
+        cus > 0) {
+      st.compute_units = cus;
+    }
+  });
+  DSD_HIP_CHECK(st.status);
+  return st;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsd_sparse_run_batch_device_static(dsd_pool* pool, int top_k, int batch,
+                                       int total_candidates, int max_candidates,
+                                       const float* d_queries, const int* d_cand_offsets,
+                                       const int* d_cand_ids, float* d_outputs, float* d_scores,
+                                       int* d_selected, int* d_selected_counts,
+                                       unsigned long long* d_fail, void* stream) {
+  return Guard([&] {
+    Require(pool != nullptr, "pool must be non-null");
+    Require(top_k >= 0, "top_k must be non-negative");
+    Require(batch >= 0 && total_candidates >= 0 && max_candidates >= 0,
+            "sizes must be non-negative");
+    if (pool->view.head_dim <= 0 || pool->view.head_dim > 128) {
+      throw std::invalid_argument("sparse decode supports head_dim in (0, 128]");
+    }
+    if (batch == 0) return;
+    if (batch > kStaticMaxBatch) {
+      throw std::invalid_argument(
+          "dsd_sparse_run_batch_device_static: batch exceeds the static scratch's 1024 "
+          "requests");
+    }
+    if (total_candidates > kStaticMaxCandidates) {
+      throw std::invalid_argument(
+          "dsd_sparse_run_batch_device_static: total_candidates exceeds the static scratch's "
+          "65536 candidates");
+    }
+    if (d_selected == nullptr &&
+        static_cast<int64_t>(batch) * std::max(1, top_k) > kStaticMaxSelected) {
+      throw std::invalid_argument(
+          "dsd_sparse_run_batch_device_static: batch * top_k exceeds the static scratch's 65536 "
+          "selected ids (pass d_selected)");
+    }
+    Require(d_queries != nullptr && d_cand_offsets != nullptr && d_outputs != nullptr,
+            "device inputs must be non-null");
+    if (total_candidates > 0) Require(d_cand_ids != nullptr, "cand_ids must be non-null");
+    int device = 0;
+    DSD_HIP_CHECK(hipGetDevice(&device));
+    Require(device >= 0 && device < kStaticMaxDevices, "device ordinal beyond 64");
+    StaticScratch& st = StaticScratchOn(device);
+    if (++st.epoch == 0) st.epoch = 1;
+    const PoolView& v = pool->view;
+    StepLaunch L;
+    L.valid = true;
+    L.certified = StepCertified(v, DSD_SCORE_CERTIFIED, max_candidates, false);
+    L.fused = StepFused(v, L.certified, true, max_candidates, top_k);
+    L.batch = batch;
+    L.total = total_candidates;
+    L.max_n = max_candidates;
+    L.top_k = top_k;
+    L.compute_units = st.compute_units;
+    L.scale = StepScale(v);
+    L.queries = d_queries;
+    L.offsets = d_cand_offsets;
+    L.ids = d_cand_ids;
+    L.outputs = d_outputs;
+    L.rec = reinterpret_cast<unsigned long long*>(st.ptr + kStaticRec);
+    L.scores = d_scores != nullptr ? d_scores : reinterpret_cast<float*>(st.ptr + kStaticMid);
+    L.lo = reinterpret_cast<float*>(st.ptr + kStaticLo);
+    L.hi = reinterpret_cast<float*>(st.ptr + kStaticHi);
+    L.selected = d_selected != nullptr ? d_selected : reinterpret_cast<int*>(st.ptr + kStaticSel);
+    L.counts = d_selected_counts != nullptr ? d_selected_counts
+                                            : reinterpret_cast<int*>(st.ptr + kStaticCounts);
+    L.exact_pages = nullptr;
+    L.fail_word = d_fail;
+    L.epoch = st.epoch;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    pool->OrderAfterPending(s);
+    EnqueueStep(v, L, s);
+  });
+}
+
 // ---------------------------------------------------------------------------
 // Dense decode (DenseCudaContext::RunBatch, src/cuda/kernels.cu:197-292).
 // ---------------------------------------------------------------------------

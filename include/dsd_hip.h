@@ -307,6 +307,34 @@ int dsd_sparse_device_status(dsd_sparse_ctx* ctx);
  * path, which never reaches a GPU hang.  No reference counterpart. */
 int dsd_sparse_set_wait_limit(dsd_sparse_ctx* ctx, unsigned spin_limit, int never_ready);
 
+/* dsd_sparse_run_batch_device without a context and without any
+ * allocation: for callers that cannot allocate device memory during a step
+ * -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  No counterpart in the reference (whose RunBatch
+ * allocates nothing per step only because its context preallocated,
+ * src/cuda/sparse_batched_attention.cu:444-528).
+ * The step's scratch (publication words, score intervals, and ids / counts
+ * when d_selected / d_selected_counts are NULL) lives in a static device
+ * array of 2.5 MiB that each GPU holds until the process ends; the call
+ * makes no hipMalloc / hipFree and no allocating library call.  Limits:
+ * batch <= 1024, total_candidates <= 65536 and, when d_selected is NULL,
+ * batch * max(1, top_k) <= 65536; larger calls fail with
+ * DSD_ERR_INVALID_ARGUMENT before any work.  Every call on one GPU shares
+ * the array, so calls that overlap on one GPU (on different streams, or
+ * from several threads) race: order them.  Ids and counts left in the
+ * array are overwritten by the next call.
+ * Arguments as dsd_sparse_run_batch_device, plus the pool and top_k of the
+ * context it replaces; selection is certified (bit-exact with sparse_cpu).
+ * d_fail (may be NULL): memory the device writes (epoch << 32) | code to
+ * when a request is skipped (codes as dsd_sparse_device_status's 1..3);
+ * the caller clears it before the call and reads it after. */
+int dsd_sparse_run_batch_device_static(dsd_pool* pool, int top_k, int batch,
+                                       int total_candidates, int max_candidates,
+                                       const float* d_queries, const int* d_cand_offsets,
+                                       const int* d_cand_ids, float* d_outputs, float* d_scores,
+                                       int* d_selected, int* d_selected_counts,
+                                       unsigned long long* d_fail, void* stream);
+
 /* Re-enqueue one stage of the last dsd_sparse_run_batch_device call on the
  * same buffers (stage 0 = score, 1 = select, 2 = attention, each as its own
  * kernel; 3 = the single-launch fused step, when the last call used it).
