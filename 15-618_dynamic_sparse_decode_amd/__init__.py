@@ -148,6 +148,8 @@ _SIGNATURES = {
                                                _c_float_p, _c_float_p]),
     "dsd_sparse_exact_rescored_pages": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p]),
     "dsd_sparse_device_status": (ctypes.c_int, [ctypes.c_void_p]),
+    "dsd_sparse_step_stamps": (ctypes.c_int, [ctypes.c_void_p, _c_int_p, _c_int_p, _c_double_p,
+                                              ctypes.c_void_p, ctypes.c_size_t]),
     "dsd_sparse_last_launch": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(LaunchInfo)]),
     "dsd_sparse_set_wait_limit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint, ctypes.c_int]),
     "dsd_dense_run_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_float_p, _c_int_p,
@@ -470,6 +472,18 @@ class SparseContext:
         info = LaunchInfo()
         _check(self._lib.dsd_sparse_last_launch(self.handle, ctypes.byref(info)))
         return info.as_dict()
+
+    def step_stamps(self):
+        """(stamps [grid][per_group] uint64, khz) of the last timed fused step."""
+        grid, per, khz = ctypes.c_int(), ctypes.c_int(), ctypes.c_double()
+        _check(self._lib.dsd_sparse_step_stamps(self.handle, ctypes.byref(grid), ctypes.byref(per),
+                                                ctypes.byref(khz), None, 0))
+        out = np.zeros((grid.value, per.value), np.uint64)
+        if out.size:
+            _check(self._lib.dsd_sparse_step_stamps(self.handle, ctypes.byref(grid),
+                                                    ctypes.byref(per), ctypes.byref(khz),
+                                                    out.ctypes.data_as(ctypes.c_void_p), out.size))
+        return out, khz.value
 
     def device_status(self) -> None:
         """Synchronize; raise the last unreported input failure of a step."""

@@ -1547,6 +1547,21 @@ int dsd_sparse_last_launch(const dsd_sparse_ctx* ctx, dsd_launch_info* out) {
   });
 }
 
+int dsd_sparse_step_stamps(const dsd_sparse_ctx* ctx, int* grid, int* per_group, double* khz,
+                           uint64_t* out, size_t capacity) {
+  return Guard([&] {
+    Require(ctx != nullptr && grid != nullptr && per_group != nullptr && khz != nullptr,
+            "pointers must be non-null");
+    *grid = ctx->stamp_grid;
+    *per_group = dsdk::FusedStepStampsPerGroup();
+    *khz = ctx->wall_khz;
+    if (out == nullptr) return;
+    const size_t n = static_cast<size_t>(ctx->stamp_grid) * static_cast<size_t>(*per_group);
+    Require(capacity >= n, "stamp buffer too small");
+    std::memcpy(out, ctx->h_stamps.ptr, sizeof(uint64_t) * n);
+  });
+}
+
 int dsd_sparse_device_status(dsd_sparse_ctx* ctx) {
   return Guard([&] {
     Require(ctx != nullptr, "context must be non-null");

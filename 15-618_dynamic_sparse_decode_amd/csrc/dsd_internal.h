@@ -122,13 +122,14 @@ void LaunchScoreBounds(const PoolView& pool, const float* d_queries,
                        float* d_lo, float* d_hi, FailReport fail, hipStream_t stream);
 
 // Top-k from certified intervals; candidates whose order is not decided by
-// disjoint intervals are rescored with the exact sequential chain.  Adds the
+// disjoint intervals get refined intervals (written back to mid/lo/hi) and,
+// where those still leave it open, the exact sequential chain.  Adds the
 // number of rescored pages to *d_exact_pages when non-null.  A request whose
 // candidate list is longer than max_candidates (the score kernels covered
 // only that many) or whose offsets leave [0, total_candidates] selects
 // nothing and is reported (kFailShape).
-void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float* d_lo,
-                           const float* d_hi, const float* d_queries,
+void LaunchSelectCertified(const PoolView& pool, float* d_mid, float* d_lo, float* d_hi,
+                           const float* d_queries,
                            const int* d_cand_offsets, const int* d_cand_ids, int batch,
                            int total_candidates, int max_candidates, float scale, int top_k,
                            int* d_selected, int* d_counts, int* d_exact_pages, FailReport fail,

@@ -69,9 +69,10 @@ constexpr int kFSlots = kFMaxCand / kWave;  // candidates (or ranks) per lane: l
 constexpr int kFRescoreGroup = 16;            // exact chains per rescore group
 static_assert(kFMaxK <= kFMaxCand, "rank slots cover the candidate slots");
 // Timing mode: per-workgroup wall clocks at start, slice scored, counter
-// ready, records read, ranked, selected, end; then the hardware ids.
-constexpr int kStampsPerGroup = 8;
-enum Stamp { kStart, kScored, kReady, kRecords, kRanked, kSelected, kEnd, kHwId };
+// ready, records read, ranked, selected, end, refinement begun and ended
+// (0 when none ran); then the hardware ids.
+constexpr int kStampsPerGroup = 10;
+enum Stamp { kStart, kScored, kReady, kRecords, kRanked, kSelected, kEnd, kRefine, kRefined, kHwId };
 
 struct FusedShared {
   uint64_t stamp[kStampsPerGroup];  // timing mode: thread 0's clocks
@@ -643,21 +644,48 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     const int cs = (n + kWave - 1) / kWave;    // candidate slots, 1..4
     const int rs = (kk + kWave - 1) / kWave;   // rank slots, 1..cs
     bool any = false;
-    switch (cs * 8 + rs) {
-      case 1 * 8 + 1: any = RankAndCertify<1, 1>(a, n, kk, page, ntok, sh); break;
-      case 2 * 8 + 1: any = RankAndCertify<2, 1>(a, n, kk, page, ntok, sh); break;
-      case 2 * 8 + 2: any = RankAndCertify<2, 2>(a, n, kk, page, ntok, sh); break;
-      case 3 * 8 + 1: any = RankAndCertify<3, 1>(a, n, kk, page, ntok, sh); break;
-      case 3 * 8 + 2: any = RankAndCertify<3, 2>(a, n, kk, page, ntok, sh); break;
-      case 3 * 8 + 3: any = RankAndCertify<3, 3>(a, n, kk, page, ntok, sh); break;
-      case 4 * 8 + 1: any = RankAndCertify<4, 1>(a, n, kk, page, ntok, sh); break;
-      case 4 * 8 + 2: any = RankAndCertify<4, 2>(a, n, kk, page, ntok, sh); break;
-      case 4 * 8 + 3: any = RankAndCertify<4, 3>(a, n, kk, page, ntok, sh); break;
-      default: any = RankAndCertify<4, 4>(a, n, kk, page, ntok, sh); break;
+    for (int pass = 0; pass < 2; ++pass) {
+      switch (cs * 8 + rs) {
+        case 1 * 8 + 1: any = RankAndCertify<1, 1>(a, n, kk, page, ntok, sh); break;
+        case 2 * 8 + 1: any = RankAndCertify<2, 1>(a, n, kk, page, ntok, sh); break;
+        case 2 * 8 + 2: any = RankAndCertify<2, 2>(a, n, kk, page, ntok, sh); break;
+        case 3 * 8 + 1: any = RankAndCertify<3, 1>(a, n, kk, page, ntok, sh); break;
+        case 3 * 8 + 2: any = RankAndCertify<3, 2>(a, n, kk, page, ntok, sh); break;
+        case 3 * 8 + 3: any = RankAndCertify<3, 3>(a, n, kk, page, ntok, sh); break;
+        case 4 * 8 + 1: any = RankAndCertify<4, 1>(a, n, kk, page, ntok, sh); break;
+        case 4 * 8 + 2: any = RankAndCertify<4, 2>(a, n, kk, page, ntok, sh); break;
+        case 4 * 8 + 3: any = RankAndCertify<4, 3>(a, n, kk, page, ntok, sh); break;
+        default: any = RankAndCertify<4, 4>(a, n, kk, page, ntok, sh); break;
+      }
+      if (!any || pass == 1) break;
+      // 4a. Some order is not decided by the intervals: the flagged pages
+      // get refined intervals (RefineScores, the whole workgroup, several
+      // waves per page), and the ranks and certification run again.
+      __syncthreads();
+      StampAt(a, sh, kRefine);
+      RefineScores(
+          sh.nflag,
+          [&](int f) -> const float* {
+            const int i = sh.flag[f];
+            const int pg = sh.cpage[i];
+            const bool live = pg >= 0 && pg < pool.capacity && sh.cntok[i] != 0;
+            return live ? pool.summaries + static_cast<size_t>(pg) * kFE : nullptr;
+          },
+          [&](int f, float m, float l, float h) {
+            // Only in LDS: the score passes of the request's other workgroups
+            // wrote the global intervals, with no ordering against this one.
+            const int i = sh.flag[f];
+            sh.mid[i] = m;
+            sh.lo[i] = l;
+            sh.hi[i] = h;
+          },
+          a.queries + static_cast<size_t>(r) * kFE, kFE, a.scale,
+          reinterpret_cast<double*>(sh.tile));
+      StampAt(a, sh, kRefined);
     }
     if (any) {
-      // 4. Some order is not decided by the intervals: rescore those pages
-      // with the exact chain, rank again and rewrite the members.
+      // 4b. What the refined intervals leave open: rescore those pages with
+      // the exact chain, rank again and rewrite the members.
       __syncthreads();
       const int nflag = sh.nflag;
       if (writer && threadIdx.x == 0 && a.exact_pages != nullptr) {

@@ -316,8 +316,8 @@ __device__ void RankSortDesc(const uint64_t* keys, const int* idx, int count,
 }
 
 __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
-    const float* __restrict__ mid, const float* __restrict__ lo,
-    const float* __restrict__ hi, const float* __restrict__ queries,
+    float* __restrict__ mid, float* __restrict__ lo,
+    float* __restrict__ hi, const float* __restrict__ queries,
     const float* __restrict__ summaries, const int* __restrict__ token_counts, int capacity,
     const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int total,
     int max_candidates, int E, float scale, int top_k, int* __restrict__ selected,
@@ -361,85 +361,115 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
   }
   __syncthreads();
 
-  // 1. The members: the kk largest keys (equal keys are the same page listed
-  //    twice, so which of them counts is immaterial).
-  int shift;
-  uint64_t prefix;
-  int need;
-  bool all;
-  RadixSelectKth(keys, n, kk, hist, &s_prefix, &s_need, &s_all, &shift, &prefix, &need, &all);
-  // The members, unordered, into the rescoring tile (idle until step 3),
-  // then in key order into skeys / sidx.
-  uint64_t* tkeys = reinterpret_cast<uint64_t*>(tile);
-  int* tidx = reinterpret_cast<int*>(tile + 2 * kCertMaxKeys);
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const uint64_t top = keys[i] >> shift;
-    bool in = top > prefix;
-    if (top == prefix) in = all || atomicAdd(&s_tie, 1) < need;
-    member[i] = in ? 1 : 0;
-    if (in) {
-      const int pos = atomicAdd(&s_count, 1);
-      tkeys[pos] = keys[i];
-      tidx[pos] = i;
-    }
-  }
-  __syncthreads();
-  RankSortDesc(tkeys, tidx, kk, skeys, sidx);
-
-  // 2. Certification.  Member intervals in rank order go to the rescoring
-  //    tile (idle until step 3): mlo = tile[0, kk), mhi = tile[kk, 2kk).
-  float* mlo = tile;
-  float* mhi = tile + kCertMaxKeys;
-  float my_min = INFINITY, my_max = -INFINITY;
-  for (int t = threadIdx.x; t < kk; t += blockDim.x) {
-    const int c = sidx[t];
-    mlo[t] = s_lo[c];
-    mhi[t] = s_hi[c];
-    my_min = fminf(my_min, s_lo[c]);
-  }
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    if (!member[i]) my_max = fmaxf(my_max, s_hi[i]);
-  }
-  for (int o = 1; o < kWave; o <<= 1) {
-    my_min = fminf(my_min, __shfl_xor(my_min, o, kWave));
-    my_max = fmaxf(my_max, __shfl_xor(my_max, o, kWave));
-  }
   const int wave = threadIdx.x / kWave;
   const int nwaves = (blockDim.x + kWave - 1) / kWave;
-  if ((threadIdx.x & (kWave - 1)) == 0) {
-    s_red[0][wave] = my_min;
-    s_red[1][wave] = my_max;
-  }
-  __syncthreads();
-  float min_t_lo = INFINITY, max_o_hi = -INFINITY;
-  for (int w = 0; w < nwaves; ++w) {
-    min_t_lo = fminf(min_t_lo, s_red[0][w]);
-    max_o_hi = fmaxf(max_o_hi, s_red[1][w]);
-  }
-  // An outsider is flagged when its hi reaches the members' smallest lo; a
-  // member when its lo reaches the outsiders' largest hi or its interval
-  // meets another member's.
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    if (!member[i] && s_hi[i] >= min_t_lo) flagged[atomicAdd(&s_nflag, 1)] = i;
-  }
-  for (int t = threadIdx.x; t < kk; t += blockDim.x) {
-    const float l = mlo[t];
-    const float h = mhi[t];
-    bool flag = l <= max_o_hi;
-    // Eight independent reads per round (an early exit would serialise them).
-    for (int u0 = 0; u0 < kk && !flag; u0 += 8) {
-#pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        const int u = u0 + v;
-        const bool in = u < kk;
-        const float lu = in ? mlo[u] : INFINITY;
-        const float hu = in ? mhi[u] : -INFINITY;
-        flag |= (u != t) & (l <= hu) & (lu <= h);
+  uint64_t* tkeys = reinterpret_cast<uint64_t*>(tile);
+  int* tidx = reinterpret_cast<int*>(tile + 2 * kCertMaxKeys);
+  // Pass 0 certifies with the score kernel's intervals; the candidates it
+  // flags get refined intervals (RefineScores, several waves per page; E a
+  // multiple of 256) and pass 1 selects and certifies again.  What pass 1
+  // leaves open gets the exact chain (step 3).
+  for (int pass = 0; pass < 2; ++pass) {
+    // 1. The members: the kk largest keys (equal keys are the same page listed
+    //    twice, so which of them counts is immaterial).
+    int shift;
+    uint64_t prefix;
+    int need;
+    bool all;
+    RadixSelectKth(keys, n, kk, hist, &s_prefix, &s_need, &s_all, &shift, &prefix, &need, &all);
+    // The members, unordered, into the rescoring tile (idle until step 3),
+    // then in key order into skeys / sidx.
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const uint64_t top = keys[i] >> shift;
+      bool in = top > prefix;
+      if (top == prefix) in = all || atomicAdd(&s_tie, 1) < need;
+      member[i] = in ? 1 : 0;
+      if (in) {
+        const int pos = atomicAdd(&s_count, 1);
+        tkeys[pos] = keys[i];
+        tidx[pos] = i;
       }
     }
-    if (flag) flagged[atomicAdd(&s_nflag, 1)] = sidx[t];
+    __syncthreads();
+    RankSortDesc(tkeys, tidx, kk, skeys, sidx);
+
+    // 2. Certification.  Member intervals in rank order go to the rescoring
+    //    tile (idle until step 3): mlo = tile[0, kk), mhi = tile[kk, 2kk).
+    float* mlo = tile;
+    float* mhi = tile + kCertMaxKeys;
+    float my_min = INFINITY, my_max = -INFINITY;
+    for (int t = threadIdx.x; t < kk; t += blockDim.x) {
+      const int c = sidx[t];
+      mlo[t] = s_lo[c];
+      mhi[t] = s_hi[c];
+      my_min = fminf(my_min, s_lo[c]);
+    }
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      if (!member[i]) my_max = fmaxf(my_max, s_hi[i]);
+    }
+    for (int o = 1; o < kWave; o <<= 1) {
+      my_min = fminf(my_min, __shfl_xor(my_min, o, kWave));
+      my_max = fmaxf(my_max, __shfl_xor(my_max, o, kWave));
+    }
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+      s_red[0][wave] = my_min;
+      s_red[1][wave] = my_max;
+    }
+    __syncthreads();
+    float min_t_lo = INFINITY, max_o_hi = -INFINITY;
+    for (int w = 0; w < nwaves; ++w) {
+      min_t_lo = fminf(min_t_lo, s_red[0][w]);
+      max_o_hi = fmaxf(max_o_hi, s_red[1][w]);
+    }
+    // An outsider is flagged when its hi reaches the members' smallest lo; a
+    // member when its lo reaches the outsiders' largest hi or its interval
+    // meets another member's.
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      if (!member[i] && s_hi[i] >= min_t_lo) flagged[atomicAdd(&s_nflag, 1)] = i;
+    }
+    for (int t = threadIdx.x; t < kk; t += blockDim.x) {
+      const float l = mlo[t];
+      const float h = mhi[t];
+      bool flag = l <= max_o_hi;
+      // Eight independent reads per round (an early exit would serialise them).
+      for (int u0 = 0; u0 < kk && !flag; u0 += 8) {
+  #pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const int u = u0 + v;
+          const bool in = u < kk;
+          const float lu = in ? mlo[u] : INFINITY;
+          const float hu = in ? mhi[u] : -INFINITY;
+          flag |= (u != t) & (l <= hu) & (lu <= h);
+        }
+      }
+      if (flag) flagged[atomicAdd(&s_nflag, 1)] = sidx[t];
+    }
+    __syncthreads();
+    if (s_nflag == 0 || pass == 1 || E % 256 != 0) break;
+    RefineScores(
+        s_nflag,
+        [&](int f) -> const float* {
+          const int pg = cand[flagged[f]];
+          const bool live = pg >= 0 && pg < capacity && token_counts[pg] != 0;
+          return live ? summaries + static_cast<size_t>(pg) * E : nullptr;
+        },
+        [&](int f, float m, float l, float h) {
+          const int c = flagged[f];
+          keys[c] = SelectKey(m, cand[c]);
+          s_lo[c] = l;
+          s_hi[c] = h;
+          mid[begin + c] = m;
+          lo[begin + c] = l;
+          hi[begin + c] = h;
+        },
+        queries + static_cast<size_t>(r) * E, E, scale, reinterpret_cast<double*>(tile));
+    if (threadIdx.x == 0) {
+      s_count = 0;
+      s_tie = 0;
+      s_nflag = 0;
+    }
+    __syncthreads();
   }
-  __syncthreads();
   const int nflag = s_nflag;
   if (nflag > 0) {
     // 3. Exact chains for the flagged candidates, then the final order over
@@ -479,8 +509,8 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
 constexpr int kRankMax = 256;
 
 __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
-    const float* __restrict__ mid, const float* __restrict__ lo,
-    const float* __restrict__ hi, const float* __restrict__ queries,
+    float* __restrict__ mid, float* __restrict__ lo,
+    float* __restrict__ hi, const float* __restrict__ queries,
     const float* __restrict__ summaries, const int* __restrict__ token_counts, int capacity,
     const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int total,
     int max_candidates, int E, float scale, int top_k, int* __restrict__ selected,
@@ -536,47 +566,75 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
     }
     return rank;
   };
-  int rank = active ? rank_of(i) : n;
-  if (active && rank < kk) s_top[rank] = i;
-  float my_min = (active && rank < kk) ? s_lo[i] : INFINITY;
-  float my_max = (active && rank >= kk) ? s_hi[i] : -INFINITY;
-  for (int o = 1; o < kWave; o <<= 1) {
-    my_min = fminf(my_min, __shfl_xor(my_min, o, kWave));
-    my_max = fmaxf(my_max, __shfl_xor(my_max, o, kWave));
-  }
   const int wave = threadIdx.x / kWave;
   const int nwaves = (blockDim.x + kWave - 1) / kWave;
-  if ((threadIdx.x & (kWave - 1)) == 0) {
-    s_red[0][wave] = my_min;
-    s_red[1][wave] = my_max;
-  }
-  __syncthreads();
-  float min_t_lo = INFINITY, max_o_hi = -INFINITY;
-  for (int w = 0; w < nwaves; ++w) {
-    min_t_lo = fminf(min_t_lo, s_red[0][w]);
-    max_o_hi = fmaxf(max_o_hi, s_red[1][w]);
-  }
-  if (active) {
-    const float l = s_lo[i];
-    const float h = s_hi[i];
-    bool flag;
-    if (rank >= kk) {
-      flag = h >= min_t_lo;
-    } else {
-      flag = l <= max_o_hi;
-      for (int j = 0; j < kk && !flag; ++j) {
-        if (j == rank) continue;
-        const int c2 = s_top[j];
-        flag = l <= s_hi[c2] && s_lo[c2] <= h;
-      }
+  const int* cand = cand_ids + begin;
+  int rank = n;
+  int nflag = 0;
+  // Pass 0 certifies with the score kernel's intervals; pages it leaves
+  // open get refined intervals (RefineScores, several waves per page; E a
+  // multiple of 256) and pass 1 certifies again.  What pass 1 leaves open
+  // gets the exact chain.
+  for (int pass = 0; pass < 2; ++pass) {
+    rank = active ? rank_of(i) : n;
+    if (active && rank < kk) s_top[rank] = i;
+    float my_min = (active && rank < kk) ? s_lo[i] : INFINITY;
+    float my_max = (active && rank >= kk) ? s_hi[i] : -INFINITY;
+    for (int o = 1; o < kWave; o <<= 1) {
+      my_min = fminf(my_min, __shfl_xor(my_min, o, kWave));
+      my_max = fmaxf(my_max, __shfl_xor(my_max, o, kWave));
     }
-    if (flag) s_flag[atomicAdd(&s_nflag, 1)] = i;
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+      s_red[0][wave] = my_min;
+      s_red[1][wave] = my_max;
+    }
+    __syncthreads();
+    float min_t_lo = INFINITY, max_o_hi = -INFINITY;
+    for (int w = 0; w < nwaves; ++w) {
+      min_t_lo = fminf(min_t_lo, s_red[0][w]);
+      max_o_hi = fmaxf(max_o_hi, s_red[1][w]);
+    }
+    if (active) {
+      const float l = s_lo[i];
+      const float h = s_hi[i];
+      bool flag;
+      if (rank >= kk) {
+        flag = h >= min_t_lo;
+      } else {
+        flag = l <= max_o_hi;
+        for (int j = 0; j < kk && !flag; ++j) {
+          if (j == rank) continue;
+          const int c2 = s_top[j];
+          flag = l <= s_hi[c2] && s_lo[c2] <= h;
+        }
+      }
+      if (flag) s_flag[atomicAdd(&s_nflag, 1)] = i;
+    }
+    __syncthreads();
+    nflag = s_nflag;
+    if (nflag == 0 || pass == 1 || E % 256 != 0) break;
+    RefineScores(
+        nflag,
+        [&](int f) -> const float* {
+          const int pg = cand[s_flag[f]];
+          const bool live = pg >= 0 && pg < capacity && token_counts[pg] != 0;
+          return live ? summaries + static_cast<size_t>(pg) * E : nullptr;
+        },
+        [&](int f, float m, float l, float h) {
+          const int c = s_flag[f];
+          s_key[c] = SelectKey(m, cand[c]);
+          s_lo[c] = l;
+          s_hi[c] = h;
+          mid[begin + c] = m;
+          lo[begin + c] = l;
+          hi[begin + c] = h;
+        },
+        queries + static_cast<size_t>(r) * E, E, scale, reinterpret_cast<double*>(tile));
+    if (i == 0) s_nflag = 0;
+    __syncthreads();
   }
-  __syncthreads();
-  const int nflag = s_nflag;
   if (nflag > 0) {
     if (threadIdx.x == 0 && exact_pages != nullptr) atomicAdd(exact_pages, nflag);
-    const int* cand = cand_ids + begin;
     RescoreChains<kSelRescoreGroup>(
         nflag, [&](int f) { return cand[s_flag[f]]; },
         [&](int f, float score) {
@@ -973,8 +1031,8 @@ void LaunchScoreBounds(const PoolView& pool, const float* d_queries,
   DSD_HIP_CHECK(hipGetLastError());
 }
 
-void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float* d_lo,
-                           const float* d_hi, const float* d_queries,
+void LaunchSelectCertified(const PoolView& pool, float* d_mid, float* d_lo, float* d_hi,
+                           const float* d_queries,
                            const int* d_cand_offsets, const int* d_cand_ids, int batch,
                            int total_candidates, int max_candidates, float scale, int top_k,
                            int* d_selected, int* d_counts, int* d_exact_pages, FailReport fail,

@@ -288,6 +288,16 @@ typedef struct dsd_launch_info {
 } dsd_launch_info;
 int dsd_sparse_last_launch(const dsd_sparse_ctx* ctx, dsd_launch_info* out);
 
+/* Per-workgroup wall-clock stamps of the context's last timed single-launch
+ * step (a host-buffer step in DSD_TIMING_EVENTS mode): *grid workgroups of
+ * *per_group stamps each -- start, slice scored, intervals ready, intervals
+ * read, ranked, selected, end, refinement begun and ended (0 when none ran),
+ * then the hardware ids (HW_ID, XCC_ID << 32) -- at *khz ticks per
+ * millisecond.  out == NULL queries the sizes only.
+ * For profiling; no reference counterpart. */
+int dsd_sparse_step_stamps(const dsd_sparse_ctx* ctx, int* grid, int* per_group, double* khz,
+                           uint64_t* out, size_t capacity);
+
 /* Synchronizes the device, then reports (as its status, with the message in
  * dsd_last_error) the last input failure any step of the context recorded
  * and not yet reported -- e.g. from dsd_sparse_run_batch_device, which

@@ -274,3 +274,52 @@ def test_certified_large_request_ties_and_duplicates(gpu, query):
         assert res["selected"][0].tolist() == selected[0].tolist(), (query, k)
         assert orc.max_abs_diff(res["outputs"], outs) <= 1e-4
     pool.close()
+
+
+@pytest.mark.parametrize("n_cand,k", [(40, 8), (300, 8)])
+def test_refined_intervals_settle_near_ties_without_the_chain(gpu, n_cand, k):
+    # Eight pages whose exact scores differ by about 1e-3: the score pass's
+    # intervals (several 1e-3 wide at these magnitudes) overlap, the refined
+    # intervals (the rounding error of each addition accounted for exactly
+    # where its binade is certain, a few 1e-5 wide) do not.  The selection
+    # must then be settled without any exact chain, every interval (refined
+    # or not) must contain the exact score, and the refined ones (which the
+    # three-kernel step writes back) must be narrower than the gaps.  40
+    # candidates take the single-launch step, 300 the three-kernel step.
+    rng = np.random.default_rng(n_cand)
+    H, D, ps = 32, 128, 16
+    E = H * D
+    scale = 1.0 / np.sqrt(np.float32(D))
+    q = rng.standard_normal(E).astype(np.float32)
+    m = int(np.argmax(np.abs(q)))
+    base = (0.2 * q + 0.25 * rng.standard_normal(E)).astype(np.float32)
+    summ = (0.25 * rng.standard_normal((n_cand, E))).astype(np.float32)
+    near = np.arange(8)
+    for j in near:
+        row = base.copy()
+        row[m] = np.float32(row[m] + j * 1e-3 / (q[m] * scale))
+        summ[j] = row
+    keys = rng.standard_normal((n_cand, ps, E)).astype(np.float32)
+    values = rng.standard_normal((n_cand, ps, E)).astype(np.float32)
+    pool = gpu.DevicePagePool(H, D, ps, n_cand)
+    page_ids = np.arange(n_cand, dtype=np.int32)
+    counts = np.full(n_cand, ps, np.int32)
+    pool.upload_pages(page_ids, counts, page_ids.astype(np.int64) * ps * E, keys, values, summ)
+    ids = rng.permutation(n_cand).astype(np.int32)
+    offs = np.array([0, n_cand], np.int32)
+    cert, (mid, lo, hi), rescored, exact = run_both_paths(gpu, pool, q[None, :], offs, ids, k)
+    ex = exact["scores"]
+    assert np.all(lo <= ex) and np.all(ex <= hi), "an interval misses the exact score"
+    _, selected, outs = orc.sparse_batch(q[None, :], keys, values, summ, counts, offs, ids,
+                                         H, D, ps, k)
+    assert cert["selected"][0].tolist() == selected[0].tolist()
+    assert sorted(selected[0].tolist()) == list(range(8))
+    assert orc.max_abs_diff(cert["outputs"], outs) <= 1e-4
+    assert rescored == 0, f"{rescored} pages needed the exact chain"
+    if n_cand > 256:
+        # the three-kernel select writes its refined intervals back (the
+        # single-launch step keeps them in LDS)
+        where = np.argsort(ids)                      # candidate position of each page id
+        widths = (hi - lo)[where[near]]
+        assert np.all(widths < 2e-4), widths
+    pool.close()
