@@ -83,6 +83,7 @@ struct FusedShared {
   float abs_p[2][kFWaves];       // the next pass may already write its own
   int fail;
   int nflag;
+  int certified;  // FastSelect's verdict, for every wave
   // selection (attention item)
   float mid[kFMaxCand];
   uint64_t key[kFMaxCand];
@@ -322,7 +323,7 @@ __device__ void ScorePass(const PoolView& pool, const FusedArgs& a, int first, i
 // (single-launch steps of one pass per slice, where the pipelined form
 // measured 0.2-0.5 us slower at BASELINE config 2).
 template <bool kPipeline, class Shared>
-__device__ void ScoreSlice(const PoolView& pool, const FusedArgs& a, int r, int c0, int c1,
+__device__ __forceinline__ void ScoreSlice(const PoolView& pool, const FusedArgs& a, int r, int c0, int c1,
                            Shared& sh) {
   if (c0 >= c1) return;
   static_assert(kFE / 4 == kFThreads, "one float4 of the query per thread");
@@ -537,6 +538,141 @@ __device__ bool RankAndCertify(const FusedArgs& a, int n, int kk, const int (&pa
   return any;
 }
 
+// ---- selection for small k (kk <= kFFastK): one wave, kk rounds ----------
+// The ballot ranks of RankAndCertify rank all n candidates with every wave;
+// for a few members it is shorter for one wave to take the best remaining
+// candidate kk times.  Same order (midpoint descending, then page id
+// ascending, then position) and the same certification, so the result is
+// the one RankAndCertify would give.
+constexpr int kFFastK = 32;
+
+__device__ __forceinline__ uint32_t OrderBits(float x) {
+  return static_cast<uint32_t>(SelectKey(x, 0) >> 32);
+}
+
+// x from a DPP source lane; lanes with no source (or outside kRowMask) read
+// 0, the identity of an unsigned maximum.
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ uint32_t DppU32(uint32_t x) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), kCtrl, kRowMask, 0xf, false));
+}
+
+// Maximum over the wave, in every lane.
+__device__ __forceinline__ uint32_t WaveMaxU32(uint32_t x) {
+  x = max(x, DppU32<kRowShr1>(x));
+  x = max(x, DppU32<kRowShr2>(x));
+  x = max(x, DppU32<kRowShr4>(x));
+  x = max(x, DppU32<kRowShr8>(x));
+  x = max(x, DppU32<kRowBcast15, 0xa>(x));
+  x = max(x, DppU32<kRowBcast31, 0xc>(x));
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), kWave - 1));
+}
+
+// Wave 0 only.  Candidate i = lane + 64m (m < CS, i < n) has interval
+// (mid, lo, hi)[m]; its page id and token count are in sh.cpage / sh.cntok.
+// Takes the best remaining candidate kk times; each round's code is short
+// and runs warm after the first (a first run of one-shot code pays for every
+// instruction-cache line it touches, which dominates a round).  Writes the
+// members in rank order to sh.top (candidate index), sh.page and sh.ntok.
+// Returns 1 when the intervals certify the selection; 0 when they do not,
+// after listing the flagged candidates in sh.flag / sh.nflag (an outsider
+// whose hi reaches the members' smallest lo; a member whose lo reaches an
+// outsider's hi or whose interval overlaps another member's) and writing
+// every candidate's key to sh.key; -1 when two midpoints are equal (the
+// ballot ranks then order them).  Nothing else is written before a -1.
+template <int CS>
+__device__ int FastSelect(int n, int kk, const float (&mid)[kFSlots], const float (&lo)[kFSlots],
+                          const float (&hi)[kFSlots], FusedShared& sh) {
+  const int lane = threadIdx.x & (kWave - 1);
+  uint32_t kh[CS];  // order bits of the midpoint; 0: empty or taken
+#pragma unroll
+  for (int m = 0; m < CS; ++m) kh[m] = lane + kWave * m < n ? OrderBits(mid[m]) : 0u;
+  float min_lo = INFINITY;  // over the members taken so far
+  bool ordered = true;
+  float m_lo = INFINITY, m_hi = -INFINITY;  // lane t: member t
+  int m_top = 0;
+#pragma nounroll
+  for (int t = 0; t < kk; ++t) {
+    uint32_t x = kh[0];
+#pragma unroll
+    for (int m = 1; m < CS; ++m) x = max(x, kh[m]);
+    const uint32_t best = WaveMaxU32(x);
+    uint64_t b[CS];
+    int count = 0;
+#pragma unroll
+    for (int m = 0; m < CS; ++m) {
+      b[m] = __ballot(kh[m] == best);
+      count += __popcll(b[m]);
+    }
+    if (count != 1) return -1;
+    int ms = 0;
+    uint64_t bm = b[0];
+#pragma unroll
+    for (int m = 1; m < CS; ++m) {
+      ms = b[m] != 0 ? m : ms;
+      bm |= b[m];
+    }
+    const int ls = __ffsll(static_cast<long long>(bm)) - 1;
+    float w_lo = ReadLane(lo[0], ls), w_hi = ReadLane(hi[0], ls);
+#pragma unroll
+    for (int m = 1; m < CS; ++m) {
+      const float l = ReadLane(lo[m], ls), h = ReadLane(hi[m], ls);
+      w_lo = ms == m ? l : w_lo;
+      w_hi = ms == m ? h : w_hi;
+    }
+#pragma unroll
+    for (int m = 0; m < CS; ++m) kh[m] = (m == ms && lane == ls) ? 0u : kh[m];
+    ordered = ordered && min_lo > w_hi;
+    min_lo = fminf(min_lo, w_lo);
+    if (lane == t) {
+      m_lo = w_lo;
+      m_hi = w_hi;
+      m_top = ls + kWave * ms;
+    }
+  }
+  if (lane < kk) {
+    sh.top[lane] = m_top;
+    sh.page[lane] = sh.cpage[m_top];
+    sh.ntok[lane] = sh.cntok[m_top];
+  }
+  float oh = -INFINITY;  // the outsiders' largest hi
+#pragma unroll
+  for (int m = 0; m < CS; ++m) oh = fmaxf(oh, kh[m] != 0u ? hi[m] : -INFINITY);
+  const float max_o_hi = WaveMax(oh);
+  if (ordered && max_o_hi < min_lo) return 1;
+  // Flags, as RankAndCertify's (members are lanes 0..kk-1 here).
+  const float pmin = DppOr<kWaveShr1>(WaveMinPrefix(m_lo), INFINITY);   // members above
+  const float smax = DppOr<kWaveShl1>(WaveMaxSuffix(m_hi), -INFINITY);  // members below
+  const uint64_t mflag =
+      __ballot(lane < kk && (m_lo <= max_o_hi || pmin <= m_hi || smax >= m_lo));
+  const uint64_t below = (1ull << lane) - 1ull;
+  int base = 0;
+#pragma unroll
+  for (int m = 0; m < CS; ++m) {
+    const int i = lane + kWave * m;
+    const uint64_t of = __ballot(kh[m] != 0u && hi[m] >= min_lo);
+    if ((of >> lane) & 1ull) sh.flag[base + __popcll(of & below)] = i;
+    base += __popcll(of);
+    if (i < n) sh.key[i] = SelectKey(mid[m], sh.cpage[i]);
+  }
+  if ((mflag >> lane) & 1ull) sh.flag[base + __popcll(mflag & below)] = m_top;
+  base += __popcll(mflag);
+  if (lane == 0) sh.nflag = base;
+  return 0;
+}
+
+__device__ __forceinline__ int FastSelectSlots(int n, int kk, const float (&mid)[kFSlots],
+                                               const float (&lo)[kFSlots],
+                                               const float (&hi)[kFSlots], FusedShared& sh) {
+  switch ((n + kWave - 1) / kWave) {
+    case 1: return FastSelect<1>(n, kk, mid, lo, hi, sh);
+    case 2: return FastSelect<2>(n, kk, mid, lo, hi, sh);
+    case 3: return FastSelect<3>(n, kk, mid, lo, hi, sh);
+    default: return FastSelect<4>(n, kk, mid, lo, hi, sh);
+  }
+}
+
 // Top-k of request r (n candidates from `begin`) from the published
 // intervals into sh.page / sh.ntok (rank order); returns the count (0 on
 // failure).  The order is that of the (score desc, page id asc) key of the
@@ -556,7 +692,7 @@ __device__ bool RankAndCertify(const FusedArgs& a, int n, int kk, const int (&pa
 //   4. Only if some pair is flagged: those pages are rescored with the exact
 //      sequential chain (as SelectCertifiedRankKernel) and ranked again.
 // The workgroup with `writer` set also writes the selection out.
-__device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r, int begin,
+__device__ __forceinline__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r, int begin,
                                 int n, bool writer, FusedShared& sh) {
   int kk = a.top_k <= 0 ? 0 : (a.top_k < n ? a.top_k : n);
   if (n > kFMaxCand) {
@@ -583,55 +719,85 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
   }
   if (threadIdx.x == 0) sh.fail = 0;
   if (wave == 0 && kk > 0) {
-    // First an ordinary (L2-cached) read; words whose tag is not current
-    // (not yet visible, or a stale cached line) are then polled coherently.
-    unsigned long long w[kFSlots][3];
-    bool ok = true;
+    // With FastSelect, two runs of one loop body (the same code, so not
+    // inlined twice): run 0 selects from made-up distinct intervals while the
+    // other slices finish, which brings FastSelect's code into the
+    // instruction cache (it writes only sh.top / sh.page / sh.ntok[0], which
+    // run 1 rewrites); run 1 waits for the published intervals and selects.
+    const bool fast = kk <= kFFastK;
+    bool timed_out = false;
+#pragma nounroll
+    for (int run = fast ? 0 : 1; run < 2; ++run) {
+      float mid[kFSlots], lo[kFSlots], hi[kFSlots];
+      if (run == 1) {
+        // First an ordinary (L2-cached) read; words whose tag is not current
+        // (not yet visible, or a stale cached line) are then polled
+        // coherently.
+        unsigned long long w[kFSlots][3];
+        bool ok = true;
 #pragma unroll
-    for (int m = 0; m < kFSlots; ++m) {
-      const int i = lane + kWave * m;
-      w[m][0] = w[m][1] = w[m][2] = static_cast<unsigned long long>(a.wait_tag) << 32;
-      if (i < n) {
-        const unsigned long long* rec = a.rec + 3 * static_cast<size_t>(begin + i);
-        w[m][0] = rec[0];
-        w[m][1] = rec[1];
-        w[m][2] = rec[2];
-        ok = ok && Current(w[m][0], a.wait_tag) && Current(w[m][1], a.wait_tag) &&
-             Current(w[m][2], a.wait_tag);
-      }
-    }
-    unsigned spins = 0;
-    while (__ballot(!ok) != 0) {
-      if (++spins >= a.spin_limit) {
-        if (lane == 0) sh.fail = 1;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-      ok = true;
-#pragma unroll
-      for (int m = 0; m < kFSlots; ++m) {
-        const int i = lane + kWave * m;
-        if (i < n) {
-          unsigned long long* rec = a.rec + 3 * static_cast<size_t>(begin + i);
-#pragma unroll
-          for (int x = 0; x < 3; ++x) {
-            if (!Current(w[m][x], a.wait_tag)) w[m][x] = LoadWord(rec + x);
+        for (int m = 0; m < kFSlots; ++m) {
+          const int i = lane + kWave * m;
+          w[m][0] = w[m][1] = w[m][2] = static_cast<unsigned long long>(a.wait_tag) << 32;
+          if (i < n) {
+            const unsigned long long* rec = a.rec + 3 * static_cast<size_t>(begin + i);
+            w[m][0] = rec[0];
+            w[m][1] = rec[1];
+            w[m][2] = rec[2];
+            ok = ok && Current(w[m][0], a.wait_tag) && Current(w[m][1], a.wait_tag) &&
+                 Current(w[m][2], a.wait_tag);
           }
-          ok = ok && Current(w[m][0], a.wait_tag) && Current(w[m][1], a.wait_tag) &&
-               Current(w[m][2], a.wait_tag);
+        }
+        unsigned spins = 0;
+        while (__ballot(!ok) != 0) {
+          if (++spins >= a.spin_limit) {
+            if (lane == 0) sh.fail = 1;
+            timed_out = true;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+          ok = true;
+#pragma unroll
+          for (int m = 0; m < kFSlots; ++m) {
+            const int i = lane + kWave * m;
+            if (i < n) {
+              unsigned long long* rec = a.rec + 3 * static_cast<size_t>(begin + i);
+#pragma unroll
+              for (int x = 0; x < 3; ++x) {
+                if (!Current(w[m][x], a.wait_tag)) w[m][x] = LoadWord(rec + x);
+              }
+              ok = ok && Current(w[m][0], a.wait_tag) && Current(w[m][1], a.wait_tag) &&
+                   Current(w[m][2], a.wait_tag);
+            }
+          }
+        }
+#pragma unroll
+        for (int m = 0; m < kFSlots; ++m) {
+          const int i = lane + kWave * m;
+          mid[m] = __uint_as_float(static_cast<uint32_t>(w[m][0]));
+          lo[m] = __uint_as_float(static_cast<uint32_t>(w[m][1]));
+          hi[m] = __uint_as_float(static_cast<uint32_t>(w[m][2]));
+          if (i < n) {
+            sh.mid[i] = mid[m];
+            sh.lo[i] = lo[m];
+            sh.hi[i] = hi[m];
+            sh.cpage[i] = page[m];
+            sh.cntok[i] = ntok[m];
+          }
+        }
+        StampAt(a, sh, kReady);
+      } else {
+#pragma unroll
+        for (int m = 0; m < kFSlots; ++m) {
+          mid[m] = lo[m] = hi[m] = -static_cast<float>(lane + kWave * m);
         }
       }
-    }
-#pragma unroll
-    for (int m = 0; m < kFSlots; ++m) {
-      const int i = lane + kWave * m;
-      if (i < n) {
-        sh.mid[i] = __uint_as_float(static_cast<uint32_t>(w[m][0]));
-        sh.lo[i] = __uint_as_float(static_cast<uint32_t>(w[m][1]));
-        sh.hi[i] = __uint_as_float(static_cast<uint32_t>(w[m][2]));
+      if (fast && !timed_out) {
+        const int verdict = FastSelectSlots(n, run == 1 ? kk : 1, mid, lo, hi, sh);
+        if (run == 1 && lane == 0) sh.certified = verdict;
       }
     }
-    StampAt(a, sh, kReady);
+    if (fast) StampAt(a, sh, kRanked);
   }
   __syncthreads();
   StampAt(a, sh, kRecords);
@@ -644,8 +810,30 @@ __device__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r,
     const int cs = (n + kWave - 1) / kWave;    // candidate slots, 1..4
     const int rs = (kk + kWave - 1) / kWave;   // rank slots, 1..cs
     bool any = false;
+    bool ballot = kk > kFFastK;  // the ballot ranks (every wave) or FastSelect
     for (int pass = 0; pass < 2; ++pass) {
-      switch (cs * 8 + rs) {
+      if (!ballot) {
+        if (pass == 1) {
+          // Select again from the refined intervals.
+          if (wave == 0) {
+            float mid[kFSlots], lo[kFSlots], hi[kFSlots];
+#pragma unroll
+            for (int m = 0; m < kFSlots; ++m) {
+              const int i = lane + kWave * m;  // < kFMaxCand: in bounds
+              mid[m] = sh.mid[i];
+              lo[m] = sh.lo[i];
+              hi[m] = sh.hi[i];
+            }
+            const int verdict = FastSelectSlots(n, kk, mid, lo, hi, sh);
+            if (lane == 0) sh.certified = verdict;
+          }
+          __syncthreads();
+        }
+        const int verdict = sh.certified;
+        ballot = verdict < 0;  // equal midpoints: rank with ballots instead
+        any = verdict == 0;
+      }
+      if (ballot) switch (cs * 8 + rs) {
         case 1 * 8 + 1: any = RankAndCertify<1, 1>(a, n, kk, page, ntok, sh); break;
         case 2 * 8 + 1: any = RankAndCertify<2, 1>(a, n, kk, page, ntok, sh); break;
         case 2 * 8 + 2: any = RankAndCertify<2, 2>(a, n, kk, page, ntok, sh); break;
@@ -731,6 +919,10 @@ __device__ __forceinline__ void AttentionItem(const PoolView& pool, const FusedA
   const int g = lane / kFLpt;
   const int j = lane % kFLpt;
   const int head_off = h * kFD + j * kFDq;
+  const int kk = SelectForRequest(pool, a, r, begin, n, group == 0, sh);
+  StampAt(a, sh, kSelected);
+  // The query row loads with the first K/V rows (it is not held through the
+  // selection, whose registers it would take).
   float q[kFDq];
   float acc[kFDq];
   {
@@ -742,8 +934,6 @@ __device__ __forceinline__ void AttentionItem(const PoolView& pool, const FusedA
       acc[i] = 0.0f;
     }
   }
-  const int kk = SelectForRequest(pool, a, r, begin, n, group == 0, sh);
-  StampAt(a, sh, kSelected);
   if (kk == 0) {
     // Nothing selected: zeros (src/cuda/sparse_batched_attention.cu:621-627).
     if (static_cast<int>(threadIdx.x) < hpw * kFD) {
@@ -786,8 +976,8 @@ __device__ __forceinline__ void AttentionItem(const PoolView& pool, const FusedA
 #pragma unroll
         for (int i = 0; i < kFDq; ++i) dot = fmaf(q[i], kv[u][i], dot);
       }
-#pragma unroll
-      for (int o = 1; o < kFLpt; o <<= 1) dot += __shfl_xor(dot, o, kWave);
+      static_assert(kFLpt == 16, "one token row per DPP row");
+      dot = RowSum16(dot);  // the token's 16 lanes: one row
       if (valid[u]) {
         const float m_new = fmaxf(m, dot);
         const float alpha = Exp2(m - m_new);

@@ -70,12 +70,6 @@ __device__ __forceinline__ float NextUp(float x) {
   return __uint_as_float(b);
 }
 
-__device__ __forceinline__ double WaveSum(double v) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
-
 // The certified interval [fl(lo*scale), fl(hi*scale)] around s_hat*scale
 // for an error bound err on the unscaled sum.
 __device__ __forceinline__ void WriteInterval(double s_hat, double err, float scale,
@@ -182,6 +176,58 @@ __device__ __forceinline__ float WaveInclusiveScan(float x) {
 // Sum over the 64 lanes (at most 6 roundings per input), in every lane.
 __device__ __forceinline__ float WaveTotal(float x) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(WaveInclusiveScan(x)), 63));
+}
+
+// A double from a DPP source lane (both halves moved); lanes with no source
+// read +0.0, the identity of a sum.
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ double DppMoveD(double x) {
+  const long long b = __double_as_longlong(x);
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(b), kCtrl, kRowMask, 0xf, false);
+  const int hi =
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(b >> 32), kCtrl, kRowMask, 0xf, false);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) |
+                              static_cast<long long>(static_cast<unsigned>(lo)));
+}
+
+// Inclusive prefix sum over the 64 lanes in double (at most 6 additions on
+// any input's path), and the wave's total in every lane.
+__device__ __forceinline__ double WaveInclusiveScanD(double x) {
+  x += DppMoveD<kRowShr1>(x);
+  x += DppMoveD<kRowShr2>(x);
+  x += DppMoveD<kRowShr4>(x);
+  x += DppMoveD<kRowShr8>(x);
+  x += DppMoveD<kRowBcast15, 0xa>(x);
+  x += DppMoveD<kRowBcast31, 0xc>(x);
+  return x;
+}
+
+__device__ __forceinline__ double ReadLaneD(double x, int lane) {
+  const long long b = __double_as_longlong(x);
+  const int lo = __builtin_amdgcn_readlane(static_cast<int>(b), lane);
+  const int hi = __builtin_amdgcn_readlane(static_cast<int>(b >> 32), lane);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) |
+                              static_cast<long long>(static_cast<unsigned>(lo)));
+}
+
+__device__ __forceinline__ double WaveSum(double v) {
+  return ReadLaneD(WaveInclusiveScanD(v), kWave - 1);
+}
+
+// Sum over each row of 16 lanes, the same value in all 16 (quad swaps, then
+// the half-row and row mirrors: the additions of a xor butterfly, so every
+// lane forms the identical sum).
+constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E, kRowMirror = 0x140, kRowHalfMirror = 0x141;
+__device__ __forceinline__ float RowSum16(float x) {
+  x = __fadd_rn(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kQuadXor1, 0xf,
+                                                           0xf, false)));
+  x = __fadd_rn(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kQuadXor2, 0xf,
+                                                           0xf, false)));
+  x = __fadd_rn(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kRowHalfMirror,
+                                                           0xf, 0xf, false)));
+  x = __fadd_rn(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kRowMirror, 0xf,
+                                                           0xf, false)));
+  return x;
 }
 
 // Orders this wave's LDS writes before its later LDS reads of other lanes'
@@ -460,12 +506,7 @@ __device__ void RefineScores(int nflag, PageOf page_of, Emit emit, const float* 
         }
       }
     }
-    double incl = run;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const double v = __shfl_up(incl, o, kWave);
-      if (lane >= o) incl += v;
-    }
+    const double incl = WaveInclusiveScanD(run);
     if (lane == kWave - 1) mine[0] = incl;  // this part's total
     __syncthreads();
     double before = 0.0, S = 0.0;
