@@ -88,8 +88,9 @@ class Workload:
     the same pages at ids + c * capacity, so steps can rotate over copies that
     share no cache line."""
 
-    def __init__(self, dsd, torch, config, copies):
-        B, lo, hi, H, D, ps, k, seed = CONFIGS[config]
+    def __init__(self, dsd, torch, config, copies, seed=None):
+        B, lo, hi, H, D, ps, k, config_seed = CONFIGS[config]
+        seed = config_seed if seed is None else seed
         self.B, self.H, self.D, self.ps, self.k, self.seed = B, H, D, ps, k, seed
         self.lo, self.hi = lo, hi
         self.E = H * D
@@ -164,6 +165,8 @@ def main() -> int:
                     help="skip the rocprofv3 counter passes (roofline.traffic = null)")
     ap.add_argument("--sweep", action="store_true",
                     help="dense crossover at config 3 and a context-length sweep (B=16, k 8)")
+    ap.add_argument("--seeds", default=None, metavar="A-B",
+                    help="the config's step over data seeds A..B (one batch each)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="internal: the launches the counter passes read")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -191,6 +194,8 @@ def main() -> int:
         return sweep(dsd, torch, args)
     if args.traffic_probe:
         return traffic_probe(dsd, torch, args)
+    if args.seeds:
+        return seed_sweep(dsd, torch, args)
 
     B, lo, hi, H, D, ps, k, seed = CONFIGS[args.config]
     E = H * D
@@ -373,6 +378,36 @@ def main() -> int:
 
     w.close()
     print(json.dumps(result), flush=True)
+    return 0
+
+
+def seed_sweep(dsd, torch, args):
+    """The config's default step (as the headline line times it) on the
+    batches of several data seeds: how the step time depends on the data
+    (near ties at the top-k boundary send a request through refined
+    intervals or the exact chain)."""
+    a, b = (int(x) for x in args.seeds.split("-"))
+    points = []
+    for seed in range(a, b + 1):
+        w = Workload(dsd, torch, args.config, 1, seed=seed)
+        stream = torch.cuda.Stream()
+        sptr = stream.cuda_stream
+        for _ in range(args.warmup):
+            w.step(sptr)
+        torch.cuda.synchronize()
+        w.ctx.exact_rescored_pages(reset=True)
+        ms = timed(torch, stream, lambda i: w.step(sptr), args.steps)
+        w.ctx.device_status()
+        rescored = w.ctx.exact_rescored_pages(reset=True) / args.steps
+        points.append({"seed": seed, "step_us": ms * 1e3, "pages": w.batch.total_candidates,
+                       "exact_rescored_pages_per_step": rescored})
+        log(f"seed {seed}: step {ms * 1e3:.1f} us ({w.batch.total_candidates} pages)")
+        w.close()
+    us = np.array([p["step_us"] for p in points])
+    print(json.dumps({"mode": "seeds", "config": args.config, "steps": args.steps,
+                      "points": points, "median_us": float(np.median(us)),
+                      "mean_us": float(np.mean(us)), "min_us": float(np.min(us)),
+                      "max_us": float(np.max(us))}), flush=True)
     return 0
 
 

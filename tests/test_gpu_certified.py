@@ -323,3 +323,74 @@ def test_refined_intervals_settle_near_ties_without_the_chain(gpu, n_cand, k):
         widths = (hi - lo)[where[near]]
         assert np.all(widths < 2e-4), widths
     pool.close()
+
+
+@pytest.mark.parametrize("k", [1, 8])
+def test_midpoint_order_reversed_by_certification(gpu, k):
+    # Every request's k-th and (k+1)-th pages (A and B) have the same
+    # products in another order: B permutes A's summary within a block where
+    # the query is constant, so their exact scores agree and the reference's
+    # sequential sums differ by rounding only, while their values are
+    # unrelated.  The score-pass midpoints then order A and B at random: in
+    # some requests (asserted) the certified selection takes the page whose
+    # midpoint is the lower one, and the selected ids and the outputs (which
+    # differ a lot between A and B) must still be sparse_cpu's.
+    rng = np.random.default_rng(1000 + k)
+    H, D, ps = 32, 128, 16
+    E = H * D
+    B = 48
+    block = np.arange(1024, 2048)
+    q0 = rng.standard_normal(E).astype(np.float32)
+    q0[block] = 0.37
+    queries = np.empty((B, E), np.float32)
+    for r in range(B):
+        q = (q0 + 0.05 * rng.standard_normal(E)).astype(np.float32)
+        q[block] = 0.37
+        queries[r] = q
+    n_high, n_low = k - 1, 24
+    cap = n_high + n_low + 2 * B
+    summ = np.empty((cap, E), np.float32)
+    for p in range(n_high):
+        summ[p] = (0.3 * q0 + 0.02 * rng.standard_normal(E)).astype(np.float32)
+    for p in range(n_high, n_high + n_low):
+        summ[p] = (0.02 * rng.standard_normal(E)).astype(np.float32)
+    first_pair = n_high + n_low
+    for r in range(B):
+        a = (0.15 * q0 + 0.02 * rng.standard_normal(E)).astype(np.float32)
+        b = a.copy()
+        b[block] = a[block][rng.permutation(block.size)]
+        summ[first_pair + 2 * r] = a
+        summ[first_pair + 2 * r + 1] = b
+    keys = rng.standard_normal((cap, ps, E)).astype(np.float32)
+    values = rng.standard_normal((cap, ps, E)).astype(np.float32)
+    counts = np.full(cap, ps, np.int32)
+    pool = gpu.DevicePagePool(H, D, ps, cap)
+    page_ids = np.arange(cap, dtype=np.int32)
+    pool.upload_pages(page_ids, counts, page_ids.astype(np.int64) * ps * E, keys, values, summ)
+    shared = np.arange(first_pair, dtype=np.int32)
+    lists = [rng.permutation(np.concatenate([shared, [first_pair + 2 * r, first_pair + 2 * r + 1]]))
+             .astype(np.int32) for r in range(B)]
+    offs = np.zeros(B + 1, np.int32)
+    offs[1:] = np.cumsum([len(x) for x in lists])
+    ids = np.concatenate(lists).astype(np.int32)
+    total = int(offs[-1])
+    with gpu.SparseContext(pool, k, B, total, selected_total(offs, k)) as ctx:
+        cert = ctx.run_batch(queries, offs, ids, output_mode=gpu.OUTPUT_OUTPUTS, want_ids=True)
+        launch = ctx.last_launch()
+        mid, lo, hi = ctx.score_bounds(total)
+    assert launch["fused"] == 1, launch
+    _, selected, outs = orc.sparse_batch(queries, keys, values, summ, counts, offs, ids,
+                                         H, D, ps, k)
+    reversed_pairs = 0
+    for r in range(B):
+        assert cert["selected"][r].tolist() == selected[r].tolist(), r
+        pa, pb = first_pair + 2 * r, first_pair + 2 * r + 1
+        at = {int(p): offs[r] + i for i, p in enumerate(lists[r])}
+        ma, mb = mid[at[pa]], mid[at[pb]]
+        won = pa if pa in selected[r].tolist() else pb
+        assert (pa in selected[r].tolist()) != (pb in selected[r].tolist())
+        if ma != mb and (pa if ma > mb else pb) != won:
+            reversed_pairs += 1
+    assert orc.max_abs_diff(cert["outputs"], outs) <= 1e-4
+    assert reversed_pairs > 0, "no request had its midpoint order reversed by certification"
+    pool.close()
