@@ -152,6 +152,28 @@ _SIGNATURES = {
                                               ctypes.c_void_p, ctypes.c_size_t]),
     "dsd_sparse_last_launch": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(LaunchInfo)]),
     "dsd_sparse_set_wait_limit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint, ctypes.c_int]),
+    "dsd_table_create": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                        ctypes.POINTER(ctypes.c_void_p)]),
+    "dsd_table_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "dsd_table_reset": (ctypes.c_int, [ctypes.c_void_p]),
+    "dsd_table_slot_pages": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p]),
+    "dsd_table_free_pages": (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
+    "dsd_table_download": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p, ctypes.c_int,
+                                          _c_int_p]),
+    "dsd_table_free_stack": (ctypes.c_int, [ctypes.c_void_p, _c_int_p, ctypes.c_int, _c_int_p]),
+    "dsd_table_admit_prompt": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                              _c_float_p, _c_float_p]),
+    "dsd_table_admit_synthetic": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                                 ctypes.c_int]),
+    "dsd_table_append": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p, _c_u8_p,
+                                        _c_u8_p, _c_float_p, _c_float_p, _c_int_p, _c_int_p]),
+    "dsd_table_release": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p, ctypes.c_int]),
+    "dsd_sparse_run_table": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                            _c_int_p, _c_float_p, ctypes.POINTER(ctypes.c_void_p),
+                                            ctypes.c_int, ctypes.c_int, _c_float_p, _c_int_p,
+                                            _c_int_p, ctypes.POINTER(StepTimings)]),
+    "dsd_sparse_last_csr": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p, _c_int_p,
+                                           ctypes.c_int]),
     "dsd_dense_run_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_float_p, _c_int_p,
                                            _c_int_p, _c_float_p, _c_double_p]),
     "dsd_dense_run_batch_device": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int] + [ctypes.c_void_p] * 5),
@@ -320,6 +342,98 @@ class DevicePagePool:
         _check(self._lib.dsd_pool_reset_transfer_stats(self.handle))
 
 
+class PageTable:
+    """Request -> page table and free-page stack of a DevicePagePool in
+    device memory (dsd_table_*): admission, append and release are kernels
+    on the pool's stream, and SparseContext.run_table packs a step's
+    candidate lists on the device from slot ids."""
+
+    def __init__(self, pool, max_slots: int, max_pages: int):
+        self._lib = load_library()
+        self.pool = pool
+        self.max_slots = max_slots
+        self.max_pages = max_pages
+        handle = ctypes.c_void_p()
+        _check(self._lib.dsd_table_create(pool.handle, max_slots, max_pages, ctypes.byref(handle)))
+        self.handle = handle
+
+    def close(self) -> None:
+        if self.handle:
+            _check(self._lib.dsd_table_destroy(self.handle))
+            self.handle = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self) -> None:
+        _check(self._lib.dsd_table_reset(self.handle))
+
+    def slot_pages(self, slot: int) -> int:
+        out = ctypes.c_int()
+        _check(self._lib.dsd_table_slot_pages(self.handle, slot, ctypes.byref(out)))
+        return out.value
+
+    def free_pages(self) -> int:
+        out = ctypes.c_int()
+        _check(self._lib.dsd_table_free_pages(self.handle, ctypes.byref(out)))
+        return out.value
+
+    def pages(self, slot: int) -> np.ndarray:
+        buf = np.zeros(max(1, self.max_pages), np.int32)
+        n = ctypes.c_int()
+        _check(self._lib.dsd_table_download(self.handle, slot, _ptr(buf, ctypes.c_int),
+                                            len(buf), ctypes.byref(n)))
+        return buf[:n.value].copy()
+
+    def free_stack(self) -> np.ndarray:
+        buf = np.zeros(max(1, self.pool.capacity), np.int32)
+        n = ctypes.c_int()
+        _check(self._lib.dsd_table_free_stack(self.handle, _ptr(buf, ctypes.c_int), len(buf),
+                                              ctypes.byref(n)))
+        return buf[:n.value].copy()
+
+    def admit_prompt(self, slot: int, keys, values) -> None:
+        k = _f32(keys).reshape(-1)
+        v = _f32(values).reshape(-1)
+        tokens = k.size // self.pool.elements
+        _check(self._lib.dsd_table_admit_prompt(self.handle, slot, tokens,
+                                                _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float)))
+
+    def admit_synthetic(self, slot: int, tokens: int, request_id: int) -> None:
+        _check(self._lib.dsd_table_admit_synthetic(self.handle, slot, tokens, request_id))
+
+    def append(self, slots, upload, fresh_page=None, keys=None, values=None, request_ids=None,
+               decode_steps=None) -> None:
+        sl = _i32(slots)
+        up = np.ascontiguousarray(upload, dtype=np.uint8)
+        fr = np.ascontiguousarray(fresh_page, dtype=np.uint8) if fresh_page is not None else None
+        k = _f32(keys).reshape(-1) if keys is not None else None
+        v = _f32(values).reshape(-1) if values is not None else None
+        rq = _i32(request_ids) if request_ids is not None else None
+        st = _i32(decode_steps) if decode_steps is not None else None
+        _check(self._lib.dsd_table_append(
+            self.handle, len(sl), _ptr(sl, ctypes.c_int),
+            _ptr(fr, ctypes.c_uint8) if fr is not None else None, _ptr(up, ctypes.c_uint8),
+            _ptr(k, ctypes.c_float) if k is not None else None,
+            _ptr(v, ctypes.c_float) if v is not None else None,
+            _ptr(rq, ctypes.c_int) if rq is not None else None,
+            _ptr(st, ctypes.c_int) if st is not None else None))
+
+    def release(self, slots, clear: bool = True) -> None:
+        sl = _i32(slots)
+        _check(self._lib.dsd_table_release(self.handle, len(sl), _ptr(sl, ctypes.c_int),
+                                           int(clear)))
+
+
 class SparseContext:
     """One sparse decode step per call (reference SparseCudaContext,
     include/dsd/cuda_sparse_attention.h:50-137)."""
@@ -439,6 +553,48 @@ class SparseContext:
                 w += c
             result["selected"] = selected
         return result
+
+    def run_table(self, table, slots, queries=None, query_rows=None, output_mode=OUTPUT_OUTPUTS,
+                  timing_mode=TIMING_NONE, want_ids=False):
+        """Step over table slots: request r's candidates are the pages of
+        slots[r] (the CSR is built on the device).  queries [B][E] or
+        query_rows (addresses of pinned rows).  Returns outputs and, with
+        want_ids, the selected ids."""
+        sl = _i32(slots)
+        batch = len(sl)
+        E = self.pool.elements
+        out = np.zeros((batch, E), np.float32)
+        sel = np.zeros(max(1, batch * max(1, self.top_k)), np.int32)
+        counts = np.zeros(max(batch, 1), np.int32)
+        q = _f32(queries).reshape(-1) if queries is not None else None
+        rows = None
+        if query_rows is not None:
+            rows = (ctypes.c_void_p * max(batch, 1))(*[int(p) for p in query_rows])
+        t = StepTimings()
+        _check(self._lib.dsd_sparse_run_table(
+            self.handle, table.handle, batch, _ptr(sl, ctypes.c_int),
+            _ptr(q, ctypes.c_float) if q is not None else None, rows, output_mode, timing_mode,
+            _ptr(out, ctypes.c_float) if output_mode != OUTPUT_NONE else None,
+            _ptr(sel, ctypes.c_int) if want_ids else None,
+            _ptr(counts, ctypes.c_int) if want_ids else None, ctypes.byref(t)))
+        result = {"outputs": out, "timings": t.as_dict()}
+        if want_ids:
+            selected, w = [], 0
+            for r in range(batch):
+                c = int(counts[r])
+                selected.append(sel[w:w + c].copy())
+                w += c
+            result["selected"] = selected
+        return result
+
+    def last_csr(self, batch):
+        """(cand_offsets, cand_ids) of the last step as its kernels read them."""
+        offs = np.zeros(batch + 1, np.int32)
+        cap = max(1, self.max_total_candidates)
+        ids = np.zeros(cap, np.int32)
+        _check(self._lib.dsd_sparse_last_csr(self.handle, batch, _ptr(offs, ctypes.c_int),
+                                             _ptr(ids, ctypes.c_int), cap))
+        return offs, ids[:int(offs[-1])].copy()
 
     def run_batch_device(self, batch, total_candidates, max_candidates, d_queries,
                          d_cand_offsets, d_cand_ids, d_outputs, d_scores=0, d_selected=0,

@@ -622,8 +622,16 @@ int dsd_pool_download_page(const dsd_pool* pool, int page_id, float* keys,
     pool->WaitPending();
     Require(keys != nullptr && values != nullptr, "download outputs must be non-null");
     pool->ValidatePage(page_id);
-    const int count = pool->host_counts[page_id];
-    if (pool->host_live[page_id] == 0 || count == 0) {
+    // The device's metadata (pages handed out by a dsd_table are not in the
+    // host mirror).
+    int count = 0;
+    uint8_t live = 0;
+    DSD_HIP_CHECK(hipMemcpyAsync(&count, pool->view.token_counts + page_id, sizeof(int),
+                                 hipMemcpyDeviceToHost, pool->stream));
+    DSD_HIP_CHECK(hipMemcpyAsync(&live, pool->view.live + page_id, 1, hipMemcpyDeviceToHost,
+                                 pool->stream));
+    pool->Sync();
+    if (live == 0 || count == 0) {
       throw std::runtime_error("cannot download a free device page");
     }
     const PoolView& v = pool->view;
@@ -779,6 +787,333 @@ int dsd_pool_reset_transfer_stats(dsd_pool* pool) {
   return Guard([&] {
     Require(pool != nullptr, "pool must be non-null");
     pool->stats = dsd_transfer_stats{};
+  });
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Request -> page table (device resident; kernels in page_table.hip)
+// ---------------------------------------------------------------------------
+namespace {
+// Pinned argument blocks that the table's kernels read directly; a block is
+// rewritten only after the work that read it is done (ring of kArgBlocks).
+constexpr int kArgBlocks = 8;
+}  // namespace
+
+struct dsd_table {
+  dsd_pool* pool = nullptr;
+  dsdk::TableView view;
+  DeviceBuffer<int> pages, npages, stack, top;
+  // Host mirror of the device counts: pages per slot, device tokens in each
+  // slot's tail page, free pages.  Page ids stay on the device.
+  std::vector<int> h_npages, h_tail;
+  int h_free = 0;
+  // staging
+  DeviceBuffer<float> d_keys, d_values;  // prompt / appended rows
+  DeviceBuffer<int> d_counts, d_plan, d_order;
+  PinnedBuffer<int> h_args[kArgBlocks];
+  hipEvent_t args_ev[kArgBlocks] = {};
+  bool args_busy[kArgBlocks] = {};
+  int args_next = 0;
+
+  ~dsd_table() {
+    for (int b = 0; b < kArgBlocks; ++b) {
+      if (args_ev[b]) {
+        if (args_busy[b]) (void)hipEventSynchronize(args_ev[b]);
+        (void)hipEventDestroy(args_ev[b]);
+      }
+    }
+  }
+  // A pinned block of at least n ints that no enqueued kernel still reads;
+  // Done(block) after the launches that read it.
+  int Acquire(size_t n) {
+    const int b = args_next;
+    args_next = (b + 1) % kArgBlocks;
+    if (args_busy[b]) {
+      DSD_HIP_CHECK(hipEventSynchronize(args_ev[b]));
+      args_busy[b] = false;
+    }
+    h_args[b].Reserve(std::max<size_t>(n, 64), hipHostMallocCoherent);
+    return b;
+  }
+  void Done(int b) {
+    DSD_HIP_CHECK(hipEventRecord(args_ev[b], pool->stream));
+    args_busy[b] = true;
+  }
+  void CheckSlot(int slot) const {
+    if (slot < 0 || slot >= view.max_slots) throw std::out_of_range("table slot out of range");
+  }
+  int PagesFor(int tokens) const {
+    return (tokens + pool->view.page_size - 1) / pool->view.page_size;
+  }
+  // Reserves a prompt's pages for an empty slot (mirror + kernel).
+  int Reserve(int slot, int tokens) {
+    CheckSlot(slot);
+    Require(tokens >= 0, "prompt tokens must be non-negative");
+    if (h_npages[slot] != 0) throw std::invalid_argument("table slot is not empty");
+    const int n = PagesFor(tokens);
+    if (n > view.max_pages) throw std::invalid_argument("prompt exceeds the table's max_pages");
+    if (n > h_free) throw std::runtime_error("page pool is exhausted");
+    h_npages[slot] = n;
+    h_tail[slot] = n == 0 ? 0 : tokens - (n - 1) * pool->view.page_size;
+    h_free -= n;
+    dsdk::LaunchTableReserve(view, slot, n, pool->stream);
+    return n;
+  }
+  const int* SlotPages(int slot) const {
+    return view.pages + static_cast<size_t>(slot) * view.max_pages;
+  }
+};
+
+extern "C" {
+
+int dsd_table_create(dsd_pool* pool, int max_slots, int max_pages, dsd_table** out) {
+  return Guard([&] {
+    Require(out != nullptr, "out must be non-null");
+    *out = nullptr;
+    Require(pool != nullptr, "pool must be non-null");
+    Require(max_slots > 0 && max_pages > 0, "table sizes must be positive");
+    Require(pool->view.elements % 4 == 0, "the table needs E % 4 == 0");
+    auto t = std::make_unique<dsd_table>();
+    t->pool = pool;
+    t->pages.Reserve(static_cast<size_t>(max_slots) * max_pages);
+    t->npages.Reserve(max_slots);
+    t->stack.Reserve(std::max(1, pool->view.capacity));
+    t->top.Reserve(1);
+    t->view.pages = t->pages.ptr;
+    t->view.npages = t->npages.ptr;
+    t->view.free_stack = t->stack.ptr;
+    t->view.free_top = t->top.ptr;
+    t->view.max_slots = max_slots;
+    t->view.max_pages = max_pages;
+    t->h_npages.assign(max_slots, 0);
+    t->h_tail.assign(max_slots, 0);
+    t->h_free = pool->view.capacity;
+    for (hipEvent_t& e : t->args_ev) {
+      DSD_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    }
+    pool->WaitPending();
+    dsdk::LaunchTableReset(t->view, pool->view.capacity, pool->stream);
+    pool->Sync();
+    *out = t.release();
+  });
+}
+
+int dsd_table_destroy(dsd_table* table) {
+  return Guard([&] {
+    if (table == nullptr) return;
+    table->pool->Sync();
+    delete table;
+  });
+}
+
+int dsd_table_reset(dsd_table* table) {
+  return Guard([&] {
+    Require(table != nullptr, "table must be non-null");
+    table->pool->WaitPending();
+    std::fill(table->h_npages.begin(), table->h_npages.end(), 0);
+    std::fill(table->h_tail.begin(), table->h_tail.end(), 0);
+    table->h_free = table->pool->view.capacity;
+    dsdk::LaunchTableReset(table->view, table->pool->view.capacity, table->pool->stream);
+    table->pool->Sync();
+  });
+}
+
+int dsd_table_slot_pages(const dsd_table* table, int slot, int* count) {
+  return Guard([&] {
+    Require(table != nullptr && count != nullptr, "pointers must be non-null");
+    table->CheckSlot(slot);
+    *count = table->h_npages[slot];
+  });
+}
+
+int dsd_table_free_pages(const dsd_table* table, int* count) {
+  return Guard([&] {
+    Require(table != nullptr && count != nullptr, "pointers must be non-null");
+    *count = table->h_free;
+  });
+}
+
+int dsd_table_download(dsd_table* table, int slot, int* page_ids, int capacity, int* count) {
+  return Guard([&] {
+    Require(table != nullptr && count != nullptr, "pointers must be non-null");
+    table->CheckSlot(slot);
+    const int n = table->h_npages[slot];
+    *count = n;
+    if (n == 0) return;
+    Require(page_ids != nullptr && capacity >= n, "page_ids must hold the slot's pages");
+    DSD_HIP_CHECK(hipMemcpyAsync(page_ids, table->SlotPages(slot), sizeof(int) * n,
+                                 hipMemcpyDeviceToHost, table->pool->stream));
+    table->pool->Sync();
+  });
+}
+
+int dsd_table_free_stack(dsd_table* table, int* page_ids, int capacity, int* count) {
+  return Guard([&] {
+    Require(table != nullptr && count != nullptr, "pointers must be non-null");
+    const int n = table->h_free;
+    *count = n;
+    if (n == 0) return;
+    Require(page_ids != nullptr && capacity >= n, "page_ids must hold the free pages");
+    DSD_HIP_CHECK(hipMemcpyAsync(page_ids, table->view.free_stack, sizeof(int) * n,
+                                 hipMemcpyDeviceToHost, table->pool->stream));
+    table->pool->Sync();
+  });
+}
+
+int dsd_table_admit_prompt(dsd_table* table, int slot, int tokens, const float* keys,
+                           const float* values) {
+  return Guard([&] {
+    Require(table != nullptr, "table must be non-null");
+    dsd_pool* pool = table->pool;
+    pool->WaitPending();
+    if (tokens > 0) Require(keys != nullptr && values != nullptr, "prompt rows must be non-null");
+    const int n = table->Reserve(slot, tokens);
+    if (n == 0) return;
+    const size_t elems = static_cast<size_t>(tokens) * pool->view.elements;
+    table->d_keys.Reserve(elems);
+    table->d_values.Reserve(elems);
+    table->d_counts.Reserve(n);
+    pool->H2D(table->d_keys.ptr, keys, sizeof(float) * elems);
+    pool->H2D(table->d_values.ptr, values, sizeof(float) * elems);
+    dsdk::LaunchTableScatter(pool->view, table->view, slot, tokens, table->d_keys.ptr,
+                             table->d_values.ptr, pool->stream);
+    dsdk::LaunchTablePromptCounts(table->view, slot, tokens, pool->view.page_size,
+                                  table->d_counts.ptr, pool->stream);
+    dsdk::LaunchFinishPageUpload(pool->view, table->SlotPages(slot), table->d_counts.ptr,
+                                 nullptr, n, pool->stream);
+  });
+}
+
+int dsd_table_admit_synthetic(dsd_table* table, int slot, int tokens, int request_id) {
+  return Guard([&] {
+    Require(table != nullptr, "table must be non-null");
+    dsd_pool* pool = table->pool;
+    pool->WaitPending();
+    const int n = table->Reserve(slot, tokens);
+    if (n == 0) return;
+    table->d_counts.Reserve(n);
+    dsdk::LaunchTablePromptCounts(table->view, slot, tokens, pool->view.page_size,
+                                  table->d_counts.ptr, pool->stream);
+    dsdk::LaunchPrefillSynthetic(pool->view, table->SlotPages(slot), table->d_counts.ptr, n,
+                                 request_id, pool->stream);
+  });
+}
+
+int dsd_table_append(dsd_table* table, int n, const int* slots, const unsigned char* fresh_page,
+                     const unsigned char* upload, const float* keys, const float* values,
+                     const int* request_ids, const int* decode_steps) {
+  return Guard([&] {
+    Require(table != nullptr, "table must be non-null");
+    dsd_pool* pool = table->pool;
+    Require(n >= 0, "token count must be non-negative");
+    if (n == 0) return;
+    Require(slots != nullptr && upload != nullptr, "slots and upload flags must be non-null");
+    const bool rows = keys != nullptr || values != nullptr;
+    if (rows) Require(keys != nullptr && values != nullptr, "keys and values go together");
+    if (!rows) {
+      Require(request_ids != nullptr && decode_steps != nullptr,
+              "synthetic payloads need request ids and decode steps");
+    }
+    pool->WaitPending();
+    const int ps = pool->view.page_size;
+    // Mirror first (all checks before anything is enqueued or changed).
+    int fresh_pages = 0, m = 0;
+    {
+      std::vector<int> seen;
+      for (int i = 0; i < n; ++i) {
+        table->CheckSlot(slots[i]);
+        seen.push_back(slots[i]);
+      }
+      std::sort(seen.begin(), seen.end());
+      if (std::adjacent_find(seen.begin(), seen.end()) != seen.end()) {
+        throw std::invalid_argument("a slot appears twice in one append");
+      }
+      for (int i = 0; i < n; ++i) {
+        const int s = slots[i];
+        const bool fresh = (fresh_page != nullptr && fresh_page[i] != 0) ||
+                           table->h_npages[s] == 0 || table->h_tail[s] >= ps;
+        if (fresh && table->h_npages[s] >= table->view.max_pages) {
+          throw std::invalid_argument("a request exceeds the table's max_pages");
+        }
+        fresh_pages += fresh ? 1 : 0;
+        m += upload[i] != 0 ? 1 : 0;
+      }
+      if (fresh_pages > table->h_free) throw std::runtime_error("page pool is exhausted");
+    }
+    for (int i = 0; i < n; ++i) {
+      const int s = slots[i];
+      const bool fresh = (fresh_page != nullptr && fresh_page[i] != 0) ||
+                         table->h_npages[s] == 0 || table->h_tail[s] >= ps;
+      if (fresh) {
+        ++table->h_npages[s];
+        table->h_tail[s] = 0;
+      }
+      if (upload[i] != 0) ++table->h_tail[s];
+    }
+    table->h_free -= fresh_pages;
+    const int b = table->Acquire(4 * static_cast<size_t>(n));
+    int* args = table->h_args[b].ptr;
+    for (int i = 0; i < n; ++i) {
+      args[i] = slots[i];
+      args[n + i] = ((fresh_page != nullptr && fresh_page[i] != 0) ? 1 : 0) |
+                    (upload[i] != 0 ? 2 : 0);
+      args[2 * n + i] = request_ids != nullptr ? request_ids[i] : 0;
+      args[3 * n + i] = decode_steps != nullptr ? decode_steps[i] : 0;
+    }
+    table->d_plan.Reserve(6 * static_cast<size_t>(m) + 1);
+    table->d_order.Reserve(std::max(1, m));
+    dsdk::LaunchTablePlanAppend(pool->view, table->view, args, n, m, table->d_plan.ptr,
+                                table->d_order.ptr, pool->stream);
+    table->Done(b);
+    if (m == 0) return;
+    if (rows) {
+      const size_t elems = static_cast<size_t>(m) * pool->view.elements;
+      table->d_keys.Reserve(elems);
+      table->d_values.Reserve(elems);
+      pool->H2D(table->d_keys.ptr, keys, sizeof(float) * elems);
+      pool->H2D(table->d_values.ptr, values, sizeof(float) * elems);
+      int* plan = table->d_plan.ptr;
+      dsdk::LaunchAppendTokens(pool->view, plan, table->d_order.ptr, plan + m + 1,
+                               plan + 2 * m + 1, plan + 3 * m + 1, table->d_keys.ptr,
+                               table->d_values.ptr, nullptr, m, pool->stream);
+    } else {
+      dsdk::LaunchAppendSynthetic(pool->view, table->d_plan.ptr, m, m, pool->stream);
+    }
+  });
+}
+
+int dsd_table_release(dsd_table* table, int n, const int* slots, int clear) {
+  return Guard([&] {
+    Require(table != nullptr, "table must be non-null");
+    Require(n >= 0, "slot count must be non-negative");
+    if (n == 0) return;
+    Require(slots != nullptr, "slots must be non-null");
+    dsd_pool* pool = table->pool;
+    pool->WaitPending();
+    std::vector<int> seen(slots, slots + n);
+    for (int s : seen) table->CheckSlot(s);
+    std::sort(seen.begin(), seen.end());
+    if (std::adjacent_find(seen.begin(), seen.end()) != seen.end()) {
+      throw std::invalid_argument("a slot appears twice in one release");
+    }
+    constexpr int kChunk = 1024;
+    for (int c0 = 0; c0 < n; c0 += kChunk) {
+      const int c = std::min(kChunk, n - c0);
+      int pages = 0;
+      for (int i = 0; i < c; ++i) pages += table->h_npages[slots[c0 + i]];
+      const int b = table->Acquire(static_cast<size_t>(c));
+      std::memcpy(table->h_args[b].ptr, slots + c0, sizeof(int) * c);
+      dsdk::LaunchTableRelease(pool->view, table->view, table->h_args[b].ptr, c, pages,
+                               clear != 0, pool->stream);
+      table->Done(b);
+      for (int i = 0; i < c; ++i) {
+        table->h_npages[slots[c0 + i]] = 0;
+        table->h_tail[slots[c0 + i]] = 0;
+      }
+      table->h_free += pages;
+    }
   });
 }
 
@@ -1183,10 +1518,14 @@ namespace {
 // pinned staging and are copied to `outputs` when it is non-null.  With
 // `rows`, request r's query is read from rows[r] (pinned memory the device
 // reads directly) instead of from `queries`.
+// With `table`, request r's candidate list is the page list of table slot
+// slots[r] (cand_offsets / cand_ids unused): the stage-in kernel builds the
+// CSR on the device, and only the queries and the slot ids cross PCIe.
 void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
               const float* const* rows, const int* cand_offsets, const int* cand_ids,
               int output_mode, int timing_mode, float* outputs, float* scores, int* selected,
-              int* selected_counts, dsd_step_timings* timings) {
+              int* selected_counts, dsd_step_timings* timings,
+              const dsd_table* table = nullptr, const int* slots = nullptr) {
     Require(ctx != nullptr, "context must be non-null");
     Require(batch >= 0, "batch must be non-negative");
     Require(output_mode >= DSD_OUTPUT_NONE && output_mode <= DSD_OUTPUT_DEBUG,
@@ -1194,15 +1533,22 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
     dsd_step_timings t{};
     if (timings != nullptr) *timings = t;
     if (batch == 0) return;
-    Require((queries != nullptr || rows != nullptr) && cand_offsets != nullptr,
-            "inputs must be non-null");
+    Require(queries != nullptr || rows != nullptr, "inputs must be non-null");
+    if (table != nullptr) {
+      Require(slots != nullptr, "slots must be non-null");
+      Require(table->pool == ctx->pool, "the table belongs to another pool");
+    } else {
+      Require(cand_offsets != nullptr, "inputs must be non-null");
+    }
     const bool want_outputs = output_mode != DSD_OUTPUT_NONE;
     const bool debug = output_mode == DSD_OUTPUT_DEBUG;
     // Ids are returned in debug mode, or in outputs mode when buffers are given.
     const bool want_ids =
         debug || (want_outputs && selected != nullptr && selected_counts != nullptr);
     const bool timing = timing_mode == DSD_TIMING_EVENTS;
-    if (want_outputs && !staged) Require(outputs != nullptr, "outputs must be non-null");
+    if (want_outputs && !staged && table == nullptr) {
+      Require(outputs != nullptr, "outputs must be non-null");
+    }
     if (debug) {
       Require(scores != nullptr && selected != nullptr && selected_counts != nullptr,
               "debug outputs must be non-null");
@@ -1211,17 +1557,26 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
     const int E = pool.view.elements;
 
     // Shape checks (the reference's PackSparseBatchInto + capacity checks,
-    // src/cuda/sparse_batched_attention.cu:24-96,600-608).
-    Require(cand_offsets[0] == 0, "cand_offsets[0] must be 0");
+    // src/cuda/sparse_batched_attention.cu:24-96,600-608); a table's counts
+    // come from its host mirror.
+    if (table == nullptr) Require(cand_offsets[0] == 0, "cand_offsets[0] must be 0");
     int max_n = 0;
     int total_sel = 0;
+    int total = 0;
     for (int r = 0; r < batch; ++r) {
-      const int n = cand_offsets[r + 1] - cand_offsets[r];
-      Require(n >= 0, "cand_offsets must be non-decreasing");
+      int n = 0;
+      if (table != nullptr) {
+        table->CheckSlot(slots[r]);
+        n = table->h_npages[slots[r]];
+      } else {
+        n = cand_offsets[r + 1] - cand_offsets[r];
+        Require(n >= 0, "cand_offsets must be non-decreasing");
+      }
       max_n = std::max(max_n, n);
       total_sel += std::min(ctx->top_k, n);
+      total += n;
     }
-    const int total = cand_offsets[batch];
+    if (table == nullptr) total = cand_offsets[batch];
     if (batch > ctx->max_batch) {
       throw std::invalid_argument("request batch exceeds sparse context capacity");
     }
@@ -1231,8 +1586,10 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
     if (total_sel > ctx->max_sel) {
       throw std::invalid_argument("selected page count exceeds sparse context capacity");
     }
-    if (total > 0) Require(cand_ids != nullptr, "cand_ids must be non-null");
-    for (int c = 0; c < total; ++c) ctx->pool->ValidatePage(cand_ids[c]);
+    if (table == nullptr) {
+      if (total > 0) Require(cand_ids != nullptr, "cand_ids must be non-null");
+      for (int c = 0; c < total; ++c) ctx->pool->ValidatePage(cand_ids[c]);
+    }
     if (rows != nullptr) {
       // Each row: non-null, 16-byte aligned, and inside a dsd_host_alloc
       // block or the context's own query staging (its row r).
@@ -1262,7 +1619,12 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
     // Host -> device through pinned staging.
     auto t0 = Clock::now();
     const size_t qn = static_cast<size_t>(batch) * E;
-    if (!staged) {
+    if (table != nullptr) {
+      if (rows == nullptr && queries != ctx->h_queries.ptr) {
+        std::memcpy(ctx->h_queries.ptr, queries, sizeof(float) * qn);
+      }
+      std::memcpy(ctx->h_offsets.ptr, slots, sizeof(int) * batch);  // the slot ids
+    } else if (!staged) {
       if (rows == nullptr) std::memcpy(ctx->h_queries.ptr, queries, sizeof(float) * qn);
       std::memcpy(ctx->h_offsets.ptr, cand_offsets, sizeof(int) * (batch + 1));
       if (total > 0) std::memcpy(ctx->h_ids.ptr, cand_ids, sizeof(int) * total);
@@ -1273,13 +1635,21 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
       // One kernel on the step's stream copies the staged inputs to the
       // device: DMA copies would each cost a copy-engine hand-off.
       dsdk::StageSegments seg;
-      seg.src[0] = reinterpret_cast<const uint32_t*>(ctx->h_offsets.ptr);
-      seg.dst[0] = reinterpret_cast<uint32_t*>(ctx->d_offsets.ptr);
-      seg.words[0] = batch + 1;
-      seg.src[1] = reinterpret_cast<const uint32_t*>(ctx->h_ids.ptr);
-      seg.dst[1] = reinterpret_cast<uint32_t*>(ctx->d_ids.ptr);
-      seg.words[1] = total;
-      seg.count = 2;
+      if (table != nullptr) {
+        seg.table = table->view;
+        seg.table_slots = ctx->h_offsets.ptr;
+        seg.table_batch = batch;
+        seg.csr_offsets = ctx->d_offsets.ptr;
+        seg.csr_ids = ctx->d_ids.ptr;
+      } else {
+        seg.src[0] = reinterpret_cast<const uint32_t*>(ctx->h_offsets.ptr);
+        seg.dst[0] = reinterpret_cast<uint32_t*>(ctx->d_offsets.ptr);
+        seg.words[0] = batch + 1;
+        seg.src[1] = reinterpret_cast<const uint32_t*>(ctx->h_ids.ptr);
+        seg.dst[1] = reinterpret_cast<uint32_t*>(ctx->d_ids.ptr);
+        seg.words[1] = total;
+        seg.count = 2;
+      }
       if (rows != nullptr) {
         std::memcpy(ctx->h_rows.ptr, rows, sizeof(const float*) * batch);
         seg.rows = ctx->h_rows.ptr;
@@ -1287,10 +1657,10 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
         seg.nrows = batch;
         seg.row_words = E;
       } else {
-        seg.src[2] = reinterpret_cast<const uint32_t*>(ctx->h_queries.ptr);
-        seg.dst[2] = reinterpret_cast<uint32_t*>(ctx->d_queries.ptr);
-        seg.words[2] = static_cast<int>(qn);
-        seg.count = 3;
+        seg.src[seg.count] = reinterpret_cast<const uint32_t*>(ctx->h_queries.ptr);
+        seg.dst[seg.count] = reinterpret_cast<uint32_t*>(ctx->d_queries.ptr);
+        seg.words[seg.count] = static_cast<int>(qn);
+        ++seg.count;
       }
       dsdk::LaunchStageIn(seg, ctx->stream);
     }
@@ -1374,6 +1744,38 @@ int dsd_sparse_run_batch(dsd_sparse_ctx* ctx, int batch, const float* queries,
   return Guard([&] {
     HostStep(ctx, batch, false, queries, nullptr, cand_offsets, cand_ids, output_mode,
              timing_mode, outputs, scores, selected, selected_counts, timings);
+  });
+}
+
+int dsd_sparse_run_table(dsd_sparse_ctx* ctx, dsd_table* table, int batch, const int* slots,
+                         const float* queries, const float* const* query_rows, int output_mode,
+                         int timing_mode, float* outputs, int* selected, int* selected_counts,
+                         dsd_step_timings* timings) {
+  return Guard([&] {
+    Require(ctx != nullptr && table != nullptr, "context and table must be non-null");
+    Require(output_mode != DSD_OUTPUT_DEBUG, "the table step has no debug mode");
+    Require(batch <= ctx->max_batch, "request batch exceeds sparse context capacity");
+    Require(queries == nullptr || query_rows == nullptr, "give queries or query_rows, not both");
+    HostStep(ctx, batch, false, queries, query_rows, nullptr, nullptr, output_mode, timing_mode,
+             outputs, nullptr, selected, selected_counts, timings, table, slots);
+  });
+}
+
+int dsd_sparse_last_csr(dsd_sparse_ctx* ctx, int batch, int* cand_offsets, int* cand_ids,
+                        int capacity) {
+  return Guard([&] {
+    Require(ctx != nullptr && cand_offsets != nullptr, "pointers must be non-null");
+    Require(batch >= 0 && batch <= ctx->max_batch, "batch out of range");
+    DSD_HIP_CHECK(hipMemcpyAsync(cand_offsets, ctx->d_offsets.ptr, sizeof(int) * (batch + 1),
+                                 hipMemcpyDeviceToHost, ctx->stream));
+    DSD_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    const int total = cand_offsets[batch];
+    Require(total >= 0 && total <= ctx->max_cand, "the last step's CSR is malformed");
+    if (total == 0) return;
+    Require(cand_ids != nullptr && capacity >= total, "cand_ids must hold the candidates");
+    DSD_HIP_CHECK(hipMemcpyAsync(cand_ids, ctx->d_ids.ptr, sizeof(int) * total,
+                                 hipMemcpyDeviceToHost, ctx->stream));
+    DSD_HIP_CHECK(hipStreamSynchronize(ctx->stream));
   });
 }
 

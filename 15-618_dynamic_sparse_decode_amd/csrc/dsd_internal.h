@@ -86,11 +86,48 @@ void LaunchAppendSynthetic(const PoolView& pool, const int* meta, int n, int num
 void LaunchMarkFree(const PoolView& pool, const int* d_page_ids, int n,
                     hipStream_t stream);
 
+// ---- request -> page table (page_table.hip) ---------------------------------
+
+// A pool's request -> page table and free-page stack in device memory.
+struct TableView {
+  int* pages = nullptr;       // [max_slots][max_pages]: slot s's pages in logical order
+  int* npages = nullptr;      // [max_slots]
+  int* free_stack = nullptr;  // [pool capacity]: free page ids, top at free_top - 1
+  int* free_top = nullptr;    // [1]
+  int max_slots = 0;
+  int max_pages = 0;
+};
+
+// Stack = [0 .. capacity-1], every slot empty.
+void LaunchTableReset(const TableView& t, int capacity, hipStream_t stream);
+// Slot `slot` (empty) takes the n pages on top of the stack, ascending.
+void LaunchTableReserve(const TableView& t, int slot, int n, hipStream_t stream);
+// d_keys / d_values: tokens x E rows (device) into the pages of `slot`.
+void LaunchTableScatter(const PoolView& pool, const TableView& t, int slot, int tokens,
+                        const float* d_keys, const float* d_values, hipStream_t stream);
+// d_counts[j] = tokens in prompt page j of a `tokens`-token prompt.
+void LaunchTablePromptCounts(const TableView& t, int slot, int tokens, int page_size,
+                             int* d_counts, hipStream_t stream);
+// One token for each of n slots: page allocation, then the plan of the m
+// uploaded tokens (layout in page_table.hip) for LaunchAppendSynthetic
+// (meta = d_plan) or LaunchAppendTokens (d_order and the plan's arrays).
+// args (device-readable, e.g. pinned): slots[n], flags[n], request ids[n],
+// decode steps[n].
+void LaunchTablePlanAppend(const PoolView& pool, const TableView& t, const int* args, int n,
+                           int m, int* d_plan, int* d_order, hipStream_t stream);
+// n <= 1024 slots (device-readable) back to the stack; `clear` also clears
+// their pages' counts, live flags and summaries.
+void LaunchTableRelease(const PoolView& pool, const TableView& t, const int* slots, int n,
+                        int released_pages, bool clear, hipStream_t stream);
+
 // Up to four segments of 4-byte words, each 16-byte aligned at both ends of
 // the copy: src in pinned host memory the device reads directly, dst in
 // device memory.  Optionally also a row gather: nrows rows of row_words
 // words (a multiple of 4), row r from rows[r] (a device-visible table of
 // device-visible, 16-byte aligned pointers) to rows_dst + r * row_words.
+// Optionally also the candidate lists of a batch from a page table: request
+// b's list is table.pages[slots[b]] (slots device-readable), written as the
+// CSR csr_offsets[table_batch + 1] / csr_ids.
 struct StageSegments {
   const uint32_t* src[4] = {};
   uint32_t* dst[4] = {};
@@ -100,6 +137,11 @@ struct StageSegments {
   float* rows_dst = nullptr;
   int nrows = 0;
   int row_words = 0;
+  TableView table;
+  const int* table_slots = nullptr;
+  int table_batch = 0;
+  int* csr_offsets = nullptr;
+  int* csr_ids = nullptr;
 };
 void LaunchStageIn(const StageSegments& s, hipStream_t stream);
 

@@ -277,6 +277,32 @@ void LaunchAppendSynthetic(const PoolView& pool, const int* meta, int n, int num
 // coherent) staging into device buffers, on the step's stream: one small
 // kernel instead of DMA copies, each of which costs a hand-off between the
 // copy engine and the compute queue (tens of microseconds per step).
+// Exclusive prefix sum of one int per thread of a kPoolThreads workgroup;
+// *total gets the sum.  Every thread calls.
+__device__ int PoolBlockScan(int x, int* scratch, int* total) {
+  constexpr int kWaves = kPoolThreads / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int incl = x;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) scratch[wave] = incl;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int v = scratch[w];
+    before += w < wave ? v : 0;
+    all += v;
+  }
+  __syncthreads();
+  *total = all;
+  return before + incl - x;
+}
+
 __global__ __launch_bounds__(kPoolThreads) void StageInKernel(StageSegments s) {
   const int tid = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
   const int stride = static_cast<int>(gridDim.x * blockDim.x);
@@ -305,6 +331,37 @@ __global__ __launch_bounds__(kPoolThreads) void StageInKernel(StageSegments s) {
       }
     }
   }
+  if (s.table_batch > 0) {
+    // The batch's candidate lists from the page table.  Every workgroup
+    // forms the same offsets (a scan of the slots' page counts, in chunks
+    // of kPoolThreads requests); workgroup 0 writes them, and request b's
+    // list is copied by workgroup b mod gridDim.x.
+    __shared__ int scan[kPoolThreads / 64];
+    __shared__ int pos_s[kPoolThreads], np_s[kPoolThreads], slot_s[kPoolThreads];
+    int base = 0;
+    for (int b0 = 0; b0 < s.table_batch; b0 += kPoolThreads) {
+      const int b = b0 + static_cast<int>(threadIdx.x);
+      const bool in = b < s.table_batch;
+      const int slot = in ? s.table_slots[b] : 0;
+      const int np = in ? s.table.npages[slot] : 0;
+      int total = 0;
+      const int pos = base + PoolBlockScan(np, scan, &total);
+      if (in && blockIdx.x == 0) s.csr_offsets[b] = pos;
+      pos_s[threadIdx.x] = pos;
+      np_s[threadIdx.x] = np;
+      slot_s[threadIdx.x] = slot;
+      __syncthreads();
+      const int chunk = min(kPoolThreads, s.table_batch - b0);
+      for (int k = 0; k < chunk; ++k) {
+        if ((b0 + k) % static_cast<int>(gridDim.x) != static_cast<int>(blockIdx.x)) continue;
+        const int* list = s.table.pages + static_cast<size_t>(slot_s[k]) * s.table.max_pages;
+        for (int j = threadIdx.x; j < np_s[k]; j += kPoolThreads) s.csr_ids[pos_s[k] + j] = list[j];
+      }
+      __syncthreads();
+      base += total;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) s.csr_offsets[s.table_batch] = base;
+  }
 }
 
 void LaunchStageIn(const StageSegments& s, hipStream_t stream) {
@@ -322,6 +379,13 @@ void LaunchStageIn(const StageSegments& s, hipStream_t stream) {
       throw std::invalid_argument("row gather needs 16-byte aligned rows of 4k words");
     }
     words += static_cast<size_t>(s.nrows) * static_cast<size_t>(s.row_words);
+  }
+  if (s.table_batch > 0) {
+    if (s.table_slots == nullptr || s.csr_offsets == nullptr || s.csr_ids == nullptr ||
+        s.table.pages == nullptr) {
+      throw std::invalid_argument("table staging needs slots, a table and CSR buffers");
+    }
+    words += static_cast<size_t>(s.table_batch) * 64;  // at least a workgroup per 4 requests
   }
   if (words == 0) return;
   size_t groups = (words / 4 + kPoolThreads - 1) / kPoolThreads + 1;

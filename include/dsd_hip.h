@@ -375,6 +375,92 @@ int dsd_sparse_score_bounds(dsd_sparse_ctx* ctx, int n, float* mid, float* lo,
  * reset != 0 zeroes the counter.  Synchronizes the device. */
 int dsd_sparse_exact_rescored_pages(dsd_sparse_ctx* ctx, int reset, int* out);
 
+/* ---- request -> page table in HBM --------------------------------------- */
+/* The reference keeps the request -> page table (PagedKvCache::
+ * request_to_pages_, include/dsd/paged_kv_cache.h:120) and the free-page
+ * list (PagePool, src/page_pool.cpp:36-44) on the host and packs every
+ * step's candidate lists there (PackSparseBatchInto,
+ * src/cuda/sparse_batched_attention.cu:24-96).  dsd_table keeps both in
+ * device memory beside a pool: max_slots request slots of at most max_pages
+ * page ids each, and a stack of free page ids with the PagePool order
+ * (initially [0 .. capacity-1], the first page handed out capacity-1).  The
+ * calls below enqueue kernels on the pool's stream and return; the host
+ * keeps only counts (pages per slot, tokens in each tail page, free pages),
+ * so it can check every call before enqueueing it and never reads page ids
+ * back unless asked (dsd_table_download).  A table owns the pages it hands
+ * out: use it, not dsd_pool_upload_* / mark_free, for those pages.  Only one
+ * table per pool. */
+typedef struct dsd_table dsd_table;
+
+int dsd_table_create(dsd_pool* pool, int max_slots, int max_pages,
+                     dsd_table** out);
+int dsd_table_destroy(dsd_table* table);
+/* Every slot empty, every page free (as at creation). */
+int dsd_table_reset(dsd_table* table);
+/* Pages of a slot; free pages (host mirror, no device access). */
+int dsd_table_slot_pages(const dsd_table* table, int slot, int* count);
+int dsd_table_free_pages(const dsd_table* table, int* count);
+/* The slot's page ids in list order, and the free stack bottom to top
+ * (synchronous downloads, for tests and observers). */
+int dsd_table_download(dsd_table* table, int slot, int* page_ids, int capacity,
+                       int* count);
+int dsd_table_free_stack(dsd_table* table, int* page_ids, int capacity,
+                         int* count);
+
+/* Prompt admission into an empty slot: ceil(tokens / page_size) pages off
+ * the stack, kept ascending (PagedKvCache::ReservePagesForRequest,
+ * src/paged_kv_cache.cpp:114-160), then the prompt's rows
+ * (keys / values: tokens x E host floats, token t to page t / page_size)
+ * and each page's summary by the host cache's rule.  Replaces
+ * ReservePagesForRequest + DevicePagePool::UploadPromptDirect
+ * (src/device_page_pool.cpp:491-624).  The caller's buffers may be reused
+ * on return. */
+int dsd_table_admit_prompt(dsd_table* table, int slot, int tokens,
+                           const float* keys, const float* values);
+/* The same with the synthetic integer-hash prompt of request_id generated
+ * on the device (DevicePagePool::PrefillPromptSynthetic,
+ * src/device_page_pool.cpp:626-679). */
+int dsd_table_admit_synthetic(dsd_table* table, int slot, int tokens,
+                              int request_id);
+/* One decode token for each of n distinct slots, in batch order
+ * (PagedKvCache::AppendTokenMetadataOnly, src/paged_kv_cache.cpp:312-351,
+ * then DevicePagePool::UploadTokensDirect / AppendTokensSynthetic,
+ * src/device_page_pool.cpp:700-983): a slot whose tail page is full, that
+ * has no page, or with fresh_page[i] != 0 takes the next page off the stack
+ * (batch order).  Tokens with upload[i] != 0 get their payload: rows of
+ * keys / values (m x E host floats, the uploaded tokens in batch order), or
+ * with keys == values == NULL the device hash of (request_ids[i],
+ * decode_steps[i]); the page summary follows the running mean.  A token
+ * without upload only takes its page (the reference uploads every token but
+ * a request's last).  fresh_page may be NULL. */
+int dsd_table_append(dsd_table* table, int n, const int* slots,
+                     const unsigned char* fresh_page, const unsigned char* upload,
+                     const float* keys, const float* values,
+                     const int* request_ids, const int* decode_steps);
+/* The pages of n distinct slots back on the stack, in list order, slots in
+ * order (PagedKvCache::ReleaseRequest, src/paged_kv_cache.cpp:354-373);
+ * clear != 0 also clears their token counts, live flags and summaries
+ * (DevicePagePool::MarkPagesFree, src/device_page_pool.cpp:989-1043). */
+int dsd_table_release(dsd_table* table, int n, const int* slots, int clear);
+
+/* The sparse step (dsd_sparse_run_batch) with request r's candidate list
+ * the page list of table slot slots[r]: the CSR is built on the device from
+ * the table, so only the queries and the slot ids cross PCIe.  Queries:
+ * `queries` ([batch][E] host floats, or the staging's own rows) or
+ * query_rows (as dsd_sparse_run_staged_rows).  Output modes NONE / OUTPUTS;
+ * outputs NULL leaves them in the staging (dsd_sparse_staging).  Replaces
+ * SparseCudaContext::RunBatch's packing
+ * (src/cuda/sparse_batched_attention.cu:24-96,554-838). */
+int dsd_sparse_run_table(dsd_sparse_ctx* ctx, dsd_table* table, int batch,
+                         const int* slots, const float* queries,
+                         const float* const* query_rows, int output_mode,
+                         int timing_mode, float* outputs, int* selected,
+                         int* selected_counts, dsd_step_timings* timings);
+/* The CSR of the last step (cand_offsets[batch + 1], cand_ids) as the step
+ * read it; synchronous.  For observers of table steps. */
+int dsd_sparse_last_csr(dsd_sparse_ctx* ctx, int batch, int* cand_offsets,
+                        int* cand_ids, int capacity);
+
 /* ---- dense decode step ------------------------------------------------- */
 /* DenseCudaContext::RunBatch (include/dsd/cuda_dense_attention.h:18-44):
  * attention over every candidate page, host buffers as above.
