@@ -811,7 +811,7 @@ struct dsd_table {
   int h_free = 0;
   // staging
   DeviceBuffer<float> d_keys, d_values;  // prompt / appended rows
-  DeviceBuffer<int> d_counts, d_plan, d_order;
+  DeviceBuffer<int> d_plan, d_order;
   PinnedBuffer<int> h_args[kArgBlocks];
   hipEvent_t args_ev[kArgBlocks] = {};
   bool args_busy[kArgBlocks] = {};
@@ -863,6 +863,17 @@ struct dsd_table {
   }
   const int* SlotPages(int slot) const {
     return view.pages + static_cast<size_t>(slot) * view.max_pages;
+  }
+  // The token counts of a prompt's n pages in a pinned block the upload
+  // kernels read (the admission's metadata transfer); Done(block) after.
+  int PromptCounts(int tokens, int n, const int** counts) {
+    const int b = Acquire(static_cast<size_t>(n));
+    int* c = h_args[b].ptr;
+    const int ps = pool->view.page_size;
+    for (int j = 0; j < n; ++j) c[j] = std::min(ps, tokens - j * ps);
+    pool->CountH2D(sizeof(int) * static_cast<size_t>(n));
+    *counts = c;
+    return b;
   }
 };
 
@@ -974,15 +985,15 @@ int dsd_table_admit_prompt(dsd_table* table, int slot, int tokens, const float* 
     const size_t elems = static_cast<size_t>(tokens) * pool->view.elements;
     table->d_keys.Reserve(elems);
     table->d_values.Reserve(elems);
-    table->d_counts.Reserve(n);
     pool->H2D(table->d_keys.ptr, keys, sizeof(float) * elems);
     pool->H2D(table->d_values.ptr, values, sizeof(float) * elems);
     dsdk::LaunchTableScatter(pool->view, table->view, slot, tokens, table->d_keys.ptr,
                              table->d_values.ptr, pool->stream);
-    dsdk::LaunchTablePromptCounts(table->view, slot, tokens, pool->view.page_size,
-                                  table->d_counts.ptr, pool->stream);
-    dsdk::LaunchFinishPageUpload(pool->view, table->SlotPages(slot), table->d_counts.ptr,
-                                 nullptr, n, pool->stream);
+    const int* counts = nullptr;
+    const int b = table->PromptCounts(tokens, n, &counts);
+    dsdk::LaunchFinishPageUpload(pool->view, table->SlotPages(slot), counts, nullptr, n,
+                                 pool->stream);
+    table->Done(b);
   });
 }
 
@@ -993,11 +1004,11 @@ int dsd_table_admit_synthetic(dsd_table* table, int slot, int tokens, int reques
     pool->WaitPending();
     const int n = table->Reserve(slot, tokens);
     if (n == 0) return;
-    table->d_counts.Reserve(n);
-    dsdk::LaunchTablePromptCounts(table->view, slot, tokens, pool->view.page_size,
-                                  table->d_counts.ptr, pool->stream);
-    dsdk::LaunchPrefillSynthetic(pool->view, table->SlotPages(slot), table->d_counts.ptr, n,
-                                 request_id, pool->stream);
+    const int* counts = nullptr;
+    const int b = table->PromptCounts(tokens, n, &counts);
+    dsdk::LaunchPrefillSynthetic(pool->view, table->SlotPages(slot), counts, n, request_id,
+                                 pool->stream);
+    table->Done(b);
   });
 }
 
@@ -1062,6 +1073,7 @@ int dsd_table_append(dsd_table* table, int n, const int* slots, const unsigned c
       args[2 * n + i] = request_ids != nullptr ? request_ids[i] : 0;
       args[3 * n + i] = decode_steps != nullptr ? decode_steps[i] : 0;
     }
+    pool->CountH2D(sizeof(int) * 4 * static_cast<size_t>(n));  // the kernel reads the block
     table->d_plan.Reserve(6 * static_cast<size_t>(m) + 1);
     table->d_order.Reserve(std::max(1, m));
     dsdk::LaunchTablePlanAppend(pool->view, table->view, args, n, m, table->d_plan.ptr,
@@ -1105,6 +1117,7 @@ int dsd_table_release(dsd_table* table, int n, const int* slots, int clear) {
       for (int i = 0; i < c; ++i) pages += table->h_npages[slots[c0 + i]];
       const int b = table->Acquire(static_cast<size_t>(c));
       std::memcpy(table->h_args[b].ptr, slots + c0, sizeof(int) * c);
+      pool->CountH2D(sizeof(int) * static_cast<size_t>(c));
       dsdk::LaunchTableRelease(pool->view, table->view, table->h_args[b].ptr, c, pages,
                                clear != 0, pool->stream);
       table->Done(b);

@@ -105,9 +105,6 @@ void LaunchTableReserve(const TableView& t, int slot, int n, hipStream_t stream)
 // d_keys / d_values: tokens x E rows (device) into the pages of `slot`.
 void LaunchTableScatter(const PoolView& pool, const TableView& t, int slot, int tokens,
                         const float* d_keys, const float* d_values, hipStream_t stream);
-// d_counts[j] = tokens in prompt page j of a `tokens`-token prompt.
-void LaunchTablePromptCounts(const TableView& t, int slot, int tokens, int page_size,
-                             int* d_counts, hipStream_t stream);
 // One token for each of n slots: page allocation, then the plan of the m
 // uploaded tokens (layout in page_table.hip) for LaunchAppendSynthetic
 // (meta = d_plan) or LaunchAppendTokens (d_order and the plan's arrays).

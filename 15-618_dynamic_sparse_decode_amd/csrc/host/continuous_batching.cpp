@@ -14,6 +14,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <deque>
+#include <memory>
 #include <numeric>
 #include <random>
 #include <stdexcept>
@@ -459,6 +460,181 @@ SparseBatchCudaResult StagedStep(SparseCudaContext& ctx, const PagedKvCache& cac
   return result;
 }
 
+// The loop's request -> page table in device memory (dsd_table beside the
+// context's pool) and the slots of the admitted requests.  In the
+// GPU-resident admission modes the loop keeps no page lists on the host:
+// admission, append and release are table kernels, and each step's
+// candidate lists are packed on the device from slot ids.  DSD_DEVICE_TABLE=0
+// keeps the host lists (the reference's PagedKvCache) and stages each step's
+// candidate lists from them instead.
+bool DeviceTableEnabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("DSD_DEVICE_TABLE");
+    return e == nullptr || std::strcmp(e, "0") != 0;
+  }();
+  return on;
+}
+
+class LoopTable {
+ public:
+  LoopTable(::dsd_pool* pool, int slots, int max_pages) {
+    detail::ThrowOnError(dsd_table_create(pool, slots, max_pages, &t_));
+    for (int s = slots - 1; s >= 0; --s) free_.push_back(s);
+  }
+  ~LoopTable() {
+    if (t_ != nullptr) (void)dsd_table_destroy(t_);
+  }
+  LoopTable(const LoopTable&) = delete;
+  LoopTable& operator=(const LoopTable&) = delete;
+  ::dsd_table* get() const { return t_; }
+  int Take(int request) {
+    if (free_.empty()) throw std::runtime_error("device page table has no free slot");
+    const int slot = free_.back();
+    free_.pop_back();
+    slot_of_[request] = slot;
+    return slot;
+  }
+  int SlotOf(int request) const { return slot_of_.at(request); }
+  // Releases the slots of `requests` (in order) in one call.
+  void Release(const std::vector<int>& requests, bool clear) {
+    if (requests.empty()) return;
+    std::vector<int> slots;
+    slots.reserve(requests.size());
+    for (int id : requests) slots.push_back(slot_of_.at(id));
+    detail::ThrowOnError(
+        dsd_table_release(t_, static_cast<int>(slots.size()), slots.data(), clear ? 1 : 0));
+    for (std::size_t i = 0; i < requests.size(); ++i) {
+      slot_of_.erase(requests[i]);
+      free_.push_back(slots[i]);
+    }
+  }
+
+ private:
+  ::dsd_table* t_ = nullptr;
+  std::vector<int> free_;
+  std::unordered_map<int, int> slot_of_;
+};
+
+// Prompt admission into the table (GPU-resident modes); with `mirror`, the
+// host cache reserves the same pages (for verification).
+void AdmitToTable(const ModelConfig& c, const ContinuousRequestSpec& s,
+                  ContinuousPromptAdmissionMode mode, LoopTable* table, PagedKvCache* mirror) {
+  const int slot = table->Take(s.request_id);
+  if (mirror != nullptr) mirror->ReservePagesForRequest(s.request_id, PromptPageCounts(c, s));
+  if (mode == ContinuousPromptAdmissionMode::kDirectGpuUpload) {
+    detail::ThrowOnError(dsd_table_admit_prompt(table->get(), slot, s.prompt_tokens,
+                                                s.prompt_keys.data(), s.prompt_values.data()));
+  } else {
+    detail::ThrowOnError(
+        dsd_table_admit_synthetic(table->get(), slot, s.prompt_tokens, s.request_id));
+  }
+}
+
+// One step of the table loop: the queries as StagedStep takes them (rows
+// in the pinned payload store read in place, the others copied into the
+// staging), candidate lists from the table.  Outputs stay in the staging.
+SparseBatchCudaResult TableStep(SparseCudaContext& ctx, const LoopTable& table,
+                                const std::vector<LiveRequest>& active, int E, int top_k,
+                                const SparseRunBatchOptions& run,
+                                std::vector<const float*>* rows, ObservedDecodeStep* observe) {
+  using detail::ThrowOnError;
+  SparseBatchCudaResult result;
+  const auto t0 = Clock::now();
+  const int B = static_cast<int>(active.size());
+  float* queries = nullptr;
+  ThrowOnError(dsd_sparse_staging(ctx.handle(), &queries, nullptr, nullptr, nullptr));
+  std::vector<int> slots(static_cast<std::size_t>(B));
+  rows->resize(static_cast<std::size_t>(B));
+  for (int b = 0; b < B; ++b) {
+    const LiveRequest& l = active[static_cast<std::size_t>(b)];
+    slots[static_cast<std::size_t>(b)] = table.SlotOf(l.a.state.request_id);
+    if (l.own) {
+      float* row = queries + static_cast<std::size_t>(b) * E;
+      std::memcpy(row, l.query_buf.data(), sizeof(float) * E);
+      (*rows)[static_cast<std::size_t>(b)] = row;
+    } else {
+      (*rows)[static_cast<std::size_t>(b)] = l.query;
+    }
+  }
+  const double layout_ms = Ms(t0, Clock::now());
+  const bool timing = run.timing_mode == SparseBatchTimingMode::kKernelEvents;
+  const bool outputs = run.output_mode != SparseBatchOutputMode::kNoOutputs || observe;
+  dsd_step_timings t{};
+  int* sel = nullptr;
+  int* sel_counts = nullptr;
+  if (observe != nullptr) {
+    observe->queries.resize(static_cast<std::size_t>(B) * E);
+    for (int b = 0; b < B; ++b) {
+      std::memcpy(observe->queries.data() + static_cast<std::size_t>(b) * E,
+                  (*rows)[static_cast<std::size_t>(b)], sizeof(float) * E);
+    }
+    observe->selected.assign(static_cast<std::size_t>(B) * std::max(1, top_k), 0);
+    observe->selected_counts.assign(static_cast<std::size_t>(B), 0);
+    sel = observe->selected.data();
+    sel_counts = observe->selected_counts.data();
+  }
+  ThrowOnError(dsd_sparse_run_table(ctx.handle(), table.get(), B, slots.data(), nullptr,
+                                    rows->data(), outputs ? DSD_OUTPUT_OUTPUTS : DSD_OUTPUT_NONE,
+                                    timing ? DSD_TIMING_EVENTS : DSD_TIMING_NONE, nullptr, sel,
+                                    sel_counts, &t));
+  if (observe != nullptr) {
+    int total = 0;
+    for (int slot : slots) {
+      int n = 0;
+      ThrowOnError(dsd_table_slot_pages(table.get(), slot, &n));
+      total += n;
+    }
+    observe->cand_offsets.assign(static_cast<std::size_t>(B) + 1, 0);
+    observe->cand_ids.assign(static_cast<std::size_t>(std::max(1, total)), 0);
+    ThrowOnError(dsd_sparse_last_csr(ctx.handle(), B, observe->cand_offsets.data(),
+                                     observe->cand_ids.data(), std::max(1, total)));
+    observe->cand_ids.resize(static_cast<std::size_t>(total));
+    int selected_total = 0;
+    for (int b = 0; b < B; ++b) selected_total += observe->selected_counts[static_cast<std::size_t>(b)];
+    observe->selected.resize(static_cast<std::size_t>(selected_total));
+    float* staged_out = nullptr;
+    ThrowOnError(dsd_sparse_staging(ctx.handle(), nullptr, nullptr, nullptr, &staged_out));
+    observe->outputs.assign(staged_out, staged_out + static_cast<std::size_t>(B) * E);
+  }
+  if (timing) {
+    result.aggregate_timings.page_scoring_ms = t.score_ms;
+    result.aggregate_timings.topk_ms = t.topk_ms;
+    result.aggregate_timings.attention_ms = t.attention_ms;
+    result.aggregate_timings.gather_ms = 0.0;  // fused into attention
+    result.aggregate_timings.total_ms = t.score_ms + t.topk_ms + t.attention_ms;
+    result.kernel_ms = result.aggregate_timings.total_ms;
+    result.runtime_overheads.time_prepare_sparse_layout_ms = layout_ms;
+    result.runtime_overheads.time_memcpy_h2d_ms = t.h2d_ms;
+    result.runtime_overheads.time_memcpy_d2h_ms = t.d2h_ms;
+    result.runtime_overheads.time_kernel_launch_ms = t.launch_ms;
+    result.runtime_overheads.time_sync_ms = t.sync_ms;
+  }
+  return result;
+}
+
+// Verification of a table step (DSD_VERIFY_STAGED): the device's candidate
+// lists must be the host cache's (kept beside the table), and the step's
+// outputs RunBatch's on those lists.
+void VerifyTableStep(SparseCudaContext& ctx, const PagedKvCache& mirror,
+                     const std::vector<LiveRequest>& active, int E) {
+  using detail::ThrowOnError;
+  const int B = static_cast<int>(active.size());
+  std::vector<int> offs(static_cast<std::size_t>(B) + 1, 0);
+  std::vector<int> want;
+  for (const auto& l : active) {
+    const auto& pages = mirror.GetRequestPages(l.a.state.request_id);
+    want.insert(want.end(), pages.begin(), pages.end());
+  }
+  std::vector<int> ids(std::max<std::size_t>(1, want.size()));
+  ThrowOnError(dsd_sparse_last_csr(ctx.handle(), B, offs.data(), ids.data(),
+                                   static_cast<int>(ids.size())));
+  ids.resize(static_cast<std::size_t>(offs[static_cast<std::size_t>(B)]));
+  if (ids != want) {
+    throw std::runtime_error("device page table differs from the host cache's page lists");
+  }
+  VerifyStagedStep(ctx, mirror, active, E);
+}
+
 void FinishStats(ContinuousBatchStats* stats, Clock::time_point wall_start,
                  const std::vector<double>& step_ms, const StageTimings& timings,
                  const RuntimeOverheadTimings& overheads, int steps, int batch_sum) {
@@ -568,6 +744,25 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
   SparseCudaContext ctx(cache, config, options.max_active_requests, max_candidates,
                         max_selected);
   ctx.ResetDeviceTransferStats();
+  const bool debug_outputs = options.run_batch_output_mode == SparseBatchOutputMode::kDebugTensors;
+  // GPU-resident admission: page lists in a device table (the host cache
+  // then only mirrors them when steps are verified).
+  const bool use_table = metadata_only && !debug_outputs && DeviceTableEnabled();
+  const bool mirror = !use_table || VerifyStagedSteps();
+  std::unique_ptr<LoopTable> table;
+  if (use_table) {
+    const int slots = options.preadmit_prompts ? static_cast<int>(specs.size())
+                                               : options.max_active_requests;
+    table = std::make_unique<LoopTable>(ctx.pool_handle(), std::max(1, slots), max_pages);
+  }
+  auto admit = [&](const ContinuousRequestSpec& s) {
+    if (use_table) {
+      AdmitToTable(config, s, options.prompt_admission_mode, table.get(),
+                   mirror ? &cache : nullptr);
+    } else {
+      AdmitPrompt(config, s, options.prompt_admission_mode, &cache, &ctx);
+    }
+  };
 
   ContinuousBatchStats stats;
   DecodePayloads payloads;
@@ -587,12 +782,11 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
   std::vector<const float*> step_rows;
   std::vector<const RequestState*> batch;
   std::vector<std::uint8_t> admitted(specs.size(), 0);
-  const bool debug_outputs = options.run_batch_output_mode == SparseBatchOutputMode::kDebugTensors;
 
   if (options.preadmit_prompts) {
     for (std::size_t i = 0; i < specs.size(); ++i) {
       const auto t0 = Clock::now();
-      AdmitPrompt(config, specs[i], options.prompt_admission_mode, &cache, &ctx);
+      admit(specs[i]);
       const double ms = Ms(t0, Clock::now());
       stats.admission_ms += ms;
       stats.prompt_preadmit_ms += ms;
@@ -617,7 +811,7 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
       const auto& s = specs[i];
       if (!admitted[i]) {
         const auto t0 = Clock::now();
-        AdmitPrompt(config, s, options.prompt_admission_mode, &cache, &ctx);
+        admit(s);
         const double ms = Ms(t0, Clock::now());
         stats.admission_ms += ms;
         stats.runtime_admission_ms += ms;
@@ -625,12 +819,21 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
       }
       if (s.decode_steps > 0) {
         LiveRequest l;
-        l.a.state = MakeRequestState(s.request_id, std::vector<float>(), cache, s.prompt_tokens);
+        if (mirror) {
+          l.a.state =
+              MakeRequestState(s.request_id, std::vector<float>(), cache, s.prompt_tokens);
+        } else {
+          l.a.state.request_id = s.request_id;
+          l.a.state.context_tokens = s.prompt_tokens;
+        }
         l.a.remaining_decode_steps = s.decode_steps;
         l.a.spec_index = i;
         l.query_buf = s.initial_query;
         l.own = true;
         active.push_back(std::move(l));
+      } else if (use_table) {
+        table->Release({s.request_id}, !options.lazy_release);
+        if (mirror) cache.ReleaseRequest(s.request_id);
       } else {
         const auto freed = cache.ReleaseRequest(s.request_id);
         if (!options.lazy_release) ctx.SyncFreedPages(freed);
@@ -673,6 +876,10 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
                               pr.output.output.end());
         }
       }
+    } else if (use_table) {
+      result = TableStep(ctx, *table, active, E, config.top_k_pages, run, &step_rows,
+                         observe ? &seen : nullptr);
+      if (VerifyStagedSteps()) VerifyTableStep(ctx, cache, active, E);
     } else {
       result = StagedStep(ctx, cache, active, E, config.top_k_pages,
                           options.max_active_requests, max_candidates, max_selected, run,
@@ -725,6 +932,9 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
     std::vector<AppendTokenResult> appended;
     std::vector<float> keys, values;
     std::vector<int> synth_requests, synth_steps;
+    // the table's append: every active request, batch order
+    std::vector<int> t_slots, t_requests, t_steps;
+    std::vector<unsigned char> t_fresh, t_upload;
     for (std::size_t li = 0; li < active.size(); ++li) {
       LiveRequest& l = active[li];
       auto& a = l.a;
@@ -743,10 +953,20 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
       }
       // Decode tokens of GPU-admitted prompts start a fresh page (:614-616).
       const bool force_new = metadata_only && dstep == 0;
-      const auto r = options.gpu_synthetic_decode_append
-                         ? cache.AppendTokenMetadataOnly(id, force_new)
-                         : (metadata_only ? cache.AppendTokenMetadataOnly(id, k, force_new)
-                                          : cache.AppendToken(id, k, v, force_new));
+      AppendTokenResult r{};
+      if (mirror) {
+        r = options.gpu_synthetic_decode_append
+                ? cache.AppendTokenMetadataOnly(id, force_new)
+                : (metadata_only ? cache.AppendTokenMetadataOnly(id, k, force_new)
+                                 : cache.AppendToken(id, k, v, force_new));
+      }
+      if (use_table) {
+        t_slots.push_back(table->SlotOf(id));
+        t_requests.push_back(id);
+        t_steps.push_back(dstep);
+        t_fresh.push_back(force_new ? 1 : 0);
+        t_upload.push_back(a.remaining_decode_steps > 1 ? 1 : 0);
+      }
       // The last decode token is never attended to, so it is not uploaded.
       if (a.remaining_decode_steps > 1) {
         appended.push_back(r);
@@ -772,7 +992,13 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
       ++stats.total_generated_tokens;
     }
     const auto t_append = Clock::now();
-    if (options.gpu_synthetic_decode_append) {
+    if (use_table) {
+      const bool rows = !options.gpu_synthetic_decode_append;
+      detail::ThrowOnError(dsd_table_append(
+          table->get(), static_cast<int>(t_slots.size()), t_slots.data(), t_fresh.data(),
+          t_upload.data(), rows ? keys.data() : nullptr, rows ? values.data() : nullptr,
+          t_requests.data(), t_steps.data()));
+    } else if (options.gpu_synthetic_decode_append) {
       ctx.AppendSyntheticTokens(cache, appended, synth_requests, synth_steps);
     } else if (metadata_only) {
       ctx.SyncAppendedTokensDirect(cache, appended, keys, values);
@@ -782,17 +1008,25 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
     stats.append_sync_ms += Ms(t_append, Clock::now());
 
     std::vector<PageId> freed;
+    std::vector<int> finished;
     active.erase(std::remove_if(active.begin(), active.end(),
                                 [&](const LiveRequest& l) {
                                   const ActiveDecodeRequest& a = l.a;
                                   if (a.remaining_decode_steps > 0) return false;
-                                  const auto ids = cache.ReleaseRequest(a.state.request_id);
-                                  freed.insert(freed.end(), ids.begin(), ids.end());
+                                  finished.push_back(a.state.request_id);
+                                  if (mirror) {
+                                    const auto ids = cache.ReleaseRequest(a.state.request_id);
+                                    freed.insert(freed.end(), ids.begin(), ids.end());
+                                  }
                                   return true;
                                 }),
                  active.end());
     const auto t_release = Clock::now();
-    if (!options.lazy_release) ctx.SyncFreedPages(freed);
+    if (use_table) {
+      table->Release(finished, !options.lazy_release);
+    } else if (!options.lazy_release) {
+      ctx.SyncFreedPages(freed);
+    }
     stats.release_sync_ms += Ms(t_release, Clock::now());
     ++step;
   }

@@ -111,16 +111,6 @@ __global__ void TableScatterKernel(PoolView pool, TableView t, int slot, int tok
   }
 }
 
-// Token counts of the prompt pages of `slot` (full pages, the last one
-// partial) for the summary kernels.
-__global__ void TablePromptCountsKernel(int tokens, int page_size, int* counts) {
-  const int n = (tokens + page_size - 1) / page_size;
-  for (int j = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); j < n;
-       j += static_cast<int>(gridDim.x * blockDim.x)) {
-    counts[j] = std::min(page_size, tokens - j * page_size);
-  }
-}
-
 // One token for each of n slots (batch order).  args: slots[n], then
 // flags[n] (bit 0: start a fresh page; bit 1: the payload is uploaded),
 // request_ids[n], decode_steps[n] -- pinned host memory read directly.
@@ -286,17 +276,6 @@ void LaunchTableScatter(const PoolView& pool, const TableView& t, int slot, int 
   hipLaunchKernelGGL(TableScatterKernel, dim3(groups), dim3(256), 0, stream, pool, t, slot,
                      tokens, reinterpret_cast<const float4*>(d_keys),
                      reinterpret_cast<const float4*>(d_values));
-  DSD_HIP_CHECK(hipGetLastError());
-}
-
-void LaunchTablePromptCounts(const TableView& t, int slot, int tokens, int page_size,
-                             int* d_counts, hipStream_t stream) {
-  const int pages = (tokens + page_size - 1) / page_size;
-  if (pages <= 0) return;
-  (void)t;
-  (void)slot;
-  hipLaunchKernelGGL(TablePromptCountsKernel, dim3((pages + 255) / 256), dim3(256), 0, stream,
-                     tokens, page_size, d_counts);
   DSD_HIP_CHECK(hipGetLastError());
 }
 

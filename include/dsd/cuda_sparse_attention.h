@@ -94,6 +94,9 @@ class SparseCudaContext {
 
   // The C-ABI step handle (device-resident entry points, dsd_hip.h).
   ::dsd_sparse_ctx* handle() const { return ctx_; }
+  // The C-ABI pool the context steps over (for a dsd_table beside it).  No
+  // reference counterpart.
+  ::dsd_pool* pool_handle() const { return device_page_pool_.handle(); }
 
  private:
   SparseBatchCudaResult RunBatchStaged(const std::vector<const RequestState*>& requests,

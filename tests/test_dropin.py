@@ -89,18 +89,23 @@ def test_reference_bench_decode_accuracy_lines(args):
     ("8", "4", "4", "64", "512", "2", "6", "7", "32", "64", "16", "4",
      "1", "1", "1", "1", "1", "0", "0"),                       # three-kernel step, no outputs
 ])
-def test_reference_continuous_driver_staged_steps_verified(args):
+@pytest.mark.parametrize("table", ["1", "0"])
+def test_reference_continuous_driver_staged_steps_verified(args, table):
     """The reference's continuous driver against libdsd.so with
-    DSD_VERIFY_STAGED=1: every step the loop stages in place (queries read
-    from the pinned payload rows or the staging, page lists from the cache)
-    is run again through RunBatch's packing path and must match it bit for
-    bit, or the run fails."""
+    DSD_VERIFY_STAGED=1: every step the loop stages (queries read from the
+    pinned payload rows or the staging; candidate lists packed on the device
+    from the page table, or with DSD_DEVICE_TABLE=0 copied from the host
+    cache) is run again through RunBatch's packing path on the host cache's
+    page lists and must match it bit for bit; with the table, the device's
+    page lists must also equal the host cache's (the reference's page order)
+    at every step.  Either failure ends the run."""
     import os
     exe = DROPIN / "bench_continuous_decode"
     if not exe.exists():
         pytest.skip(f"{exe} not built (needs the reference tree: make -C oracle dropin)")
-    print(f"[dropin] bench_continuous_decode {' '.join(args)} (verified)", flush=True)
-    env = dict(os.environ, DSD_VERIFY_STAGED="1")
+    print(f"[dropin] bench_continuous_decode {' '.join(args)} (verified, table {table})",
+          flush=True)
+    env = dict(os.environ, DSD_VERIFY_STAGED="1", DSD_DEVICE_TABLE=table)
     proc = subprocess.run([str(exe), *args], capture_output=True, text=True, timeout=300, env=env)
     assert proc.returncode == 0, proc.stdout + proc.stderr
     assert "continuous_sparse_tokens_per_second=" in proc.stdout, proc.stdout
