@@ -165,6 +165,11 @@ _SIGNATURES = {
                                               _c_float_p, _c_float_p]),
     "dsd_table_admit_synthetic": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                                  ctypes.c_int]),
+    "dsd_table_staging_init": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int]),
+    "dsd_table_stage_prompt": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                              _c_float_p, _c_float_p]),
+    "dsd_table_admit_staged": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_int]),
     "dsd_table_append": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p, _c_u8_p,
                                         _c_u8_p, _c_float_p, _c_float_p, _c_int_p, _c_int_p]),
     "dsd_table_release": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p, ctypes.c_int]),
@@ -407,6 +412,18 @@ class PageTable:
         tokens = k.size // self.pool.elements
         _check(self._lib.dsd_table_admit_prompt(self.handle, slot, tokens,
                                                 _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float)))
+
+    def staging_init(self, buffers: int, max_tokens: int) -> None:
+        _check(self._lib.dsd_table_staging_init(self.handle, buffers, max_tokens))
+
+    def stage_prompt(self, buffer: int, keys, values) -> None:
+        k = _f32(keys).reshape(-1)
+        v = _f32(values).reshape(-1)
+        _check(self._lib.dsd_table_stage_prompt(self.handle, buffer, k.size // self.pool.elements,
+                                                _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float)))
+
+    def admit_staged(self, slot: int, buffer: int, tokens: int) -> None:
+        _check(self._lib.dsd_table_admit_staged(self.handle, slot, buffer, tokens))
 
     def admit_synthetic(self, slot: int, tokens: int, request_id: int) -> None:
         _check(self._lib.dsd_table_admit_synthetic(self.handle, slot, tokens, request_id))

@@ -816,6 +816,19 @@ struct dsd_table {
   hipEvent_t args_ev[kArgBlocks] = {};
   bool args_busy[kArgBlocks] = {};
   int args_next = 0;
+  // Prompt staging ahead of admission (dsd_table_staging_init): device
+  // buffers filled on a copy stream of their own, from a pinned ring; a
+  // buffer is ready when stg_ready fires and free again when the admission
+  // that read it has finished (stg_free).
+  hipStream_t copy_stream = nullptr;
+  int stg_tokens = 0;
+  std::vector<std::unique_ptr<DeviceBuffer<float>>> stg_k, stg_v;
+  std::vector<hipEvent_t> stg_ready, stg_free;
+  std::vector<char> stg_freed;  // stg_free recorded since the last staging
+  PinnedBuffer<char> ring[kStageBuffers];
+  hipEvent_t ring_ev[kStageBuffers] = {};
+  bool ring_busy[kStageBuffers] = {};
+  int ring_next = 0;
 
   ~dsd_table() {
     for (int b = 0; b < kArgBlocks; ++b) {
@@ -823,6 +836,33 @@ struct dsd_table {
         if (args_busy[b]) (void)hipEventSynchronize(args_ev[b]);
         (void)hipEventDestroy(args_ev[b]);
       }
+    }
+    if (copy_stream != nullptr) (void)hipStreamSynchronize(copy_stream);
+    for (int b = 0; b < kStageBuffers; ++b) {
+      if (ring_ev[b]) (void)hipEventDestroy(ring_ev[b]);
+    }
+    for (hipEvent_t e : stg_ready) (void)hipEventDestroy(e);
+    for (hipEvent_t e : stg_free) {
+      (void)hipEventSynchronize(e);
+      (void)hipEventDestroy(e);
+    }
+    if (copy_stream != nullptr) (void)hipStreamDestroy(copy_stream);
+  }
+  // A pageable host block into device memory on the copy stream, through
+  // the pinned ring (host threads fill one chunk while the DMA moves the
+  // previous one).
+  void CopyIn(float* dst, const float* src, size_t bytes) {
+    const char* s = reinterpret_cast<const char*>(src);
+    char* d = reinterpret_cast<char*>(dst);
+    for (size_t off = 0; off < bytes; off += kStageChunkBytes) {
+      const size_t n = std::min(kStageChunkBytes, bytes - off);
+      const int b = ring_next;
+      ring_next = (b + 1) % kStageBuffers;
+      if (ring_busy[b]) DSD_HIP_CHECK(hipEventSynchronize(ring_ev[b]));
+      ParallelCopy(ring[b].ptr, s + off, n);
+      DSD_HIP_CHECK(hipMemcpyAsync(d + off, ring[b].ptr, n, hipMemcpyHostToDevice, copy_stream));
+      DSD_HIP_CHECK(hipEventRecord(ring_ev[b], copy_stream));
+      ring_busy[b] = true;
     }
   }
   // A pinned block of at least n ints that no enqueued kernel still reads;
@@ -994,6 +1034,80 @@ int dsd_table_admit_prompt(dsd_table* table, int slot, int tokens, const float* 
     dsdk::LaunchFinishPageUpload(pool->view, table->SlotPages(slot), counts, nullptr, n,
                                  pool->stream);
     table->Done(b);
+  });
+}
+
+int dsd_table_staging_init(dsd_table* table, int buffers, int max_tokens) {
+  return Guard([&] {
+    Require(table != nullptr, "table must be non-null");
+    Require(buffers > 0 && max_tokens > 0, "staging sizes must be positive");
+    Require(table->copy_stream == nullptr, "the table's staging is already set up");
+    DSD_HIP_CHECK(hipStreamCreateWithFlags(&table->copy_stream, hipStreamNonBlocking));
+    const size_t elems = static_cast<size_t>(max_tokens) * table->pool->view.elements;
+    table->stg_tokens = max_tokens;
+    for (int b = 0; b < buffers; ++b) {
+      table->stg_k.push_back(std::make_unique<DeviceBuffer<float>>());
+      table->stg_v.push_back(std::make_unique<DeviceBuffer<float>>());
+      table->stg_k.back()->Reserve(elems);
+      table->stg_v.back()->Reserve(elems);
+      hipEvent_t ready = nullptr, freed = nullptr;
+      DSD_HIP_CHECK(hipEventCreateWithFlags(&ready, hipEventDisableTiming));
+      DSD_HIP_CHECK(hipEventCreateWithFlags(&freed, hipEventDisableTiming));
+      table->stg_ready.push_back(ready);
+      table->stg_free.push_back(freed);
+      table->stg_freed.push_back(0);
+    }
+    for (int b = 0; b < kStageBuffers; ++b) {
+      table->ring[b].Reserve(kStageChunkBytes);
+      DSD_HIP_CHECK(hipEventCreateWithFlags(&table->ring_ev[b], hipEventDisableTiming));
+    }
+  });
+}
+
+int dsd_table_stage_prompt(dsd_table* table, int buffer, int tokens, const float* keys,
+                           const float* values) {
+  return Guard([&] {
+    Require(table != nullptr, "table must be non-null");
+    Require(table->copy_stream != nullptr, "call dsd_table_staging_init first");
+    Require(buffer >= 0 && buffer < static_cast<int>(table->stg_k.size()),
+            "staging buffer out of range");
+    Require(tokens >= 0 && tokens <= table->stg_tokens, "prompt exceeds the staging buffers");
+    if (tokens > 0) Require(keys != nullptr && values != nullptr, "prompt rows must be non-null");
+    // The last admission from this buffer has read it.
+    if (table->stg_freed[buffer]) DSD_HIP_CHECK(hipEventSynchronize(table->stg_free[buffer]));
+    const size_t bytes =
+        sizeof(float) * static_cast<size_t>(tokens) * table->pool->view.elements;
+    table->CopyIn(table->stg_k[buffer]->ptr, keys, bytes);
+    table->CopyIn(table->stg_v[buffer]->ptr, values, bytes);
+    DSD_HIP_CHECK(hipEventRecord(table->stg_ready[buffer], table->copy_stream));
+  });
+}
+
+int dsd_table_admit_staged(dsd_table* table, int slot, int buffer, int tokens) {
+  return Guard([&] {
+    Require(table != nullptr, "table must be non-null");
+    Require(table->copy_stream != nullptr, "call dsd_table_staging_init first");
+    Require(buffer >= 0 && buffer < static_cast<int>(table->stg_k.size()),
+            "staging buffer out of range");
+    Require(tokens <= table->stg_tokens, "prompt exceeds the staging buffers");
+    dsd_pool* pool = table->pool;
+    pool->WaitPending();
+    const int n = table->Reserve(slot, tokens);
+    if (n == 0) return;
+    // The admission's bytes crossed PCIe on the copy stream.
+    const size_t bytes = sizeof(float) * static_cast<size_t>(tokens) * pool->view.elements;
+    pool->CountH2D(bytes);
+    pool->CountH2D(bytes);
+    DSD_HIP_CHECK(hipStreamWaitEvent(pool->stream, table->stg_ready[buffer], 0));
+    dsdk::LaunchTableScatter(pool->view, table->view, slot, tokens, table->stg_k[buffer]->ptr,
+                             table->stg_v[buffer]->ptr, pool->stream);
+    const int* counts = nullptr;
+    const int b = table->PromptCounts(tokens, n, &counts);
+    dsdk::LaunchFinishPageUpload(pool->view, table->SlotPages(slot), counts, nullptr, n,
+                                 pool->stream);
+    table->Done(b);
+    DSD_HIP_CHECK(hipEventRecord(table->stg_free[buffer], pool->stream));
+    table->stg_freed[buffer] = 1;
   });
 }
 

@@ -13,8 +13,11 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <condition_variable>
 #include <deque>
 #include <memory>
+#include <mutex>
+#include <thread>
 #include <numeric>
 #include <random>
 #include <stdexcept>
@@ -475,6 +478,15 @@ bool DeviceTableEnabled() {
   return on;
 }
 
+bool PrefetchEnabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("DSD_PREFETCH");
+    return e == nullptr || std::strcmp(e, "0") != 0;
+  }();
+  return on;
+}
+constexpr int kPrefetchDepth = 8;
+
 class LoopTable {
  public:
   LoopTable(::dsd_pool* pool, int slots, int max_pages) {
@@ -515,13 +527,99 @@ class LoopTable {
   std::unordered_map<int, int> slot_of_;
 };
 
+// Prompt uploads ahead of admission (direct GPU upload through the table):
+// a host thread of its own uploads the prompts in admission order (the
+// workload's order) into `depth` device staging buffers in turn, on the
+// table's copy stream, so the PCIe transfers run while the loop steps;
+// admission then only waits for its prompt's upload on the device and
+// fills its pages from the staging buffer.  The pages are still reserved at
+// admission, in the reference's order.
+class PromptPrefetcher {
+ public:
+  PromptPrefetcher(::dsd_table* table, const std::vector<ContinuousRequestSpec>& specs,
+                   int depth)
+      : table_(table), specs_(specs), depth_(depth) {
+    int max_tokens = 1;
+    for (const auto& s : specs) max_tokens = std::max(max_tokens, s.prompt_tokens);
+    detail::ThrowOnError(dsd_table_staging_init(table, depth, max_tokens));
+    thread_ = std::thread([this] { Run(); });
+  }
+  ~PromptPrefetcher() {
+    {
+      std::lock_guard<std::mutex> lock(mu_);
+      stop_ = true;
+    }
+    cv_.notify_all();
+    thread_.join();
+  }
+  PromptPrefetcher(const PromptPrefetcher&) = delete;
+  PromptPrefetcher& operator=(const PromptPrefetcher&) = delete;
+  // The staging buffer holding request i's prompt once its upload is
+  // enqueued (call in increasing i, then Admitted(i)).
+  int Await(std::size_t i) {
+    std::unique_lock<std::mutex> lock(mu_);
+    cv_.wait(lock, [&] { return staged_ > i || !error_.empty(); });
+    if (!error_.empty()) throw std::runtime_error("prompt upload failed: " + error_);
+    return static_cast<int>(i % static_cast<std::size_t>(depth_));
+  }
+  void Admitted(std::size_t i) {
+    {
+      std::lock_guard<std::mutex> lock(mu_);
+      admitted_ = i + 1;
+    }
+    cv_.notify_all();
+  }
+
+ private:
+  void Run() {
+    const std::size_t depth = static_cast<std::size_t>(depth_);
+    for (std::size_t i = 0; i < specs_.size(); ++i) {
+      {
+        // The buffer's previous prompt (request i - depth) is admitted.
+        std::unique_lock<std::mutex> lock(mu_);
+        cv_.wait(lock, [&] { return stop_ || i < depth || admitted_ >= i - depth + 1; });
+        if (stop_) return;
+      }
+      const auto& s = specs_[i];
+      if (dsd_table_stage_prompt(table_, static_cast<int>(i % depth), s.prompt_tokens,
+                                 s.prompt_keys.data(), s.prompt_values.data()) != 0) {
+        std::lock_guard<std::mutex> lock(mu_);
+        error_ = dsd_last_error();
+        cv_.notify_all();
+        return;
+      }
+      {
+        std::lock_guard<std::mutex> lock(mu_);
+        staged_ = i + 1;
+      }
+      cv_.notify_all();
+    }
+  }
+
+  ::dsd_table* table_;
+  const std::vector<ContinuousRequestSpec>& specs_;
+  int depth_;
+  std::mutex mu_;
+  std::condition_variable cv_;
+  std::size_t staged_ = 0, admitted_ = 0;
+  bool stop_ = false;
+  std::string error_;
+  std::thread thread_;
+};
+
 // Prompt admission into the table (GPU-resident modes); with `mirror`, the
 // host cache reserves the same pages (for verification).
-void AdmitToTable(const ModelConfig& c, const ContinuousRequestSpec& s,
-                  ContinuousPromptAdmissionMode mode, LoopTable* table, PagedKvCache* mirror) {
+void AdmitToTable(const ModelConfig& c, const ContinuousRequestSpec& s, std::size_t index,
+                  ContinuousPromptAdmissionMode mode, LoopTable* table, PagedKvCache* mirror,
+                  PromptPrefetcher* prefetch) {
   const int slot = table->Take(s.request_id);
   if (mirror != nullptr) mirror->ReservePagesForRequest(s.request_id, PromptPageCounts(c, s));
-  if (mode == ContinuousPromptAdmissionMode::kDirectGpuUpload) {
+  if (prefetch != nullptr) {
+    const int buffer = prefetch->Await(index);
+    detail::ThrowOnError(
+        dsd_table_admit_staged(table->get(), slot, buffer, s.prompt_tokens));
+    prefetch->Admitted(index);
+  } else if (mode == ContinuousPromptAdmissionMode::kDirectGpuUpload) {
     detail::ThrowOnError(dsd_table_admit_prompt(table->get(), slot, s.prompt_tokens,
                                                 s.prompt_keys.data(), s.prompt_values.data()));
   } else {
@@ -755,12 +853,20 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
                                                : options.max_active_requests;
     table = std::make_unique<LoopTable>(ctx.pool_handle(), std::max(1, slots), max_pages);
   }
-  auto admit = [&](const ContinuousRequestSpec& s) {
+  // Direct uploads at runtime admission overlap the steps (DSD_PREFETCH=0:
+  // synchronous uploads at admission, as the reference).
+  std::unique_ptr<PromptPrefetcher> prefetch;
+  if (use_table && !options.preadmit_prompts &&
+      options.prompt_admission_mode == ContinuousPromptAdmissionMode::kDirectGpuUpload &&
+      PrefetchEnabled()) {
+    prefetch = std::make_unique<PromptPrefetcher>(table->get(), specs, kPrefetchDepth);
+  }
+  auto admit = [&](std::size_t i) {
     if (use_table) {
-      AdmitToTable(config, s, options.prompt_admission_mode, table.get(),
-                   mirror ? &cache : nullptr);
+      AdmitToTable(config, specs[i], i, options.prompt_admission_mode, table.get(),
+                   mirror ? &cache : nullptr, prefetch.get());
     } else {
-      AdmitPrompt(config, s, options.prompt_admission_mode, &cache, &ctx);
+      AdmitPrompt(config, specs[i], options.prompt_admission_mode, &cache, &ctx);
     }
   };
 
@@ -786,7 +892,7 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
   if (options.preadmit_prompts) {
     for (std::size_t i = 0; i < specs.size(); ++i) {
       const auto t0 = Clock::now();
-      admit(specs[i]);
+      admit(i);
       const double ms = Ms(t0, Clock::now());
       stats.admission_ms += ms;
       stats.prompt_preadmit_ms += ms;
@@ -811,7 +917,7 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
       const auto& s = specs[i];
       if (!admitted[i]) {
         const auto t0 = Clock::now();
-        admit(s);
+        admit(i);
         const double ms = Ms(t0, Clock::now());
         stats.admission_ms += ms;
         stats.runtime_admission_ms += ms;

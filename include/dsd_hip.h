@@ -422,6 +422,23 @@ int dsd_table_admit_prompt(dsd_table* table, int slot, int tokens,
  * src/device_page_pool.cpp:626-679). */
 int dsd_table_admit_synthetic(dsd_table* table, int slot, int tokens,
                               int request_id);
+/* Prompt upload ahead of admission, so that it overlaps the decode steps
+ * (the reference admits synchronously, src/continuous_batching.cpp:208-239).
+ * dsd_table_staging_init makes `buffers` device staging buffers of up to
+ * max_tokens tokens and a copy stream.  dsd_table_stage_prompt uploads a
+ * prompt (tokens x E host rows, pageable) into staging buffer `buffer` on
+ * that stream and returns once the host rows have been copied out (the DMA
+ * may still run).  dsd_table_admit_staged is dsd_table_admit_prompt from a
+ * staged buffer: the pool's stream waits for that buffer's upload, then
+ * pages are reserved, filled from it (device to device) and summarised.
+ * dsd_table_stage_prompt waits for the previous admission from the same
+ * buffer to have read it.  It may run on another host thread than the other
+ * calls; the caller orders each buffer's staging after the admission
+ * call that consumed its previous contents. */
+int dsd_table_staging_init(dsd_table* table, int buffers, int max_tokens);
+int dsd_table_stage_prompt(dsd_table* table, int buffer, int tokens,
+                           const float* keys, const float* values);
+int dsd_table_admit_staged(dsd_table* table, int slot, int buffer, int tokens);
 /* One decode token for each of n distinct slots, in batch order
  * (PagedKvCache::AppendTokenMetadataOnly, src/paged_kv_cache.cpp:312-351,
  * then DevicePagePool::UploadTokensDirect / AppendTokensSynthetic,

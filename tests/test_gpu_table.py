@@ -205,3 +205,42 @@ def test_table_rejects_what_the_host_mirror_forbids(gpu):
     assert sorted(table.free_stack().tolist()) == list(range(10))
     table.close()
     pool.close()
+
+
+def test_staged_admission_equals_direct_admission(gpu):
+    # Prompts uploaded ahead of admission into two staging buffers (reused
+    # in turn) and admitted from them give the same pages, page contents and
+    # summaries as dsd_table_admit_prompt on a second pool and table.
+    H, D, ps = 4, 32, 8
+    E = H * D
+    cap = 200
+    rng = np.random.default_rng(17)
+    a = gpu.DevicePagePool(H, D, ps, cap)
+    b = gpu.DevicePagePool(H, D, ps, cap)
+    ta = gpu.PageTable(a, 6, 40)
+    tb = gpu.PageTable(b, 6, 40)
+    ta.staging_init(2, 40 * ps)
+    prompts = [rng.standard_normal((t, E)).astype(np.float32) for t in (37, 0, 160, 9, 81, 8)]
+    values = [rng.standard_normal(p.shape).astype(np.float32) for p in prompts]
+    for slot, (k, v) in enumerate(zip(prompts, values)):
+        ta.stage_prompt(slot % 2, k, v)
+        ta.admit_staged(slot, slot % 2, len(k))
+        tb.admit_prompt(slot, k, v)
+        if slot == 2:
+            ta.release([0])
+            tb.release([0])
+    for slot in range(1, 6):
+        pa, pb = ta.pages(slot), tb.pages(slot)
+        assert pa.tolist() == pb.tolist()
+        for p in pa:
+            ka, va = a.download_page(int(p))
+            kb, vb = b.download_page(int(p))
+            assert np.array_equal(ka.view(np.uint32), kb.view(np.uint32))
+            assert np.array_equal(va.view(np.uint32), vb.view(np.uint32))
+        if len(pa):
+            assert np.array_equal(a.download_summaries(pa).view(np.uint32),
+                                  b.download_summaries(pb).view(np.uint32))
+    for t in (ta, tb):
+        t.close()
+    a.close()
+    b.close()
