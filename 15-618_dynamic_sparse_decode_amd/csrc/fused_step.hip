@@ -859,6 +859,10 @@ __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const Fuse
             const bool live = pg >= 0 && pg < pool.capacity && sh.cntok[i] != 0;
             return live ? pool.summaries + static_cast<size_t>(pg) * kFE : nullptr;
           },
+          [&](int f) {
+            const int i = sh.flag[f];
+            return dsd_refine::FirstPassBound(sh.lo[i], sh.hi[i], a.scale, kFE);
+          },
           [&](int f, float m, float l, float h) {
             // Only in LDS: the score passes of the request's other workgroups
             // wrote the global intervals, with no ordering against this one.

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include "dsd_internal.h"
+#include "refine_lane.h"
 
 #include <cmath>
 #include <cstdint>
@@ -396,68 +397,35 @@ __device__ void RescoreChains(int nflag, PageOf page_of, Emit emit, const float*
 
 // ---- refined intervals -------------------------------------------------------
 // A much narrower certified interval for one page's reference score, for the
-// pages whose order the first intervals leave open.  The reference sum is
-// acc_0 = 0, acc_j = fl(acc_{j-1} + p_j); exactly, acc_n = S - sum_j e_j with
-// S = sum p_j and e_j = acc_{j-1} + p_j - acc_j the rounding error of step j.
-// With the exact prefix sums T_j and a bound B >= |acc_j - T_j| for every j
-// (Higham, Accuracy and Stability, 2nd ed., eq. 4.3: |acc_j - T_j| <= u
-// sum_{i<=j} |acc_i|), the binade of |acc_j| is certain when [|T_j| - B,
-// |T_j| + B] lies inside one binade [2^e, 2^(e+1)).  If so, and acc_{j-1}'s
-// binade is certainly >= e, acc_{j-1} lies on acc_j's grid (multiples of
-// 2^(e-23)), so fl(acc_{j-1} + p_j) = acc_{j-1} + round_e(p_j) and
-// e_j = p_j - round_e(p_j) is known exactly -- unless p_j is a tie on that
-// grid (the result then depends on acc_{j-1}'s last bit).  Every other step
-// contributes |e_j| <= half the grid spacing of the largest binade acc_j can
-// be in.  The first step is exact (acc_1 = p_1).  The interval is
-// S - K -+ (U + slack), K = the known errors, U = the others' half spacings.
-// On random data it is 20-40 times narrower than the sum-of-prefixes bound.
-
-__device__ __forceinline__ int BinadeOf(double x) {  // floor(log2 x), x > 0 normal
-  return static_cast<int>((__double_as_longlong(x) >> 52) & 0x7ff) - 1023;
-}
-
-__device__ __forceinline__ double Pow2(int e) {  // -1022 <= e <= 1023
-  return __longlong_as_double(static_cast<long long>(e + 1023) << 52);
-}
-
-// Where |acc| can lie given |acc - t| <= B: *certain with binade *e, and
-// *half = half the largest grid spacing of any float in that range.
-__device__ __forceinline__ void ClassifyStep(double t, double B, bool* certain, int* e,
-                                             double* half) {
-  const double a = fabs(t);
-  const double lo = a - B;
-  const double hi = a + B;
-  const int eh = hi >= 0x1p-126 ? BinadeOf(hi) : -127;
-  *half = eh >= -126 ? Pow2(eh - 24) : 0x1p-150;
-  *certain = false;
-  *e = 0;
-  if (lo >= 0x1p-126) {
-    const int el = BinadeOf(lo);
-    *certain = el == eh;
-    *e = el;
-  }
-}
+// pages whose order the first intervals leave open: the rounding error of
+// every addition whose binade is certain is accounted for exactly, the
+// others by half a grid spacing (refine_lane.h states the rule; each lane
+// runs its steps there).  B >= |acc_j - T_j| comes from the page's
+// first-pass interval (dsd_refine::FirstPassBound).  The interval is
+// S - K -+ (U + slack), K = the known errors, U = the others' bound; on
+// random data it is about 30 times narrower than the first-pass interval.
 
 // Refined intervals of nflag pages: page_of(f) gives the f-th page's summary
-// row (nullptr: an all-zero summary), emit(f, mid, lo, hi) receives its
-// interval (in lane 0 of one wave).  q: the request's query (E floats).
-// E % 256 == 0; rows 16-byte aligned.  Called by the whole workgroup (its
-// waves take `parts` waves per page, 1..8, so a few flagged pages use every
-// wave); scratch holds 8 doubles per wave (LDS).
+// row (nullptr: an all-zero summary), bound_of(f) its B, emit(f, mid, lo,
+// hi) receives its interval (in lane 0 of the page's first wave).  q: the request's query (E floats).  E % 256 == 0; rows
+// 16-byte aligned.  Called by the whole workgroup (its waves take `parts`
+// waves per page, 1..8, so a few flagged pages use every wave); returns
+// after a barrier, so every wave sees what emit wrote.  scratch holds 8
+// doubles per wave (LDS).
 //
 // Wave `part` of a page takes the elements [part*E/parts, (part+1)*E/parts),
-// lane l the block of Lp = E/(64*parts) consecutive ones in it.  Sweep 1:
-// the block's double sum, its float local prefix range and sizes for the
-// bound; the blocks' starts come from a wave scan plus the earlier parts'
-// totals (LDS).  Sweep 2 classifies each step.  A block whose whole range of
-// acc (start and local prefixes, widened by B and the float error of the
-// local prefix) lies in one binade e takes the fast path: every step is
-// certain with grid 2^(e-23) on both sides, so e_j = p_j - c_j*2^(e-23) with
-// c_j = rint(p_j/2^(e-23)) (a tie: c_j = p_j/2^(e-23) itself, and half a
-// spacing of doubt).  Other blocks classify step by step.
-template <class PageOf, class Emit>
-__device__ void RefineScores(int nflag, PageOf page_of, Emit emit, const float* __restrict__ q,
-                             int E, float scale, double* scratch) {
+// lane l the block of Lp = E/(64*parts) consecutive ones in it, as float4
+// chunks.  The products of the first kKeep chunks stay in registers between
+// the sweeps (all of them when Lp <= 4*kKeep: one load round trip); later
+// chunks are loaded again.  Sweep 1: the block's double sum; the blocks'
+// starts come from a wave scan plus the earlier parts' totals (LDS, one
+// barrier).  Sweep 2: every step through dsd_refine::Sweep2Step,
+// straight-line code with no divergence between lanes; each wave's sums go
+// to LDS (one barrier) and each page's first wave combines its parts.
+template <class PageOf, class BoundOf, class Emit>
+__device__ void RefineScores(int nflag, PageOf page_of, BoundOf bound_of, Emit emit,
+                             const float* __restrict__ q, int E, float scale, double* scratch) {
+  constexpr int kKeep = 2;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nwaves = static_cast<int>(blockDim.x) / kWave;
@@ -466,12 +434,13 @@ __device__ void RefineScores(int nflag, PageOf page_of, Emit emit, const float* 
   while (parts < 8 && parts * 2 * busy <= nwaves && (E / (kWave * parts * 2)) % 4 == 0) parts *= 2;
   const int per_round = nwaves / parts;
   const int Lp = E / (kWave * parts);
+  const int nch = Lp / 4;
   const int slot = wave / parts;
   const int part = wave - slot * parts;
+  // LDS per wave: [0] its part's total, [3] K, [4] U; a page's first wave
+  // also [6] the page's total S and [7] its B.
   double* mine = scratch + 8 * wave;
   const double* page_parts = scratch + 8 * (slot * parts);
-  constexpr double u = 0x1p-24;
-  const double n = static_cast<double>(E);
   for (int f0 = 0; f0 < nflag; f0 += per_round) {
     const int f = f0 + slot;
     const bool active = slot < per_round && f < nflag;  // uniform per wave
@@ -479,31 +448,37 @@ __device__ void RefineScores(int nflag, PageOf page_of, Emit emit, const float* 
     const size_t first = static_cast<size_t>(part) * (E / parts) + static_cast<size_t>(lane) * Lp;
     const float4* q4 = reinterpret_cast<const float4*>(q + first);
     const float4* s4 = s == nullptr ? nullptr : reinterpret_cast<const float4*>(s + first);
-    auto products = [&](int j4, float (&p)[4]) {
-      const float4 a = q4[j4];
-      const float4 b = s4 != nullptr ? s4[j4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    auto products = [&](int c, float (&p)[4]) {
+      const float4 a = q4[c];
+      const float4 b = s4 != nullptr ? s4[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       p[0] = __fmul_rn(a.x, b.x);
       p[1] = __fmul_rn(a.y, b.y);
       p[2] = __fmul_rn(a.z, b.z);
       p[3] = __fmul_rn(a.w, b.w);
     };
-    // Sweep 1.
+    // Sweep 1 (the kept chunks' loads are all issued before their use).
+    float keep[kKeep][4];
     double run = 0.0;
-    float loc = 0.0f, lmin = 0.0f, lmax = 0.0f, abs_loc = 0.0f, abs_p = 0.0f;
+    double B = 0.0;
     if (active) {
-#pragma unroll 1
-      for (int j4 = 0; j4 < Lp / 4; ++j4) {
-        float p[4];
-        products(j4, p);
+      B = bound_of(f);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          run += static_cast<double>(p[i]);
-          loc = __fadd_rn(loc, p[i]);
-          lmin = fminf(lmin, loc);
-          lmax = fmaxf(lmax, loc);
-          abs_loc = __fadd_rn(abs_loc, fabsf(loc));
-          abs_p = __fadd_rn(abs_p, fabsf(p[i]));
+      for (int c = 0; c < kKeep; ++c) {
+        if (c < nch) products(c, keep[c]);
+      }
+#pragma unroll
+      for (int c = 0; c < kKeep; ++c) {
+        if (c < nch) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) run += static_cast<double>(keep[c][i]);
         }
+      }
+#pragma unroll 1
+      for (int c = kKeep; c < nch; ++c) {
+        float p[4];
+        products(c, p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) run += static_cast<double>(p[i]);
       }
     }
     const double incl = WaveInclusiveScanD(run);
@@ -515,132 +490,58 @@ __device__ void RefineScores(int nflag, PageOf page_of, Emit emit, const float* 
       if (k < part) before += tk;
       S += tk;
     }
-    const double start = before + (incl - run);  // T before this lane's first step
-    // Float sums of non-negative terms: (1 + 2^-16) covers their rounding
-    // (fewer than 2^8 terms per lane); the local prefix loc_j is within
-    // Lp*u*sum|p| of its exact value, which widens every bound below.
-    const double abs_p_d = static_cast<double>(abs_p) * (1.0 + 0x1p-16);
-    const double loc_err = static_cast<double>(Lp) * u * abs_p_d;
-    const double abs_t =
-        WaveSum(static_cast<double>(Lp) * fabs(start) +
-                (static_cast<double>(abs_loc) + static_cast<double>(Lp) * loc_err) *
-                    (1.0 + 0x1p-16));
-    const double abs_pw = WaveSum(abs_p_d);
-    if (lane == 0) {
-      mine[1] = abs_t;
-      mine[2] = abs_pw;
-    }
-    __syncthreads();
-    double sum_abs_t = 0.0, sum_abs_p = 0.0;
-    for (int k = 0; k < parts; ++k) {
-      sum_abs_t += page_parts[8 * k + 1];
-      sum_abs_p += page_parts[8 * k + 2];
-    }
-    // |acc_j - T_j| <= u sum|acc_i| <= u (sum|T_i| + n B)  =>  B below, plus
-    // the double rounding of the prefix sums.
-    const double eps_t = (n + 64.0) * 0x1p-53 * sum_abs_p;
-    const double B = 1.001 * u * (sum_abs_t * (1.0 + 0x1p-40) + n * eps_t) / (1.0 - n * u) + eps_t;
-    // Sweep 2.
-    double K = 0.0, U = 0.0, abs_k = 0.0;
+    // Sweep 2 from T before this lane's first step.
+    dsd_refine::Sweep2 s2;
     if (active) {
-      // The range of T over this lane's steps (its start included).
-      const double wid = B + loc_err + eps_t;
-      const double ta = start + static_cast<double>(lmin) - wid;
-      const double tb = start + static_cast<double>(lmax) + wid;
-      const bool same_sign = ta > 0.0 || tb < 0.0;
-      const double amin = same_sign ? fmin(fabs(ta), fabs(tb)) : 0.0;
-      const double amax = fmax(fabs(ta), fabs(tb));
+      const double start = before + (incl - run);
       const bool global_first = part == 0 && lane == 0;
-      // (The fast path's float scaling by 2^(23-e) needs -100 <= e <= 100.)
-      if (same_sign && amin >= 0x1p-100 && amax < 0x1p100 && BinadeOf(amin) == BinadeOf(amax) &&
-          !global_first) {
-        // Fast path: one binade e throughout.
-        const int e = BinadeOf(amin);
-        const float inv = __int_as_float((127 + 23 - e) << 23);  // 2^(23-e), e <= 127+23
-        double csum = 0.0;
-        int ties = 0;
-#pragma unroll 1
-        for (int j4 = 0; j4 < Lp / 4; ++j4) {
-          float p[4];
-          products(j4, p);
+      s2.t = start;
+      s2.prev = dsd_refine::CertainField(start, B);
+#pragma unroll
+      for (int c = 0; c < kKeep; ++c) {
+        if (c < nch) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float x = __fmul_rn(p[i], inv);  // exact (|x| <= 2^25 or x rounds to 0)
-            const float r = rintf(x);
-            const bool tie = fabsf(__fsub_rn(x, r)) == 0.5f;
-            csum += static_cast<double>(tie ? x : r);
-            ties += tie ? 1 : 0;
-          }
-        }
-        const double sp = Pow2(e - 23);
-        K = run - csum * sp;  // sum of p_j - c_j sp, exact but for the two double sums
-        abs_k = 0.5 * sp * static_cast<double>(Lp);
-        U = 0.5 * sp * static_cast<double>(ties);
-      } else {
-        double t = start;
-        bool prev_certain;
-        int prev_e;
-        double half;
-        ClassifyStep(start, B, &prev_certain, &prev_e, &half);
-#pragma unroll 1
-        for (int j4 = 0; j4 < Lp / 4; ++j4) {
-          float p[4];
-          products(j4, p);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const double pd = static_cast<double>(p[i]);
-            t += pd;
-            bool certain;
-            int e;
-            ClassifyStep(t, B, &certain, &e, &half);
-            if (global_first && j4 == 0 && i == 0) {
-              // acc_1 = fl(0 + p_1) = p_1: exact.
-            } else if (certain && prev_certain && prev_e >= e) {
-              const double sp = Pow2(e - 23);
-              const double x = pd * Pow2(23 - e);  // exact
-              const double c = rint(x);
-              if (fabs(x - c) == 0.5) {
-                U += 0.5 * sp;  // a tie: +-sp/2 by acc_{j-1}'s last bit
-              } else {
-                const double err = pd - c * sp;  // exact
-                K += err;
-                abs_k += fabs(err);
-              }
-            } else {
-              U += half;
-            }
-            prev_certain = certain;
-            prev_e = e;
+            dsd_refine::Sweep2Step(s2, keep[c][i], B, global_first && c == 0 && i == 0);
           }
         }
       }
+#pragma unroll 1
+      for (int c = kKeep; c < nch; ++c) {
+        float p[4];
+        products(c, p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dsd_refine::Sweep2Step(s2, p[i], B, false);
+      }
     }
-    K = WaveSum(K);
-    U = WaveSum(U);
-    abs_k = WaveSum(abs_k);
+    const float K = WaveTotal(s2.K);
+    const float U = WaveTotal(s2.U);
     if (lane == 0) {
-      mine[3] = K;
-      mine[4] = U;
-      mine[5] = abs_k;
+      mine[3] = static_cast<double>(K);
+      mine[4] = static_cast<double>(U);
+      if (part == 0) {
+        mine[6] = S;
+        mine[7] = B;
+      }
     }
     __syncthreads();
+    // Lane 0 of each page's first wave combines its parts.  Those waves'
+    // slots are only rewritten after the next round's first barrier, which
+    // this wave reaches after this.
     if (active && part == 0 && lane == 0) {
-      double Kt = 0.0, Ut = 0.0, akt = 0.0;
+      double Kt = 0.0, Ut = 0.0;
       for (int k = 0; k < parts; ++k) {
         Kt += page_parts[8 * k + 3];
         Ut += page_parts[8 * k + 4];
-        akt += page_parts[8 * k + 5];
       }
-      // Double rounding of S, K and U: each a sum of at most n + 64 terms
-      // bounded by the sums of their magnitudes.
-      const double slack = (n + 64.0) * 0x1p-52 * (sum_abs_p + akt + Ut) + 0x1p-1074;
-      const double center = S - Kt;
+      const double center = mine[6] - Kt;
+      const double half = dsd_refine::HalfWidth(center, Ut * (1.0 + 0x1p-16), mine[7], E);
       float m_, l_, h_;
-      WriteInterval(center, Ut + slack + fabs(center) * 0x1p-52, scale, &m_, &l_, &h_, 0);
+      WriteInterval(center, half, scale, &m_, &l_, &h_, 0);
       emit(f, m_, l_, h_);
     }
-    __syncthreads();
   }
+  __syncthreads();
 }
 
 // ---- attention helpers ------------------------------------------------------

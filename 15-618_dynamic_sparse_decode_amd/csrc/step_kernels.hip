@@ -453,6 +453,10 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
           const bool live = pg >= 0 && pg < capacity && token_counts[pg] != 0;
           return live ? summaries + static_cast<size_t>(pg) * E : nullptr;
         },
+        [&](int f) {
+          const int c = flagged[f];
+          return dsd_refine::FirstPassBound(s_lo[c], s_hi[c], scale, E);
+        },
         [&](int f, float m, float l, float h) {
           const int c = flagged[f];
           keys[c] = SelectKey(m, cand[c]);
@@ -619,6 +623,10 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
           const int pg = cand[s_flag[f]];
           const bool live = pg >= 0 && pg < capacity && token_counts[pg] != 0;
           return live ? summaries + static_cast<size_t>(pg) * E : nullptr;
+        },
+        [&](int f) {
+          const int c = s_flag[f];
+          return dsd_refine::FirstPassBound(s_lo[c], s_hi[c], scale, E);
         },
         [&](int f, float m, float l, float h) {
           const int c = s_flag[f];
