@@ -570,16 +570,20 @@ __device__ __forceinline__ uint32_t WaveMaxU32(uint32_t x) {
 }
 
 // Wave 0 only.  Candidate i = lane + 64m (m < CS, i < n) has interval
-// (mid, lo, hi)[m]; its page id and token count are in sh.cpage / sh.cntok.
-// Takes the best remaining candidate kk times; each round's code is short
-// and runs warm after the first (a first run of one-shot code pays for every
-// instruction-cache line it touches, which dominates a round).  Writes the
-// members in rank order to sh.top (candidate index), sh.page and sh.ntok.
-// Returns 1 when the intervals certify the selection; 0 when they do not,
-// after listing the flagged candidates in sh.flag / sh.nflag (an outsider
-// whose hi reaches the members' smallest lo; a member whose lo reaches an
-// outsider's hi or whose interval overlaps another member's) and writing
-// every candidate's key to sh.key; -1 when two midpoints are equal (the
+// (mid, lo, hi)[m], the same values as sh.mid / sh.lo / sh.hi[i]; its page id
+// and token count are in sh.cpage / sh.cntok.  Takes the best remaining
+// candidate kk times: a round is a wave maximum of the midpoints' order bits,
+// one ballot per slot and the winner's index kept in lane t, so it stays
+// short and runs warm after the first (a first run of one-shot code pays for
+// every instruction-cache line it touches, which dominates a round).  The
+// members' intervals are then read once from LDS, lane t holding member t,
+// for the certification.  Writes the members in rank order to sh.top
+// (candidate index), sh.page and sh.ntok.  Returns 1 when the intervals
+// certify the selection; 0 when they do not, after listing the flagged
+// candidates in sh.flag / sh.nflag (an outsider whose hi reaches the
+// members' smallest lo; a member whose lo reaches an outsider's hi or whose
+// interval overlaps another member's) and writing every candidate's key to
+// sh.key; -1 when a round's maximum is not unique (equal midpoints: the
 // ballot ranks then order them).  Nothing else is written before a -1.
 template <int CS>
 __device__ int FastSelect(int n, int kk, const float (&mid)[kFSlots], const float (&lo)[kFSlots],
@@ -588,58 +592,46 @@ __device__ int FastSelect(int n, int kk, const float (&mid)[kFSlots], const floa
   uint32_t kh[CS];  // order bits of the midpoint; 0: empty or taken
 #pragma unroll
   for (int m = 0; m < CS; ++m) kh[m] = lane + kWave * m < n ? OrderBits(mid[m]) : 0u;
-  float min_lo = INFINITY;  // over the members taken so far
-  bool ordered = true;
-  float m_lo = INFINITY, m_hi = -INFINITY;  // lane t: member t
-  int m_top = 0;
+  int m_top = 0;     // lane t: candidate index of member t
+  bool dup = false;  // some round's maximum was not unique
 #pragma nounroll
   for (int t = 0; t < kk; ++t) {
     uint32_t x = kh[0];
 #pragma unroll
     for (int m = 1; m < CS; ++m) x = max(x, kh[m]);
     const uint32_t best = WaveMaxU32(x);
-    uint64_t b[CS];
     int count = 0;
+    int winner = -1;
 #pragma unroll
     for (int m = 0; m < CS; ++m) {
-      b[m] = __ballot(kh[m] == best);
-      count += __popcll(b[m]);
+      const uint64_t b = __ballot(kh[m] == best);
+      count += __popcll(b);
+      winner = (winner < 0 && b != 0) ? kWave * m + __ffsll(static_cast<long long>(b)) - 1
+                                      : winner;
     }
-    if (count != 1) return -1;
-    int ms = 0;
-    uint64_t bm = b[0];
+    dup = dup || count != 1;
+    m_top = lane == t ? winner : m_top;
 #pragma unroll
-    for (int m = 1; m < CS; ++m) {
-      ms = b[m] != 0 ? m : ms;
-      bm |= b[m];
-    }
-    const int ls = __ffsll(static_cast<long long>(bm)) - 1;
-    float w_lo = ReadLane(lo[0], ls), w_hi = ReadLane(hi[0], ls);
-#pragma unroll
-    for (int m = 1; m < CS; ++m) {
-      const float l = ReadLane(lo[m], ls), h = ReadLane(hi[m], ls);
-      w_lo = ms == m ? l : w_lo;
-      w_hi = ms == m ? h : w_hi;
-    }
-#pragma unroll
-    for (int m = 0; m < CS; ++m) kh[m] = (m == ms && lane == ls) ? 0u : kh[m];
-    ordered = ordered && min_lo > w_hi;
-    min_lo = fminf(min_lo, w_lo);
-    if (lane == t) {
-      m_lo = w_lo;
-      m_hi = w_hi;
-      m_top = ls + kWave * ms;
-    }
+    for (int m = 0; m < CS; ++m) kh[m] = lane + kWave * m == winner ? 0u : kh[m];
   }
+  if (dup) return -1;
+  float m_lo = INFINITY, m_hi = -INFINITY;
   if (lane < kk) {
     sh.top[lane] = m_top;
     sh.page[lane] = sh.cpage[m_top];
     sh.ntok[lane] = sh.cntok[m_top];
+    m_lo = sh.lo[m_top];
+    m_hi = sh.hi[m_top];
   }
   float oh = -INFINITY;  // the outsiders' largest hi
 #pragma unroll
   for (int m = 0; m < CS; ++m) oh = fmaxf(oh, kh[m] != 0u ? hi[m] : -INFINITY);
   const float max_o_hi = WaveMax(oh);
+  const float min_lo = ReadLane(WaveMinPrefix(m_lo), kWave - 1);
+  // Members in order: each one's lo above the next one's hi (lo <= hi, so
+  // adjacent pairs decide every pair).
+  const float next_hi = DppOr<kWaveShl1>(m_hi, -INFINITY);
+  const bool ordered = __ballot(lane + 1 < kk && !(m_lo > next_hi)) == 0;
   if (ordered && max_o_hi < min_lo) return 1;
   // Flags, as RankAndCertify's (members are lanes 0..kk-1 here).
   const float pmin = DppOr<kWaveShr1>(WaveMinPrefix(m_lo), INFINITY);   // members above
