@@ -1275,7 +1275,8 @@ struct StepLaunch {
   unsigned long long* rec = nullptr;  // [3 * total] publication words
   int* exact_pages = nullptr;         // may be null
   unsigned long long* fail_word = nullptr;
-  unsigned epoch = 0;  // fresh (non-zero) for every launch
+  unsigned epoch = 0;  // fresh (non-zero, below 2^30) for every launch
+  const unsigned* epoch_src = nullptr;  // captured launches: the device epoch counter
   unsigned spin_limit = kDefaultSpinLimit;
   bool never_ready = false;
   dsdk::FailReport Fail() const {
@@ -1285,6 +1286,15 @@ struct StepLaunch {
     return f;
   }
 };
+
+// Whether work enqueued on `s` is being captured into a graph.  A captured
+// step cannot take its epoch from the host (every replay would reuse it) nor
+// wait on events recorded outside the capture.
+bool StreamCapturing(hipStream_t s) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  DSD_HIP_CHECK(hipStreamIsCapturing(s, &status));
+  return status == hipStreamCaptureStatusActive;
+}
 
 float StepScale(const PoolView& v) {
   return 1.0f / std::sqrt(static_cast<float>(v.head_dim));
@@ -1355,7 +1365,9 @@ dsdk::FusedArgs FusedStepArgs(const PoolView& v, const StepLaunch& L) {
   a.outputs = L.outputs;
   a.rec = L.rec;
   a.epoch = L.epoch;
-  a.wait_tag = L.never_ready ? (L.epoch ^ 0x80000000u) : L.epoch;
+  a.wait_mask = L.never_ready ? 0x80000000u : 0u;
+  a.wait_tag = L.epoch | a.wait_mask;
+  a.epoch_src = L.epoch_src;
   a.spin_limit = L.spin_limit;
   a.exact_pages = L.exact_pages;
   a.fail = L.Fail();
@@ -1387,6 +1399,8 @@ struct dsd_sparse_ctx {
   DeviceBuffer<int> d_offsets, d_ids, d_selected, d_counts, d_exact_pages;
   // fused-step publication words (see fused_step.hip)
   DeviceBuffer<unsigned long long> d_rec;
+  // The epoch counter of captured fused launches (advanced on the device).
+  DeviceBuffer<unsigned> d_epoch;
   // The epoch of the step being enqueued: it tags the fused step's
   // publication words and every failure report of the step's kernels.
   unsigned epoch = 0;
@@ -1418,9 +1432,10 @@ struct dsd_sparse_ctx {
     if (ev_switch) (void)hipEventDestroy(ev_switch);
   }
 
-  // A fresh epoch for the next launch (never 0: the words start at 0).
+  // A fresh epoch for the next launch (never 0: the words start at 0; below
+  // 2^30, where the device epochs of captured launches never are).
   void NextEpoch() {
-    if (++epoch == 0) epoch = 1;
+    if (++epoch >= 0x40000000u) epoch = 1;
   }
   // Every launch shares the context's scratch (intervals, publication words,
   // ids).  Launches on one stream are ordered by it; a launch on another
@@ -1584,6 +1599,8 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     ctx->d_hi.Reserve(P);
     ctx->d_exact_pages.Reserve(1);
     DSD_HIP_CHECK(hipMemset(ctx->d_exact_pages.ptr, 0, sizeof(int)));
+    ctx->d_epoch.Reserve(1);
+    DSD_HIP_CHECK(hipMemset(ctx->d_epoch.ptr, 0, sizeof(unsigned)));
     {
       const size_t rec = 3 * P;
       // The largest fused grid: one head per workgroup.
@@ -1994,8 +2011,19 @@ int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
     if (d_selected != nullptr) L.selected = d_selected;
     if (d_selected_counts != nullptr) L.counts = d_selected_counts;
     hipStream_t s = stream != nullptr ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
-    ctx->pool->OrderAfterPending(s);
-    ctx->OrderOn(s);
+    if (StreamCapturing(s)) {
+      // Captured into a graph: the epoch comes from the device, and the
+      // caller orders the graph's replays against the context's other work.
+      if (ctx->pool->pending) {
+        throw std::invalid_argument(
+            "a pool append is still pending: synchronise before capturing a step");
+      }
+      L.epoch_src = ctx->d_epoch.ptr;
+      ctx->last_stream = nullptr;
+    } else {
+      ctx->pool->OrderAfterPending(s);
+      ctx->OrderOn(s);
+    }
     ctx->Enqueue(&L, s, false);
     ctx->last = L;
   });
@@ -2131,7 +2159,8 @@ constexpr size_t kStaticLo = Align256(kStaticMid + sizeof(float) * kStaticMaxCan
 constexpr size_t kStaticHi = Align256(kStaticLo + sizeof(float) * kStaticMaxCandidates);
 constexpr size_t kStaticSel = Align256(kStaticHi + sizeof(float) * kStaticMaxCandidates);
 constexpr size_t kStaticCounts = Align256(kStaticSel + sizeof(int) * kStaticMaxSelected);
-constexpr size_t kStaticBytes = Align256(kStaticCounts + sizeof(int) * kStaticMaxBatch);
+constexpr size_t kStaticEpoch = Align256(kStaticCounts + sizeof(int) * kStaticMaxBatch);
+constexpr size_t kStaticBytes = Align256(kStaticEpoch + sizeof(unsigned));
 
 }  // namespace
 
@@ -2215,7 +2244,7 @@ int dsd_sparse_run_batch_device_static(dsd_pool* pool, int top_k, int batch,
     DSD_HIP_CHECK(hipGetDevice(&device));
     Require(device >= 0 && device < kStaticMaxDevices, "device ordinal beyond 64");
     StaticScratch& st = StaticScratchOn(device);
-    if (++st.epoch == 0) st.epoch = 1;
+    if (++st.epoch >= 0x40000000u) st.epoch = 1;
     const PoolView& v = pool->view;
     StepLaunch L;
     L.valid = true;
@@ -2242,7 +2271,17 @@ int dsd_sparse_run_batch_device_static(dsd_pool* pool, int top_k, int batch,
     L.fail_word = d_fail;
     L.epoch = st.epoch;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    pool->OrderAfterPending(s);
+    if (StreamCapturing(s)) {
+      // Captured into a graph: the epoch comes from the device (a word of
+      // the static scratch, zero at load).
+      if (pool->pending) {
+        throw std::invalid_argument(
+            "a pool append is still pending: synchronise before capturing a step");
+      }
+      L.epoch_src = reinterpret_cast<const unsigned*>(st.ptr + kStaticEpoch);
+    } else {
+      pool->OrderAfterPending(s);
+    }
     EnqueueStep(v, L, s);
   });
 }

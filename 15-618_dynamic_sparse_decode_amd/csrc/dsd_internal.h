@@ -229,8 +229,14 @@ struct FusedArgs {
   int* exact_pages = nullptr;         // may be null
   FailReport fail;                    // kFailWait / kFailShape / kFailPageId
   unsigned spin_limit = 0;            // polls of a cross-workgroup wait before it gives up
-  unsigned wait_tag = 0;              // the tag the waits look for: epoch (a test
-                                      // sets another, so every wait gives up)
+  unsigned wait_tag = 0;              // the tag the waits look for: epoch | wait_mask
+  unsigned wait_mask = 0;             // 0, or a bit no epoch has (a test hook: every
+                                      // wait gives up)
+  // Non-null for launches captured into a graph: the device counter that
+  // LaunchFusedStep advances in a one-thread kernel just before the step;
+  // the step reads its epoch there (so every replay tags afresh) instead of
+  // `epoch`.  Host epochs lie in [1, 2^30), device epochs in [2^30, 2^31).
+  const unsigned* epoch_src = nullptr;
   unsigned long long* stamps = nullptr;  // null, or [grid][FusedStepStampsPerGroup()]:
                                          // clocks at start, slice scored, counter
                                          // ready, records read, ranked, selected,

@@ -586,8 +586,8 @@ __device__ __forceinline__ uint32_t WaveMaxU32(uint32_t x) {
 // sh.key; -1 when a round's maximum is not unique (equal midpoints: the
 // ballot ranks then order them).  Nothing else is written before a -1.
 template <int CS>
-__device__ int FastSelect(int n, int kk, const float (&mid)[kFSlots], const float (&lo)[kFSlots],
-                          const float (&hi)[kFSlots], FusedShared& sh) {
+__device__ int FastSelect(int n, int kk, const float (&mid)[kFSlots], const float (&hi)[kFSlots],
+                          FusedShared& sh) {
   const int lane = threadIdx.x & (kWave - 1);
   uint32_t kh[CS];  // order bits of the midpoint; 0: empty or taken
 #pragma unroll
@@ -655,13 +655,12 @@ __device__ int FastSelect(int n, int kk, const float (&mid)[kFSlots], const floa
 }
 
 __device__ __forceinline__ int FastSelectSlots(int n, int kk, const float (&mid)[kFSlots],
-                                               const float (&lo)[kFSlots],
                                                const float (&hi)[kFSlots], FusedShared& sh) {
   switch ((n + kWave - 1) / kWave) {
-    case 1: return FastSelect<1>(n, kk, mid, lo, hi, sh);
-    case 2: return FastSelect<2>(n, kk, mid, lo, hi, sh);
-    case 3: return FastSelect<3>(n, kk, mid, lo, hi, sh);
-    default: return FastSelect<4>(n, kk, mid, lo, hi, sh);
+    case 1: return FastSelect<1>(n, kk, mid, hi, sh);
+    case 2: return FastSelect<2>(n, kk, mid, hi, sh);
+    case 3: return FastSelect<3>(n, kk, mid, hi, sh);
+    default: return FastSelect<4>(n, kk, mid, hi, sh);
   }
 }
 
@@ -785,7 +784,7 @@ __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const Fuse
         }
       }
       if (fast && !timed_out) {
-        const int verdict = FastSelectSlots(n, run == 1 ? kk : 1, mid, lo, hi, sh);
+        const int verdict = FastSelectSlots(n, run == 1 ? kk : 1, mid, hi, sh);
         if (run == 1 && lane == 0) sh.certified = verdict;
       }
     }
@@ -808,15 +807,14 @@ __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const Fuse
         if (pass == 1) {
           // Select again from the refined intervals.
           if (wave == 0) {
-            float mid[kFSlots], lo[kFSlots], hi[kFSlots];
+            float mid[kFSlots], hi[kFSlots];
 #pragma unroll
             for (int m = 0; m < kFSlots; ++m) {
               const int i = lane + kWave * m;  // < kFMaxCand: in bounds
               mid[m] = sh.mid[i];
-              lo[m] = sh.lo[i];
               hi[m] = sh.hi[i];
             }
-            const int verdict = FastSelectSlots(n, kk, mid, lo, hi, sh);
+            const int verdict = FastSelectSlots(n, kk, mid, hi, sh);
             if (lane == 0) sh.certified = verdict;
           }
           __syncthreads();
@@ -1037,6 +1035,12 @@ __device__ __forceinline__ void AttentionItem(const PoolView& pool, const FusedA
 template <bool kMultiPass>
 __global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, FusedArgs a) {
   __shared__ FusedShared sh;
+  if (a.epoch_src != nullptr) {
+    // Replayed from a captured graph: the epoch the bump kernel just set.
+    a.epoch = *a.epoch_src;
+    a.wait_tag = a.epoch | a.wait_mask;
+    a.fail.epoch = a.epoch;
+  }
   if (a.stamps != nullptr && threadIdx.x == 0) {
     for (int i = 0; i < kStampsPerGroup; ++i) sh.stamp[i] = 0;
   }
@@ -1158,6 +1162,12 @@ int FusedStepGrid(const PoolView& pool, int batch, int heads_per_group) {
 
 int FusedStepStampsPerGroup() { return kStampsPerGroup; }
 
+// One thread advances the device epoch counter of captured steps, within
+// [2^30, 2^31) (host epochs stay below 2^30, so the two never meet).
+__global__ void EpochBumpKernel(unsigned* epoch) {
+  if (threadIdx.x == 0) *epoch = ((*epoch + 1u) & 0x3FFFFFFFu) | 0x40000000u;
+}
+
 void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t stream) {
   if (args.batch <= 0) return;
   const int hpw = args.heads_per_group;
@@ -1166,6 +1176,11 @@ void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t st
   }
   if (pool.num_heads % hpw != 0) throw std::invalid_argument("heads per group must divide num_heads");
   const int grid = FusedStepGrid(pool, args.batch, hpw);
+  if (args.epoch_src != nullptr) {
+    hipLaunchKernelGGL(EpochBumpKernel, dim3(1), dim3(kWave), 0, stream,
+                       const_cast<unsigned*>(args.epoch_src));
+    DSD_HIP_CHECK(hipGetLastError());
+  }
   if (FusedStepMultiPass(pool, args.max_candidates, hpw)) {
     hipLaunchKernelGGL(FusedStepKernel<true>, dim3(grid), dim3(kFThreads), 0, stream, pool, args);
   } else {

@@ -139,6 +139,9 @@ class Workload:
         self.pool.close()
 
 
+GRAPH_STEPS = 10  # steps per captured graph in the graph-replay timing
+
+
 def timed(torch, stream, fn, steps):
     """Average ms of `steps` back-to-back calls of fn(i) on `stream`,
     bracketed by HIP events and synchronisations."""
@@ -221,6 +224,25 @@ def main() -> int:
     launch = w.ctx.last_launch()
     log(f"step {ms_per_step * 1e3:.1f} us over {args.steps} steps; "
         f"{rescored} pages rescored exactly; launch {launch}")
+
+    # The step captured into a graph, GRAPH_STEPS steps per graph, replayed
+    # back to back (a captured fused step takes its epoch from a device
+    # counter that a one-thread kernel in the graph advances).
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(GRAPH_STEPS):
+            w.step(sptr)
+    torch.cuda.synchronize()
+
+    def replay(i):
+        with torch.cuda.stream(stream):
+            graph.replay()
+
+    replay(0)
+    graph_ms = timed(torch, stream, replay, max(2, args.steps // GRAPH_STEPS)) / GRAPH_STEPS
+    w.ctx.device_status()
+    log(f"graph replay ({GRAPH_STEPS} steps per graph): {graph_ms * 1e3:.1f} us per step")
 
     # Per-kernel average durations: K back-to-back launches of one kernel on
     # the same stream.  Stages 0-2 are the three-kernel step (score, select,
@@ -382,6 +404,11 @@ def main() -> int:
                                / HBM_PEAK_GBPS},
         "step_phases_us": {k[:-3]: phases[k] * 1e3
                            for k in ("score_ms", "topk_ms", "attention_ms", "kernel_ms")},
+        "graph_replay": {"us_per_step": graph_ms * 1e3, "tokens_per_s": B / (graph_ms * 1e-3),
+                         "steps_per_graph": GRAPH_STEPS,
+                         "note": "the device step captured into a graph (torch.cuda.CUDAGraph), "
+                                 "replayed back to back; each captured fused step adds a "
+                                 "one-thread epoch kernel; not the headline value"},
         "host_path": {"us_per_step": host_ms * 1e3, "tokens_per_s": B / (host_ms * 1e-3),
                       "steps": host_steps,
                       "note": "dsd_sparse_run_batch with host buffers (queries and CSR in, "

@@ -265,7 +265,15 @@ int dsd_host_free(void* p);
  * request's outputs are zeros, and dsd_sparse_device_status reports it.
  * Steps on one context share its scratch: a step on a stream other than the
  * previous step's first waits for the previous stream's work, so that
- * stream must still be valid then (it is used for an event record). */
+ * stream must still be valid then (it is used for an event record).
+ * Graph capture: on a stream that is capturing, the call records the step
+ * into the graph.  A captured single-launch step takes its epoch (the tag
+ * of the words its workgroups exchange) from a device counter that a
+ * one-thread kernel, captured with it, advances on every replay, so each
+ * replay reads its own inputs.  The caller orders the graph's replays
+ * against the context's other steps (no event wait is captured), and a
+ * pool append must have completed (dsd_pool_* synchronised) before the
+ * capture, or the call fails with DSD_ERR_INVALID_ARGUMENT. */
 int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
                                 int total_candidates, int max_candidates,
                                 const float* d_queries,
@@ -337,7 +345,9 @@ int dsd_sparse_set_wait_limit(dsd_sparse_ctx* ctx, unsigned spin_limit, int neve
  * context it replaces; selection is certified (bit-exact with sparse_cpu).
  * d_fail (may be NULL): memory the device writes (epoch << 32) | code to
  * when a request is skipped (codes as dsd_sparse_device_status's 1..3);
- * the caller clears it before the call and reads it after. */
+ * the caller clears it before the call and reads it after.
+ * Under graph capture the step's epoch is a device counter kept in the same
+ * static array, as for dsd_sparse_run_batch_device. */
 int dsd_sparse_run_batch_device_static(dsd_pool* pool, int top_k, int batch,
                                        int total_candidates, int max_candidates,
                                        const float* d_queries, const int* d_cand_offsets,
