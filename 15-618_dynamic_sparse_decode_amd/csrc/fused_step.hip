@@ -686,7 +686,7 @@ __device__ __forceinline__ int FastSelectSlots(int n, int kk, const float (&mid)
 __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r, int begin,
                                 int n, bool writer, FusedShared& sh) {
   int kk = a.top_k <= 0 ? 0 : (a.top_k < n ? a.top_k : n);
-  if (n > kFMaxCand) {
+  if (n > a.max_candidates || n > kFMaxCand) {
     // The caller's max_candidates understated the CSR: select nothing (the
     // outputs are zeros) and report it to the host.
     if (writer && threadIdx.x == 0) ReportFailure(a.fail, kFailShape);
@@ -1052,9 +1052,9 @@ __global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, Fuse
   // scored or selected, zero outputs) and reported.
   int begin, n;
   RequestRange(a.cand_offsets, r, a.total, g == 0 ? a.fail : FailReport{}, &begin, &n);
-  // A request beyond kFMaxCand selects nothing (reported by the selection):
-  // its slices are not scored.
-  if (n <= kFMaxCand) {
+  // A request beyond the caller's max_candidates (or kFMaxCand) selects
+  // nothing (reported by the selection): its slices are not scored.
+  if (n <= a.max_candidates && n <= kFMaxCand) {
     ScoreSlice<kMultiPass>(pool, a, r, begin + (g * n) / groups,
                            begin + ((g + 1) * n) / groups, sh);
   }

@@ -276,7 +276,7 @@ def test_certified_large_request_ties_and_duplicates(gpu, query):
     pool.close()
 
 
-@pytest.mark.parametrize("n_cand,k", [(40, 8), (300, 8)])
+@pytest.mark.parametrize("n_cand,k", [(40, 8), (600, 8)])
 def test_refined_intervals_settle_near_ties_without_the_chain(gpu, n_cand, k):
     # Eight pages whose exact scores differ by about 1e-3: the score pass's
     # intervals (several 1e-3 wide at these magnitudes) overlap, the refined
@@ -285,7 +285,7 @@ def test_refined_intervals_settle_near_ties_without_the_chain(gpu, n_cand, k):
     # must then be settled without any exact chain, every interval (refined
     # or not) must contain the exact score, and the refined ones (which the
     # three-kernel step writes back) must be narrower than the gaps.  40
-    # candidates take the single-launch step, 300 the three-kernel step.
+    # candidates take the single-launch step, 600 the three-kernel step.
     rng = np.random.default_rng(n_cand)
     H, D, ps = 32, 128, 16
     E = H * D
@@ -316,7 +316,7 @@ def test_refined_intervals_settle_near_ties_without_the_chain(gpu, n_cand, k):
     assert sorted(selected[0].tolist()) == list(range(8))
     assert orc.max_abs_diff(cert["outputs"], outs) <= 1e-4
     assert rescored == 0, f"{rescored} pages needed the exact chain"
-    if n_cand > 256:
+    if n_cand > 512:
         # the three-kernel select writes its refined intervals back (the
         # single-launch step keeps them in LDS)
         where = np.argsort(ids)                      # candidate position of each page id

@@ -76,8 +76,8 @@ def test_device_failure_does_not_fail_a_later_host_step(gpu, fused):
     q, offs, ids, out = device_inputs(batch)
     _, selected, outs = oracle_step(batch, 8)
     with make_ctx(gpu, pool, 8, batch, fused) as ctx:
-        # understated: 200 < 300 (fused: the selector holds 256; three-kernel:
-        # only 200 candidates were scored)
+        # understated: 200 < 300 (fused: the kernel checks each request
+        # against it; three-kernel: only 200 candidates were scored)
         ctx.run_batch_device(batch.batch, batch.total_candidates, 200, q.data_ptr(),
                              offs.data_ptr(), ids.data_ptr(), out.data_ptr(),
                              stream=torch.cuda.current_stream().cuda_stream)

@@ -123,8 +123,9 @@ def test_fused_phase_timings_are_reported(gpu):
 
 def test_fused_device_path_reports_understated_max_candidates(gpu):
     # The device entry point trusts max_candidates; a request larger than the
-    # 256 the fused selector holds is caught by the kernel's own check, gives
-    # zeros for that request, and is reported at the next synchronising call.
+    # max_candidates the caller stated is caught by the kernel's own check,
+    # gives zeros for that request, and is reported at the next synchronising
+    # call.
     import torch
 
     lengths = [300 * PS, 40]                     # 300 candidates in request 0

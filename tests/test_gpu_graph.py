@@ -32,7 +32,7 @@ def device(a):
 @pytest.mark.parametrize("entry", ["context", "static"])
 @pytest.mark.parametrize("lengths,fused", [
     ([629, 861, 1710, 1002, 1185, 2015], True),       # the single-launch step
-    ([300 * PS, 40, 2100, 16 * PS], False),           # > 256 candidates: three kernels
+    ([600 * PS, 40, 2100, 16 * PS], False),           # > 512 candidates: three kernels
 ])
 def test_graph_replays_follow_new_inputs(gpu, entry, lengths, fused):
     import torch

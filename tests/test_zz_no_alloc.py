@@ -71,7 +71,7 @@ def both_entries(gpu, pool, k, queries, offs, ids, static_ids):
 
 @pytest.mark.parametrize("lengths,k,fused", [
     (None, 8, True),                                  # the fused step
-    ([300 * PS, 40, 2100, 16 * PS], 8, False),        # > 256 candidates: three kernels
+    ([600 * PS, 40, 2100, 16 * PS], 8, False),        # > 512 candidates: three kernels
 ])
 def test_static_entry_equals_the_context_entry(gpu, lengths, k, fused):
     if lengths is None:
