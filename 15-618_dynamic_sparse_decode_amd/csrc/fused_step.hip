@@ -838,8 +838,11 @@ __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const Fuse
       if (!any || pass == 1) break;
       // 4a. Some order is not decided by the intervals: the flagged pages
       // get refined intervals (RefineScores, the whole workgroup, several
-      // waves per page), and the ranks and certification run again.
+      // waves per page), and the ranks and certification run again; more
+      // flagged pages than that pays for go straight to the exact chains
+      // (sh.nflag read after the barrier: wave 0 wrote it).
       __syncthreads();
+      if (!RefineWorthwhile(sh.nflag)) break;
       StampAt(a, sh, kRefine);
       RefineScores(
           sh.nflag,

@@ -445,7 +445,7 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
       if (flag) flagged[atomicAdd(&s_nflag, 1)] = sidx[t];
     }
     __syncthreads();
-    if (s_nflag == 0 || pass == 1 || E % 256 != 0) break;
+    if (s_nflag == 0 || pass == 1 || E % 256 != 0 || !RefineWorthwhile(s_nflag)) break;
     RefineScores(
         s_nflag,
         [&](int f) -> const float* {
@@ -616,7 +616,7 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
     }
     __syncthreads();
     nflag = s_nflag;
-    if (nflag == 0 || pass == 1 || E % 256 != 0) break;
+    if (nflag == 0 || pass == 1 || E % 256 != 0 || !RefineWorthwhile(nflag)) break;
     RefineScores(
         nflag,
         [&](int f) -> const float* {
