@@ -332,6 +332,9 @@ def main() -> int:
                    "GBps": select_bytes / (stage_ms[1] * 1e-3) / 1e9},
         "attention": {"us": stage_ms[2] * 1e3, "bytes": attn_bytes,
                       "GBps": attn_bytes / (stage_ms[2] * 1e-3) / 1e9},
+        "note": "each kernel of the three-kernel step launched alone, back to back; the select "
+                "re-runs on intervals that its previous run may have refined and with its code "
+                "warm, so it reads low; step_phases_us times the phases of one real step",
     }
     if fused_ms is not None:
         stages["fused_step"] = {"us": fused_ms * 1e3, "bytes": step_bytes,
