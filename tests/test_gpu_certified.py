@@ -9,6 +9,8 @@ same products in another order, so the sequential sums differ only by
 rounding; duplicated summaries: exactly equal scores)."""
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -276,16 +278,25 @@ def test_certified_large_request_ties_and_duplicates(gpu, query):
     pool.close()
 
 
-@pytest.mark.parametrize("n_cand,k", [(40, 8), (600, 8)])
-def test_refined_intervals_settle_near_ties_without_the_chain(gpu, n_cand, k):
-    # Eight pages whose exact scores differ by about 1e-3: the score pass's
-    # intervals (several 1e-3 wide at these magnitudes) overlap, the refined
-    # intervals (the rounding error of each addition accounted for exactly
-    # where its binade is certain, a few 1e-5 wide) do not.  The selection
-    # must then be settled without any exact chain, every interval (refined
-    # or not) must contain the exact score, and the refined ones (which the
-    # three-kernel step writes back) must be narrower than the gaps.  40
-    # candidates take the single-launch step, 600 the three-kernel step.
+@pytest.mark.parametrize("n_cand,k,near_count,fused_env", [
+    (40, 8, 8, None), (600, 8, 8, None), (40, 8, 12, None), (600, 8, 12, None),
+    (40, 2, 2, "0"), (40, 8, 8, "0"),
+])
+def test_refined_intervals_settle_near_ties_without_the_chain(gpu, n_cand, k, near_count,
+                                                              fused_env):
+    # near_count pages whose exact scores differ by about 1e-3: the score
+    # pass's intervals (several 1e-3 wide at these magnitudes) overlap, the
+    # refined intervals (the rounding error of each addition accounted for
+    # exactly where its binade is certain, a few 1e-5 wide) do not.  With 8
+    # such pages (every one flagged) the selection must be settled without
+    # any exact chain, every interval (refined or not) must contain the
+    # exact score, and the refined ones (which the three-kernel step writes
+    # back) must be narrower than the gaps.  With more flagged pages than
+    # half the workgroup's waves (8 of 16; 2 of the 4 in the three-kernel
+    # select for at most 256 candidates, DSD_FUSED_STEP=0) the refinement
+    # is skipped and the flagged pages take the exact chain.  40 candidates
+    # take the single-launch step unless it is switched off, 600 the
+    # three-kernel step.
     rng = np.random.default_rng(n_cand)
     H, D, ps = 32, 128, 16
     E = H * D
@@ -294,7 +305,7 @@ def test_refined_intervals_settle_near_ties_without_the_chain(gpu, n_cand, k):
     m = int(np.argmax(np.abs(q)))
     base = (0.2 * q + 0.25 * rng.standard_normal(E)).astype(np.float32)
     summ = (0.25 * rng.standard_normal((n_cand, E))).astype(np.float32)
-    near = np.arange(8)
+    near = np.arange(near_count)
     for j in near:
         row = base.copy()
         row[m] = np.float32(row[m] + j * 1e-3 / (q[m] * scale))
@@ -307,14 +318,31 @@ def test_refined_intervals_settle_near_ties_without_the_chain(gpu, n_cand, k):
     pool.upload_pages(page_ids, counts, page_ids.astype(np.int64) * ps * E, keys, values, summ)
     ids = rng.permutation(n_cand).astype(np.int32)
     offs = np.array([0, n_cand], np.int32)
-    cert, (mid, lo, hi), rescored, exact = run_both_paths(gpu, pool, q[None, :], offs, ids, k)
+    old = os.environ.get("DSD_FUSED_STEP")
+    if fused_env is not None:
+        os.environ["DSD_FUSED_STEP"] = fused_env
+    try:
+        cert, (mid, lo, hi), rescored, exact = run_both_paths(gpu, pool, q[None, :], offs, ids,
+                                                              k)
+    finally:
+        if old is None:
+            os.environ.pop("DSD_FUSED_STEP", None)
+        else:
+            os.environ["DSD_FUSED_STEP"] = old
+    limit = 2 if (fused_env == "0" and n_cand <= 256) else 8
     ex = exact["scores"]
     assert np.all(lo <= ex) and np.all(ex <= hi), "an interval misses the exact score"
     _, selected, outs = orc.sparse_batch(q[None, :], keys, values, summ, counts, offs, ids,
                                          H, D, ps, k)
     assert cert["selected"][0].tolist() == selected[0].tolist()
-    assert sorted(selected[0].tolist()) == list(range(8))
+    assert sorted(selected[0].tolist()) == list(range(near_count - k, near_count))
     assert orc.max_abs_diff(cert["outputs"], outs) <= 1e-4
+    if near_count > limit:
+        # the members overlap each other; the outsiders within an interval's
+        # width of the smallest member are flagged too
+        assert limit < rescored <= near_count, f"{rescored} pages took the exact chain"
+        pool.close()
+        return
     assert rescored == 0, f"{rescored} pages needed the exact chain"
     if n_cand > 512:
         # the three-kernel select writes its refined intervals back (the
