@@ -895,10 +895,11 @@ struct dsd_table {
     const int n = PagesFor(tokens);
     if (n > view.max_pages) throw std::invalid_argument("prompt exceeds the table's max_pages");
     if (n > h_free) throw std::runtime_error("page pool is exhausted");
+    // The mirror follows the device only once the kernel is enqueued.
+    dsdk::LaunchTableReserve(view, slot, n, pool->stream);
     h_npages[slot] = n;
     h_tail[slot] = n == 0 ? 0 : tokens - (n - 1) * pool->view.page_size;
     h_free -= n;
-    dsdk::LaunchTableReserve(view, slot, n, pool->stream);
     return n;
   }
   const int* SlotPages(int slot) const {
@@ -926,6 +927,17 @@ int dsd_table_create(dsd_pool* pool, int max_slots, int max_pages, dsd_table** o
     Require(pool != nullptr, "pool must be non-null");
     Require(max_slots > 0 && max_pages > 0, "table sizes must be positive");
     Require(pool->view.elements % 4 == 0, "the table needs E % 4 == 0");
+    {
+      // Admission ranks a prompt's popped page ids in LDS (4 bytes a page).
+      int device = 0, lds = 0;
+      DSD_HIP_CHECK(hipGetDevice(&device));
+      DSD_HIP_CHECK(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
+      if (static_cast<int64_t>(max_pages) * static_cast<int64_t>(sizeof(int)) > lds) {
+        throw std::invalid_argument("table max_pages exceeds what one admission can rank in LDS (" +
+                                    std::to_string(lds / static_cast<int>(sizeof(int))) +
+                                    " pages)");
+      }
+    }
     auto t = std::make_unique<dsd_table>();
     t->pool = pool;
     t->pages.Reserve(static_cast<size_t>(max_slots) * max_pages);
@@ -1167,17 +1179,6 @@ int dsd_table_append(dsd_table* table, int n, const int* slots, const unsigned c
       }
       if (fresh_pages > table->h_free) throw std::runtime_error("page pool is exhausted");
     }
-    for (int i = 0; i < n; ++i) {
-      const int s = slots[i];
-      const bool fresh = (fresh_page != nullptr && fresh_page[i] != 0) ||
-                         table->h_npages[s] == 0 || table->h_tail[s] >= ps;
-      if (fresh) {
-        ++table->h_npages[s];
-        table->h_tail[s] = 0;
-      }
-      if (upload[i] != 0) ++table->h_tail[s];
-    }
-    table->h_free -= fresh_pages;
     const int b = table->Acquire(4 * static_cast<size_t>(n));
     int* args = table->h_args[b].ptr;
     for (int i = 0; i < n; ++i) {
@@ -1193,6 +1194,19 @@ int dsd_table_append(dsd_table* table, int n, const int* slots, const unsigned c
     dsdk::LaunchTablePlanAppend(pool->view, table->view, args, n, m, table->d_plan.ptr,
                                 table->d_order.ptr, pool->stream);
     table->Done(b);
+    // The plan kernel is enqueued: the device pops the fresh pages, so the
+    // mirror follows now (before the payload kernels).
+    for (int i = 0; i < n; ++i) {
+      const int s = slots[i];
+      const bool fresh = (fresh_page != nullptr && fresh_page[i] != 0) ||
+                         table->h_npages[s] == 0 || table->h_tail[s] >= ps;
+      if (fresh) {
+        ++table->h_npages[s];
+        table->h_tail[s] = 0;
+      }
+      if (upload[i] != 0) ++table->h_tail[s];
+    }
+    table->h_free -= fresh_pages;
     if (m == 0) return;
     if (rows) {
       const size_t elems = static_cast<size_t>(m) * pool->view.elements;
@@ -1464,6 +1478,11 @@ struct dsd_sparse_ctx {
     }
     if (code == dsdk::kFailPageId) {
       throw std::out_of_range("a candidate page id of the step is outside the pool");
+    }
+    if (code == dsdk::kFailSelect) {
+      throw std::runtime_error(
+          "decode step: a selection slot held an id that is not one of the request's "
+          "candidates (written as -1, not attended)");
     }
     throw std::runtime_error("fused decode step: wait for page selection timed out");
   }

@@ -49,7 +49,10 @@ struct FailReport {
   unsigned long long* word = nullptr;  // null: failures are not reported
   unsigned epoch = 0;
 };
-enum FailCode { kFailWait = 1, kFailShape = 2, kFailPageId = 3 };
+// kFailSelect: a selection kernel was about to emit an id that is not the
+// page of one of the request's candidates (an internal invariant; the slot
+// is written as -1 and never attended).
+enum FailCode { kFailWait = 1, kFailShape = 2, kFailPageId = 3, kFailSelect = 4 };
 
 // ---- pool kernels (pool_kernels.hip) --------------------------------------
 
@@ -161,13 +164,16 @@ void LaunchScoreBounds(const PoolView& pool, const float* d_queries,
                        float* d_lo, float* d_hi, FailReport fail, hipStream_t stream);
 
 // Top-k from certified intervals; candidates whose order is not decided by
-// disjoint intervals get refined intervals (written back to mid/lo/hi) and,
-// where those still leave it open, the exact sequential chain.  Adds the
+// disjoint intervals get refined intervals (kept in LDS: mid/lo/hi stay the
+// score kernel's first-pass intervals, so the select can run again on the
+// same buffers) and, where those still leave it open, the exact sequential
+// chain.  Adds the
 // number of rescored pages to *d_exact_pages when non-null.  A request whose
 // candidate list is longer than max_candidates (the score kernels covered
 // only that many) or whose offsets leave [0, total_candidates] selects
 // nothing and is reported (kFailShape).
-void LaunchSelectCertified(const PoolView& pool, float* d_mid, float* d_lo, float* d_hi,
+void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float* d_lo,
+                           const float* d_hi,
                            const float* d_queries,
                            const int* d_cand_offsets, const int* d_cand_ids, int batch,
                            int total_candidates, int max_candidates, float scale, int top_k,
@@ -227,7 +233,7 @@ struct FusedArgs {
   unsigned long long* rec = nullptr;
   unsigned epoch = 0;
   int* exact_pages = nullptr;         // may be null
-  FailReport fail;                    // kFailWait / kFailShape / kFailPageId
+  FailReport fail;                    // kFailWait / kFailShape / kFailPageId / kFailSelect
   unsigned spin_limit = 0;            // polls of a cross-workgroup wait before it gives up
   unsigned wait_tag = 0;              // the tag the waits look for: epoch | wait_mask
   unsigned wait_mask = 0;             // 0, or a bit no epoch has (a test hook: every

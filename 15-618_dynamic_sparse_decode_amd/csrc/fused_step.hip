@@ -587,7 +587,7 @@ __device__ __forceinline__ uint32_t WaveMaxU32(uint32_t x) {
 // ballot ranks then order them).  Nothing else is written before a -1.
 template <int CS>
 __device__ int FastSelect(int n, int kk, const float (&mid)[kFSlots], const float (&hi)[kFSlots],
-                          FusedShared& sh) {
+                          FusedShared& sh, bool dry) {
   const int lane = threadIdx.x & (kWave - 1);
   uint32_t kh[CS];  // order bits of the midpoint; 0: empty or taken
 #pragma unroll
@@ -617,11 +617,16 @@ __device__ int FastSelect(int n, int kk, const float (&mid)[kFSlots], const floa
   if (dup) return -1;
   float m_lo = INFINITY, m_hi = -INFINITY;
   if (lane < kk) {
-    sh.top[lane] = m_top;
-    sh.page[lane] = sh.cpage[m_top];
-    sh.ntok[lane] = sh.cntok[m_top];
-    m_lo = sh.lo[m_top];
-    m_hi = sh.hi[m_top];
+    if (dry) {
+      // The warm-up: the members' intervals are the made-up midpoints.
+      m_lo = m_hi = -static_cast<float>(m_top);
+    } else {
+      sh.top[lane] = m_top;
+      sh.page[lane] = sh.cpage[m_top];
+      sh.ntok[lane] = sh.cntok[m_top];
+      m_lo = sh.lo[m_top];
+      m_hi = sh.hi[m_top];
+    }
   }
   float oh = -INFINITY;  // the outsiders' largest hi
 #pragma unroll
@@ -633,6 +638,7 @@ __device__ int FastSelect(int n, int kk, const float (&mid)[kFSlots], const floa
   const float next_hi = DppOr<kWaveShl1>(m_hi, -INFINITY);
   const bool ordered = __ballot(lane + 1 < kk && !(m_lo > next_hi)) == 0;
   if (ordered && max_o_hi < min_lo) return 1;
+  if (dry) return 0;
   // Flags, as RankAndCertify's (members are lanes 0..kk-1 here).
   const float pmin = DppOr<kWaveShr1>(WaveMinPrefix(m_lo), INFINITY);   // members above
   const float smax = DppOr<kWaveShl1>(WaveMaxSuffix(m_hi), -INFINITY);  // members below
@@ -655,12 +661,13 @@ __device__ int FastSelect(int n, int kk, const float (&mid)[kFSlots], const floa
 }
 
 __device__ __forceinline__ int FastSelectSlots(int n, int kk, const float (&mid)[kFSlots],
-                                               const float (&hi)[kFSlots], FusedShared& sh) {
+                                               const float (&hi)[kFSlots], FusedShared& sh,
+                                               bool dry) {
   switch ((n + kWave - 1) / kWave) {
-    case 1: return FastSelect<1>(n, kk, mid, hi, sh);
-    case 2: return FastSelect<2>(n, kk, mid, hi, sh);
-    case 3: return FastSelect<3>(n, kk, mid, hi, sh);
-    default: return FastSelect<4>(n, kk, mid, hi, sh);
+    case 1: return FastSelect<1>(n, kk, mid, hi, sh, dry);
+    case 2: return FastSelect<2>(n, kk, mid, hi, sh, dry);
+    case 3: return FastSelect<3>(n, kk, mid, hi, sh, dry);
+    default: return FastSelect<4>(n, kk, mid, hi, sh, dry);
   }
 }
 
@@ -711,10 +718,11 @@ __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const Fuse
   if (threadIdx.x == 0) sh.fail = 0;
   if (wave == 0 && kk > 0) {
     // With FastSelect, two runs of one loop body (the same code, so not
-    // inlined twice): run 0 selects from made-up distinct intervals while the
-    // other slices finish, which brings FastSelect's code into the
-    // instruction cache (it writes only sh.top / sh.page / sh.ntok[0], which
-    // run 1 rewrites); run 1 waits for the published intervals and selects.
+    // inlined twice): run 0 selects one member from made-up distinct
+    // intervals while the other slices finish, which brings FastSelect's
+    // code into the instruction cache; it is a dry run (no LDS reads or
+    // writes of candidate state, its verdict unused).  Run 1 waits for the
+    // published intervals and selects.
     const bool fast = kk <= kFFastK;
     bool timed_out = false;
 #pragma nounroll
@@ -784,7 +792,7 @@ __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const Fuse
         }
       }
       if (fast && !timed_out) {
-        const int verdict = FastSelectSlots(n, run == 1 ? kk : 1, mid, hi, sh);
+        const int verdict = FastSelectSlots(n, run == 1 ? kk : 1, mid, hi, sh, run == 0);
         if (run == 1 && lane == 0) sh.certified = verdict;
       }
     }
@@ -814,7 +822,7 @@ __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const Fuse
               mid[m] = sh.mid[i];
               hi[m] = sh.hi[i];
             }
-            const int verdict = FastSelectSlots(n, kk, mid, hi, sh);
+            const int verdict = FastSelectSlots(n, kk, mid, hi, sh, false);
             if (lane == 0) sh.certified = verdict;
           }
           __syncthreads();
@@ -887,13 +895,23 @@ __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const Fuse
       ParallelRanks(sh, n);
       const int i = threadIdx.x;
       if (i < n && sh.rank[i] < kk) {
+        sh.top[sh.rank[i]] = i;
         sh.page[sh.rank[i]] = sh.cpage[i];
         sh.ntok[sh.rank[i]] = sh.cntok[i];
       }
       __syncthreads();
     }
     if (writer && static_cast<int>(threadIdx.x) < kk) {
-      a.selected[static_cast<size_t>(r) * a.sel_stride + threadIdx.x] = sh.page[threadIdx.x];
+      // Every rank below kk holds the page of one of the request's
+      // candidates (sh.top its index, sh.cpage its id); a slot that does not
+      // is reported and written as -1 (the attention never loads through
+      // it: sh.page starts at -1 and sh.ntok at 0 in every launch).
+      const int t = threadIdx.x;
+      const int i = sh.top[t];
+      const int pg = sh.page[t];
+      const bool ok = i >= 0 && i < n && sh.cpage[i] == pg;
+      if (!ok) ReportFailure(a.fail, kFailSelect);
+      a.selected[static_cast<size_t>(r) * a.sel_stride + t] = ok ? pg : -1;
     }
   }
   if (writer && threadIdx.x == 0) a.counts[r] = kk;
@@ -1046,6 +1064,15 @@ __global__ __launch_bounds__(kFThreads) void FusedStepKernel(PoolView pool, Fuse
   }
   if (a.stamps != nullptr && threadIdx.x == 0) {
     for (int i = 0; i < kStampsPerGroup; ++i) sh.stamp[i] = 0;
+  }
+  if (threadIdx.x < kFMaxK) {
+    // No member slot keeps a previous workgroup's LDS: an unwritten slot
+    // reads as no page with no tokens.  Slots below 64 are set by wave 0,
+    // which alone writes them before the selection's first barrier; the
+    // others are written only after that barrier.
+    sh.top[threadIdx.x] = -1;
+    sh.page[threadIdx.x] = -1;
+    sh.ntok[threadIdx.x] = 0;
   }
   StampAt(a, sh, kStart);
   const int groups = pool.num_heads / a.heads_per_group;

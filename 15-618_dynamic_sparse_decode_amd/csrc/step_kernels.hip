@@ -316,8 +316,8 @@ __device__ void RankSortDesc(const uint64_t* keys, const int* idx, int count,
 }
 
 __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
-    float* __restrict__ mid, float* __restrict__ lo,
-    float* __restrict__ hi, const float* __restrict__ queries,
+    const float* __restrict__ mid, const float* __restrict__ lo,
+    const float* __restrict__ hi, const float* __restrict__ queries,
     const float* __restrict__ summaries, const int* __restrict__ token_counts, int capacity,
     const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int total,
     int max_candidates, int E, float scale, int top_k, int* __restrict__ selected,
@@ -459,12 +459,12 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
         },
         [&](int f, float m, float l, float h) {
           const int c = flagged[f];
+          // LDS only: the global intervals stay the score kernel's
+          // first-pass ones, which a later select over the same buffers
+          // (a stage replay) needs for FirstPassBound's precondition.
           keys[c] = SelectKey(m, cand[c]);
           s_lo[c] = l;
           s_hi[c] = h;
-          mid[begin + c] = m;
-          lo[begin + c] = l;
-          hi[begin + c] = h;
         },
         queries + static_cast<size_t>(r) * E, E, scale, reinterpret_cast<double*>(tile));
     if (threadIdx.x == 0) {
@@ -513,8 +513,8 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
 constexpr int kRankMax = 256;
 
 __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
-    float* __restrict__ mid, float* __restrict__ lo,
-    float* __restrict__ hi, const float* __restrict__ queries,
+    const float* __restrict__ mid, const float* __restrict__ lo,
+    const float* __restrict__ hi, const float* __restrict__ queries,
     const float* __restrict__ summaries, const int* __restrict__ token_counts, int capacity,
     const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int total,
     int max_candidates, int E, float scale, int top_k, int* __restrict__ selected,
@@ -630,12 +630,10 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
         },
         [&](int f, float m, float l, float h) {
           const int c = s_flag[f];
+          // LDS only (see SelectCertifiedKernel).
           s_key[c] = SelectKey(m, cand[c]);
           s_lo[c] = l;
           s_hi[c] = h;
-          mid[begin + c] = m;
-          lo[begin + c] = l;
-          hi[begin + c] = h;
         },
         queries + static_cast<size_t>(r) * E, E, scale, reinterpret_cast<double*>(tile));
     if (i == 0) s_nflag = 0;
@@ -1039,7 +1037,8 @@ void LaunchScoreBounds(const PoolView& pool, const float* d_queries,
   DSD_HIP_CHECK(hipGetLastError());
 }
 
-void LaunchSelectCertified(const PoolView& pool, float* d_mid, float* d_lo, float* d_hi,
+void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float* d_lo,
+                           const float* d_hi,
                            const float* d_queries,
                            const int* d_cand_offsets, const int* d_cand_ids, int batch,
                            int total_candidates, int max_candidates, float scale, int top_k,

@@ -12,9 +12,10 @@ HBM; the timed region is K steps on one HIP stream bracketed by HIP events.
     python bench.py --sweep        dense crossover and context-length sweep
 
 Prints one JSON line (the driver contract).  `roofline` is the dominant
-kernel (the single-launch step where the step uses it) against 8 TB/s, its
-average duration measured by HIP events around K back-to-back launches on
-the same stream; `traffic` is that kernel's HBM bytes per launch from two
+kernel (the single-launch step where the step uses it) against 8 TB/s; its
+duration is the timed step's when the step is that one launch (HIP events
+around the K timed steps on the launch stream), else the attention stage's
+over K back-to-back launches; `traffic` is that kernel's HBM bytes per launch from two
 rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) run as child processes of
 this bench, scaled by what the counters read for a plain copy of known size.
 `roofline_cold` is the same kernel with the steps rotating over disjoint
@@ -246,10 +247,31 @@ def main() -> int:
 
     # Per-kernel average durations: K back-to-back launches of one kernel on
     # the same stream.  Stages 0-2 are the three-kernel step (score, select,
-    # attention); stage 3 is the single-launch fused step.
+    # attention); stage 3 is the single-launch fused step.  Every replay block
+    # ends with the context's device status (a failure any replay recorded
+    # raises here), and the ids / outputs it leaves must be the timed step's.
+    sel_ref = w.sel.cpu().numpy().copy()
+    cnt_ref = w.counts.cpu().numpy().copy()
+    out_ref = w.out.cpu().numpy().copy()
+
+    def check_replay(stage):
+        if stage in (1, 3):
+            assert np.array_equal(w.counts.cpu().numpy(), cnt_ref), f"stage {stage} counts"
+            sel_now = w.sel.cpu().numpy()
+            for r in range(B):
+                c = int(cnt_ref[r])
+                assert np.array_equal(sel_now[r, :c], sel_ref[r, :c]), \
+                    f"stage {stage} replays: request {r} ids {sel_now[r, :c]} != {sel_ref[r, :c]}"
+        if stage in (2, 3):
+            d = float(np.max(np.abs(w.out.cpu().numpy() - out_ref)))
+            assert d <= 1e-4, f"stage {stage} replays: outputs differ by {d}"
+
     def replay_ms(stage):
         w.ctx.replay_stage(stage, sptr)
-        return timed(torch, stream, lambda i: w.ctx.replay_stage(stage, sptr), args.steps)
+        ms = timed(torch, stream, lambda i: w.ctx.replay_stage(stage, sptr), args.steps)
+        w.ctx.device_status()
+        check_replay(stage)
+        return ms
 
     stage_ms = [replay_ms(stage) for stage in range(3)]
     fused_ms = replay_ms(3) if launch["fused"] else None
@@ -258,9 +280,9 @@ def main() -> int:
     if fused_ms is not None:
         log(f"fused single-launch step kernel: {fused_ms * 1e3:.1f} us")
 
-    # Algorithmic bytes per launch (fp32).
-    sel_h = w.sel.cpu().numpy()
-    cnt_h = w.counts.cpu().numpy()
+    # Algorithmic bytes per launch (fp32), over the timed step's selection.
+    sel_h = sel_ref
+    cnt_h = cnt_ref
     sel_tokens = int(sum(int(batch.token_counts[sel_h[r, j]])
                          for r in range(B) for j in range(int(cnt_h[r]))))
     P = batch.total_candidates
@@ -341,7 +363,9 @@ def main() -> int:
                                 "GBps": step_bytes / (fused_ms * 1e-3) / 1e9}
         roof_kernel = ("FusedStepKernel: page scoring + certified top-k + fused gather/"
                        "attention in one launch")
-        roof_name, roof_bytes, roof_ms = "FusedStepKernel", step_bytes, fused_ms
+        # The step is this one launch: its duration is the timed step's
+        # (events around the K timed steps, launch gaps included).
+        roof_name, roof_bytes, roof_ms = "FusedStepKernel", step_bytes, ms_per_step
         cold_ms = cold_step_ms
     else:
         roof_kernel = "AttentionFastKernel<128,16,8,4> (fused gather + online softmax)"
@@ -385,7 +409,12 @@ def main() -> int:
                      "unit": "GB/s", "frac": roof_gbps / HBM_PEAK_GBPS,
                      "traffic": traffic["bytes"], "traffic_source": traffic["source"],
                      "kernel": roof_kernel, "bytes_per_launch": roof_bytes,
-                     "us_per_launch": roof_ms * 1e3},
+                     "us_per_launch": roof_ms * 1e3,
+                     "duration_source": ("the timed steps (one launch per step; HIP events "
+                                         "around the K steps on the launch stream)"
+                                         if fused_ms is not None else
+                                         "the attention stage replayed back to back "
+                                         "(HIP events on the launch stream)")},
         # The same kernel with every launch on a copy of the batch last
         # touched `copies` launches earlier: its bytes come from HBM, not the
         # MALL that holds a repeated 86 MB step.

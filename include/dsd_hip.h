@@ -311,7 +311,10 @@ int dsd_sparse_step_stamps(const dsd_sparse_ctx* ctx, int* grid, int* per_group,
  * and not yet reported -- e.g. from dsd_sparse_run_batch_device, which
  * cannot report it itself -- and clears it: DSD_ERR_INVALID_ARGUMENT for a
  * candidate list that does not fit the step's sizes, DSD_ERR_OUT_OF_RANGE
- * for a page id outside the pool, DSD_ERR_RUNTIME for a timed-out wait.
+ * for a page id outside the pool, DSD_ERR_RUNTIME for a timed-out wait or
+ * for a selection slot that did not hold one of the request's candidates
+ * (an internal invariant the step checks before it writes each id: such a
+ * slot is written as -1 and never attended).
  * Host-buffer steps report their own failures when they return.  No
  * reference counterpart (the reference's RunBatch checks on the host,
  * src/cuda/sparse_batched_attention.cu:600-608). */
@@ -344,7 +347,8 @@ int dsd_sparse_set_wait_limit(dsd_sparse_ctx* ctx, unsigned spin_limit, int neve
  * Arguments as dsd_sparse_run_batch_device, plus the pool and top_k of the
  * context it replaces; selection is certified (bit-exact with sparse_cpu).
  * d_fail (may be NULL): memory the device writes (epoch << 32) | code to
- * when a request is skipped (codes as dsd_sparse_device_status's 1..3);
+ * when a request is skipped (1 timed-out wait, 2 sizes, 3 page id outside
+ * the pool, 4 selection slot not a candidate: as dsd_sparse_device_status);
  * the caller clears it before the call and reads it after.
  * Under graph capture the step's epoch is a device counter kept in the same
  * static array, as for dsd_sparse_run_batch_device. */

@@ -89,6 +89,40 @@ def test_static_entry_equals_the_context_entry(gpu, lengths, k, fused):
         assert second["out_st"].shape[0] == n
 
 
+def test_static_entry_allocates_nothing(gpu):
+    """After a first call on the device (which looks up the scratch's
+    address and loads the kernels), further calls -- the fused step and the
+    three-kernel step, ids kept in the scratch -- leave the device's free
+    memory unchanged: no hipMalloc, no hipFree, no allocating library call."""
+    import torch
+    batch = gpu.SyntheticBatch(H, D, PS, [300, 517, 600 * PS, 90], seed=5)
+    with gpu.DevicePagePool(H, D, PS, batch.capacity) as pool:
+        batch.upload(pool)
+        B = batch.batch
+        cases = []
+        for n in (2, B):  # two requests: fused; all four (> 512 candidates): three kernels
+            queries, offs, ids = sub_batch(batch, n)
+            cases.append((n, int(offs[-1]), int(np.max(np.diff(offs))), device(queries),
+                          device(offs), device(ids), torch.zeros((n, E), device="cuda:0")))
+        fail = torch.zeros(1, dtype=torch.int64, device="cuda:0")
+        stream = torch.cuda.current_stream().cuda_stream
+
+        def calls():
+            for n, total, max_n, q, o, i, out in cases:
+                gpu.sparse_run_batch_device_static(pool, 8, n, total, max_n, q.data_ptr(),
+                                                   o.data_ptr(), i.data_ptr(), out.data_ptr(),
+                                                   d_fail=fail.data_ptr(), stream=stream)
+            torch.cuda.synchronize()
+
+        calls()
+        free_before = torch.cuda.mem_get_info()[0]
+        for _ in range(3):
+            calls()
+        free_after = torch.cuda.mem_get_info()[0]
+        assert int(fail.item()) == 0
+        assert free_after == free_before, (free_before, free_after)
+
+
 def test_static_entry_rejects_sizes_beyond_its_scratch(gpu):
     batch = gpu.SyntheticBatch(H, D, PS, [64], seed=1)
     with gpu.DevicePagePool(H, D, PS, batch.capacity) as pool:
