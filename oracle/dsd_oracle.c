@@ -39,7 +39,10 @@ void oracle_page_summary(const float* keys, int token_count, int elements,
   }
 }
 
-/* src/paged_kv_cache.cpp:231-238 */
+/* src/paged_kv_cache.cpp:231-238 (AppendToken; AppendTokenMetadataOnly
+ * :299-306 is the same loop).  Pinned bit for bit against the reference's own
+ * PagedKvCache compiled in oracle/_ref (tests/test_oracle.py,
+ * test_append_summary_matches_compiled_reference). */
 void oracle_append_summary(float* summary, const float* key, int old_count,
                            int elements) {
   const float old_c = (float)old_count;

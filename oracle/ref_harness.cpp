@@ -6,7 +6,9 @@
 // product's synthetic-data generator) against the reference's own code:
 // BuildSyntheticBatch (src/synthetic_data.cpp:23-68), the sparse_cpu step
 // (src/decode_pipeline.cpp:13-46), dense_cpu (src/reference_kernels.cpp:196)
-// and BuildSyntheticContinuousWorkload (src/continuous_batching.cpp:336-381).
+// BuildSyntheticContinuousWorkload (src/continuous_batching.cpp:336-381)
+// and the decode-token running mean (PagedKvCache::AppendToken /
+// AppendTokenMetadataOnly, src/paged_kv_cache.cpp:182-306).
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -14,6 +16,7 @@
 #include "dsd/config.h"
 #include "dsd/continuous_batching.h"
 #include "dsd/decode_pipeline.h"
+#include "dsd/paged_kv_cache.h"
 #include "dsd/reference_kernels.h"
 #include "dsd/synthetic_data.h"
 
@@ -115,6 +118,37 @@ void ref_batch_dense_cpu(void* handle, float* outputs) {
     std::memcpy(outputs + r * static_cast<std::size_t>(ept), out.output.data(),
                 sizeof(float) * static_cast<std::size_t>(ept));
   }
+}
+
+// Decode-token appends through the reference's own PagedKvCache
+// (src/paged_kv_cache.cpp:182-242 AppendToken, :244-306
+// AppendTokenMetadataOnly): `tokens` rows of keys (and values) appended to
+// request 0 in order, a fresh page forced where force_new[t] != 0; the
+// cache's summary row of every page the request holds is copied out in list
+// order (n_pages rows of heads * head_dim floats, at most max_pages), with
+// each page's token count.  metadata_only selects AppendTokenMetadataOnly
+// (values unused).  Returns the page count.
+int ref_append_tokens(int heads, int head_dim, int page_size, int capacity, int tokens,
+                      const float* keys, const float* values, const unsigned char* force_new,
+                      int metadata_only, int max_pages, float* summaries, int* token_counts) {
+  const auto config = MakeConfig(heads, head_dim, page_size, 8);
+  dsd::PagedKvCache cache(config, capacity, metadata_only == 0);
+  const std::size_t ept = static_cast<std::size_t>(heads) * head_dim;
+  std::vector<int> pages;
+  for (int t = 0; t < tokens; ++t) {
+    const bool fresh = force_new != nullptr && force_new[t] != 0;
+    const auto res = metadata_only != 0
+                         ? cache.AppendTokenMetadataOnly(0, keys + t * ept, fresh)
+                         : cache.AppendToken(0, keys + t * ept, values + t * ept, fresh);
+    if (res.allocated_new_page) pages.push_back(res.page_id);
+  }
+  const int n = static_cast<int>(pages.size());
+  for (int j = 0; j < n && j < max_pages; ++j) {
+    const float* s = cache.PageSummaryPool().data() + static_cast<std::size_t>(pages[j]) * ept;
+    std::memcpy(summaries + j * ept, s, sizeof(float) * ept);
+    token_counts[j] = cache.Pages()[static_cast<std::size_t>(pages[j])].token_count;
+  }
+  return n;
 }
 
 // Continuous workload (src/continuous_batching.cpp:336-381).  Returns the

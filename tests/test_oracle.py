@@ -132,6 +132,53 @@ def test_oracle_matches_compiled_reference(spec):
     assert np.array_equal(dense.reshape(-1).view(np.uint32), c["ref_dense_out"].view(np.uint32))
 
 
+@pytest.mark.skipif(not REF.exists(), reason="oracle/_ref not built (no reference tree)")
+@pytest.mark.parametrize("metadata_only", [0, 1])
+def test_append_summary_matches_compiled_reference(metadata_only):
+    # oracle_append_summary against the reference's own running mean
+    # (PagedKvCache::AppendToken / AppendTokenMetadataOnly,
+    # src/paged_kv_cache.cpp:231-238, 299-306): 29 decode tokens appended to
+    # one request, fresh pages forced at two places, the summary of every page
+    # it holds compared bit for bit.  A reciprocal multiply in place of the
+    # division (a plausible slip) must not reproduce the reference.
+    ref = ctypes.CDLL(str(REF))
+    H, D, ps, cap, T = 2, 16, 5, 64, 29
+    E = H * D
+    rng = np.random.default_rng(17 + metadata_only)
+    keys = rng.standard_normal((T, E)).astype(np.float32)
+    keys[::7] *= np.float32(1e3)
+    keys[3::11] *= np.float32(1e-3)
+    values = rng.standard_normal((T, E)).astype(np.float32)
+    force = np.zeros(T, np.uint8)
+    force[[9, 17]] = 1
+    summ = np.zeros((cap, E), np.float32)
+    counts = np.zeros(cap, np.int32)
+    fp = ctypes.POINTER(ctypes.c_float)
+    ip = ctypes.POINTER(ctypes.c_int)
+    ref.ref_append_tokens.restype = ctypes.c_int
+    n = ref.ref_append_tokens(H, D, ps, cap, T, keys.ctypes.data_as(fp), values.ctypes.data_as(fp),
+                              force.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)),
+                              metadata_only, cap, summ.ctypes.data_as(fp), counts.ctypes.data_as(ip))
+    # the same appends through the oracle (and through the slip)
+    pages, slip = [], []
+    for t in range(T):
+        if force[t] or not pages or pages[-1][1] >= ps:
+            pages.append([np.zeros(E, np.float32), 0])
+            slip.append(np.zeros(E, np.float32))
+        s, c = pages[-1]
+        pages[-1][0] = orc.append_summary(s, keys[t], c)
+        old, new = np.float32(c), np.float32(c + 1)
+        slip[-1] = ((slip[-1] * old).astype(np.float32) + keys[t]).astype(np.float32) * \
+            (np.float32(1.0) / new)
+        pages[-1][1] = c + 1
+    assert n == len(pages)
+    assert counts[:n].tolist() == [c for _, c in pages]
+    for j in range(n):
+        assert np.array_equal(summ[j].view(np.uint32), pages[j][0].view(np.uint32)), j
+    assert any(not np.array_equal(summ[j].view(np.uint32), slip[j].astype(np.float32).view(np.uint32))
+               for j in range(n))
+
+
 # ---- closed forms and invariants -------------------------------------------
 def test_summary_closed_form_arithmetic_sequence():
     # test_reference.cpp:252-307 pattern: keys 1..(4*8); the per-element mean of
