@@ -70,9 +70,39 @@ std::uint32_t StepSeed(int request_id, int decode_step, int stream) {
   return x;
 }
 
+// The payload distribution of the synthetic serving workload: the
+// reference's U(-1, 1) (src/continuous_batching.cpp:35-42), or N(0, 1) when
+// the environment sets DSD_PAYLOAD_DIST=normal (BASELINE config 5 states
+// N(0, 1) decode K/V; the reference has no such mode).  Read once.
+bool NormalPayloads() {
+  static const bool normal = [] {
+    const char* e = std::getenv("DSD_PAYLOAD_DIST");
+    return e != nullptr && std::strcmp(e, "normal") == 0;
+  }();
+  return normal;
+}
+
+// N(0, 1) floats by the Box-Muller transform (Box and Muller, Ann. Math.
+// Statist. 29(2), 1958) on consecutive pairs of 32-bit draws a, b:
+// u1 = (a + 1/2) 2^-32 in (0, 1), u2 = b 2^-32, r = sqrt(-2 ln u1),
+// z0 = fl(r cos(2 pi u2)), z1 = fl(r sin(2 pi u2)), in double with libm; an
+// odd count ends with a pair's z0.
+std::vector<float> Normal(int count, std::mt19937& rng) {
+  std::vector<float> v(static_cast<std::size_t>(count));
+  for (int i = 0; i < count; i += 2) {
+    const double u1 = (static_cast<double>(rng()) + 0.5) * 0x1p-32;
+    const double u2 = static_cast<double>(rng()) * 0x1p-32;
+    const double r = std::sqrt(-2.0 * std::log(u1));
+    const double t = 6.283185307179586476925 * u2;
+    v[static_cast<std::size_t>(i)] = static_cast<float>(r * std::cos(t));
+    if (i + 1 < count) v[static_cast<std::size_t>(i) + 1] = static_cast<float>(r * std::sin(t));
+  }
+  return v;
+}
+
 std::vector<float> TokenVector(int count, int request_id, int decode_step, int stream) {
   std::mt19937 rng(StepSeed(request_id, decode_step, stream));
-  return Uniform(count, rng);
+  return NormalPayloads() ? Normal(count, rng) : Uniform(count, rng);
 }
 
 int CapacityFor(const ModelConfig& c, const std::vector<ContinuousRequestSpec>& specs) {
@@ -765,6 +795,10 @@ void FinishStats(ContinuousBatchStats* stats, Clock::time_point wall_start,
 
 }  // namespace
 
+std::vector<float> ContinuousTokenVector(int count, int request_id, int decode_step, int stream) {
+  return TokenVector(count, request_id, decode_step, stream);
+}
+
 void SetContinuousStepObserver(ContinuousStepObserver observer, int every) {
   g_observer = std::move(observer);
   g_observe_every = g_observer ? every : 0;
@@ -791,10 +825,29 @@ std::vector<ContinuousRequestSpec> BuildSyntheticContinuousWorkload(
     s.arrival_step = arrival(rng);
     s.prompt_tokens = prompt(rng);
     s.decode_steps = decode(rng);
-    s.prompt_keys = Uniform(s.prompt_tokens * E, rng);
-    s.prompt_values = Uniform(s.prompt_tokens * E, rng);
-    s.initial_query = Uniform(E, rng);
+    if (NormalPayloads()) {
+      // The reference stream advances past the payload's draws (one per
+      // float) as in the U(-1, 1) mode, so arrivals and lengths stay the
+      // reference's; the N(0, 1) payloads are drawn below.
+      rng.discard(2ull * static_cast<unsigned long long>(s.prompt_tokens) * E + E);
+    } else {
+      s.prompt_keys = Uniform(s.prompt_tokens * E, rng);
+      s.prompt_values = Uniform(s.prompt_tokens * E, rng);
+      s.initial_query = Uniform(E, rng);
+    }
     specs.push_back(std::move(s));
+  }
+  if (NormalPayloads()) {
+    // Request r's prompt keys, values and initial query, in that order, from
+    // its own engine std::mt19937(StepSeed(r, seed, 3)) (stream 3: the
+    // decode tokens use 0-2), so the host workers draw them in parallel.
+    dsd_host::Workers::Get().ParallelFor(static_cast<int>(specs.size()), [&](int i) {
+      ContinuousRequestSpec& s = specs[static_cast<std::size_t>(i)];
+      std::mt19937 prng(StepSeed(s.request_id, seed, 3));
+      s.prompt_keys = Normal(s.prompt_tokens * E, prng);
+      s.prompt_values = Normal(s.prompt_tokens * E, prng);
+      s.initial_query = Normal(E, prng);
+    });
   }
   std::sort(specs.begin(), specs.end(),
             [](const ContinuousRequestSpec& a, const ContinuousRequestSpec& b) {

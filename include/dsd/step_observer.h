@@ -38,4 +38,11 @@ using ContinuousStepObserver = std::function<void(const ObservedDecodeStep&)>;
 // loop starts.
 void SetContinuousStepObserver(ContinuousStepObserver observer, int every);
 
+// The decode payload the serving loop generates for (request, decode step,
+// stream): stream 0 = the query after that step, 1 = the appended key, 2 =
+// the appended value.  The reference's DeterministicTokenVector
+// (src/continuous_batching.cpp:53-59), U(-1, 1) on std::mt19937(MixSeed);
+// N(0, 1) by Box-Muller on the same engine when DSD_PAYLOAD_DIST=normal.
+std::vector<float> ContinuousTokenVector(int count, int request_id, int decode_step, int stream);
+
 }  // namespace dsd

@@ -353,6 +353,41 @@ static float oracle_uniform_pm1(oracle_mt* g) {
   return u * 2.0f + -1.0f;
 }
 
+/* N(0, 1) floats by the Box-Muller transform on consecutive draw pairs
+ * (a, b): u1 = (a + 1/2) 2^-32, u2 = b 2^-32, r = sqrt(-2 ln u1),
+ * z0 = (float)(r cos(2 pi u2)), z1 = (float)(r sin(2 pi u2)), in double; an
+ * odd count ends with a pair's z0.  The serving loop's N(0, 1) payload mode
+ * (DSD_PAYLOAD_DIST=normal; the reference has no such mode, so this is the
+ * restatement the loop's generator is checked against). */
+static void oracle_normals(oracle_mt* g, int count, float* out) {
+  int i;
+  for (i = 0; i < count; i += 2) {
+    const double u1 = ((double)oracle_mt_draw(g) + 0.5) * 0x1p-32;
+    const double u2 = (double)oracle_mt_draw(g) * 0x1p-32;
+    const double r = sqrt(-2.0 * log(u1));
+    const double t = 6.283185307179586476925 * u2;
+    out[i] = (float)(r * cos(t));
+    if (i + 1 < count) out[i + 1] = (float)(r * sin(t));
+  }
+}
+
+void oracle_token_vector_normal(int count, int request_id, int decode_step, int stream,
+                                float* out) {
+  oracle_mt g;
+  oracle_mt_seed(&g, oracle_mix_seed(request_id, decode_step, stream));
+  oracle_normals(&g, count, out);
+}
+
+void oracle_prompt_normal(int seed, int request_id, int prompt_tokens, int elements,
+                          float* keys, float* values, float* query) {
+  oracle_mt g;
+  const int n = prompt_tokens * elements;
+  oracle_mt_seed(&g, oracle_mix_seed(request_id, seed, 3));
+  oracle_normals(&g, n, keys);
+  oracle_normals(&g, n, values);
+  oracle_normals(&g, elements, query);
+}
+
 /* DeterministicTokenVector (src/continuous_batching.cpp:53-59). */
 void oracle_token_vector(int count, int request_id, int decode_step, int stream,
                          float* out) {

@@ -116,6 +116,18 @@ uint32_t oracle_mix_seed(int request_id, int decode_step, int stream);
 void oracle_token_vector(int count, int request_id, int decode_step, int stream,
                          float* out);
 
+/* The serving loop's N(0, 1) payload mode (DSD_PAYLOAD_DIST=normal; no
+ * reference counterpart): Box-Muller on pairs of std::mt19937 draws
+ * (u1 = (a + 1/2) 2^-32, u2 = b 2^-32, r = sqrt(-2 ln u1), r cos / r sin of
+ * 2 pi u2, in double).  Decode tokens: from mt19937(MixSeed(request_id,
+ * decode_step, stream)), as oracle_token_vector.  Prompt payloads of request
+ * r: keys (prompt_tokens * elements), values, then the initial query, from
+ * one mt19937(MixSeed(r, seed, 3)). */
+void oracle_token_vector_normal(int count, int request_id, int decode_step, int stream,
+                                float* out);
+void oracle_prompt_normal(int seed, int request_id, int prompt_tokens, int elements,
+                          float* keys, float* values, float* query);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,6 +17,10 @@
 //     (oracle_append_summary, src/paged_kv_cache.cpp:299-306);
 //   * the query: the initial query at decode step 0, else
 //     DeterministicTokenVector(E, id, decode_step, 0).
+// With DSD_PAYLOAD_DIST=normal (the N(0, 1) payload mode) the prompts and
+// decode tokens are the N(0, 1) generator's (oracle_prompt_normal /
+// oracle_token_vector_normal restate it; the prompts are checked against
+// that restatement on the CPU).
 // Then the oracle's sparse_cpu rows (score, top-k with the reference's
 // tie-break on the real page ids, gather + attention) give the expected
 // selection, which must equal the device's id for id, and the expected
@@ -32,6 +36,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <map>
+#include <string>
 #include <vector>
 
 #include "dsd/continuous_batching.h"
@@ -44,6 +49,17 @@ struct Args {
   int num_requests, max_active, window, min_prompt, max_prompt, min_decode, max_decode, seed;
   int heads, head_dim, page_size, top_k, every, precompute;
 };
+
+// The decode payload generator of the mode the loop runs in: the reference's
+// U(-1, 1), or N(0, 1) when DSD_PAYLOAD_DIST=normal (oracle restatements).
+void token_vector(int count, int request_id, int decode_step, int stream, float* out) {
+  const char* e = std::getenv("DSD_PAYLOAD_DIST");
+  if (e != nullptr && std::string(e) == "normal") {
+    oracle_token_vector_normal(count, request_id, decode_step, stream, out);
+  } else {
+    oracle_token_vector(count, request_id, decode_step, stream, out);
+  }
+}
 
 int Check(const Args& a, const std::vector<dsd::ContinuousRequestSpec>& specs,
           const dsd::ObservedDecodeStep& s, double* worst, long* requests) {
@@ -96,8 +112,8 @@ int Check(const Args& a, const std::vector<dsd::ContinuousRequestSpec>& specs,
       const int off = i % ps;
       float* k = keys.data() + (static_cast<size_t>(j) * ps + off) * E;
       float* v = values.data() + (static_cast<size_t>(j) * ps + off) * E;
-      oracle_token_vector(E, rid, i, 1, k);
-      oracle_token_vector(E, rid, i, 2, v);
+      token_vector(E, rid, i, 1, k);
+      token_vector(E, rid, i, 2, v);
       oracle_append_summary(summ.data() + static_cast<size_t>(j) * E, k, off, E);
       counts[j] = off + 1;
     }
@@ -105,7 +121,7 @@ int Check(const Args& a, const std::vector<dsd::ContinuousRequestSpec>& specs,
     if (d == 0) {
       q = sp.initial_query;
     } else {
-      oracle_token_vector(E, rid, d, 0, q.data());
+      token_vector(E, rid, d, 0, q.data());
     }
     const float* got_q = s.queries.data() + static_cast<size_t>(b) * E;
     if (!std::equal(q.begin(), q.end(), got_q)) {

@@ -107,3 +107,64 @@ def our_workload(*args):
 ])
 def test_continuous_workload_equals_the_references(args):
     assert our_workload(*args) == ref_workload(*args)
+
+
+# ---- the N(0, 1) payload mode (DSD_PAYLOAD_DIST=normal) ------------------------
+# BASELINE config 5 states N(0, 1) K/V; the reference's generator is
+# U(-1, 1) and stays the default.  In the N(0, 1) mode the workload's
+# arrivals, prompt lengths and decode counts must still be the reference's
+# (the reference stream advances past each payload as before), and every
+# payload must equal the oracle's Box-Muller restatement
+# (oracle_prompt_normal, oracle_token_vector_normal).
+
+def fnv1a(a):
+    h = 1469598103934665603
+    for byte in np.ascontiguousarray(a, np.float32).tobytes():
+        h = ((h ^ byte) * 1099511628211) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def normal_workload(*args, tokens=False):
+    import os
+    subprocess.run(["make", "-s", "-C", str(NATIVE), "build/workload_dump"], check=True)
+    env = dict(os.environ, DSD_PAYLOAD_DIST="normal")
+    cmd = [str(NATIVE / "build" / "workload_dump"), *map(str, args)] + (["tokens"] if tokens else [])
+    out = subprocess.run(cmd, capture_output=True, text=True, check=True, timeout=600,
+                         env=env).stdout
+    rows = [line.split() for line in out.strip().splitlines()]
+    return ([tuple(int(x) for x in r) for r in rows if r[0] != "T"],
+            [tuple(int(x) for x in r[1:]) for r in rows if r[0] == "T"])
+
+
+@needs_ref
+def test_normal_payload_mode_keeps_the_reference_workload_shape():
+    args = (2, 8, 16, 8, 128, 64, 1024, 4096, 16, 64, 7)
+    got, _ = normal_workload(*args)
+    want = ref_workload(*args)
+    assert [g[:4] for g in got] == [w[:4] for w in want]
+    # the payloads themselves differ from the U(-1, 1) ones
+    assert all(g[4] != w[4] for g, w in zip(got[:8], want[:8]))
+
+
+def test_normal_payloads_equal_the_oracle_restatement():
+    H, D, seed = 2, 8, 7
+    E = H * D
+    args = (H, D, 16, 8, 16, 8, 16, 64, 1, 5, seed)
+    specs, tokens = normal_workload(*args, tokens=True)
+    lib = orc.lib()
+    for rid, arrival, prompt, decode, hk, hv, hq in specs:
+        keys = np.empty(prompt * E, np.float32)
+        values = np.empty(prompt * E, np.float32)
+        query = np.empty(E, np.float32)
+        lib.oracle_prompt_normal(seed, rid, prompt, E, orc.P(keys), orc.P(values), orc.P(query))
+        assert (fnv1a(keys), fnv1a(values), fnv1a(query)) == (hk, hv, hq), rid
+    assert len(tokens) == 5
+    for rid, step, stream, h in tokens:
+        v = np.empty(E, np.float32)
+        lib.oracle_token_vector_normal(E, rid, step, stream, orc.P(v))
+        assert fnv1a(v) == h, (rid, step, stream)
+    # the restatement is N(0, 1): moments of a long draw
+    big = np.empty(200000, np.float32)
+    lib.oracle_token_vector_normal(len(big), 3, 4, 1, orc.P(big))
+    assert abs(float(big.mean())) < 0.01 and abs(float(big.std()) - 1.0) < 0.01
+    assert abs(float(np.mean(np.abs(big))) - np.sqrt(2.0 / np.pi)) < 0.01
