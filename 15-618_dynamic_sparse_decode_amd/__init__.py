@@ -95,6 +95,16 @@ class StepTimings(ctypes.Structure):
         return {n: float(getattr(self, n)) for n, _ in self._fields_}
 
 
+class AsyncStep(ctypes.Structure):
+    _fields_ = [("ticket", ctypes.c_longlong), ("batch", ctypes.c_int), ("fused", ctypes.c_int)] + [
+        (n, ctypes.c_double) for n in (
+            "start_ms", "done_ms", "score_ms", "topk_ms", "attention_ms", "kernel_ms")]
+
+    def as_dict(self):
+        return {n: (float(getattr(self, n)) if t is ctypes.c_double else int(getattr(self, n)))
+                for n, t in self._fields_}
+
+
 # name -> (restype, argtypes)
 _SIGNATURES = {
     "dsd_last_error": (ctypes.c_char_p, []),
@@ -179,6 +189,16 @@ _SIGNATURES = {
                                             _c_int_p, ctypes.POINTER(StepTimings)]),
     "dsd_sparse_last_csr": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p, _c_int_p,
                                            ctypes.c_int]),
+    "dsd_sparse_last_selection": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p,
+                                                 _c_int_p]),
+    "dsd_sparse_run_table_async": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                                  _c_int_p, _c_float_p,
+                                                  ctypes.POINTER(ctypes.c_void_p), ctypes.c_int,
+                                                  ctypes.c_int, ctypes.POINTER(ctypes.c_longlong),
+                                                  ctypes.POINTER(StepTimings)]),
+    "dsd_sparse_async_wait": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_longlong]),
+    "dsd_sparse_async_collect": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(AsyncStep),
+                                                ctypes.c_int, _c_int_p]),
     "dsd_dense_run_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_float_p, _c_int_p,
                                            _c_int_p, _c_float_p, _c_double_p]),
     "dsd_dense_run_batch_device": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int] + [ctypes.c_void_p] * 5),
@@ -603,6 +623,66 @@ class SparseContext:
                 w += c
             result["selected"] = selected
         return result
+
+    def run_table_async(self, table, slots, queries=None, query_rows=None,
+                        output_mode=OUTPUT_OUTPUTS, timing_mode=TIMING_NONE):
+        """run_table enqueued without a wait: returns the step's ticket (0
+        for an empty batch).  queries are copied at the call; query_rows
+        (addresses in HostBlock memory) are read when the step runs and
+        must stay unchanged until async_wait(ticket) returns."""
+        sl = _i32(slots)
+        batch = len(sl)
+        q = _f32(queries).reshape(-1) if queries is not None else None
+        rows = None
+        if query_rows is not None:
+            rows = (ctypes.c_void_p * max(batch, 1))(*[int(p) for p in query_rows])
+        ticket = ctypes.c_longlong(0)
+        t = StepTimings()
+        _check(self._lib.dsd_sparse_run_table_async(
+            self.handle, table.handle, batch, _ptr(sl, ctypes.c_int),
+            _ptr(q, ctypes.c_float) if q is not None else None, rows, output_mode, timing_mode,
+            ctypes.byref(ticket), ctypes.byref(t)))
+        return int(ticket.value)
+
+    def async_wait(self, ticket: int) -> None:
+        """Blocks until every asynchronous step up to `ticket` has completed
+        (raising the failure one of them reported)."""
+        _check(self._lib.dsd_sparse_async_wait(self.handle, int(ticket)))
+
+    def async_collect(self):
+        """Waits for every enqueued asynchronous step; returns their records
+        (dicts, oldest first)."""
+        out = []
+        buf = (AsyncStep * 64)()
+        n = ctypes.c_int(0)
+        while True:
+            _check(self._lib.dsd_sparse_async_collect(self.handle, buf, 64, ctypes.byref(n)))
+            if n.value == 0:
+                return out
+            out.extend(buf[i].as_dict() for i in range(n.value))
+
+    def last_selection(self, batch):
+        """The selected ids of the last step on the context's stream, one
+        array per request (synchronous)."""
+        kk = max(1, self.top_k)
+        sel = np.zeros(max(1, batch * kk), np.int32)
+        counts = np.zeros(max(1, batch), np.int32)
+        _check(self._lib.dsd_sparse_last_selection(self.handle, batch, _ptr(sel, ctypes.c_int),
+                                                   _ptr(counts, ctypes.c_int)))
+        result, w = [], 0
+        for r in range(batch):
+            c = int(counts[r])
+            result.append(sel[w:w + c].copy())
+            w += c
+        return result
+
+    def staged_outputs(self, batch):
+        """The staging's outputs [batch][E] (where table steps leave them)."""
+        out_st = ctypes.c_void_p()
+        _check(self._lib.dsd_sparse_staging(self.handle, None, None, None, ctypes.byref(out_st)))
+        E = self.pool.elements
+        buf = (ctypes.c_float * (batch * E)).from_address(out_st.value)
+        return np.ctypeslib.as_array(buf).reshape(batch, E).copy()
 
     def last_csr(self, batch):
         """(cand_offsets, cand_ids) of the last step as its kernels read them."""

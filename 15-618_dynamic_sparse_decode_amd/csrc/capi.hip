@@ -8,11 +8,13 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <deque>
 #include <map>
 #include <memory>
 #include <mutex>
 #include <numeric>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "dsd_hip.h"
@@ -56,6 +58,27 @@ void Require(bool ok, const char* message) {
 using Clock = std::chrono::steady_clock;
 double MsSince(Clock::time_point t0) {
   return std::chrono::duration<double, std::milli>(Clock::now() - t0).count();
+}
+
+// Spins until *word >= target: a progress word the device stores with a
+// system-scope release (dsdk::ProgressMark, dsdk::LaunchStepMark).  Every
+// few thousand polls it asks `stream` for an error, so a failed launch or a
+// device fault is reported rather than spun on.
+void AwaitWord(const unsigned long long* word, unsigned long long target, hipStream_t stream) {
+  for (unsigned long it = 1;; ++it) {
+    if (__hip_atomic_load(word, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) >= target) return;
+    if (it % 4096 == 0) {
+      const hipError_t e = hipStreamQuery(stream);
+      if (e == hipSuccess) {
+        if (__hip_atomic_load(word, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) >= target) {
+          return;
+        }
+        throw std::runtime_error("the stream is idle but an awaited progress mark never came");
+      }
+      if (e != hipErrorNotReady) DSD_HIP_CHECK(e);
+      std::this_thread::yield();
+    }
+  }
 }
 
 // Grow-only device buffer.
@@ -815,6 +838,11 @@ struct dsd_table {
   PinnedBuffer<int> h_args[kArgBlocks];
   hipEvent_t args_ev[kArgBlocks] = {};
   bool args_busy[kArgBlocks] = {};
+  // A block whose reader stores a progress mark instead (the per-step
+  // append and release): the mark's sequence number, 0 when none pending.
+  unsigned long long args_seq[kArgBlocks] = {};
+  PinnedBuffer<unsigned long long> h_progress;  // the marks' word
+  unsigned long long progress_seq = 0;
   int args_next = 0;
   // Prompt staging ahead of admission (dsd_table_staging_init): device
   // buffers filled on a copy stream of their own, from a pinned ring; a
@@ -831,6 +859,7 @@ struct dsd_table {
   int ring_next = 0;
 
   ~dsd_table() {
+    if (progress_seq != 0) (void)hipStreamSynchronize(pool->stream);
     for (int b = 0; b < kArgBlocks; ++b) {
       if (args_ev[b]) {
         if (args_busy[b]) (void)hipEventSynchronize(args_ev[b]);
@@ -874,12 +903,24 @@ struct dsd_table {
       DSD_HIP_CHECK(hipEventSynchronize(args_ev[b]));
       args_busy[b] = false;
     }
+    if (args_seq[b] != 0) {
+      AwaitWord(h_progress.ptr, args_seq[b], pool->stream);
+      args_seq[b] = 0;
+    }
     h_args[b].Reserve(std::max<size_t>(n, 64), hipHostMallocCoherent);
     return b;
   }
   void Done(int b) {
     DSD_HIP_CHECK(hipEventRecord(args_ev[b], pool->stream));
     args_busy[b] = true;
+  }
+  // Done(b) by a progress mark the launch's last kernel stores (no event
+  // barrier on the stream).
+  dsdk::ProgressMark Mark(int b) {
+    h_progress.Reserve(1, hipHostMallocCoherent);
+    if (progress_seq == 0) h_progress.ptr[0] = 0;
+    args_seq[b] = ++progress_seq;
+    return dsdk::ProgressMark{h_progress.ptr, args_seq[b]};
   }
   void CheckSlot(int slot) const {
     if (slot < 0 || slot >= view.max_slots) throw std::out_of_range("table slot out of range");
@@ -953,8 +994,12 @@ int dsd_table_create(dsd_pool* pool, int max_slots, int max_pages, dsd_table** o
     t->h_npages.assign(max_slots, 0);
     t->h_tail.assign(max_slots, 0);
     t->h_free = pool->view.capacity;
+    // The argument blocks' events only tell the host that the kernels which
+    // read a block have finished: no system-scope fence (a cache writeback
+    // and invalidate that stalls the stream for microseconds).
     for (hipEvent_t& e : t->args_ev) {
-      DSD_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+      DSD_HIP_CHECK(
+          hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventDisableSystemFence));
     }
     pool->WaitPending();
     dsdk::LaunchTableReset(t->view, pool->view.capacity, pool->stream);
@@ -1192,8 +1237,7 @@ int dsd_table_append(dsd_table* table, int n, const int* slots, const unsigned c
     table->d_plan.Reserve(6 * static_cast<size_t>(m) + 1);
     table->d_order.Reserve(std::max(1, m));
     dsdk::LaunchTablePlanAppend(pool->view, table->view, args, n, m, table->d_plan.ptr,
-                                table->d_order.ptr, pool->stream);
-    table->Done(b);
+                                table->d_order.ptr, pool->stream, table->Mark(b));
     // The plan kernel is enqueued: the device pops the fresh pages, so the
     // mirror follows now (before the payload kernels).
     for (int i = 0; i < n; ++i) {
@@ -1247,8 +1291,7 @@ int dsd_table_release(dsd_table* table, int n, const int* slots, int clear) {
       std::memcpy(table->h_args[b].ptr, slots + c0, sizeof(int) * c);
       pool->CountH2D(sizeof(int) * static_cast<size_t>(c));
       dsdk::LaunchTableRelease(pool->view, table->view, table->h_args[b].ptr, c, pages,
-                               clear != 0, pool->stream);
-      table->Done(b);
+                               clear != 0, pool->stream, table->Mark(b));
       for (int i = 0; i < c; ++i) {
         table->h_npages[slots[c0 + i]] = 0;
         table->h_tail[slots[c0 + i]] = 0;
@@ -1399,6 +1442,34 @@ void EnqueueStep(const PoolView& v, const StepLaunch& L, hipStream_t s) {
   EnqueueAttentionStage(v, L, s);
 }
 
+// One in-flight asynchronous table step: the pinned words its stage-in
+// kernel reads (slot ids, query row pointers, a copied query block), its
+// progress words and, when timed, its fused-step stamps or stage events.
+// A slot is reused only after the step that last used it has completed and
+// been harvested.  The step records no event unless it is a timed
+// three-kernel step: each event's barrier idles the stream for microseconds.
+struct AsyncSlot {
+  PinnedBuffer<int> slots;
+  PinnedBuffer<const float*> rows;
+  PinnedBuffer<float> queries;
+  PinnedBuffer<unsigned long long> stamps;
+  // words[0]: the ticket, stored by the step-mark kernel after the step;
+  // words[1]: the device clock then; words[2]: the clock as the stage-in
+  // started.
+  PinnedBuffer<unsigned long long> words;
+  // k[0..3] around score / select / attention (timed three-kernel steps)
+  hipEvent_t k[4] = {};
+  bool busy = false;
+  bool timed = false;
+  bool fused = false;
+  bool new_timeline = false;  // the first step of a timeline
+  int batch = 0;
+  int stamp_grid = 0;
+  unsigned epoch = 0;
+  long long ticket = 0;
+};
+constexpr int kAsyncDepth = 4;
+
 }  // namespace
 
 struct dsd_sparse_ctx {
@@ -1439,7 +1510,25 @@ struct dsd_sparse_ctx {
 
   StepLaunch last;  // the last step's launch (replays re-enqueue its stages)
 
+  // Asynchronous table steps (dsd_sparse_run_table_async): a ring of
+  // in-flight slots, the tickets handed out and harvested, the timeline's
+  // base (the device clock as its first step started: a timeline starts
+  // whenever nothing is in flight and every record has been collected) and
+  // the harvested records, oldest first.
+  AsyncSlot async[kAsyncDepth];
+  int async_next = 0;
+  long long async_issued = 0;
+  long long async_harvested = 0;
+  unsigned long long async_base = 0;
+  std::deque<dsd_async_step> async_records;
+
   ~dsd_sparse_ctx() {
+    // (dsd_sparse_destroy has waited for the device)
+    for (AsyncSlot& a : async) {
+      for (hipEvent_t e : a.k) {
+        if (e) (void)hipEventDestroy(e);
+      }
+    }
     for (hipEvent_t& e : ev) {
       if (e) (void)hipEventDestroy(e);
     }
@@ -1520,26 +1609,28 @@ struct dsd_sparse_ctx {
   }
 
   // The single-launch step with per-workgroup clock stamps written straight
-  // into pinned host memory (timing mode).
-  void EnqueueFusedStamped(const StepLaunch& L, hipStream_t s) {
+  // into pinned host memory (timing mode); returns the stamped grid.
+  int EnqueueFusedStamped(const StepLaunch& L, hipStream_t s,
+                          PinnedBuffer<unsigned long long>* stamps) {
     dsdk::FusedArgs a = FusedStepArgs(pool->view, L);
-    stamp_grid = dsdk::FusedStepGrid(pool->view, L.batch, a.heads_per_group);
-    if (static_cast<size_t>(stamp_grid) * dsdk::FusedStepStampsPerGroup() > h_stamps.count) {
+    const int grid = dsdk::FusedStepGrid(pool->view, L.batch, a.heads_per_group);
+    if (static_cast<size_t>(grid) * dsdk::FusedStepStampsPerGroup() > stamps->count) {
       throw std::runtime_error("fused step stamps exceed their buffer");
     }
-    a.stamps = h_stamps.ptr;
+    a.stamps = stamps->ptr;
     dsdk::LaunchFusedStep(pool->view, a, s);
+    return grid;
   }
-  // Phase split of the last timed fused launch from its workgroup stamps
-  // (start, slice scored, counter ready, records read, ranked, selected,
-  // end): first start -> last slice scored -> last selection -> last end.
-  void FusedPhases(double* score_ms, double* select_ms, double* attention_ms) const {
+  // Phase split of a timed fused launch from its workgroup stamps (start,
+  // slice scored, counter ready, records read, ranked, selected, end):
+  // first start -> last slice scored -> last selection -> last end.
+  void FusedPhases(const unsigned long long* st, int grid, double* score_ms,
+                   double* select_ms, double* attention_ms) const {
     *score_ms = *select_ms = *attention_ms = 0.0;
-    if (stamp_grid <= 0 || wall_khz <= 0.0) return;
+    if (grid <= 0 || wall_khz <= 0.0) return;
     const int per = dsdk::FusedStepStampsPerGroup();
-    const unsigned long long* st = h_stamps.ptr;
     unsigned long long t0 = ~0ull, t_score = 0, t_select = 0, t_end = 0;
-    for (int g = 0; g < stamp_grid; ++g) {
+    for (int g = 0; g < grid; ++g) {
       t0 = std::min(t0, st[per * g + 0]);
       t_score = std::max(t_score, st[per * g + 1]);
       t_select = std::max(t_select, st[per * g + 5]);
@@ -1552,27 +1643,32 @@ struct dsd_sparse_ctx {
     *select_ms = static_cast<double>(t_select - t_score) / wall_khz;
     *attention_ms = static_cast<double>(t_end - t_select) / wall_khz;
   }
-  // Enqueues a step (fresh epoch); with timing, events around the stages
-  // (ev[0] .. ev[3]) and, for the fused step, the workgroup stamps.
-  void Enqueue(StepLaunch* L, hipStream_t s, bool timing) {
+  // Enqueues a step (fresh epoch); with timing, events k[0] .. k[3] around
+  // the stages (a fused launch: k[0] and k[3]) and, for the fused step, the
+  // workgroup stamps into `stamps` (their grid in *stamped).
+  void Enqueue(StepLaunch* L, hipStream_t s, bool timing, hipEvent_t* k = nullptr,
+               PinnedBuffer<unsigned long long>* stamps = nullptr, int* stamped = nullptr) {
     Fresh(L);
     const PoolView& v = pool->view;
     if (!timing) {
       EnqueueStep(v, *L, s);
       return;
     }
-    DSD_HIP_CHECK(hipEventRecord(ev[0], s));
+    if (k == nullptr) k = ev;
+    if (stamps == nullptr) stamps = &h_stamps;
+    if (stamped == nullptr) stamped = &stamp_grid;
+    DSD_HIP_CHECK(hipEventRecord(k[0], s));
     if (L->fused) {
-      EnqueueFusedStamped(*L, s);
-      DSD_HIP_CHECK(hipEventRecord(ev[3], s));
+      *stamped = EnqueueFusedStamped(*L, s, stamps);
+      DSD_HIP_CHECK(hipEventRecord(k[3], s));
       return;
     }
     EnqueueScoreStage(v, *L, s);
-    DSD_HIP_CHECK(hipEventRecord(ev[1], s));
+    DSD_HIP_CHECK(hipEventRecord(k[1], s));
     EnqueueSelectStage(v, *L, s);
-    DSD_HIP_CHECK(hipEventRecord(ev[2], s));
+    DSD_HIP_CHECK(hipEventRecord(k[2], s));
     EnqueueAttentionStage(v, *L, s);
-    DSD_HIP_CHECK(hipEventRecord(ev[3], s));
+    DSD_HIP_CHECK(hipEventRecord(k[3], s));
   }
 };
 
@@ -1602,7 +1698,11 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     // an enqueued append and before any later pool work, with no cross-
     // stream waits (each costs several microseconds of host time per step).
     ctx->stream = pool->stream;
-    for (hipEvent_t& e : ctx->ev) DSD_HIP_CHECK(hipEventCreate(&e));
+    // Timing events only (the host waits on the stream itself): no
+    // system-scope fence, which would stall the stream between the stages.
+    for (hipEvent_t& e : ctx->ev) {
+      DSD_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
+    }
     DSD_HIP_CHECK(hipEventCreateWithFlags(&ctx->ev_switch, hipEventDisableTiming));
     const size_t E = static_cast<size_t>(pool->view.elements);
     const size_t B = static_cast<size_t>(std::max(1, max_batch));
@@ -1676,6 +1776,59 @@ void* dsd_sparse_stream(dsd_sparse_ctx* ctx) {
 
 namespace {
 
+// Waits for an asynchronous step, frees its ring slot and appends its
+// record (device times from the timeline's base event).  A failure the step
+// reported is thrown here (its outputs are then zeros for the request
+// concerned), and the record is dropped.
+void HarvestAsync(dsd_sparse_ctx* ctx, AsyncSlot& a) {
+  AwaitWord(a.words.ptr, static_cast<unsigned long long>(a.ticket), ctx->stream);
+  a.busy = false;
+  ctx->async_harvested = std::max(ctx->async_harvested, a.ticket);
+  ctx->CheckFailure(a.epoch);
+  dsd_async_step r{};
+  r.ticket = a.ticket;
+  r.batch = a.batch;
+  r.fused = a.fused ? 1 : 0;
+  const unsigned long long start =
+      __hip_atomic_load(a.words.ptr + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  const unsigned long long end =
+      __hip_atomic_load(a.words.ptr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  if (a.new_timeline) ctx->async_base = start;
+  const double khz = ctx->wall_khz > 0.0 ? ctx->wall_khz : 1.0e5;
+  r.start_ms = static_cast<double>(static_cast<long long>(start - ctx->async_base)) / khz;
+  r.done_ms = static_cast<double>(static_cast<long long>(end - ctx->async_base)) / khz;
+  if (a.timed && a.fused) {
+    ctx->FusedPhases(a.stamps.ptr, a.stamp_grid, &r.score_ms, &r.topk_ms, &r.attention_ms);
+    r.kernel_ms = r.score_ms + r.topk_ms + r.attention_ms;
+  } else if (a.timed) {
+    // (the stream has passed them; the runtime reports them complete once
+    // it has seen that)
+    DSD_HIP_CHECK(hipEventSynchronize(a.k[3]));
+    float x = 0.f, y = 0.f, z = 0.f;
+    DSD_HIP_CHECK(hipEventElapsedTime(&x, a.k[0], a.k[1]));
+    DSD_HIP_CHECK(hipEventElapsedTime(&y, a.k[1], a.k[2]));
+    DSD_HIP_CHECK(hipEventElapsedTime(&z, a.k[2], a.k[3]));
+    r.score_ms = x;
+    r.topk_ms = y;
+    r.attention_ms = z;
+    r.kernel_ms = static_cast<double>(x) + y + z;
+  }
+  ctx->async_records.push_back(r);
+}
+
+// Harvests, oldest first, every in-flight asynchronous step whose ticket is
+// at most `ticket`.
+void HarvestThrough(dsd_sparse_ctx* ctx, long long ticket) {
+  for (;;) {
+    AsyncSlot* oldest = nullptr;
+    for (AsyncSlot& a : ctx->async) {
+      if (a.busy && (oldest == nullptr || a.ticket < oldest->ticket)) oldest = &a;
+    }
+    if (oldest == nullptr || oldest->ticket > ticket) return;
+    HarvestAsync(ctx, *oldest);
+  }
+}
+
 // One host-buffer step.  Inputs are copied into the context's pinned
 // staging unless `staged` (the caller wrote them there); outputs land in the
 // pinned staging and are copied to `outputs` when it is non-null.  With
@@ -1684,11 +1837,16 @@ namespace {
 // With `table`, request r's candidate list is the page list of table slot
 // slots[r] (cand_offsets / cand_ids unused): the stage-in kernel builds the
 // CSR on the device, and only the queries and the slot ids cross PCIe.
+// With `async` (table steps only), the step's pinned inputs go to that ring
+// slot instead of the context's staging, its events are recorded there, and
+// the call returns once the step is enqueued: no wait, no results (the
+// outputs stay in the staging; the slot is harvested later).
 void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
               const float* const* rows, const int* cand_offsets, const int* cand_ids,
               int output_mode, int timing_mode, float* outputs, float* scores, int* selected,
               int* selected_counts, dsd_step_timings* timings,
-              const dsd_table* table = nullptr, const int* slots = nullptr) {
+              const dsd_table* table = nullptr, const int* slots = nullptr,
+              AsyncSlot* async = nullptr) {
     Require(ctx != nullptr, "context must be non-null");
     Require(batch >= 0, "batch must be non-negative");
     Require(output_mode >= DSD_OUTPUT_NONE && output_mode <= DSD_OUTPUT_DEBUG,
@@ -1702,6 +1860,7 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
       Require(table->pool == ctx->pool, "the table belongs to another pool");
     } else {
       Require(cand_offsets != nullptr, "inputs must be non-null");
+      Require(async == nullptr, "only table steps run asynchronously");
     }
     const bool want_outputs = output_mode != DSD_OUTPUT_NONE;
     const bool debug = output_mode == DSD_OUTPUT_DEBUG;
@@ -1763,10 +1922,12 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
         Require(reinterpret_cast<uintptr_t>(rows[r]) % 16 == 0,
                 "query rows must be 16-byte aligned");
       }
+      // (An asynchronous step may not read the staging, which the next
+      // synchronous step rewrites.)
       std::vector<const float*> foreign;
       std::vector<int> foreign_at;
       for (int r = 0; r < batch; ++r) {
-        if (rows[r] != ctx->h_queries.ptr + static_cast<size_t>(r) * E) {
+        if (async != nullptr || rows[r] != ctx->h_queries.ptr + static_cast<size_t>(r) * E) {
           foreign.push_back(rows[r]);
           foreign_at.push_back(r);
         }
@@ -1779,14 +1940,28 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
       }
     }
 
-    // Host -> device through pinned staging.
+    // Host -> device through pinned staging (an asynchronous step's ring
+    // slot, or the context's staging).
     auto t0 = Clock::now();
     const size_t qn = static_cast<size_t>(batch) * E;
-    if (table != nullptr) {
-      if (rows == nullptr && queries != ctx->h_queries.ptr) {
-        std::memcpy(ctx->h_queries.ptr, queries, sizeof(float) * qn);
+    int* stage_slots = ctx->h_offsets.ptr;
+    const float** stage_rows = ctx->h_rows.ptr;
+    float* stage_queries = ctx->h_queries.ptr;
+    if (async != nullptr) {
+      async->slots.Reserve(static_cast<size_t>(ctx->max_batch) + 1, hipHostMallocCoherent);
+      async->rows.Reserve(static_cast<size_t>(ctx->max_batch) + 1, hipHostMallocCoherent);
+      stage_slots = async->slots.ptr;
+      stage_rows = async->rows.ptr;
+      if (rows == nullptr) {
+        async->queries.Reserve(static_cast<size_t>(ctx->max_batch) * E, hipHostMallocCoherent);
+        stage_queries = async->queries.ptr;
       }
-      std::memcpy(ctx->h_offsets.ptr, slots, sizeof(int) * batch);  // the slot ids
+    }
+    if (table != nullptr) {
+      if (rows == nullptr && queries != stage_queries) {
+        std::memcpy(stage_queries, queries, sizeof(float) * qn);
+      }
+      std::memcpy(stage_slots, slots, sizeof(int) * batch);  // the slot ids
     } else if (!staged) {
       if (rows == nullptr) std::memcpy(ctx->h_queries.ptr, queries, sizeof(float) * qn);
       std::memcpy(ctx->h_offsets.ptr, cand_offsets, sizeof(int) * (batch + 1));
@@ -1798,9 +1973,10 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
       // One kernel on the step's stream copies the staged inputs to the
       // device: DMA copies would each cost a copy-engine hand-off.
       dsdk::StageSegments seg;
+      if (async != nullptr) seg.start_stamp = async->words.ptr + 2;
       if (table != nullptr) {
         seg.table = table->view;
-        seg.table_slots = ctx->h_offsets.ptr;
+        seg.table_slots = stage_slots;
         seg.table_batch = batch;
         seg.csr_offsets = ctx->d_offsets.ptr;
         seg.csr_ids = ctx->d_ids.ptr;
@@ -1814,13 +1990,13 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
         seg.count = 2;
       }
       if (rows != nullptr) {
-        std::memcpy(ctx->h_rows.ptr, rows, sizeof(const float*) * batch);
-        seg.rows = ctx->h_rows.ptr;
+        std::memcpy(stage_rows, rows, sizeof(const float*) * batch);
+        seg.rows = stage_rows;
         seg.rows_dst = ctx->d_queries.ptr;
         seg.nrows = batch;
         seg.row_words = E;
       } else {
-        seg.src[seg.count] = reinterpret_cast<const uint32_t*>(ctx->h_queries.ptr);
+        seg.src[seg.count] = reinterpret_cast<const uint32_t*>(stage_queries);
         seg.dst[seg.count] = reinterpret_cast<uint32_t*>(ctx->d_queries.ptr);
         seg.words[seg.count] = static_cast<int>(qn);
         ++seg.count;
@@ -1836,6 +2012,28 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
     // The attention writes the outputs straight into the pinned staging.
     L.outputs = ctx->h_outputs.ptr;
     t0 = Clock::now();
+    if (async != nullptr) {
+      async->stamps.Reserve(std::max<size_t>(1, ctx->h_stamps.count), hipHostMallocCoherent);
+      async->stamp_grid = 0;
+      if (timing && L.fused) {
+        // Timed by its workgroup stamps alone (no events).
+        ctx->Fresh(&L);
+        async->stamp_grid = ctx->EnqueueFusedStamped(L, ctx->stream, &async->stamps);
+      } else {
+        ctx->Enqueue(&L, ctx->stream, timing, async->k, &async->stamps, &async->stamp_grid);
+      }
+      dsdk::LaunchStepMark(async->words.ptr, static_cast<unsigned long long>(async->ticket),
+                           ctx->stream);
+      ctx->last = L;
+      async->busy = true;
+      async->timed = timing;
+      async->fused = L.fused;
+      async->batch = batch;
+      async->epoch = L.epoch;
+      t.launch_ms = MsSince(t0);
+      if (timings != nullptr) *timings = t;
+      return;
+    }
     ctx->Enqueue(&L, ctx->stream, timing);
     ctx->last = L;
     t.launch_ms = MsSince(t0);
@@ -1869,7 +2067,8 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
       // One kernel: its event time, split at the workgroup clock stamps.
       float k = 0.f;
       DSD_HIP_CHECK(hipEventElapsedTime(&k, ctx->ev[0], ctx->ev[3]));
-      ctx->FusedPhases(&t.score_ms, &t.topk_ms, &t.attention_ms);
+      ctx->FusedPhases(ctx->h_stamps.ptr, ctx->stamp_grid, &t.score_ms, &t.topk_ms,
+                       &t.attention_ms);
       t.kernel_ms = k;
     } else if (timing) {
       float a = 0.f, b = 0.f, c = 0.f;
@@ -1921,6 +2120,97 @@ int dsd_sparse_run_table(dsd_sparse_ctx* ctx, dsd_table* table, int batch, const
     Require(queries == nullptr || query_rows == nullptr, "give queries or query_rows, not both");
     HostStep(ctx, batch, false, queries, query_rows, nullptr, nullptr, output_mode, timing_mode,
              outputs, nullptr, selected, selected_counts, timings, table, slots);
+  });
+}
+
+int dsd_sparse_run_table_async(dsd_sparse_ctx* ctx, dsd_table* table, int batch,
+                               const int* slots, const float* queries,
+                               const float* const* query_rows, int output_mode, int timing_mode,
+                               long long* ticket, dsd_step_timings* host_timings) {
+  return Guard([&] {
+    Require(ticket != nullptr, "ticket must be non-null");
+    *ticket = 0;
+    if (host_timings != nullptr) *host_timings = dsd_step_timings{};
+    Require(ctx != nullptr && table != nullptr, "context and table must be non-null");
+    Require(output_mode != DSD_OUTPUT_DEBUG, "the table step has no debug mode");
+    Require(batch >= 0 && batch <= ctx->max_batch,
+            "request batch exceeds sparse context capacity");
+    Require(queries == nullptr || query_rows == nullptr, "give queries or query_rows, not both");
+    if (batch == 0) return;
+    // The ring slot this step takes: its previous step must have completed.
+    AsyncSlot& a = ctx->async[ctx->async_next];
+    const auto t0 = Clock::now();
+    if (a.busy) HarvestThrough(ctx, a.ticket);
+    const double wait_ms = MsSince(t0);
+    if (a.words.ptr == nullptr) {
+      a.words.Reserve(4, hipHostMallocCoherent);
+      for (int i = 0; i < 4; ++i) a.words.ptr[i] = 0;
+      // (timing only: no system-scope fence)
+      for (hipEvent_t& e : a.k) {
+        DSD_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
+      }
+    }
+    bool in_flight = false;
+    for (const AsyncSlot& o : ctx->async) in_flight = in_flight || o.busy;
+    a.new_timeline = !in_flight && ctx->async_records.empty();
+    a.ticket = ctx->async_issued + 1;
+    dsd_step_timings t{};
+    HostStep(ctx, batch, false, queries, query_rows, nullptr, nullptr, output_mode, timing_mode,
+             nullptr, nullptr, nullptr, nullptr, &t, table, slots, &a);
+    ctx->async_issued = a.ticket;
+    ctx->async_next = (ctx->async_next + 1) % kAsyncDepth;
+    *ticket = a.ticket;
+    t.sync_ms = wait_ms;
+    if (host_timings != nullptr) *host_timings = t;
+  });
+}
+
+int dsd_sparse_async_wait(dsd_sparse_ctx* ctx, long long ticket) {
+  return Guard([&] {
+    Require(ctx != nullptr, "context must be non-null");
+    Require(ticket <= ctx->async_issued, "the ticket was not issued by this context");
+    HarvestThrough(ctx, ticket);
+  });
+}
+
+int dsd_sparse_async_collect(dsd_sparse_ctx* ctx, dsd_async_step* steps, int capacity,
+                             int* count) {
+  return Guard([&] {
+    Require(ctx != nullptr && count != nullptr, "context and count must be non-null");
+    *count = 0;
+    Require(capacity >= 0, "capacity must be non-negative");
+    Require(capacity == 0 || steps != nullptr, "steps must be non-null");
+    HarvestThrough(ctx, ctx->async_issued);
+    const int n = static_cast<int>(
+        std::min<size_t>(static_cast<size_t>(capacity), ctx->async_records.size()));
+    for (int i = 0; i < n; ++i) {
+      steps[i] = ctx->async_records.front();
+      ctx->async_records.pop_front();
+    }
+    *count = n;
+  });
+}
+
+int dsd_sparse_last_selection(dsd_sparse_ctx* ctx, int batch, int* selected,
+                              int* selected_counts) {
+  return Guard([&] {
+    Require(ctx != nullptr && selected != nullptr && selected_counts != nullptr,
+            "pointers must be non-null");
+    Require(batch >= 0 && batch <= ctx->max_batch, "batch out of range");
+    if (batch == 0) return;
+    const size_t kk = static_cast<size_t>(std::max(1, ctx->top_k));
+    DSD_HIP_CHECK(hipMemcpyAsync(ctx->h_selected.ptr, ctx->d_selected.ptr,
+                                 sizeof(int) * kk * batch, hipMemcpyDeviceToHost, ctx->stream));
+    DSD_HIP_CHECK(hipMemcpyAsync(ctx->h_counts.ptr, ctx->d_counts.ptr, sizeof(int) * batch,
+                                 hipMemcpyDeviceToHost, ctx->stream));
+    DSD_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    int w = 0;
+    for (int r = 0; r < batch; ++r) {
+      const int cnt = ctx->h_counts.ptr[r];
+      Require(cnt >= 0 && static_cast<size_t>(cnt) <= kk, "the last step's counts are malformed");
+      selected_counts[r] = cnt;
+      for (int q = 0; q < cnt; ++q) selected[w++] = ctx->h_selected.ptr[r * kk + q];
+    }
   });
 }
 

@@ -101,6 +101,21 @@ struct TableView {
   int max_pages = 0;
 };
 
+// A host-visible progress word: once the kernels of a launch have read their
+// host-side arguments, the launch's last kernel stores `seq` into *word
+// (pinned, coherent; a release at system scope).  The host polls the word
+// instead of recording an event, whose barrier idles the stream for
+// microseconds.  word == nullptr: no mark.
+struct ProgressMark {
+  unsigned long long* word = nullptr;
+  unsigned long long seq = 0;
+};
+__device__ inline void StoreProgress(const ProgressMark& m) {
+  if (m.word != nullptr) {
+    __hip_atomic_store(m.word, m.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
 // Stack = [0 .. capacity-1], every slot empty.
 void LaunchTableReset(const TableView& t, int capacity, hipStream_t stream);
 // Slot `slot` (empty) takes the n pages on top of the stack, ascending.
@@ -112,13 +127,16 @@ void LaunchTableScatter(const PoolView& pool, const TableView& t, int slot, int 
 // uploaded tokens (layout in page_table.hip) for LaunchAppendSynthetic
 // (meta = d_plan) or LaunchAppendTokens (d_order and the plan's arrays).
 // args (device-readable, e.g. pinned): slots[n], flags[n], request ids[n],
-// decode steps[n].
+// decode steps[n].  `mark` is stored once args has been read.
 void LaunchTablePlanAppend(const PoolView& pool, const TableView& t, const int* args, int n,
-                           int m, int* d_plan, int* d_order, hipStream_t stream);
+                           int m, int* d_plan, int* d_order, hipStream_t stream,
+                           ProgressMark mark = {});
 // n <= 1024 slots (device-readable) back to the stack; `clear` also clears
-// their pages' counts, live flags and summaries.
+// their pages' counts, live flags and summaries.  `mark` is stored once
+// slots has been read.
 void LaunchTableRelease(const PoolView& pool, const TableView& t, const int* slots, int n,
-                        int released_pages, bool clear, hipStream_t stream);
+                        int released_pages, bool clear, hipStream_t stream,
+                        ProgressMark mark = {});
 
 // Up to four segments of 4-byte words, each 16-byte aligned at both ends of
 // the copy: src in pinned host memory the device reads directly, dst in
@@ -142,8 +160,15 @@ struct StageSegments {
   int table_batch = 0;
   int* csr_offsets = nullptr;
   int* csr_ids = nullptr;
+  // When non-null: the device clock (wall_clock64) as workgroup 0 starts,
+  // stored here (pinned) -- an asynchronous step's start stamp.
+  unsigned long long* start_stamp = nullptr;
 };
 void LaunchStageIn(const StageSegments& s, hipStream_t stream);
+// An asynchronous step's completion mark, after every earlier kernel on the
+// stream: words[1] = the device clock, then words[0] = ticket (a release at
+// system scope; words pinned and coherent).
+void LaunchStepMark(unsigned long long* words, unsigned long long ticket, hipStream_t stream);
 
 // ---- decode-step kernels (step_kernels.hip) --------------------------------
 

@@ -637,6 +637,79 @@ class PromptPrefetcher {
   std::thread thread_;
 };
 
+// DSD_PIPELINE=0 keeps the table loop's synchronous step (the reference's
+// RunBatch shape: the host waits for every step).  By default the loop
+// enqueues each step, its append and its release on the pool's stream
+// without waiting (dsd_sparse_run_table_async) and forms the next step while
+// the device runs them; the steps' device times are collected at the end.
+bool PipelineEnabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("DSD_PIPELINE");
+    return e == nullptr || std::strcmp(e, "0") != 0;
+  }();
+  return on;
+}
+
+// The pinned payload rows of the pipelined loop, one slab per step in a ring
+// of kSlabs.  The device reads a step's query rows when the step runs and
+// its appended K/V rows when the append's copy runs, so the host writes
+// step j's slab only after step j - kSlabs (for K/V, the step after it,
+// which follows its append on the stream) has completed.  A query slab
+// holds the queries generated after the previous step in rows
+// [0, max_active) (row = the request's place in that step's batch) and the
+// initial queries of the requests admitted for step j in rows
+// [max_active, 2 max_active); a K/V slab holds the step's uploaded tokens in
+// batch order.
+class PayloadSlabs {
+ public:
+  static constexpr int kSlabs = 6;
+  PayloadSlabs(int max_active, int E, bool kv) : max_(max_active), E_(E) {
+    const std::size_t rows = static_cast<std::size_t>(max_active) * static_cast<std::size_t>(E);
+    for (int i = 0; i < kSlabs; ++i) {
+      q_.emplace_back(2 * rows);
+      if (kv) {
+        k_.emplace_back(rows);
+        v_.emplace_back(rows);
+      }
+    }
+  }
+  float* Query(long long step, int row) const {
+    return q_[Index(step)].data() + static_cast<std::size_t>(row) * static_cast<std::size_t>(E_);
+  }
+  float* Admitted(long long step, int n) const { return Query(step, max_ + n); }
+  float* Keys(long long step) const { return k_[Index(step)].data(); }
+  float* Values(long long step) const { return v_[Index(step)].data(); }
+
+ private:
+  static std::size_t Index(long long step) { return static_cast<std::size_t>(step % kSlabs); }
+  int max_, E_;
+  std::vector<PinnedFloats> q_, k_, v_;
+};
+
+// The pipelined loop's step tickets (index = the loop's step number) and
+// the waits that guard the payload slabs.
+class StepTickets {
+ public:
+  explicit StepTickets(::dsd_sparse_ctx* ctx) : ctx_(ctx) {}
+  // On scope exit (also by an exception) every enqueued step has finished
+  // before the slabs it reads are freed.
+  ~StepTickets() {
+    if (!tickets_.empty()) (void)dsd_device_synchronize();
+  }
+  StepTickets(const StepTickets&) = delete;
+  StepTickets& operator=(const StepTickets&) = delete;
+  void Push(long long ticket) { tickets_.push_back(ticket); }
+  // Blocks until loop step `step` (if it ran) has completed.
+  void WaitFor(long long step) const {
+    if (step < 0 || step >= static_cast<long long>(tickets_.size())) return;
+    detail::ThrowOnError(dsd_sparse_async_wait(ctx_, tickets_[static_cast<std::size_t>(step)]));
+  }
+
+ private:
+  ::dsd_sparse_ctx* ctx_;
+  std::vector<long long> tickets_;
+};
+
 // Prompt admission into the table (GPU-resident modes); with `mirror`, the
 // host cache reserves the same pages (for verification).
 void AdmitToTable(const ModelConfig& c, const ContinuousRequestSpec& s, std::size_t index,
@@ -656,6 +729,31 @@ void AdmitToTable(const ModelConfig& c, const ContinuousRequestSpec& s, std::siz
     detail::ThrowOnError(
         dsd_table_admit_synthetic(table->get(), slot, s.prompt_tokens, s.request_id));
   }
+}
+
+// The observed step's page lists and outputs, once it has completed (its
+// queries and selection are filled by the caller).
+void ObserveTableStep(SparseCudaContext& ctx, const LoopTable& table,
+                      const std::vector<int>& slots, int E, ObservedDecodeStep* observe) {
+  using detail::ThrowOnError;
+  const int B = static_cast<int>(slots.size());
+  int total = 0;
+  for (int slot : slots) {
+    int n = 0;
+    ThrowOnError(dsd_table_slot_pages(table.get(), slot, &n));
+    total += n;
+  }
+  observe->cand_offsets.assign(static_cast<std::size_t>(B) + 1, 0);
+  observe->cand_ids.assign(static_cast<std::size_t>(std::max(1, total)), 0);
+  ThrowOnError(dsd_sparse_last_csr(ctx.handle(), B, observe->cand_offsets.data(),
+                                   observe->cand_ids.data(), std::max(1, total)));
+  observe->cand_ids.resize(static_cast<std::size_t>(total));
+  int selected_total = 0;
+  for (int b = 0; b < B; ++b) selected_total += observe->selected_counts[static_cast<std::size_t>(b)];
+  observe->selected.resize(static_cast<std::size_t>(selected_total));
+  float* staged_out = nullptr;
+  ThrowOnError(dsd_sparse_staging(ctx.handle(), nullptr, nullptr, nullptr, &staged_out));
+  observe->outputs.assign(staged_out, staged_out + static_cast<std::size_t>(B) * E);
 }
 
 // One step of the table loop: the queries as StagedStep takes them (rows
@@ -705,25 +803,7 @@ SparseBatchCudaResult TableStep(SparseCudaContext& ctx, const LoopTable& table,
                                     rows->data(), outputs ? DSD_OUTPUT_OUTPUTS : DSD_OUTPUT_NONE,
                                     timing ? DSD_TIMING_EVENTS : DSD_TIMING_NONE, nullptr, sel,
                                     sel_counts, &t));
-  if (observe != nullptr) {
-    int total = 0;
-    for (int slot : slots) {
-      int n = 0;
-      ThrowOnError(dsd_table_slot_pages(table.get(), slot, &n));
-      total += n;
-    }
-    observe->cand_offsets.assign(static_cast<std::size_t>(B) + 1, 0);
-    observe->cand_ids.assign(static_cast<std::size_t>(std::max(1, total)), 0);
-    ThrowOnError(dsd_sparse_last_csr(ctx.handle(), B, observe->cand_offsets.data(),
-                                     observe->cand_ids.data(), std::max(1, total)));
-    observe->cand_ids.resize(static_cast<std::size_t>(total));
-    int selected_total = 0;
-    for (int b = 0; b < B; ++b) selected_total += observe->selected_counts[static_cast<std::size_t>(b)];
-    observe->selected.resize(static_cast<std::size_t>(selected_total));
-    float* staged_out = nullptr;
-    ThrowOnError(dsd_sparse_staging(ctx.handle(), nullptr, nullptr, nullptr, &staged_out));
-    observe->outputs.assign(staged_out, staged_out + static_cast<std::size_t>(B) * E);
-  }
+  if (observe != nullptr) ObserveTableStep(ctx, table, slots, E, observe);
   if (timing) {
     result.aggregate_timings.page_scoring_ms = t.score_ms;
     result.aggregate_timings.topk_ms = t.topk_ms;
@@ -738,6 +818,84 @@ SparseBatchCudaResult TableStep(SparseCudaContext& ctx, const LoopTable& table,
     result.runtime_overheads.time_sync_ms = t.sync_ms;
   }
   return result;
+}
+
+// One step of the pipelined table loop (PipelineEnabled): every query row
+// lies in pinned memory that stays unchanged until the step has completed
+// (the payload store or a payload slab).  The step is enqueued and not
+// waited for, unless it is observed; its device times are collected at the
+// end of the loop (CollectPipelinedSteps).
+SparseBatchCudaResult PipelinedTableStep(SparseCudaContext& ctx, const LoopTable& table,
+                                         const std::vector<LiveRequest>& active, int E,
+                                         int top_k, const SparseRunBatchOptions& run,
+                                         std::vector<const float*>* rows,
+                                         ObservedDecodeStep* observe, long long* ticket) {
+  using detail::ThrowOnError;
+  SparseBatchCudaResult result;
+  const auto t0 = Clock::now();
+  const int B = static_cast<int>(active.size());
+  std::vector<int> slots(static_cast<std::size_t>(B));
+  rows->resize(static_cast<std::size_t>(B));
+  for (int b = 0; b < B; ++b) {
+    const LiveRequest& l = active[static_cast<std::size_t>(b)];
+    if (l.own) throw std::logic_error("a pipelined step's query is not in pinned memory");
+    slots[static_cast<std::size_t>(b)] = table.SlotOf(l.a.state.request_id);
+    (*rows)[static_cast<std::size_t>(b)] = l.query;
+  }
+  const double layout_ms = Ms(t0, Clock::now());
+  const bool timing = run.timing_mode == SparseBatchTimingMode::kKernelEvents;
+  const bool outputs = run.output_mode != SparseBatchOutputMode::kNoOutputs || observe;
+  dsd_step_timings t{};
+  ThrowOnError(dsd_sparse_run_table_async(
+      ctx.handle(), table.get(), B, slots.data(), nullptr, rows->data(),
+      outputs ? DSD_OUTPUT_OUTPUTS : DSD_OUTPUT_NONE,
+      timing ? DSD_TIMING_EVENTS : DSD_TIMING_NONE, ticket, &t));
+  if (observe != nullptr) {
+    ThrowOnError(dsd_sparse_async_wait(ctx.handle(), *ticket));
+    observe->queries.resize(static_cast<std::size_t>(B) * E);
+    for (int b = 0; b < B; ++b) {
+      std::memcpy(observe->queries.data() + static_cast<std::size_t>(b) * E,
+                  (*rows)[static_cast<std::size_t>(b)], sizeof(float) * E);
+    }
+    observe->selected.assign(static_cast<std::size_t>(B) * std::max(1, top_k), 0);
+    observe->selected_counts.assign(static_cast<std::size_t>(B), 0);
+    ThrowOnError(dsd_sparse_last_selection(ctx.handle(), B, observe->selected.data(),
+                                           observe->selected_counts.data()));
+    ObserveTableStep(ctx, table, slots, E, observe);
+  }
+  if (timing) {
+    result.runtime_overheads.time_prepare_sparse_layout_ms = layout_ms;
+    result.runtime_overheads.time_memcpy_h2d_ms = t.h2d_ms;
+    result.runtime_overheads.time_kernel_launch_ms = t.launch_ms;
+    result.runtime_overheads.time_sync_ms = t.sync_ms;  // waits for a free ring slot
+  }
+  return result;
+}
+
+// The pipelined loop's step records, once every step has completed: a
+// step's time is its device time from its first command (the stage-in) to
+// its last (the attention), as the device ran it -- gaps while the host was
+// still enqueuing it included; the stage times are the kernel events'.
+void CollectPipelinedSteps(SparseCudaContext& ctx, bool timing, std::vector<double>* step_ms,
+                           StageTimings* timings) {
+  step_ms->clear();
+  std::vector<dsd_async_step> recs(256);
+  for (;;) {
+    int n = 0;
+    detail::ThrowOnError(
+        dsd_sparse_async_collect(ctx.handle(), recs.data(), static_cast<int>(recs.size()), &n));
+    if (n == 0) return;
+    for (int i = 0; i < n; ++i) {
+      const dsd_async_step& r = recs[static_cast<std::size_t>(i)];
+      step_ms->push_back(r.done_ms - r.start_ms);
+      if (timing) {
+        timings->page_scoring_ms += r.score_ms;
+        timings->topk_ms += r.topk_ms;
+        timings->attention_ms += r.attention_ms;
+        timings->total_ms += r.score_ms + r.topk_ms + r.attention_ms;
+      }
+    }
+  }
 }
 
 // Verification of a table step (DSD_VERIFY_STAGED): the device's candidate
@@ -900,6 +1058,7 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
   // then only mirrors them when steps are verified).
   const bool use_table = metadata_only && !debug_outputs && DeviceTableEnabled();
   const bool mirror = !use_table || VerifyStagedSteps();
+  const bool pipelined = use_table && !VerifyStagedSteps() && PipelineEnabled();
   std::unique_ptr<LoopTable> table;
   if (use_table) {
     const int slots = options.preadmit_prompts ? static_cast<int>(specs.size())
@@ -941,6 +1100,16 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
   std::vector<const float*> step_rows;
   std::vector<const RequestState*> batch;
   std::vector<std::uint8_t> admitted(specs.size(), 0);
+  // The pipelined loop's pinned payload rows and its step tickets; the
+  // tickets' scope ends first, waiting for every enqueued step before the
+  // rows those steps read are freed.
+  std::unique_ptr<PayloadSlabs> slabs;
+  if (pipelined) {
+    slabs = std::make_unique<PayloadSlabs>(options.max_active_requests, E,
+                                           !options.gpu_synthetic_decode_append);
+  }
+  StepTickets tickets(ctx.handle());
+  int admitted_this_step = 0;
 
   if (options.preadmit_prompts) {
     for (std::size_t i = 0; i < specs.size(); ++i) {
@@ -987,8 +1156,17 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
         }
         l.a.remaining_decode_steps = s.decode_steps;
         l.a.spec_index = i;
-        l.query_buf = s.initial_query;
-        l.own = true;
+        if (pipelined) {
+          // Into the step's query slab (rows the step reads in place).
+          if (admitted_this_step == 0) tickets.WaitFor(steps_run - PayloadSlabs::kSlabs);
+          float* row = slabs->Admitted(steps_run, admitted_this_step++);
+          std::memcpy(row, s.initial_query.data(), sizeof(float) * E);
+          l.query = row;
+          l.own = false;
+        } else {
+          l.query_buf = s.initial_query;
+          l.own = true;
+        }
         active.push_back(std::move(l));
       } else if (use_table) {
         table->Release({s.request_id}, !options.lazy_release);
@@ -1035,6 +1213,12 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
                               pr.output.output.end());
         }
       }
+    } else if (pipelined) {
+      long long ticket = 0;
+      result = PipelinedTableStep(ctx, *table, active, E, config.top_k_pages, run, &step_rows,
+                                  observe ? &seen : nullptr, &ticket);
+      tickets.Push(ticket);
+      admitted_this_step = 0;
     } else if (use_table) {
       result = TableStep(ctx, *table, active, E, config.top_k_pages, run, &step_rows,
                          observe ? &seen : nullptr);
@@ -1068,10 +1252,29 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
     const bool gen_kv =
         !options.gpu_synthetic_decode_append && !options.precompute_decode_payloads;
     const bool gen_q = !options.precompute_decode_payloads;
-    std::vector<std::vector<float>> gen_k(gen_kv ? active.size() : 0);
-    std::vector<std::vector<float>> gen_v(gen_kv ? active.size() : 0);
+    std::vector<std::vector<float>> gen_k(gen_kv && !pipelined ? active.size() : 0);
+    std::vector<std::vector<float>> gen_v(gen_kv && !pipelined ? active.size() : 0);
+    // The pipelined loop writes the step's uploaded K/V rows (batch order,
+    // up_row) and the next step's queries straight into their slabs, once
+    // the steps that read those slabs last have completed.
+    const long long this_step = steps_run - 1;
+    const bool kv_rows = pipelined && !options.gpu_synthetic_decode_append;
+    std::vector<int> up_row(active.size(), -1);
+    float* kv_keys = nullptr;
+    float* kv_values = nullptr;
+    if (kv_rows) {
+      int m = 0;
+      for (std::size_t li = 0; li < active.size(); ++li) {
+        if (active[li].a.remaining_decode_steps > 1) up_row[li] = m++;
+      }
+      tickets.WaitFor(this_step - PayloadSlabs::kSlabs + 1);
+      kv_keys = slabs->Keys(this_step);
+      kv_values = slabs->Values(this_step);
+    }
+    if (pipelined && gen_q) tickets.WaitFor(steps_run - PayloadSlabs::kSlabs);
     if (gen_kv || gen_q) {
       const int per = (gen_kv ? 2 : 0) + (gen_q ? 1 : 0);
+      const std::size_t row_bytes = sizeof(float) * static_cast<std::size_t>(E);
       dsd_host::Workers::Get().ParallelFor(
           static_cast<int>(active.size()) * per, [&](int t) {
             const int i = t / per;
@@ -1079,10 +1282,18 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
             LiveRequest& l = active[static_cast<std::size_t>(i)];
             const int id = l.a.state.request_id;
             const int dstep = l.a.decode_step_index;
-            if (gen_kv && which == 0) {
-              gen_k[static_cast<std::size_t>(i)] = TokenVector(E, id, dstep, 1);
-            } else if (gen_kv && which == 1) {
-              gen_v[static_cast<std::size_t>(i)] = TokenVector(E, id, dstep, 2);
+            const int up = up_row[static_cast<std::size_t>(i)];
+            if (gen_kv && which < 2) {
+              std::vector<float> kv = TokenVector(E, id, dstep, which + 1);
+              if (!pipelined) {
+                (which == 0 ? gen_k : gen_v)[static_cast<std::size_t>(i)] = std::move(kv);
+              } else if (up >= 0) {
+                float* dst = (which == 0 ? kv_keys : kv_values) + static_cast<std::size_t>(up) * E;
+                std::memcpy(dst, kv.data(), row_bytes);
+              }
+            } else if (pipelined) {
+              const std::vector<float> q = TokenVector(E, id, dstep + 1, 0);
+              std::memcpy(slabs->Query(steps_run, i), q.data(), row_bytes);
             } else {
               l.query_buf = TokenVector(E, id, dstep + 1, 0);  // the next step's query
             }
@@ -1105,10 +1316,12 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
         if (options.precompute_decode_payloads) {
           k = Row(payloads.keys[a.spec_index], dstep, E);
           v = Row(payloads.values[a.spec_index], dstep, E);
-        } else {
+        } else if (!pipelined) {
           k = gen_k[li].data();
           v = gen_v[li].data();
         }
+        // (pipelined, generated: the rows are already in the K/V slab; no
+        // host cache mirrors a pipelined loop)
       }
       // Decode tokens of GPU-admitted prompts start a fresh page (:614-616).
       const bool force_new = metadata_only && dstep == 0;
@@ -1132,6 +1345,12 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
         if (options.gpu_synthetic_decode_append) {
           synth_requests.push_back(id);
           synth_steps.push_back(dstep);
+        } else if (kv_rows) {
+          if (k != nullptr) {  // precomputed rows into the slab
+            const std::size_t at = static_cast<std::size_t>(up_row[li]) * E;
+            std::memcpy(kv_keys + at, k, sizeof(float) * E);
+            std::memcpy(kv_values + at, v, sizeof(float) * E);
+          }
         } else if (metadata_only) {
           keys.insert(keys.end(), k, k + E);
           values.insert(values.end(), v, v + E);
@@ -1143,6 +1362,9 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
       if (options.precompute_decode_payloads) {
         l.query = payloads.NextQuery(a.spec_index, dstep, E);
         l.own = false;
+      } else if (pipelined) {
+        l.query = slabs->Query(steps_run, static_cast<int>(li));  // generated above
+        l.own = false;
       } else {
         l.own = true;  // query_buf already holds it (generated above)
       }
@@ -1153,9 +1375,11 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
     const auto t_append = Clock::now();
     if (use_table) {
       const bool rows = !options.gpu_synthetic_decode_append;
+      const float* k_rows = kv_rows ? kv_keys : keys.data();
+      const float* v_rows = kv_rows ? kv_values : values.data();
       detail::ThrowOnError(dsd_table_append(
           table->get(), static_cast<int>(t_slots.size()), t_slots.data(), t_fresh.data(),
-          t_upload.data(), rows ? keys.data() : nullptr, rows ? values.data() : nullptr,
+          t_upload.data(), rows ? k_rows : nullptr, rows ? v_rows : nullptr,
           t_requests.data(), t_steps.data()));
     } else if (options.gpu_synthetic_decode_append) {
       ctx.AppendSyntheticTokens(cache, appended, synth_requests, synth_steps);
@@ -1188,6 +1412,10 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
     }
     stats.release_sync_ms += Ms(t_release, Clock::now());
     ++step;
+  }
+  if (pipelined) {
+    CollectPipelinedSteps(ctx, options.run_batch_timing_mode == SparseBatchTimingMode::kKernelEvents,
+                          &step_ms, &timings);
   }
   FinishStats(&stats, wall_start, step_ms, timings, overheads, steps_run, batch_sum);
   Add(&stats.device_transfer_stats, ctx.DeviceTransfers());

@@ -126,7 +126,7 @@ __global__ void TableScatterKernel(PoolView pool, TableView t, int slot, int tok
 // receives it, and a fresh page it opened keeps no tokens.
 __global__ __launch_bounds__(kTableThreads) void TablePlanAppendKernel(
     PoolView pool, TableView t, const int* __restrict__ args, int n, int m, int* plan,
-    int* order) {
+    int* order, ProgressMark mark) {
   __shared__ int scan[kTableWaves + 1];
   const int* slots = args;
   const int* flags = args + n;
@@ -185,6 +185,8 @@ __global__ __launch_bounds__(kTableThreads) void TablePlanAppendKernel(
     plan[m] = m;  // seg_start[m]
     *t.free_top = top - new_base;
   }
+  __syncthreads();  // every thread has read its arguments
+  if (threadIdx.x == 0) StoreProgress(mark);
 }
 
 // Release of n <= 1024 slots (batch order): their pages go back on the stack
@@ -241,7 +243,7 @@ __global__ __launch_bounds__(kTableThreads) void TableReleaseKernel(
 }
 
 __global__ __launch_bounds__(kTableThreads) void TableReleaseFinishKernel(
-    TableView t, const int* __restrict__ slots, int n) {
+    TableView t, const int* __restrict__ slots, int n, ProgressMark mark) {
   __shared__ int scan[kTableWaves + 1];
   const int i = static_cast<int>(threadIdx.x);
   const int slot = i < n ? slots[i] : 0;
@@ -250,6 +252,9 @@ __global__ __launch_bounds__(kTableThreads) void TableReleaseFinishKernel(
   (void)BlockExclusiveScan(np, scan, &total);  // reads every count first
   if (i < n) t.npages[slot] = 0;
   if (i == 0) *t.free_top += total;
+  // (the scan's barriers follow every thread's read of slots; the release
+  // kernel before this one has finished reading them)
+  if (i == 0) StoreProgress(mark);
 }
 
 }  // namespace
@@ -280,15 +285,16 @@ void LaunchTableScatter(const PoolView& pool, const TableView& t, int slot, int 
 }
 
 void LaunchTablePlanAppend(const PoolView& pool, const TableView& t, const int* args, int n,
-                           int m, int* d_plan, int* d_order, hipStream_t stream) {
+                           int m, int* d_plan, int* d_order, hipStream_t stream,
+                           ProgressMark mark) {
   if (n <= 0) return;
   hipLaunchKernelGGL(TablePlanAppendKernel, dim3(1), dim3(kTableThreads), 0, stream, pool, t,
-                     args, n, m, d_plan, d_order);
+                     args, n, m, d_plan, d_order, mark);
   DSD_HIP_CHECK(hipGetLastError());
 }
 
 void LaunchTableRelease(const PoolView& pool, const TableView& t, const int* slots, int n,
-                        int released_pages, bool clear, hipStream_t stream) {
+                        int released_pages, bool clear, hipStream_t stream, ProgressMark mark) {
   if (n <= 0) return;
   if (n > kTableThreads) throw std::invalid_argument("at most 1024 slots per release launch");
   const int groups = clear ? std::max(1, std::min(256, released_pages)) : 1;
@@ -296,7 +302,7 @@ void LaunchTableRelease(const PoolView& pool, const TableView& t, const int* slo
                      slots, n, clear ? 1 : 0);
   DSD_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(TableReleaseFinishKernel, dim3(1), dim3(kTableThreads), 0, stream, t, slots,
-                     n);
+                     n, mark);
   DSD_HIP_CHECK(hipGetLastError());
 }
 

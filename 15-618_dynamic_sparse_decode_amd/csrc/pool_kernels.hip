@@ -304,6 +304,10 @@ __device__ int PoolBlockScan(int x, int* scratch, int* total) {
 }
 
 __global__ __launch_bounds__(kPoolThreads) void StageInKernel(StageSegments s) {
+  if (s.start_stamp != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+    __hip_atomic_store(s.start_stamp, static_cast<unsigned long long>(wall_clock64()),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
   const int tid = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
   const int stride = static_cast<int>(gridDim.x * blockDim.x);
   for (int k = 0; k < s.count; ++k) {
@@ -362,6 +366,21 @@ __global__ __launch_bounds__(kPoolThreads) void StageInKernel(StageSegments s) {
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) s.csr_offsets[s.table_batch] = base;
   }
+}
+
+__global__ __launch_bounds__(64) void StepMarkKernel(unsigned long long* words,
+                                                     unsigned long long ticket) {
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(words + 1, static_cast<unsigned long long>(wall_clock64()),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(words, ticket, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
+void LaunchStepMark(unsigned long long* words, unsigned long long ticket, hipStream_t stream) {
+  if (words == nullptr) throw std::invalid_argument("step mark needs its words");
+  hipLaunchKernelGGL(StepMarkKernel, dim3(1), dim3(64), 0, stream, words, ticket);
+  DSD_HIP_CHECK(hipGetLastError());
 }
 
 void LaunchStageIn(const StageSegments& s, hipStream_t stream) {

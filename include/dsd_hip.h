@@ -491,6 +491,59 @@ int dsd_sparse_run_table(dsd_sparse_ctx* ctx, dsd_table* table, int batch,
  * read it; synchronous.  For observers of table steps. */
 int dsd_sparse_last_csr(dsd_sparse_ctx* ctx, int batch, int* cand_offsets,
                         int* cand_ids, int capacity);
+/* The selected ids of the last step on the context's stream, packed per
+ * request as dsd_sparse_run_batch returns them (selected[sum of counts],
+ * selected_counts[batch]); synchronous.  For observers of table steps. */
+int dsd_sparse_last_selection(dsd_sparse_ctx* ctx, int batch, int* selected,
+                              int* selected_counts);
+
+/* ---- asynchronous table steps ------------------------------------------ */
+/* The serving loop's step without a host wait: the reference's loop calls
+ * SparseCudaContext::RunBatch and waits for every step
+ * (src/continuous_batching.cpp:497-696,
+ * src/cuda/sparse_batched_attention.cu:554-838); here the host enqueues a
+ * step, the step's append and release (dsd_table_append / _release, on the
+ * same stream), and goes on to the next step while the device runs them.
+ *
+ * dsd_sparse_run_table_async is dsd_sparse_run_table that returns once the
+ * step is enqueued, with *ticket its sequence number (0: batch was 0,
+ * nothing enqueued).  Its slot ids and a `queries` block are copied at the
+ * call; query_rows (dsd_host_alloc memory) are read by the device when the
+ * step runs, so the caller keeps them unchanged until the step has
+ * completed (dsd_sparse_async_wait).  Outputs stay in the staging
+ * (dsd_sparse_staging), where later steps overwrite them; no ids are
+ * returned (dsd_sparse_last_selection after a wait).  At most 4 steps are in
+ * flight: a call first waits for the step enqueued 4 calls before it.
+ * host_timings (may be NULL) gets the host side: h2d_ms staging, launch_ms
+ * enqueue, sync_ms the wait for a free ring slot.
+ *
+ * dsd_sparse_async_wait blocks until every step up to `ticket` has completed;
+ * dsd_sparse_async_collect until every enqueued step has, then hands over up
+ * to `capacity` of the oldest records (*count of them; call again for the
+ * rest).  A failure a step reported (the codes of dsd_sparse_device_status)
+ * is returned by the call that waits for that step; its record is dropped.
+ * A record's times are device event times from a base recorded before the
+ * first step of its timeline (a timeline starts when nothing is in flight
+ * and every record has been collected). */
+typedef struct dsd_async_step {
+  long long ticket;
+  int batch;
+  int fused;
+  double start_ms;     /* the step's first command (the stage-in) */
+  double done_ms;      /* its last command */
+  double score_ms;     /* DSD_TIMING_EVENTS only, as dsd_step_timings */
+  double topk_ms;
+  double attention_ms;
+  double kernel_ms;
+} dsd_async_step;
+int dsd_sparse_run_table_async(dsd_sparse_ctx* ctx, dsd_table* table, int batch,
+                               const int* slots, const float* queries,
+                               const float* const* query_rows, int output_mode,
+                               int timing_mode, long long* ticket,
+                               dsd_step_timings* host_timings);
+int dsd_sparse_async_wait(dsd_sparse_ctx* ctx, long long ticket);
+int dsd_sparse_async_collect(dsd_sparse_ctx* ctx, dsd_async_step* steps, int capacity,
+                             int* count);
 
 /* ---- dense decode step ------------------------------------------------- */
 /* DenseCudaContext::RunBatch (include/dsd/cuda_dense_attention.h:18-44):

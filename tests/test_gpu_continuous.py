@@ -12,8 +12,10 @@ tests/test_generators.py) and its decode tokens come from the reference's
 DeterministicTokenVector, U(-1, 1).  Every 7th step's requests are rebuilt
 independently from those generators and the oracle's sparse_cpu rows must
 give the same selection (id for id) and outputs within 1e-4.  Both ways of
-holding the next query are covered: generated in the loop (copied into the
-step's staging) and precomputed into pinned rows the step reads in place.
+holding the next query are covered: generated in the loop (into the
+pipelined loop's pinned payload slabs, or copied into the step's staging
+when the host waits for every step) and precomputed into pinned rows the
+step reads in place.
 The third case runs the loop on BASELINE config 5's own data: N(0, 1)
 prompts, decode K/V and queries (DSD_PAYLOAD_DIST=normal), rebuilt by the
 oracle's restatement of that generator."""
@@ -32,16 +34,19 @@ EXE = pathlib.Path(__file__).resolve().parent / "native" / "build" / "continuous
 CONFIG5 = ["128", "32", "64", "1024", "4096", "16", "64", "7", "32", "128", "16", "8"]
 
 
-@pytest.mark.parametrize("precompute,dist", [("0", "uniform"), ("1", "uniform"), ("0", "normal")])
-def test_config5_serving_loop_steps_match_the_oracle(gpu, precompute, dist):
+@pytest.mark.parametrize("precompute,dist,pipeline", [("0", "uniform", "1"), ("1", "uniform", "1"),
+                                                      ("0", "normal", "1"), ("0", "uniform", "0")])
+def test_config5_serving_loop_steps_match_the_oracle(gpu, precompute, dist, pipeline):
     # dist "normal": BASELINE config 5's own data, N(0, 1) prompts, decode K/V
     # and queries (DSD_PAYLOAD_DIST=normal); the reference's U(-1, 1) is the
-    # default
+    # default.  pipeline "1" (the default): unobserved steps, their appends
+    # and releases are enqueued without host waits; "0" (DSD_PIPELINE=0):
+    # the host waits for every step.
     if not EXE.exists():
         pytest.fail(f"{EXE} is not built (__graft_entry__.build() builds tests/native)")
     print(f"[continuous_check] config 5, every 7th step, precompute={precompute}, "
-          f"payloads {dist}", flush=True)
-    env = dict(os.environ, DSD_PAYLOAD_DIST=dist)
+          f"payloads {dist}, pipeline {pipeline}", flush=True)
+    env = dict(os.environ, DSD_PAYLOAD_DIST=dist, DSD_PIPELINE=pipeline)
     proc = subprocess.run([str(EXE), *CONFIG5, "7", precompute], capture_output=True,
                           text=True, timeout=900, env=env)
     out = proc.stdout + proc.stderr
