@@ -147,6 +147,9 @@ _SIGNATURES = {
                                                   ctypes.POINTER(StepTimings)]),
     "dsd_host_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
     "dsd_host_free": (ctypes.c_int, [ctypes.c_void_p]),
+    "dsd_device_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
+    "dsd_device_upload": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
+    "dsd_device_free": (ctypes.c_int, [ctypes.c_void_p]),
     "dsd_sparse_run_batch_device": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_int] * 3
                                     + [ctypes.c_void_p] * 8),
     "dsd_sparse_run_batch_device_static": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_int] * 4
@@ -765,6 +768,35 @@ class HostBlock:
         if self.address:
             self.array = None
             _check(self._lib.dsd_host_free(ctypes.c_void_p(self.address)))
+            self.address = 0
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+class DeviceBlock:
+    """Device memory from dsd_device_alloc (float32 elements); rows inside
+    it may be passed as query rows, as HostBlock rows may."""
+
+    def __init__(self, count: int):
+        self._lib = load_library()
+        p = ctypes.c_void_p()
+        _check(self._lib.dsd_device_alloc(4 * count, ctypes.byref(p)))
+        self.address = p.value
+        self.count = count
+
+    def upload(self, values, offset: int = 0) -> None:
+        """Copies float32 values into elements [offset, offset + len)."""
+        v = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+        _check(self._lib.dsd_device_upload(ctypes.c_void_p(self.address + 4 * offset),
+                                           v.ctypes.data_as(ctypes.c_void_p), 4 * v.size))
+
+    def close(self) -> None:
+        if self.address:
+            _check(self._lib.dsd_device_free(ctypes.c_void_p(self.address)))
             self.address = 0
 
     def __enter__(self):

@@ -155,14 +155,23 @@ bool IsPinnedHost(const void* p) {
   return attr.type == hipMemoryTypeHost;
 }
 
-// The pinned blocks handed out by dsd_host_alloc (start -> bytes), so a step
-// that reads query rows straight from host memory can check that every row
-// lies inside memory the device may read.
-class HostBlocks {
+// The blocks handed out by dsd_host_alloc (pinned) and dsd_device_alloc
+// (start -> bytes), so a step that reads query rows in place can check that
+// every row lies inside memory the device may read.
+class RowBlocks {
  public:
-  static HostBlocks& Get() {
-    static HostBlocks blocks;
+  static RowBlocks& Host() {
+    static RowBlocks blocks;
     return blocks;
+  }
+  static RowBlocks& Device() {
+    static RowBlocks blocks;
+    return blocks;
+  }
+  // Whether [p, p + bytes) lies inside one block.
+  bool Holds(const void* p, size_t bytes) {
+    const float* row = static_cast<const float*>(p);
+    return FirstOutside(&row, 1, bytes) < 0;
   }
   void Add(void* p, size_t bytes) {
     std::lock_guard<std::mutex> lock(mu_);
@@ -917,8 +926,6 @@ struct dsd_table {
   // Done(b) by a progress mark the launch's last kernel stores (no event
   // barrier on the stream).
   dsdk::ProgressMark Mark(int b) {
-    h_progress.Reserve(1, hipHostMallocCoherent);
-    if (progress_seq == 0) h_progress.ptr[0] = 0;
     args_seq[b] = ++progress_seq;
     return dsdk::ProgressMark{h_progress.ptr, args_seq[b]};
   }
@@ -1001,6 +1008,10 @@ int dsd_table_create(dsd_pool* pool, int max_slots, int max_pages, dsd_table** o
       DSD_HIP_CHECK(
           hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventDisableSystemFence));
     }
+    t->h_progress.Reserve(1, hipHostMallocCoherent);
+    t->h_progress.ptr[0] = 0;
+    for (PinnedBuffer<int>& b : t->h_args) b.Reserve(256, hipHostMallocCoherent);
+    dsdk::PreloadTableKernels();
     pool->WaitPending();
     dsdk::LaunchTableReset(t->view, pool->view.capacity, pool->stream);
     pool->Sync();
@@ -1755,6 +1766,21 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     ctx->h_ids.Reserve(P, hipHostMallocCoherent);
     ctx->h_selected.Reserve(B * K);
     ctx->h_counts.Reserve(B);
+    // The asynchronous steps' ring slots (a copied query block is reserved
+    // at its first use), so the first steps pay no pinned allocation.
+    for (AsyncSlot& a : ctx->async) {
+      a.slots.Reserve(B + 1, hipHostMallocCoherent);
+      a.rows.Reserve(B + 1, hipHostMallocCoherent);
+      a.stamps.Reserve(std::max<size_t>(1, ctx->h_stamps.count), hipHostMallocCoherent);
+      a.words.Reserve(4, hipHostMallocCoherent);
+      for (int i = 0; i < 4; ++i) a.words.ptr[i] = 0;
+      for (hipEvent_t& e : a.k) {
+        DSD_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
+      }
+    }
+    dsdk::PreloadStepKernels();
+    dsdk::PreloadFusedKernels();
+    dsdk::PreloadPoolKernels();
     *out_ctx = ctx.release();
   });
 }
@@ -1932,11 +1958,13 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
           foreign_at.push_back(r);
         }
       }
-      const int bad = HostBlocks::Get().FirstOutside(foreign.data(),
-                                                     static_cast<int>(foreign.size()), row_bytes);
-      if (bad >= 0) {
-        throw std::invalid_argument("query row " + std::to_string(foreign_at[bad]) +
-                                    " is not in dsd_host_alloc memory");
+      for (size_t f = 0; f < foreign.size(); ++f) {
+        if (RowBlocks::Host().Holds(foreign[f], row_bytes) ||
+            RowBlocks::Device().Holds(foreign[f], row_bytes)) {
+          continue;
+        }
+        throw std::invalid_argument("query row " + std::to_string(foreign_at[f]) +
+                                    " is not in dsd_host_alloc or dsd_device_alloc memory");
       }
     }
 
@@ -2142,14 +2170,6 @@ int dsd_sparse_run_table_async(dsd_sparse_ctx* ctx, dsd_table* table, int batch,
     const auto t0 = Clock::now();
     if (a.busy) HarvestThrough(ctx, a.ticket);
     const double wait_ms = MsSince(t0);
-    if (a.words.ptr == nullptr) {
-      a.words.Reserve(4, hipHostMallocCoherent);
-      for (int i = 0; i < 4; ++i) a.words.ptr[i] = 0;
-      // (timing only: no system-scope fence)
-      for (hipEvent_t& e : a.k) {
-        DSD_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
-      }
-    }
     bool in_flight = false;
     for (const AsyncSlot& o : ctx->async) in_flight = in_flight || o.busy;
     a.new_timeline = !in_flight && ctx->async_records.empty();
@@ -2277,7 +2297,7 @@ int dsd_host_alloc(size_t bytes, void** out) {
     *out = nullptr;
     void* p = nullptr;
     DSD_HIP_CHECK(hipHostMalloc(&p, bytes, hipHostMallocCoherent));
-    HostBlocks::Get().Add(p, bytes);
+    RowBlocks::Host().Add(p, bytes);
     *out = p;
   });
 }
@@ -2285,8 +2305,40 @@ int dsd_host_alloc(size_t bytes, void** out) {
 int dsd_host_free(void* p) {
   return Guard([&] {
     if (p == nullptr) return;
-    Require(HostBlocks::Get().Remove(p), "pointer was not returned by dsd_host_alloc");
+    Require(RowBlocks::Host().Remove(p), "pointer was not returned by dsd_host_alloc");
     DSD_HIP_CHECK(hipHostFree(p));
+  });
+}
+
+int dsd_device_alloc(size_t bytes, void** out) {
+  return Guard([&] {
+    Require(out != nullptr, "out must be non-null");
+    Require(bytes > 0, "bytes must be positive");
+    *out = nullptr;
+    void* p = nullptr;
+    DSD_HIP_CHECK(hipMalloc(&p, bytes));
+    RowBlocks::Device().Add(p, bytes);
+    *out = p;
+  });
+}
+
+int dsd_device_upload(void* dst, const void* src, size_t bytes) {
+  return Guard([&] {
+    if (bytes == 0) return;
+    Require(dst != nullptr && src != nullptr, "pointers must be non-null");
+    Require(RowBlocks::Device().Holds(dst, bytes),
+            "the destination is not inside one dsd_device_alloc block");
+    DSD_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  });
+}
+
+int dsd_device_free(void* p) {
+  return Guard([&] {
+    if (p == nullptr) return;
+    Require(RowBlocks::Device().Remove(p), "pointer was not returned by dsd_device_alloc");
+    // Steps enqueued without a wait may still read it.
+    DSD_HIP_CHECK(hipDeviceSynchronize());
+    DSD_HIP_CHECK(hipFree(p));
   });
 }
 

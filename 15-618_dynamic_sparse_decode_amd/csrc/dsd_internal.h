@@ -38,6 +38,21 @@ inline void CheckHip(hipError_t status, const char* expr) {
 
 #define DSD_HIP_CHECK(expr) ::dsdk::CheckHip((expr), #expr)
 
+// Loads a kernel's code on the current device now: the runtime otherwise
+// loads it at its first launch, about a millisecond for the step kernels,
+// which would land in the first step a caller runs (and times).
+template <typename K>
+void PreloadKernel(K kernel) {
+  hipFuncAttributes attr{};
+  DSD_HIP_CHECK(hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel)));
+}
+// The hot kernels of each translation unit (sparse contexts and tables
+// call these at creation).
+void PreloadStepKernels();
+void PreloadFusedKernels();
+void PreloadPoolKernels();
+void PreloadTableKernels();
+
 // Where a step's kernels report an input they cannot use: they store
 // (epoch << 32) | code into *word, a host-visible pinned word, so the host
 // can tell which launch failed.  Codes: 1 a cross-workgroup wait of the

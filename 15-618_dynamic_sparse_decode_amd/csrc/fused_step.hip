@@ -1219,4 +1219,11 @@ void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t st
   DSD_HIP_CHECK(hipGetLastError());
 }
 
+void PreloadFusedKernels() {
+  PreloadKernel(FusedStepKernel<true>);
+  PreloadKernel(FusedStepKernel<false>);
+  PreloadKernel(ScorePagesKernel);
+  PreloadKernel(EpochBumpKernel);
+}
+
 }  // namespace dsdk

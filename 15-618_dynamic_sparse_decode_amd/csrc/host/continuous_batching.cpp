@@ -271,16 +271,65 @@ class PinnedFloats {
   float* ptr_ = nullptr;
 };
 
+// A dsd_device_alloc block of floats (HBM rows the steps read in place).
+class DeviceFloats {
+ public:
+  DeviceFloats() = default;
+  DeviceFloats(const float* host, std::size_t count) {
+    if (count == 0) return;
+    void* p = nullptr;
+    detail::ThrowOnError(dsd_device_alloc(sizeof(float) * count, &p));
+    ptr_ = static_cast<float*>(p);
+    detail::ThrowOnError(dsd_device_upload(ptr_, host, sizeof(float) * count));
+  }
+  DeviceFloats(DeviceFloats&& o) noexcept : ptr_(o.ptr_) { o.ptr_ = nullptr; }
+  DeviceFloats& operator=(DeviceFloats&& o) noexcept {
+    std::swap(ptr_, o.ptr_);
+    return *this;
+  }
+  DeviceFloats(const DeviceFloats&) = delete;
+  DeviceFloats& operator=(const DeviceFloats&) = delete;
+  ~DeviceFloats() {
+    if (ptr_ != nullptr) (void)dsd_device_free(ptr_);
+  }
+  const float* data() const { return ptr_; }
+
+ private:
+  float* ptr_ = nullptr;
+};
+
+// DSD_QUERY_STORE=host keeps the pipelined loop's precomputed queries in
+// pinned host memory only, read across PCIe by every step's stage-in.  By
+// default the store is also uploaded to HBM with the payloads, where a
+// model's own queries would be, and the steps read it there.
+bool DeviceQueryStore() {
+  static const bool on = [] {
+    const char* e = std::getenv("DSD_QUERY_STORE");
+    return e == nullptr || std::strcmp(e, "host") != 0;
+  }();
+  return on;
+}
+
 // The precomputed payloads (src/continuous_batching.cpp:272-300, :444-454): every
 // request's next-step queries in one pinned block, request i's rows from
-// query_row0[i] on, and the appended keys / values per request.
+// query_row0[i] on (and, for the pipelined loop, a copy in HBM), and the
+// appended keys / values per request.
 struct DecodePayloads {
   PinnedFloats queries;
+  DeviceFloats device_queries;
+  std::size_t query_rows = 0;
   std::vector<std::size_t> query_row0;
   std::vector<std::vector<float>> keys, values;
+  std::size_t RowOf(std::size_t spec, int step, int E) const {
+    return (query_row0[spec] + static_cast<std::size_t>(step)) * static_cast<std::size_t>(E);
+  }
   const float* NextQuery(std::size_t spec, int step, int E) const {
-    return queries.data() + (query_row0[spec] + static_cast<std::size_t>(step)) *
-                                static_cast<std::size_t>(E);
+    return queries.data() + RowOf(spec, step, E);
+  }
+  // The HBM copy's row, or nullptr without one.
+  const float* NextQueryDevice(std::size_t spec, int step, int E) const {
+    return device_queries.data() == nullptr ? nullptr
+                                            : device_queries.data() + RowOf(spec, step, E);
   }
 };
 
@@ -297,6 +346,7 @@ DecodePayloads BuildPayloads(const ModelConfig& c,
     rows += static_cast<std::size_t>(std::max(0, specs[i].decode_steps));
   }
   p.queries = PinnedFloats(rows * static_cast<std::size_t>(E));
+  p.query_rows = rows;
   if (kv) {
     p.keys.resize(specs.size());
     p.values.resize(specs.size());
@@ -338,6 +388,9 @@ struct LiveRequest {
   const float* query = nullptr;  // payload-store row when !own
   std::vector<float> query_buf;  // the query when own
   bool own = true;
+  // The same query in HBM (the pipelined loop's device query store), read
+  // by the step instead of `query`; nullptr when there is none.
+  const float* device_query = nullptr;
   const float* Query() const { return own ? query_buf.data() : query; }
 };
 
@@ -840,7 +893,7 @@ SparseBatchCudaResult PipelinedTableStep(SparseCudaContext& ctx, const LoopTable
     const LiveRequest& l = active[static_cast<std::size_t>(b)];
     if (l.own) throw std::logic_error("a pipelined step's query is not in pinned memory");
     slots[static_cast<std::size_t>(b)] = table.SlotOf(l.a.state.request_id);
-    (*rows)[static_cast<std::size_t>(b)] = l.query;
+    (*rows)[static_cast<std::size_t>(b)] = l.device_query != nullptr ? l.device_query : l.query;
   }
   const double layout_ms = Ms(t0, Clock::now());
   const bool timing = run.timing_mode == SparseBatchTimingMode::kKernelEvents;
@@ -853,9 +906,9 @@ SparseBatchCudaResult PipelinedTableStep(SparseCudaContext& ctx, const LoopTable
   if (observe != nullptr) {
     ThrowOnError(dsd_sparse_async_wait(ctx.handle(), *ticket));
     observe->queries.resize(static_cast<std::size_t>(B) * E);
-    for (int b = 0; b < B; ++b) {
+    for (int b = 0; b < B; ++b) {  // (the host rows)
       std::memcpy(observe->queries.data() + static_cast<std::size_t>(b) * E,
-                  (*rows)[static_cast<std::size_t>(b)], sizeof(float) * E);
+                  active[static_cast<std::size_t>(b)].Query(), sizeof(float) * E);
     }
     observe->selected.assign(static_cast<std::size_t>(B) * std::max(1, top_k), 0);
     observe->selected_counts.assign(static_cast<std::size_t>(B), 0);
@@ -1087,6 +1140,10 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
   if (options.precompute_decode_payloads) {
     const auto t0 = Clock::now();
     payloads = BuildPayloads(config, specs, !options.gpu_synthetic_decode_append);
+    if (pipelined && DeviceQueryStore()) {
+      payloads.device_queries =
+          DeviceFloats(payloads.queries.data(), payloads.query_rows * static_cast<std::size_t>(E));
+    }
     stats.decode_payload_prep_ms = Ms(t0, Clock::now());
   }
   std::vector<double> step_ms;
@@ -1361,6 +1418,7 @@ ContinuousBatchStats RunContinuousSparseDecode(const ModelConfig& config,
       // read when the step is staged.
       if (options.precompute_decode_payloads) {
         l.query = payloads.NextQuery(a.spec_index, dstep, E);
+        l.device_query = payloads.NextQueryDevice(a.spec_index, dstep, E);
         l.own = false;
       } else if (pipelined) {
         l.query = slabs->Query(steps_run, static_cast<int>(li));  // generated above

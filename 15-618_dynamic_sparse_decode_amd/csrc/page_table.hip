@@ -306,4 +306,12 @@ void LaunchTableRelease(const PoolView& pool, const TableView& t, const int* slo
   DSD_HIP_CHECK(hipGetLastError());
 }
 
+void PreloadTableKernels() {
+  PreloadKernel(TablePlanAppendKernel);
+  PreloadKernel(TableReleaseKernel);
+  PreloadKernel(TableReleaseFinishKernel);
+  PreloadKernel(TableReserveKernel);
+  PreloadKernel(TableScatterKernel);
+}
+
 }  // namespace dsdk

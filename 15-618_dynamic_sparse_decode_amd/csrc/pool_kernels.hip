@@ -427,4 +427,11 @@ void LaunchMarkFree(const PoolView& pool, const int* d_page_ids, int n,
   DSD_HIP_CHECK(hipGetLastError());
 }
 
+void PreloadPoolKernels() {
+  PreloadKernel(StageInKernel);
+  PreloadKernel(StepMarkKernel);
+  PreloadKernel(AppendSyntheticKernel);
+  PreloadKernel(AppendTokensKernel);
+}
+
 }  // namespace dsdk

@@ -1124,4 +1124,11 @@ void LaunchAttention(const PoolView& pool, const AttentionArgs& args,
   DSD_HIP_CHECK(hipGetLastError());
 }
 
+void PreloadStepKernels() {
+  PreloadKernel(SelectAttnVariant().fn);
+  PreloadKernel(SelectCertifiedKernel);
+  PreloadKernel(SelectCertifiedRankKernel);
+  PreloadKernel(ScoreBoundGenericKernel);
+}
+
 }  // namespace dsdk

@@ -234,7 +234,8 @@ int dsd_sparse_run_staged(dsd_sparse_ctx* ctx, int batch, int output_mode,
 /* dsd_sparse_run_staged with request r's query read from query_rows[r]
  * (E floats) instead of the staging's queries; the candidate lists come
  * from the staging as before.  Every row must be 16-byte aligned and lie
- * inside a dsd_host_alloc block, or be the staging's own row r; anything
+ * inside a dsd_host_alloc or dsd_device_alloc block, or be the staging's
+ * own row r; anything
  * else fails with DSD_ERR_INVALID_ARGUMENT before any work.  The rows are
  * read by the device directly (no host copy), and the call returns after
  * the step, so they may change once it has returned.
@@ -252,6 +253,19 @@ int dsd_sparse_run_staged_rows(dsd_sparse_ctx* ctx, int batch,
  * counterpart: the memory behind dsd_sparse_run_staged_rows. */
 int dsd_host_alloc(size_t bytes, void** out);
 int dsd_host_free(void* p);
+
+/* Device memory whose rows the steps above accept as query rows, as they
+ * accept dsd_host_alloc rows: for queries that already live in HBM, as a
+ * model's own outputs do, so the step's stage-in reads them from HBM
+ * instead of across PCIe.  dsd_device_upload copies bytes of host memory
+ * (any kind) into such a block, synchronously; dsd_device_free takes only
+ * pointers from dsd_device_alloc (NULL is a no-op) and waits for the
+ * device first.  No reference counterpart: the reference's queries are host
+ * vectors copied in every step (src/cuda/sparse_batched_attention.cu:
+ * 24-96,600-640). */
+int dsd_device_alloc(size_t bytes, void** out);
+int dsd_device_upload(void* dst, const void* src, size_t bytes);
+int dsd_device_free(void* p);
 
 /* Device-resident step: every pointer is device memory and the call only
  * enqueues work on `stream` (a hipStream_t; NULL = the context's stream).

@@ -146,6 +146,49 @@ def test_async_pipeline_with_release_and_readmission(gpu):
         pool.close()
 
 
+def test_async_steps_read_query_rows_in_device_blocks(gpu):
+    """Query rows in dsd_device_alloc memory (HBM), mixed with pinned host
+    rows in one step, as the pipelined loop's device query store passes
+    them; both step forms agree with the oracle."""
+    rng = np.random.default_rng(76)
+    prompts = [8 * PS + 1, 25 * PS, 13 * PS + 9]
+    pool, table, mirror, ctx = setup(gpu, rng, prompts)
+    slots = [2, 0, 1]
+    dev = gpu.DeviceBlock(4 * len(slots) * E)
+    host = gpu.HostBlock(len(slots) * E)
+    try:
+        for step in range(4):
+            q = rng.standard_normal((len(slots), E)).astype(np.float32)
+            expected = mirror.oracle_step(q, [table.pages(s) for s in slots], H, D, K)
+            rows = []
+            for r in range(len(slots)):
+                if (r + step) % 2 == 0:
+                    off = (step * len(slots) + r) * E
+                    dev.upload(q[r], off)
+                    rows.append(dev.address + 4 * off)
+                else:
+                    host.array[r * E:(r + 1) * E] = q[r]
+                    rows.append(host.address + 4 * r * E)
+            t = ctx.run_table_async(table, slots, query_rows=rows)
+            ctx.async_wait(t)
+            check(ctx, len(slots), expected)
+            res = ctx.run_table(table, slots, query_rows=rows, want_ids=True)
+            (_, selected, outs), _, _ = expected
+            for r in range(len(slots)):
+                assert res["selected"][r].tolist() == selected[r].tolist()
+            assert orc.max_abs_diff(res["outputs"], outs) <= 1e-4
+            append_behind(rng, table, mirror, slots, fresh=step == 0)
+        with pytest.raises(gpu.InvalidArgument):  # past the block's end
+            ctx.run_table_async(table, slots[:1], query_rows=[dev.address + 4 * (dev.count - E + 4)])
+        ctx.async_collect()
+    finally:
+        ctx.close()
+        dev.close()
+        host.close()
+        table.close()
+        pool.close()
+
+
 def test_async_timed_three_kernel_steps(gpu):
     """Requests of more than 256 pages take the three-kernel step, timed by
     stage events; their records carry the stage times."""
