@@ -150,6 +150,8 @@ _SIGNATURES = {
     "dsd_device_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
     "dsd_device_upload": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
     "dsd_device_free": (ctypes.c_int, [ctypes.c_void_p]),
+    "dsd_synthetic_batch": (ctypes.c_int, [ctypes.c_int] * 9 + [_c_int_p, _c_float_p, _c_float_p,
+                                                                _c_float_p]),
     "dsd_sparse_run_batch_device": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_int] * 3
                                     + [ctypes.c_void_p] * 8),
     "dsd_sparse_run_batch_device_static": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_int] * 4
@@ -903,6 +905,39 @@ class SyntheticBatch:
             (B, E), dtype=dtype)
         self._key_pool = None
         self._value_pool = None
+        self.generator = "per-request PCG64 streams"
+
+    @classmethod
+    def reference(cls, num_heads, head_dim, page_size, batch, min_context, max_context, seed,
+                  distribution="normal", capacity=None):
+        """The batch in the reference's draw order (BuildSyntheticBatch,
+        src/synthetic_data.cpp:23-68): one std::mt19937(seed), the context
+        lengths, then per request its pages' keys, values, then its query
+        (dsd_synthetic_batch).  distribution "uniform" is the reference's
+        own U(-1, 1), value for value; "normal" draws
+        std::normal_distribution<float>(0, 1) on the same engine in the
+        same order.  One engine, so it is generated sequentially."""
+        lib = load_library()
+        lengths = np.zeros(max(batch, 1), np.int32)
+        dist = {"uniform": 0, "normal": 1}[distribution]
+        args = [num_heads, head_dim, page_size, batch, min_context, max_context, seed, dist]
+        _check(lib.dsd_synthetic_batch(*args, 0, _ptr(lengths, ctypes.c_int), None, None, None))
+        self = cls(num_heads, head_dim, page_size, lengths[:batch].tolist(), seed,
+                   capacity=capacity)
+        E = self.elements
+        kp = np.empty((self.capacity, page_size, E), np.float32)
+        vp = np.empty_like(kp)
+        q = np.empty((batch, E), np.float32)
+        _check(lib.dsd_synthetic_batch(*args, self.capacity, _ptr(lengths, ctypes.c_int),
+                                       _ptr(kp, ctypes.c_float), _ptr(vp, ctypes.c_float),
+                                       _ptr(q, ctypes.c_float)))
+        live = np.zeros(self.capacity, bool)
+        live[self.cand_ids] = True
+        kp[~live] = 0.0
+        vp[~live] = 0.0
+        self._key_pool, self._value_pool, self.queries = kp, vp, q
+        self.generator = f"reference draw order, {distribution}"
+        return self
 
     @property
     def batch(self):
@@ -923,6 +958,8 @@ class SyntheticBatch:
     def request_pages(self, r: int, out_keys=None, out_values=None):
         """Keys and values of request r's pages, [n_r][page_size][E] each
         (written into out_keys / out_values when given)."""
+        if self._streams is None or self.generator.startswith("reference"):
+            raise ValueError("request_pages needs the per-request streams")
         n = self.pages_per[r]
         shape = (n, self.page_size, self.elements)
         k = np.empty(shape, self.dtype) if out_keys is None else out_keys

@@ -13,6 +13,7 @@
 #include <memory>
 #include <mutex>
 #include <numeric>
+#include <random>
 #include <string>
 #include <thread>
 #include <vector>
@@ -2287,6 +2288,61 @@ int dsd_sparse_run_staged_rows(dsd_sparse_ctx* ctx, int batch, const float* cons
     Require(batch <= ctx->max_batch, "request batch exceeds sparse context capacity");
     HostStep(ctx, batch, true, nullptr, query_rows, ctx->h_offsets.ptr, ctx->h_ids.ptr,
              output_mode, timing_mode, nullptr, nullptr, selected, selected_counts, timings);
+  });
+}
+
+int dsd_synthetic_batch(int num_heads, int head_dim, int page_size, int batch,
+                        int min_context_tokens, int max_context_tokens, int seed,
+                        int distribution, int capacity_pages, int* context_tokens,
+                        float* key_pool, float* value_pool, float* queries) {
+  return Guard([&] {
+    Require(num_heads > 0 && head_dim > 0 && page_size > 0, "model shape must be positive");
+    Require(batch >= 0, "batch must be non-negative");
+    Require(min_context_tokens >= 0 && min_context_tokens <= max_context_tokens,
+            "context range must be 0 <= min <= max");
+    Require(distribution == DSD_SYNTHETIC_UNIFORM || distribution == DSD_SYNTHETIC_NORMAL,
+            "unknown distribution");
+    Require(context_tokens != nullptr, "context_tokens must be non-null");
+    // The reference's draw order (src/synthetic_data.cpp:23-68): one engine;
+    // every context length first, then per request and page the keys, then
+    // the values, then the request's query; one distribution object per
+    // vector, as the reference's Uniform() makes.
+    std::mt19937 rng(static_cast<std::mt19937::result_type>(seed));
+    std::uniform_int_distribution<int> length(min_context_tokens, max_context_tokens);
+    long long pages = 0;
+    for (int r = 0; r < batch; ++r) {
+      context_tokens[r] = length(rng);
+      pages += (context_tokens[r] + page_size - 1) / page_size;
+    }
+    if (key_pool == nullptr && value_pool == nullptr && queries == nullptr) return;
+    Require(key_pool != nullptr && value_pool != nullptr && queries != nullptr,
+            "key_pool, value_pool and queries go together");
+    Require(pages <= capacity_pages, "the batch's pages exceed capacity_pages");
+    const size_t E = static_cast<size_t>(num_heads) * static_cast<size_t>(head_dim);
+    const size_t page_floats = static_cast<size_t>(page_size) * E;
+    auto fill = [&](float* out, size_t n) {
+      if (distribution == DSD_SYNTHETIC_UNIFORM) {
+        std::uniform_real_distribution<float> dist(-1.0f, 1.0f);
+        for (size_t i = 0; i < n; ++i) out[i] = dist(rng);
+      } else {
+        std::normal_distribution<float> dist(0.0f, 1.0f);
+        for (size_t i = 0; i < n; ++i) out[i] = dist(rng);
+      }
+    };
+    long long g = 0;  // the batch's page g is pool page capacity - 1 - g (LIFO)
+    for (int r = 0; r < batch; ++r) {
+      const int n = context_tokens[r];
+      const int count = (n + page_size - 1) / page_size;
+      for (int j = 0; j < count; ++j, ++g) {
+        const size_t row = static_cast<size_t>(capacity_pages - 1 - g) * page_floats;
+        const size_t tokens = static_cast<size_t>(std::min(page_size, n - j * page_size));
+        std::fill(key_pool + row, key_pool + row + page_floats, 0.0f);
+        std::fill(value_pool + row, value_pool + row + page_floats, 0.0f);
+        fill(key_pool + row, tokens * E);
+        fill(value_pool + row, tokens * E);
+      }
+      fill(queries + static_cast<size_t>(r) * E, E);
+    }
   });
 }
 

@@ -57,9 +57,25 @@ CONFIGS = {
     4: (64, 4096, 16384, 32, 128, 64, 32, 13),
 }
 
-DATA = ("synthetic: N(0,1) fp32, one numpy PCG64 stream per request "
-        "(SeedSequence(seed).spawn(B+1)); context lengths in the reference draw order "
-        "(mt19937 + uniform_int)")
+# Configs 1 and 2 are generated in the reference's draw order
+# (BuildSyntheticBatch, src/synthetic_data.cpp:23-68) with N(0,1) values:
+# one std::mt19937(seed); the lengths (uniform_int_distribution); then per
+# request its pages' keys, values and its query from
+# std::normal_distribution<float> on the same engine.  That is one sequential
+# stream (about 10 s at config 2); configs 3 and 4 (8.6G and 5.6G values)
+# use one numpy stream per request instead, generated in parallel.
+REFERENCE_ORDER_CONFIGS = (1, 2)
+DATA_REFERENCE = ("synthetic: N(0,1) fp32 in the reference draw order: std::mt19937(seed), "
+                  "context lengths (uniform_int_distribution), then per request its pages' "
+                  "keys, values and its query from std::normal_distribution<float> "
+                  "(BuildSyntheticBatch's order, src/synthetic_data.cpp:23-68)")
+DATA_STREAMS = ("synthetic: N(0,1) fp32, one numpy PCG64 stream per request "
+                "(SeedSequence(seed).spawn(B+1)); context lengths in the reference draw "
+                "order (mt19937 + uniform_int)")
+
+
+def data_for(config):
+    return DATA_REFERENCE if config in REFERENCE_ORDER_CONFIGS else DATA_STREAMS
 
 
 def load_package():
@@ -98,8 +114,13 @@ class Workload:
         self.E = H * D
         self.lengths = dsd.reference_context_lengths(B, lo, hi, seed)
         t0 = time.time()
-        self.batch = dsd.SyntheticBatch(H, D, ps, self.lengths, seed=seed)
-        kp = self.batch.key_pool  # generated here (parallel streams)
+        if config in REFERENCE_ORDER_CONFIGS:
+            self.batch = dsd.SyntheticBatch.reference(H, D, ps, B, lo, hi, seed, "normal")
+            if self.batch.context_lengths != list(self.lengths):
+                raise RuntimeError("the generator's lengths differ from the reference draw")
+        else:
+            self.batch = dsd.SyntheticBatch(H, D, ps, self.lengths, seed=seed)
+        kp = self.batch.key_pool  # generated here
         log(f"config {config}: B={B} pages={self.batch.total_candidates} "
             f"tokens={sum(self.lengths)} generated in {time.time() - t0:.1f}s")
         self.copies = copies
@@ -393,7 +414,7 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": DATA,
+        "data": data_for(args.config),
         "config": {
             "workload": f"BASELINE config {args.config}: sparse decode step, B={B}, ctx "
                         f"U[{lo},{hi}] (seed {seed}), {H}x{D}, page {ps}, top-k {k}",
@@ -638,7 +659,7 @@ def sweep(dsd, torch, args):
         ctx.close()
         pool.close()
         del batch
-    print(json.dumps({"mode": "sweep", "data": DATA, "points": rows}), flush=True)
+    print(json.dumps({"mode": "sweep", "data": DATA_STREAMS, "points": rows}), flush=True)
     return 0
 
 

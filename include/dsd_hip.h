@@ -267,6 +267,26 @@ int dsd_device_alloc(size_t bytes, void** out);
 int dsd_device_upload(void* dst, const void* src, size_t bytes);
 int dsd_device_free(void* p);
 
+/* ---- synthetic inputs --------------------------------------------------- */
+/* BuildSyntheticBatch's draw order (src/synthetic_data.cpp:23-68): one
+ * std::mt19937(seed); the batch's context lengths first
+ * (uniform_int_distribution<int>(min, max)) into context_tokens[batch]; then
+ * for each request, page by page, its keys, then its values, then the
+ * request's query.  DSD_SYNTHETIC_UNIFORM draws U(-1, 1) as the reference
+ * does (its values bit for bit); DSD_SYNTHETIC_NORMAL draws
+ * std::normal_distribution<float>(0, 1) on the same engine in the same
+ * order (the benchmark's N(0, 1) inputs).  The batch's page g (requests in
+ * order, pages in logical order) is pool page capacity_pages - 1 - g, as the
+ * reference's LIFO page pool hands them out; key_pool / value_pool are
+ * [capacity_pages][page_size][E], queries [batch][E], rows past a page's
+ * tokens zero.  With key_pool, value_pool and queries all NULL only the
+ * lengths are drawn. */
+enum { DSD_SYNTHETIC_UNIFORM = 0, DSD_SYNTHETIC_NORMAL = 1 };
+int dsd_synthetic_batch(int num_heads, int head_dim, int page_size, int batch,
+                        int min_context_tokens, int max_context_tokens, int seed,
+                        int distribution, int capacity_pages, int* context_tokens,
+                        float* key_pool, float* value_pool, float* queries);
+
 /* Device-resident step: every pointer is device memory and the call only
  * enqueues work on `stream` (a hipStream_t; NULL = the context's stream).
  * total_candidates and max_candidates (largest n_r) must describe the CSR.
