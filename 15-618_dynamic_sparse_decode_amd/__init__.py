@@ -80,7 +80,7 @@ class PoolArrays(ctypes.Structure):
 class LaunchInfo(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "fused", "certified", "multi_pass", "heads_per_group", "grid",
-        "score_pages_per_group")]
+        "score_pages_per_group", "wide")]
 
     def as_dict(self):
         return {n: int(getattr(self, n)) for n, _ in self._fields_}

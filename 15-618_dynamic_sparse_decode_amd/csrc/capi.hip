@@ -1328,6 +1328,7 @@ struct StepLaunch {
   bool valid = false;
   bool certified = false;
   bool fused = false;
+  bool wide = false;  // the wide single launch (requests beyond the fused step's 256)
   int batch = 0, total = 0, max_n = 0;
   int top_k = 0;
   int compute_units = 256;
@@ -1342,6 +1343,9 @@ struct StepLaunch {
   float* lo = nullptr;
   float* hi = nullptr;
   unsigned long long* rec = nullptr;  // [3 * total] publication words
+  unsigned long long* sel_rec = nullptr;  // wide step: tagged ids, then counts
+  unsigned long long* cnt_rec = nullptr;
+  unsigned* wide_counters = nullptr;
   int* exact_pages = nullptr;         // may be null
   unsigned long long* fail_word = nullptr;
   unsigned epoch = 0;  // fresh (non-zero, below 2^30) for every launch
@@ -1443,8 +1447,33 @@ dsdk::FusedArgs FusedStepArgs(const PoolView& v, const StepLaunch& L) {
   return a;
 }
 
+// The wide step's arguments (dsdk::WideArgs): the fused step's, the score
+// slices of the stand-alone score kernel, and its scratch.
+dsdk::WideArgs WideStepArgs(const PoolView& v, const StepLaunch& L) {
+  dsdk::WideArgs w;
+  w.a = FusedStepArgs(v, L);
+  w.sel_rec = L.sel_rec;
+  w.cnt_rec = L.cnt_rec;
+  w.counters = L.wide_counters;
+  w.pages_per_group = dsdk::ScorePagesPerGroup(L.total);
+  w.groups = (L.max_n + w.pages_per_group - 1) / w.pages_per_group;
+  // Every score slice ahead of every attention item.  An attention item
+  // whose id falls in the first dispatch round occupies a CU from the
+  // launch on while it waits for its request's select; on 32 requests of
+  // 2048 pages the step spanned 379 us with all slices first and 427-489 us
+  // with 4 to 16 requests between a request's slices and its attention.
+  int lag = L.batch;
+  if (const char* env = std::getenv("DSD_WIDE_LAG")) lag = std::atoi(env);
+  w.lag = std::max(0, std::min(lag, L.batch));
+  return w;
+}
+
 // The whole step: one launch (fused) or score, select and attention.
 void EnqueueStep(const PoolView& v, const StepLaunch& L, hipStream_t s) {
+  if (L.wide) {
+    dsdk::LaunchWideStep(v, WideStepArgs(v, L), s);
+    return;
+  }
   if (L.fused) {
     dsdk::LaunchFusedStep(v, FusedStepArgs(v, L), s);
     return;
@@ -1474,6 +1503,7 @@ struct AsyncSlot {
   bool busy = false;
   bool timed = false;
   bool fused = false;
+  bool wide = false;
   bool new_timeline = false;  // the first step of a timeline
   int batch = 0;
   int stamp_grid = 0;
@@ -1498,6 +1528,11 @@ struct dsd_sparse_ctx {
   DeviceBuffer<unsigned long long> d_rec;
   // The epoch counter of captured fused launches (advanced on the device).
   DeviceBuffer<unsigned> d_epoch;
+  // The wide step's tagged selections ([max_batch][k] ids, then
+  // [max_batch] counts) and counters ([2 + max_batch], zero between
+  // launches).
+  DeviceBuffer<unsigned long long> d_sel_rec;
+  DeviceBuffer<unsigned> d_wide_counters;
   // The epoch of the step being enqueued: it tags the fused step's
   // publication words and every failure report of the step's kernels.
   unsigned epoch = 0;
@@ -1511,6 +1546,7 @@ struct dsd_sparse_ctx {
   int compute_units = 256;
   int score_mode = DSD_SCORE_CERTIFIED;
   bool fused_enabled = true;
+  bool wide_enabled = true;
   PinnedBuffer<float> h_queries, h_scores, h_outputs;
   PinnedBuffer<int> h_offsets, h_ids, h_selected, h_counts;
   // The step kernels' failure word: (epoch << 32) | code, pinned, coherent.
@@ -1596,12 +1632,20 @@ struct dsd_sparse_ctx {
     L.valid = true;
     L.certified = StepCertified(v, score_mode, max_n, need_exact_scores);
     L.fused = StepFused(v, L.certified, fused_enabled, max_n, top_k);
+    // The wide step takes the batches the single launch cannot (a request
+    // beyond 256 candidates); DSD_FUSED_STEP=0 alone keeps three kernels.
+    L.wide = !L.fused && L.certified && wide_enabled && batch > 0 &&
+             !dsdk::FusedStepSupported(v, max_n, top_k) &&
+             dsdk::WideStepSupported(v, max_n, top_k);
     L.batch = batch;
     L.total = total;
     L.max_n = max_n;
     L.top_k = top_k;
     L.compute_units = compute_units;
     L.scale = StepScale(v);
+    L.sel_rec = d_sel_rec.ptr;
+    L.cnt_rec = d_sel_rec.ptr + static_cast<size_t>(max_batch) * std::max(1, top_k);
+    L.wide_counters = d_wide_counters.ptr;
     L.scores = d_scores.ptr;
     L.selected = d_selected.ptr;
     L.counts = d_counts.ptr;
@@ -1670,6 +1714,21 @@ struct dsd_sparse_ctx {
     if (stamps == nullptr) stamps = &h_stamps;
     if (stamped == nullptr) stamped = &stamp_grid;
     DSD_HIP_CHECK(hipEventRecord(k[0], s));
+    if (L->wide) {
+      // One launch whose stages overlap: its whole time, and per-workgroup
+      // stamps.
+      dsdk::WideArgs w = WideStepArgs(v, *L);
+      const int grid = dsdk::WideStepGrid(v, L->batch, w.groups);
+      if (static_cast<size_t>(grid) * dsdk::WideStepStampsPerGroup() <= stamps->count) {
+        w.a.stamps = stamps->ptr;
+        *stamped = grid;
+      } else {
+        *stamped = 0;
+      }
+      dsdk::LaunchWideStep(v, w, s);
+      DSD_HIP_CHECK(hipEventRecord(k[3], s));
+      return;
+    }
     if (L->fused) {
       *stamped = EnqueueFusedStamped(*L, s, stamps);
       DSD_HIP_CHECK(hipEventRecord(k[3], s));
@@ -1732,6 +1791,10 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     DSD_HIP_CHECK(hipMemset(ctx->d_exact_pages.ptr, 0, sizeof(int)));
     ctx->d_epoch.Reserve(1);
     DSD_HIP_CHECK(hipMemset(ctx->d_epoch.ptr, 0, sizeof(unsigned)));
+    ctx->d_sel_rec.Reserve(B * K + B);
+    DSD_HIP_CHECK(hipMemset(ctx->d_sel_rec.ptr, 0, (B * K + B) * sizeof(unsigned long long)));
+    ctx->d_wide_counters.Reserve(B + 2);
+    DSD_HIP_CHECK(hipMemset(ctx->d_wide_counters.ptr, 0, (B + 2) * sizeof(unsigned)));
     {
       const size_t rec = 3 * P;
       // The largest fused grid: one head per workgroup.
@@ -1756,6 +1819,9 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     }
     if (const char* env = std::getenv("DSD_FUSED_STEP")) {
       ctx->fused_enabled = std::strcmp(env, "0") != 0;
+    }
+    if (const char* env = std::getenv("DSD_WIDE_STEP")) {
+      ctx->wide_enabled = std::strcmp(env, "0") != 0;
     }
     // The host step's staging: the step's kernels read the inputs from here
     // and write the outputs here directly (no DMA copies).
@@ -1827,6 +1893,11 @@ void HarvestAsync(dsd_sparse_ctx* ctx, AsyncSlot& a) {
   if (a.timed && a.fused) {
     ctx->FusedPhases(a.stamps.ptr, a.stamp_grid, &r.score_ms, &r.topk_ms, &r.attention_ms);
     r.kernel_ms = r.score_ms + r.topk_ms + r.attention_ms;
+  } else if (a.timed && a.wide) {
+    DSD_HIP_CHECK(hipEventSynchronize(a.k[3]));
+    float k = 0.f;
+    DSD_HIP_CHECK(hipEventElapsedTime(&k, a.k[0], a.k[3]));
+    r.kernel_ms = k;  // (its stages overlap: no split)
   } else if (a.timed) {
     // (the stream has passed them; the runtime reports them complete once
     // it has seen that)
@@ -2057,6 +2128,7 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
       async->busy = true;
       async->timed = timing;
       async->fused = L.fused;
+      async->wide = L.wide;
       async->batch = batch;
       async->epoch = L.epoch;
       t.launch_ms = MsSince(t0);
@@ -2098,6 +2170,11 @@ void HostStep(dsd_sparse_ctx* ctx, int batch, bool staged, const float* queries,
       DSD_HIP_CHECK(hipEventElapsedTime(&k, ctx->ev[0], ctx->ev[3]));
       ctx->FusedPhases(ctx->h_stamps.ptr, ctx->stamp_grid, &t.score_ms, &t.topk_ms,
                        &t.attention_ms);
+      t.kernel_ms = k;
+    } else if (timing && L.wide) {
+      // The wide step's stages overlap: only its whole time (kernel_ms).
+      float k = 0.f;
+      DSD_HIP_CHECK(hipEventElapsedTime(&k, ctx->ev[0], ctx->ev[3]));
       t.kernel_ms = k;
     } else if (timing) {
       float a = 0.f, b = 0.f, c = 0.f;
@@ -2436,6 +2513,7 @@ int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
             "a pool append is still pending: synchronise before capturing a step");
       }
       L.epoch_src = ctx->d_epoch.ptr;
+      L.wide = false;  // the wide step takes its epoch from the host: three kernels
       ctx->last_stream = nullptr;
     } else {
       ctx->pool->OrderAfterPending(s);
@@ -2452,7 +2530,10 @@ int dsd_sparse_replay_stage(dsd_sparse_ctx* ctx, int stage, void* stream) {
     Require(ctx->last.valid, "no previous step to replay");
     hipStream_t s = stream != nullptr ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
     Require(stage >= 0 && stage <= 3, "stage must be 0, 1, 2 or 3");
-    if (stage == 3) Require(ctx->last.fused, "the last step did not use the single-launch kernel");
+    if (stage == 3) {
+      Require(ctx->last.fused || ctx->last.wide,
+              "the last step did not use a single-launch kernel");
+    }
     ctx->pool->OrderAfterPending(s);
     ctx->OrderOn(s);
     StepLaunch L = ctx->last;
@@ -2507,8 +2588,13 @@ int dsd_sparse_last_launch(const dsd_sparse_ctx* ctx, dsd_launch_info* out) {
     const dsdk::PoolView& v = ctx->pool->view;
     *out = dsd_launch_info{};
     out->fused = L.fused ? 1 : 0;
+    out->wide = L.wide ? 1 : 0;
     out->certified = L.certified ? 1 : 0;
-    if (L.fused) {
+    if (L.wide) {
+      const int per = dsdk::ScorePagesPerGroup(L.total);
+      out->score_pages_per_group = per;
+      out->grid = dsdk::WideStepGrid(v, L.batch, (L.max_n + per - 1) / per);
+    } else if (L.fused) {
       const int hpw = dsdk::FusedStepHeadsPerGroup(v, L.batch, ctx->compute_units);
       out->heads_per_group = hpw;
       out->multi_pass = dsdk::FusedStepMultiPass(v, L.max_n, hpw) ? 1 : 0;
@@ -2527,7 +2613,8 @@ int dsd_sparse_step_stamps(const dsd_sparse_ctx* ctx, int* grid, int* per_group,
     Require(ctx != nullptr && grid != nullptr && per_group != nullptr && khz != nullptr,
             "pointers must be non-null");
     *grid = ctx->stamp_grid;
-    *per_group = dsdk::FusedStepStampsPerGroup();
+    *per_group = ctx->last.wide ? dsdk::WideStepStampsPerGroup()
+                                : dsdk::FusedStepStampsPerGroup();
     *khz = ctx->wall_khz;
     if (out == nullptr) return;
     const size_t n = static_cast<size_t>(ctx->stamp_grid) * static_cast<size_t>(*per_group);

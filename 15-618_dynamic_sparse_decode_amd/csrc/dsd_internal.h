@@ -304,6 +304,36 @@ bool FusedStepMultiPass(const PoolView& pool, int max_candidates, int heads_per_
 int ScorePagesPerGroup(int total_candidates);
 void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t stream);
 
+// The wide step (step_kernels.hip): the certified three-kernel step for
+// E = 4096, head_dim 128 and up to WideStepMaxCandidates() candidates per
+// request in one launch: a workgroup per score slice (groups per request),
+// then a workgroup per (request, head pair) of attention; the last slice of
+// a request to finish selects it.  a: as for LaunchFusedStep (rec: the
+// interval words, 3 per candidate; sel_stride = top_k; no epoch_src).
+// sel_rec: [batch][sel_stride] tagged selected ids; cnt_rec: [batch] tagged
+// counts; counters: [1] finished workgroups, [2 .. 2 + batch) arrivals, zero
+// between launches (the kernel's last workgroup resets them).
+struct WideArgs {
+  FusedArgs a;
+  unsigned long long* sel_rec = nullptr;
+  unsigned long long* cnt_rec = nullptr;
+  unsigned* counters = nullptr;
+  int pages_per_group = 0;  // candidates per score item (a multiple of 8)
+  int groups = 0;           // score items per request
+  int lag = 0;              // a request's attention items follow the score
+                            // items of the request `lag` places later
+};
+bool WideStepSupported(const PoolView& pool, int max_candidates, int top_k);
+int WideStepMaxCandidates();
+int WideStepGrid(const PoolView& pool, int batch, int groups);
+// Timing mode (FusedArgs::stamps): per workgroup the clocks at start, select
+// start and end (0 when it selected nothing), end, and in slot 1 the item
+// kind (bits 0-7: 0 score slice, 1 attention item) and request (bits 8+).
+int WideStepStampsPerGroup();
+void LaunchWideStep(const PoolView& pool, const WideArgs& w, hipStream_t stream);
+// One thread advances a captured step's device epoch counter (see FusedArgs).
+void LaunchEpochBump(unsigned* epoch, hipStream_t stream);
+
 // Certified intervals for E = 4096 with the fused step's score passes
 // (float, query staged in LDS, 8..64 pages per 1024-thread workgroup).
 void LaunchScorePages(const PoolView& pool, const float* d_queries, const int* d_cand_offsets,

@@ -9,6 +9,7 @@
 #include <cstdlib>
 
 #include "dsd_internal.h"
+#include "score_slice.h"
 #include "step_common.h"
 
 namespace dsdk {
@@ -315,26 +316,52 @@ __device__ void RankSortDesc(const uint64_t* keys, const int* idx, int count,
   __syncthreads();
 }
 
-__global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
-    const float* __restrict__ mid, const float* __restrict__ lo,
-    const float* __restrict__ hi, const float* __restrict__ queries,
-    const float* __restrict__ summaries, const int* __restrict__ token_counts, int capacity,
-    const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int total,
-    int max_candidates, int E, float scale, int top_k, int* __restrict__ selected,
-    int* __restrict__ counts, int* __restrict__ exact_pages, FailReport fail) {
-  __shared__ uint64_t keys[kCertMaxKeys];   // by candidate
-  __shared__ float s_lo[kCertMaxKeys];
-  __shared__ float s_hi[kCertMaxKeys];
-  __shared__ uint8_t member[kCertMaxKeys];  // by candidate
-  __shared__ uint64_t skeys[kCertMaxKeys];  // the members, then the final set, sorted
-  __shared__ int sidx[kCertMaxKeys];
-  __shared__ int flagged[kCertMaxKeys];
-  __shared__ int hist[256];
-  __shared__ __align__(16) float tile[RescoreFloats<kSelRescoreGroup>()];
-  __shared__ float s_red[2][kSelThreads / kWave];
-  __shared__ unsigned long long s_prefix;
-  __shared__ int s_need, s_all, s_count, s_tie, s_nflag;
-  const int r = blockIdx.x;
+// The LDS of one request's certified select (kSelThreads threads).
+struct CertShared {
+  uint64_t keys[kCertMaxKeys];   // by candidate
+  float s_lo[kCertMaxKeys];
+  float s_hi[kCertMaxKeys];
+  uint8_t member[kCertMaxKeys];  // by candidate
+  uint64_t skeys[kCertMaxKeys];  // the members, then the final set, sorted
+  int sidx[kCertMaxKeys];
+  int flagged[kCertMaxKeys];
+  int hist[256];
+  alignas(16) float tile[RescoreFloats<kSelRescoreGroup>()];
+  float s_red[2][kSelThreads / kWave];
+  unsigned long long s_prefix;
+  int s_need, s_all, s_count, s_tie, s_nflag, s_bad;
+};
+
+// Request r's certified top-k (up to kCertMaxKeys candidates, the whole
+// workgroup of kSelThreads threads).  load(c, &mid, &lo, &hi) gives candidate
+// c's first-pass interval (c indexes the batch's CSR); with kPolled it may
+// report that an interval never became readable (false), and the request
+// then selects nothing (kFailWait).  emit(i, page) writes member i of the
+// selection (rank order), emit_count(kk) the count; emit_count runs once, in
+// thread 0, after the emits.
+template <bool kPolled, class Load, class Emit, class EmitCount>
+__device__ __forceinline__ void SelectCertifiedRequest(
+    CertShared& sh, int r, Load load, Emit emit, EmitCount emit_count,
+    const float* __restrict__ queries, const float* __restrict__ summaries,
+    const int* __restrict__ token_counts, int capacity, const int* __restrict__ cand_offsets,
+    const int* __restrict__ cand_ids, int total, int max_candidates, int E, float scale,
+    int top_k, int* __restrict__ exact_pages, FailReport fail) {
+  uint64_t* keys = sh.keys;
+  float* s_lo = sh.s_lo;
+  float* s_hi = sh.s_hi;
+  uint8_t* member = sh.member;
+  uint64_t* skeys = sh.skeys;
+  int* sidx = sh.sidx;
+  int* flagged = sh.flagged;
+  int* hist = sh.hist;
+  float* tile = sh.tile;
+  float (&s_red)[2][kSelThreads / kWave] = sh.s_red;
+  unsigned long long& s_prefix = sh.s_prefix;
+  int& s_need = sh.s_need;
+  int& s_all = sh.s_all;
+  int& s_count = sh.s_count;
+  int& s_tie = sh.s_tie;
+  int& s_nflag = sh.s_nflag;
   int begin, n;
   RequestRange(cand_offsets, r, total, fail, &begin, &n);
   if (n > max_candidates || n > kCertMaxKeys) {
@@ -345,14 +372,20 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
   }
   const int kk = top_k <= 0 ? 0 : (top_k < n ? top_k : n);
   if (kk == 0) {
-    if (threadIdx.x == 0) counts[r] = 0;
+    if (threadIdx.x == 0) emit_count(0);
     return;
   }
   const int* cand = cand_ids + begin;
+  if constexpr (kPolled) {
+    if (threadIdx.x == 0) sh.s_bad = 0;
+    __syncthreads();
+  }
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    keys[i] = SelectKey(mid[begin + i], cand[i]);
-    s_lo[i] = lo[begin + i];
-    s_hi[i] = hi[begin + i];
+    float m, l, h;
+    if (!load(begin + i, &m, &l, &h)) sh.s_bad = 1;
+    keys[i] = SelectKey(m, cand[i]);
+    s_lo[i] = l;
+    s_hi[i] = h;
   }
   if (threadIdx.x == 0) {
     s_count = 0;
@@ -360,6 +393,15 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
     s_nflag = 0;
   }
   __syncthreads();
+  if constexpr (kPolled) {
+    if (sh.s_bad != 0) {
+      if (threadIdx.x == 0) {
+        ReportFailure(fail, kFailWait);
+        emit_count(0);
+      }
+      return;
+    }
+  }
 
   const int wave = threadIdx.x / kWave;
   const int nwaves = (blockDim.x + kWave - 1) / kWave;
@@ -502,9 +544,32 @@ __global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
     RankSortDesc(skeys, sidx, s_count, tkeys, tidx);
   }
   const uint64_t* final_keys = nflag > 0 ? tkeys : skeys;
+  for (int i = threadIdx.x; i < kk; i += blockDim.x) emit(i, KeyPage(final_keys[i]));
+  if constexpr (kPolled) __syncthreads();  // every member out before the count
+  if (threadIdx.x == 0) emit_count(kk);
+}
+
+__global__ __launch_bounds__(kSelThreads) void SelectCertifiedKernel(
+    const float* __restrict__ mid, const float* __restrict__ lo,
+    const float* __restrict__ hi, const float* __restrict__ queries,
+    const float* __restrict__ summaries, const int* __restrict__ token_counts, int capacity,
+    const int* __restrict__ cand_offsets, const int* __restrict__ cand_ids, int total,
+    int max_candidates, int E, float scale, int top_k, int* __restrict__ selected,
+    int* __restrict__ counts, int* __restrict__ exact_pages, FailReport fail) {
+  __shared__ CertShared sh;
+  const int r = blockIdx.x;
   int* out = selected + static_cast<size_t>(r) * top_k;
-  for (int i = threadIdx.x; i < kk; i += blockDim.x) out[i] = KeyPage(final_keys[i]);
-  if (threadIdx.x == 0) counts[r] = kk;
+  SelectCertifiedRequest<false>(
+      sh, r,
+      [&](int c, float* m, float* l, float* h) {
+        *m = mid[c];
+        *l = lo[c];
+        *h = hi[c];
+        return true;
+      },
+      [&](int i, int page) { out[i] = page; }, [&](int kk) { counts[r] = kk; }, queries,
+      summaries, token_counts, capacity, cand_offsets, cand_ids, total, max_candidates, E,
+      scale, top_k, exact_pages, fail);
 }
 
 // Certified select for up to 256 candidates per request: thread i owns
@@ -822,28 +887,29 @@ __global__ __launch_bounds__(kAttnThreads) void AttentionKernel(
 // LPT lanes per token (each owns D/LPT contiguous dims), 64/LPT tokens per
 // chunk, UNROLL chunks whose K and V rows are all requested before any is
 // consumed (bytes in flight per wave = UNROLL * 64/LPT * 2 * D * 4).
-template <int D, int LPT, int WAVES, int UNROLL>
-__global__ __launch_bounds__(WAVES * kWave) void AttentionFastKernel(
-    PoolView pool, AttentionArgs args) {
+template <int WAVES, int D>
+struct AttnFastShared {
+  float m[WAVES];
+  float l[WAVES];
+  alignas(16) float acc[WAVES][D];
+};
+
+// Head h of request r over the `count` pages of `list` (global or LDS), by
+// WAVES waves whose thread index within the head is tid; ends with a
+// workgroup barrier (every thread of the workgroup must call it).
+template <int D, int LPT, int WAVES, int UNROLL, class List>
+__device__ __forceinline__ void AttentionFastHead(const PoolView& pool, const AttentionArgs& args,
+                                                  int h, int r, int tid, List list, int count,
+                                                  AttnFastShared<WAVES, D>& sh) {
   constexpr int DQ = D / LPT;
   constexpr int TPC = kWave / LPT;
   static_assert(DQ % 4 == 0, "float4 rows");
-  const int h = blockIdx.x;
-  const int r = blockIdx.y;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
   const int g = lane / LPT;
   const int j = lane % LPT;
   const int E = pool.elements;
   const int ps = pool.page_size;
-  int start, count;
-  if (args.list_stride > 0) {
-    start = r * args.list_stride;
-    count = args.list_counts[r];
-  } else {
-    start = args.list_offsets[r];
-    count = args.list_offsets[r + 1] - start;
-  }
   const int head_off = h * D + j * DQ;
   float q[DQ];
   float acc[DQ];
@@ -870,7 +936,7 @@ __global__ __launch_bounds__(WAVES * kWave) void AttentionFastKernel(
       if (f < total) {
         const int slot = f / ps;
         const int t = f - slot * ps;
-        const int page = args.list_ids[start + slot];
+        const int page = list[slot];
         valid[u] = InPool(page, pool.capacity) && t < pool.token_counts[page];
         if (valid[u]) {
           const size_t off = static_cast<size_t>(page) * pool.page_elems +
@@ -914,9 +980,9 @@ __global__ __launch_bounds__(WAVES * kWave) void AttentionFastKernel(
 #pragma unroll
     for (int i = 0; i < DQ; ++i) acc[i] += __shfl_xor(acc[i], o, kWave);
   }
-  __shared__ float s_m[WAVES];
-  __shared__ float s_l[WAVES];
-  __shared__ __align__(16) float s_acc[WAVES][D];
+  float* s_m = sh.m;
+  float* s_l = sh.l;
+  float (&s_acc)[WAVES][D] = sh.acc;
   if (g == 0) {
     if (j == 0) {
       s_m[wave] = wm;
@@ -930,7 +996,7 @@ __global__ __launch_bounds__(WAVES * kWave) void AttentionFastKernel(
 #pragma unroll
   for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, s_m[w]);
   float* out = args.outputs + static_cast<size_t>(r) * E + static_cast<size_t>(h) * D;
-  for (int d = threadIdx.x; d < D; d += WAVES * kWave) {
+  for (int d = tid; d < D; d += WAVES * kWave) {
     float lt = 0.0f;
     float at = 0.0f;
     if (mx != -INFINITY) {
@@ -942,6 +1008,243 @@ __global__ __launch_bounds__(WAVES * kWave) void AttentionFastKernel(
       }
     }
     out[d] = lt == 0.0f ? 0.0f : at / lt;
+  }
+}
+
+template <int D, int LPT, int WAVES, int UNROLL>
+__global__ __launch_bounds__(WAVES * kWave) void AttentionFastKernel(
+    PoolView pool, AttentionArgs args) {
+  __shared__ AttnFastShared<WAVES, D> sh;
+  const int r = blockIdx.y;
+  int start, count;
+  if (args.list_stride > 0) {
+    start = r * args.list_stride;
+    count = args.list_counts[r];
+  } else {
+    start = args.list_offsets[r];
+    count = args.list_offsets[r + 1] - start;
+  }
+  AttentionFastHead<D, LPT, WAVES, UNROLL>(pool, args, blockIdx.x, r, threadIdx.x,
+                                           args.list_ids + start, count, sh);
+}
+
+
+// ---------------------------------------------------------------------------
+// 4. The wide step: the three-kernel step (E = 4096, head_dim 128, up to
+// kCertMaxKeys candidates per request) in one launch.
+//
+// Workgroup i does one item: a score slice (request r, slice x: candidates
+// [P*x, P*x + P), G slices per request) or an attention item (request r,
+// heads 2p and 2p + 1: waves 0-7 take one head, waves 8-15 the other).  The
+// workgroup that scores a request's last slice (an arrival counter per
+// request) runs that request's certified select.  Items are ordered request
+// by request, with each request's attention items placed after the score
+// slices of the request `lag` places later (WideItemOf): by the time they
+// are dispatched their select has usually finished, and HBM streams K/V for
+// early requests while later ones still score and select.  The stages of
+// different requests overlap instead of running one after another with HBM
+// idle between them (reference: the score -> top-k -> attention sequence
+// of src/cuda/sparse_batched_attention.cu:665-762 and its k > 16 path,
+// :703-731).
+//
+// Intervals, selected ids and counts cross workgroups as epoch-tagged
+// words (score_slice.h): no fences.
+//
+// Every wait ends.  A score slice never waits; the select that follows a
+// request's last slice waits only for interval words that the request's
+// slices wrote before they arrived.  An attention item waits for its
+// request's select, that is for score slices with lower ids.  Workgroup i
+// goes to XCD i mod 8 and each XCD dispatches its share in id order.  Take
+// the lowest-id attention item that waits: on every XCD, everything before
+// the slices it waits for is a score slice (which finishes) or an attention
+// item with a lower id (which, by the choice, does not wait forever), so
+// those slices are dispatched, run and arrive, and the select runs.  The
+// polls are bounded anyway (kFailWait, zero outputs, never a hang).  The
+// last workgroup to finish resets the arrival counters for the next launch.
+//
+// A persistent form (one workgroup per CU taking items from a counter)
+// spilled 188 bytes per lane: values the compiler hoisted out of the item
+// loop stay live across all three item kinds.
+// ---------------------------------------------------------------------------
+constexpr int kWideAttnWaves = kFWaves / 2;  // one head per half-workgroup
+constexpr int kWideStamps = 5;  // per workgroup in timing mode
+
+struct WideShared {
+  union {
+    ScoreShared score;
+    CertShared cert;
+    AttnFastShared<kWideAttnWaves, 128> attn[2];
+  };
+  int page[kCertMaxKeys];  // an attention item's selected pages
+  int last;
+  int count;
+  unsigned long long stamp[3];  // timing mode: start, select start and end
+};
+
+// A tagged word once it carries `tag` (spin_limit polls, sleeping between),
+// or false.
+__device__ __forceinline__ bool AwaitTagged(unsigned long long* p, unsigned tag,
+                                            unsigned spin_limit, unsigned long long* out) {
+  unsigned long long w = LoadWord(p);
+  for (unsigned i = 0; static_cast<unsigned>(w >> 32) != tag; ++i) {
+    if (i >= spin_limit) return false;
+    __builtin_amdgcn_s_sleep(1);
+    w = LoadWord(p);
+  }
+  *out = w;
+  return true;
+}
+
+// Item i's kind (0 score slice, 1 attention), request and slice or head
+// pair: request r's G slices, then (for r >= lag) request r - lag's Q head
+// pairs, request by request; after the last request the remaining lag
+// requests' head pairs.
+__device__ __forceinline__ int WideItemOf(int i, int batch, int G, int Q, int lag, int* r,
+                                          int* sub) {
+  const int head = lag * G;
+  if (i < head) {
+    *r = i / G;
+    *sub = i - *r * G;
+    return 0;
+  }
+  const int block = G + Q;
+  const int j = (i - head) / block;
+  if (j < batch - lag) {
+    const int off = i - head - j * block;
+    if (off < G) {
+      *r = lag + j;
+      *sub = off;
+      return 0;
+    }
+    *r = j;
+    *sub = off - G;
+    return 1;
+  }
+  const int t = i - head - (batch - lag) * block;
+  *r = batch - lag + t / Q;
+  *sub = t - (t / Q) * Q;
+  return 1;
+}
+
+__global__ __launch_bounds__(kFThreads) void WideStepKernel(PoolView pool, WideArgs w) {
+  __shared__ WideShared sh;
+  // (no captured form: the host runs captured steps in three kernels)
+  const FusedArgs& a = w.a;
+  const int pairs = pool.num_heads / 2;
+  const int stride = a.sel_stride;
+  int item_r, item_sub;
+  const int kind = WideItemOf(static_cast<int>(blockIdx.x), a.batch, w.groups, pairs, w.lag,
+                              &item_r, &item_sub);
+  // Timing mode: thread 0's clocks (start, select start and end, end) and
+  // the item kind, written out at the end.
+  // (kept in LDS: a register would stay live across the whole item)
+  if (a.stamps != nullptr && threadIdx.x == 0) {
+    sh.stamp[0] = wall_clock64();
+    sh.stamp[1] = 0;
+    sh.stamp[2] = 0;
+  }
+  if (kind == 0) {
+    const int r = item_r;
+    const int x = item_sub;
+    int begin, n;
+    if (RequestRange(a.cand_offsets, r, a.total, x == 0 ? a.fail : FailReport{}, &begin, &n)) {
+      const int c0 = x * w.pages_per_group;
+      if (c0 < n) {
+        const int c1 = n - c0 < w.pages_per_group ? n : c0 + w.pages_per_group;
+        ScoreSlice<true>(pool, a, r, begin + c0, begin + c1, sh.score);
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(w.counters + 2 + r, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      sh.last = prev == static_cast<unsigned>(w.groups - 1) ? 1 : 0;
+    }
+    __syncthreads();
+    if (sh.last != 0) {
+      if (a.stamps != nullptr && threadIdx.x == 0) sh.stamp[1] = wall_clock64();
+      unsigned long long* sel = w.sel_rec + static_cast<size_t>(r) * stride;
+      int* out = a.selected + static_cast<size_t>(r) * stride;
+      SelectCertifiedRequest<true>(
+          sh.cert, r,
+          [&](int c, float* m, float* l, float* h) {
+            unsigned long long* p = a.rec + 3 * static_cast<size_t>(c);
+            unsigned long long w0 = 0, w1 = 0, w2 = 0;
+            const bool ok = AwaitTagged(p, a.wait_tag, a.spin_limit, &w0) &&
+                            AwaitTagged(p + 1, a.wait_tag, a.spin_limit, &w1) &&
+                            AwaitTagged(p + 2, a.wait_tag, a.spin_limit, &w2);
+            *m = __uint_as_float(static_cast<uint32_t>(w0));
+            *l = __uint_as_float(static_cast<uint32_t>(w1));
+            *h = __uint_as_float(static_cast<uint32_t>(w2));
+            return ok;
+          },
+          [&](int i, int page) {
+            out[i] = page;
+            PutTagged(sel + i, a.epoch, static_cast<uint32_t>(page));
+          },
+          [&](int kk) {
+            a.counts[r] = kk;
+            PutTagged(w.cnt_rec + r, a.epoch, static_cast<uint32_t>(kk));
+          },
+          a.queries, pool.summaries, pool.token_counts, pool.capacity, a.cand_offsets,
+          a.cand_ids, a.total, a.max_candidates, pool.elements, a.scale, a.top_k,
+          a.exact_pages, a.fail);
+      if (a.stamps != nullptr && threadIdx.x == 0) sh.stamp[2] = wall_clock64();
+    }
+  } else {
+    const int r = item_r;
+    const int hp = item_sub;
+    if (threadIdx.x == 0) {
+      unsigned long long word = 0;
+      int count = 0;
+      if (AwaitTagged(w.cnt_rec + r, a.wait_tag, a.spin_limit, &word)) {
+        count = static_cast<int>(static_cast<uint32_t>(word));
+      } else {
+        ReportFailure(a.fail, kFailWait);
+      }
+      sh.count = count < stride ? count : stride;
+    }
+    __syncthreads();
+    const int count = sh.count;
+    unsigned long long* sel = w.sel_rec + static_cast<size_t>(r) * stride;
+    for (int i = threadIdx.x; i < count; i += blockDim.x) {
+      unsigned long long word = 0;
+      int page = -1;  // never attended (InPool fails)
+      if (AwaitTagged(sel + i, a.wait_tag, a.spin_limit, &word)) {
+        page = static_cast<int>(static_cast<uint32_t>(word));
+      } else {
+        ReportFailure(a.fail, kFailWait);
+      }
+      sh.page[i] = page;
+    }
+    __syncthreads();
+    AttentionArgs args;
+    args.queries = a.queries;
+    args.scale = a.scale;
+    args.outputs = a.outputs;
+    const int half = threadIdx.x / (kWideAttnWaves * kWave);
+    AttentionFastHead<128, 16, kWideAttnWaves, 4>(pool, args, 2 * hp + half, r,
+                                                  threadIdx.x - half * kWideAttnWaves * kWave,
+                                                  sh.page, count, sh.attn[half]);
+  }
+  if (a.stamps != nullptr && threadIdx.x == 0) {
+    unsigned long long* st = a.stamps + static_cast<size_t>(kWideStamps) * blockIdx.x;
+    st[0] = sh.stamp[0];
+    st[1] = static_cast<unsigned long long>(kind) | (static_cast<unsigned long long>(item_r) << 8);
+    st[2] = sh.stamp[1];
+    st[3] = sh.stamp[2];
+    st[4] = wall_clock64();
+  }
+  if (threadIdx.x == 0) {
+    // The last workgroup to finish: every slice has arrived.
+    const unsigned prev =
+        __hip_atomic_fetch_add(w.counters + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == gridDim.x - 1) {
+      for (int q = 0; q < a.batch; ++q) {
+        __hip_atomic_store(w.counters + 2 + q, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __hip_atomic_store(w.counters + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -1074,6 +1377,42 @@ void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float
 
 int SelectMaxCandidates() { return kSelectMaxKeys; }
 
+bool WideStepSupported(const PoolView& pool, int max_candidates, int top_k) {
+  return pool.elements == kFE && pool.head_dim == 128 && pool.num_heads % 2 == 0 &&
+         pool.page_size > 0 && max_candidates > 0 && max_candidates <= kCertMaxKeys &&
+         top_k <= kCertMaxKeys;
+}
+
+int WideStepMaxCandidates() { return kCertMaxKeys; }
+
+int WideStepStampsPerGroup() { return kWideStamps; }
+
+int WideStepGrid(const PoolView& pool, int batch, int groups) {
+  return batch * groups + batch * (pool.num_heads / 2);
+}
+
+void LaunchWideStep(const PoolView& pool, const WideArgs& w, hipStream_t stream) {
+  if (w.a.batch <= 0) return;
+  if (!WideStepSupported(pool, w.a.max_candidates, w.a.top_k)) {
+    throw std::invalid_argument("the wide step needs E = 4096, head_dim 128, an even head "
+                                "count and at most 2048 candidates per request");
+  }
+  if (w.pages_per_group <= 0 || w.pages_per_group % kFPagesPerPass != 0 ||
+      static_cast<long long>(w.groups) * w.pages_per_group < w.a.max_candidates) {
+    throw std::invalid_argument("wide step slices do not cover max_candidates");
+  }
+  if (w.a.rec == nullptr || w.sel_rec == nullptr || w.cnt_rec == nullptr ||
+      w.counters == nullptr || w.a.sel_stride < (w.a.top_k > 0 ? w.a.top_k : 1)) {
+    throw std::invalid_argument("wide step scratch missing");
+  }
+  if (w.a.epoch_src != nullptr) {
+    throw std::invalid_argument("the wide step takes its epoch from the host (not captured)");
+  }
+  const int grid = WideStepGrid(pool, w.a.batch, w.groups);
+  hipLaunchKernelGGL(WideStepKernel, dim3(grid), dim3(kFThreads), 0, stream, pool, w);
+  DSD_HIP_CHECK(hipGetLastError());
+}
+
 void LaunchSelectTopK(const float* d_scores, const int* d_cand_offsets,
                       const int* d_cand_ids, int batch, int total_candidates,
                       int max_candidates, int top_k, int* d_selected, int* d_counts,
@@ -1125,6 +1464,7 @@ void LaunchAttention(const PoolView& pool, const AttentionArgs& args,
 }
 
 void PreloadStepKernels() {
+  PreloadKernel(WideStepKernel);
   PreloadKernel(SelectAttnVariant().fn);
   PreloadKernel(SelectCertifiedKernel);
   PreloadKernel(SelectCertifiedRankKernel);

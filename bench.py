@@ -266,6 +266,13 @@ def main() -> int:
     w.ctx.device_status()
     log(f"graph replay ({GRAPH_STEPS} steps per graph): {graph_ms * 1e3:.1f} us per step")
 
+    # One eager step again: a captured step runs in three kernels when the
+    # eager one is the wide launch, and the replays below re-run the last
+    # step's form.
+    w.step(sptr)
+    torch.cuda.synchronize()
+    w.ctx.device_status()
+
     # Per-kernel average durations: K back-to-back launches of one kernel on
     # the same stream.  Stages 0-2 are the three-kernel step (score, select,
     # attention); stage 3 is the single-launch fused step.  Every replay block
@@ -295,11 +302,12 @@ def main() -> int:
         return ms
 
     stage_ms = [replay_ms(stage) for stage in range(3)]
-    fused_ms = replay_ms(3) if launch["fused"] else None
+    wide = bool(launch.get("wide"))
+    fused_ms = replay_ms(3) if launch["fused"] or wide else None
     log("three-kernel stages us: score %.1f select %.1f attention %.1f"
         % tuple(x * 1e3 for x in stage_ms))
     if fused_ms is not None:
-        log(f"fused single-launch step kernel: {fused_ms * 1e3:.1f} us")
+        log(f"{'wide' if wide else 'fused'} single-launch step kernel: {fused_ms * 1e3:.1f} us")
 
     # Algorithmic bytes per launch (fp32), over the timed step's selection.
     sel_h = sel_ref
@@ -376,17 +384,23 @@ def main() -> int:
         "attention": {"us": stage_ms[2] * 1e3, "bytes": attn_bytes,
                       "GBps": attn_bytes / (stage_ms[2] * 1e-3) / 1e9},
         "note": "each kernel of the three-kernel step launched alone, back to back; the select "
-                "re-runs on intervals that its previous run may have refined and with its code "
-                "warm, so it reads low; step_phases_us times the phases of one real step",
+                "re-runs with its code warm, so it reads low; step_phases_us times the phases "
+                "of one real step",
     }
     if fused_ms is not None:
-        stages["fused_step"] = {"us": fused_ms * 1e3, "bytes": step_bytes,
-                                "GBps": step_bytes / (fused_ms * 1e-3) / 1e9}
-        roof_kernel = ("FusedStepKernel: page scoring + certified top-k + fused gather/"
-                       "attention in one launch")
+        stages["wide_step" if wide else "fused_step"] = {
+            "us": fused_ms * 1e3, "bytes": step_bytes,
+            "GBps": step_bytes / (fused_ms * 1e-3) / 1e9}
+        if wide:
+            roof_kernel = ("WideStepKernel: score slices, certified top-k (by each request's "
+                           "last slice) and fused gather/attention in one launch")
+        else:
+            roof_kernel = ("FusedStepKernel: page scoring + certified top-k + fused gather/"
+                           "attention in one launch")
         # The step is this one launch: its duration is the timed step's
         # (events around the K timed steps, launch gaps included).
-        roof_name, roof_bytes, roof_ms = "FusedStepKernel", step_bytes, ms_per_step
+        roof_name = "WideStepKernel" if wide else "FusedStepKernel"
+        roof_bytes, roof_ms = step_bytes, ms_per_step
         cold_ms = cold_step_ms
     else:
         roof_kernel = "AttentionFastKernel<128,16,8,4> (fused gather + online softmax)"

@@ -319,14 +319,19 @@ int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
 /* The launch form of the context's last step (for tests and benchmarks
  * that must know which kernels ran).  No reference counterpart. */
 typedef struct dsd_launch_info {
-  int fused;                 /* 1: the single-launch step, 0: three kernels */
+  int fused;                 /* 1: the single-launch step, 0: otherwise */
   int certified;             /* 1: certified scoring, 0: exact chains */
   int multi_pass;            /* fused: slices span several 8-page passes */
   int heads_per_group;       /* fused: heads per 1024-thread workgroup */
-  int grid;                  /* fused: workgroups; three-kernel at E = 4096:
-                                score workgroups */
-  int score_pages_per_group; /* three-kernel at E = 4096: pages per score
-                                workgroup */
+  int grid;                  /* fused, wide: workgroups; three-kernel at
+                                E = 4096: score workgroups */
+  int score_pages_per_group; /* wide, three-kernel at E = 4096: pages per
+                                score workgroup */
+  int wide;                  /* 1: the wide single launch (257 to 2048
+                                candidates per request: score slices, the
+                                select and the attention overlap in one
+                                kernel; DSD_WIDE_STEP=0 at context creation
+                                gives three kernels) */
 } dsd_launch_info;
 int dsd_sparse_last_launch(const dsd_sparse_ctx* ctx, dsd_launch_info* out);
 
@@ -335,7 +340,10 @@ int dsd_sparse_last_launch(const dsd_sparse_ctx* ctx, dsd_launch_info* out);
  * *per_group stamps each -- start, slice scored, intervals ready, intervals
  * read, ranked, selected, end, refinement begun and ended (0 when none ran),
  * then the hardware ids (HW_ID, XCC_ID << 32) -- at *khz ticks per
- * millisecond.  out == NULL queries the sizes only.
+ * millisecond.  For the wide launch (dsd_launch_info.wide) the stamps are
+ * start, item kind (0 score slice, 1 attention), select start and end (0
+ * when the workgroup selected nothing), end.  out == NULL queries the sizes
+ * only.
  * For profiling; no reference counterpart. */
 int dsd_sparse_step_stamps(const dsd_sparse_ctx* ctx, int* grid, int* per_group, double* khz,
                            uint64_t* out, size_t capacity);

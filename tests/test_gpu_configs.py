@@ -2,9 +2,11 @@
 bench times, against the oracle.
 
     config 3: B=32, 32768 tokens each (2048 pages of 16), top-k 64, seed 11
-              -> the three-kernel step, 128 pages per score workgroup, the
-                 2048-candidate certified select; also dense over the same
-                 pages (the crossover's dense side) against dense_cpu
+              -> the wide single launch: 128 pages per score slice, the
+                 2048-candidate certified select by each request's last
+                 slice, attention by head pairs; bit-equal to the same step
+                 in three kernels; also dense over the same pages (the
+                 crossover's dense side) against dense_cpu
     config 4: B=64, contexts U[4096, 16384] (seed 13), page 64, top-k 32
               -> the single-launch step, multi-pass form, 8 heads per
                  workgroup
@@ -19,6 +21,7 @@ HBM."""
 from __future__ import annotations
 
 import concurrent.futures as cf
+import os
 import threading
 
 import numpy as np
@@ -97,14 +100,29 @@ def device_step_equals_host_step(gpu, batch, ctx, res):
     return ctx.last_launch()
 
 
-def test_config3_full_batch_three_kernel_step(gpu):
+def test_config3_full_batch_wide_step(gpu):
     lengths = gpu.reference_context_lengths(32, 32768, 32768, 11)
     batch, pool, ctx, res, dense_out = run_config(gpu, lengths, 16, 64, 11, dense=True)
     assert batch.total_candidates == 65536
     info = ctx.last_launch()
-    assert info["fused"] == 0 and info["certified"] == 1, info
-    assert info["score_pages_per_group"] == 128 and info["grid"] == 32 * 16, info
+    assert info["wide"] == 1 and info["fused"] == 0 and info["certified"] == 1, info
+    # 16 score slices of 128 pages and 16 head pairs per request
+    assert info["score_pages_per_group"] == 128 and info["grid"] == 32 * 16 + 32 * 16, info
     assert device_step_equals_host_step(gpu, batch, ctx, res) == info
+    # The same step in three kernels (DSD_WIDE_STEP=0): bit-equal.
+    sel_total = int(sum(min(64, int(n)) for n in np.diff(batch.cand_offsets)))
+    os.environ["DSD_WIDE_STEP"] = "0"
+    try:
+        three = gpu.SparseContext(pool, 64, batch.batch, batch.total_candidates, sel_total)
+    finally:
+        del os.environ["DSD_WIDE_STEP"]
+    res3 = three.run_batch(batch.queries, batch.cand_offsets, batch.cand_ids,
+                           output_mode=gpu.OUTPUT_OUTPUTS, want_ids=True)
+    assert three.last_launch()["wide"] == 0
+    for r in range(batch.batch):
+        assert res3["selected"][r].tolist() == res["selected"][r].tolist(), r
+    assert np.array_equal(res3["outputs"].view(np.uint32), res["outputs"].view(np.uint32))
+    three.close()
     # dense_gpu on the identical inputs vs dense_cpu (the crossover's other side)
     dense, _ = gpu.dense_run_batch(pool, batch.queries, batch.cand_offsets, batch.cand_ids)
     diff = orc.max_abs_diff(dense, dense_out)
