@@ -98,7 +98,8 @@ class StepTimings(ctypes.Structure):
 class AsyncStep(ctypes.Structure):
     _fields_ = [("ticket", ctypes.c_longlong), ("batch", ctypes.c_int), ("fused", ctypes.c_int)] + [
         (n, ctypes.c_double) for n in (
-            "start_ms", "done_ms", "score_ms", "topk_ms", "attention_ms", "kernel_ms")]
+            "start_ms", "done_ms", "score_ms", "topk_ms", "attention_ms", "kernel_ms")] + [
+        ("wide", ctypes.c_int)]
 
     def as_dict(self):
         return {n: (float(getattr(self, n)) if t is ctypes.c_double else int(getattr(self, n)))

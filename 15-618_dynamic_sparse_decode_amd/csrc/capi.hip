@@ -1329,6 +1329,10 @@ struct StepLaunch {
   bool certified = false;
   bool fused = false;
   bool wide = false;  // the wide single launch (requests beyond the fused step's 256)
+  // A batch the wide step takes, whether or not it runs (DSD_WIDE_STEP=0,
+  // graph capture): three-kernel steps split its heads as the wide step
+  // does, so both forms give the same outputs.
+  bool wide_shape = false;
   int batch = 0, total = 0, max_n = 0;
   int top_k = 0;
   int compute_units = 256;
@@ -1415,6 +1419,7 @@ void EnqueueAttentionStage(const PoolView& v, const StepLaunch& L, hipStream_t s
   a.batch = L.batch;
   a.scale = L.scale;
   a.outputs = L.outputs;
+  a.wide_partition = L.wide_shape;
   dsdk::LaunchAttention(v, a, s);
 }
 
@@ -1465,6 +1470,8 @@ dsdk::WideArgs WideStepArgs(const PoolView& v, const StepLaunch& L) {
   int lag = L.batch;
   if (const char* env = std::getenv("DSD_WIDE_LAG")) lag = std::atoi(env);
   w.lag = std::max(0, std::min(lag, L.batch));
+  if (const char* env = std::getenv("DSD_WIDE_TICKETS")) w.tickets = std::atoi(env) != 0;
+  w.items = dsdk::WideStepItems(v, L.batch, w.groups);
   return w;
 }
 
@@ -1634,9 +1641,10 @@ struct dsd_sparse_ctx {
     L.fused = StepFused(v, L.certified, fused_enabled, max_n, top_k);
     // The wide step takes the batches the single launch cannot (a request
     // beyond 256 candidates); DSD_FUSED_STEP=0 alone keeps three kernels.
-    L.wide = !L.fused && L.certified && wide_enabled && batch > 0 &&
-             !dsdk::FusedStepSupported(v, max_n, top_k) &&
-             dsdk::WideStepSupported(v, max_n, top_k);
+    L.wide_shape = !L.fused && L.certified && batch > 0 &&
+                   !dsdk::FusedStepSupported(v, max_n, top_k) &&
+                   dsdk::WideStepSupported(v, max_n, top_k);
+    L.wide = L.wide_shape && wide_enabled;
     L.batch = batch;
     L.total = total;
     L.max_n = max_n;
@@ -1718,10 +1726,9 @@ struct dsd_sparse_ctx {
       // One launch whose stages overlap: its whole time, and per-workgroup
       // stamps.
       dsdk::WideArgs w = WideStepArgs(v, *L);
-      const int grid = dsdk::WideStepGrid(v, L->batch, w.groups);
-      if (static_cast<size_t>(grid) * dsdk::WideStepStampsPerGroup() <= stamps->count) {
+      if (static_cast<size_t>(w.items) * dsdk::WideStepStampsPerGroup() <= stamps->count) {
         w.a.stamps = stamps->ptr;
-        *stamped = grid;
+        *stamped = w.items;
       } else {
         *stamped = 0;
       }
@@ -1882,6 +1889,7 @@ void HarvestAsync(dsd_sparse_ctx* ctx, AsyncSlot& a) {
   r.ticket = a.ticket;
   r.batch = a.batch;
   r.fused = a.fused ? 1 : 0;
+  r.wide = a.wide ? 1 : 0;
   const unsigned long long start =
       __hip_atomic_load(a.words.ptr + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   const unsigned long long end =
@@ -2591,9 +2599,9 @@ int dsd_sparse_last_launch(const dsd_sparse_ctx* ctx, dsd_launch_info* out) {
     out->wide = L.wide ? 1 : 0;
     out->certified = L.certified ? 1 : 0;
     if (L.wide) {
-      const int per = dsdk::ScorePagesPerGroup(L.total);
-      out->score_pages_per_group = per;
-      out->grid = dsdk::WideStepGrid(v, L.batch, (L.max_n + per - 1) / per);
+      const dsdk::WideArgs w = WideStepArgs(v, L);
+      out->score_pages_per_group = w.pages_per_group;
+      out->grid = dsdk::WideStepGrid(w.items, w.tickets);
     } else if (L.fused) {
       const int hpw = dsdk::FusedStepHeadsPerGroup(v, L.batch, ctx->compute_units);
       out->heads_per_group = hpw;
@@ -2754,6 +2762,11 @@ int dsd_sparse_run_batch_device_static(dsd_pool* pool, int top_k, int batch,
     L.valid = true;
     L.certified = StepCertified(v, DSD_SCORE_CERTIFIED, max_candidates, false);
     L.fused = StepFused(v, L.certified, true, max_candidates, top_k);
+    // (three kernels where a context would run the wide step, with its
+    // attention partition: the same outputs)
+    L.wide_shape = !L.fused && L.certified && batch > 0 &&
+                   !dsdk::FusedStepSupported(v, max_candidates, top_k) &&
+                   dsdk::WideStepSupported(v, max_candidates, top_k);
     L.batch = batch;
     L.total = total_candidates;
     L.max_n = max_candidates;

@@ -243,6 +243,9 @@ struct AttentionArgs {
   int batch = 0;
   float scale = 0.0f;
   float* outputs = nullptr;  // [batch][E]
+  // D = 128, E = 4096: split each head as the wide step's attention items
+  // do (bit-identical outputs), for the batches that step takes.
+  bool wide_partition = false;
 };
 void LaunchAttention(const PoolView& pool, const AttentionArgs& args,
                      hipStream_t stream);
@@ -306,13 +309,14 @@ void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t st
 
 // The wide step (step_kernels.hip): the certified three-kernel step for
 // E = 4096, head_dim 128 and up to WideStepMaxCandidates() candidates per
-// request in one launch: a workgroup per score slice (groups per request),
-// then a workgroup per (request, head pair) of attention; the last slice of
-// a request to finish selects it.  a: as for LaunchFusedStep (rec: the
-// interval words, 3 per candidate; sel_stride = top_k; no epoch_src).
-// sel_rec: [batch][sel_stride] tagged selected ids; cnt_rec: [batch] tagged
-// counts; counters: [1] finished workgroups, [2 .. 2 + batch) arrivals, zero
-// between launches (the kernel's last workgroup resets them).
+// request in one launch: score slices (groups per request), then one
+// attention item per (request, head), taken by workgroups in start order;
+// the last slice of a request to finish selects it.  a: as for
+// LaunchFusedStep (rec: the interval words, 3 per candidate; sel_stride =
+// top_k; no epoch_src).  sel_rec: [batch][sel_stride] tagged selected ids;
+// cnt_rec: [batch] tagged counts; counters: [0] item tickets, [1] finished
+// workgroups, [2 .. 2 + batch) arrivals, zero between launches (the
+// kernel's last workgroup resets them).
 struct WideArgs {
   FusedArgs a;
   unsigned long long* sel_rec = nullptr;
@@ -322,13 +326,21 @@ struct WideArgs {
   int groups = 0;           // score items per request
   int lag = 0;              // a request's attention items follow the score
                             // items of the request `lag` places later
+  int items = 0;            // WideStepItems
+  bool tickets = true;      // items in the order workgroups start (a
+                            // counter in counters[0]), not by workgroup id
 };
 bool WideStepSupported(const PoolView& pool, int max_candidates, int top_k);
 int WideStepMaxCandidates();
-int WideStepGrid(const PoolView& pool, int batch, int groups);
-// Timing mode (FusedArgs::stamps): per workgroup the clocks at start, select
+// Score slices plus attention items.
+int WideStepItems(const PoolView& pool, int batch, int groups);
+// Workgroups launched: with tickets, half as many again as items (spares let
+// an XCD whose CUs free up early take items another XCD would have run).
+int WideStepGrid(int items, bool tickets);
+// Timing mode (FusedArgs::stamps): per item the clocks at start, select
 // start and end (0 when it selected nothing), end, and in slot 1 the item
-// kind (bits 0-7: 0 score slice, 1 attention item) and request (bits 8+).
+// kind (bits 0-7: 0 score slice, 1 attention item), request (bits 8-31) and
+// the workgroup that ran it (bits 32+).
 int WideStepStampsPerGroup();
 void LaunchWideStep(const PoolView& pool, const WideArgs& w, hipStream_t stream);
 // One thread advances a captured step's device epoch counter (see FusedArgs).

@@ -1033,19 +1033,29 @@ __global__ __launch_bounds__(WAVES * kWave) void AttentionFastKernel(
 // 4. The wide step: the three-kernel step (E = 4096, head_dim 128, up to
 // kCertMaxKeys candidates per request) in one launch.
 //
-// Workgroup i does one item: a score slice (request r, slice x: candidates
-// [P*x, P*x + P), G slices per request) or an attention item (request r,
-// heads 2p and 2p + 1: waves 0-7 take one head, waves 8-15 the other).  The
+// Items: score slices (request r, slice x: candidates [P*x, P*x + P), G
+// slices per request) and attention items (request r, head h).  The
 // workgroup that scores a request's last slice (an arrival counter per
-// request) runs that request's certified select.  Items are ordered request
-// by request, with each request's attention items placed after the score
-// slices of the request `lag` places later (WideItemOf): by the time they
-// are dispatched their select has usually finished, and HBM streams K/V for
-// early requests while later ones still score and select.  The stages of
-// different requests overlap instead of running one after another with HBM
-// idle between them (reference: the score -> top-k -> attention sequence
-// of src/cuda/sparse_batched_attention.cu:665-762 and its k > 16 path,
-// :703-731).
+// request) runs that request's certified select.  Every score slice comes
+// before every attention item (WideItemOf with lag = batch): an attention
+// item dispatched in the first round would hold its CU from the launch on
+// while it waits for its select (at 32 requests of 2048 pages the step
+// spanned 379 us with all slices first, 427-489 us with 4 to 16 requests'
+// slices between a request's slices and its attention).  HBM streams K/V
+// for the requests selected first while the others still score and select:
+// the stages of different requests overlap instead of running one after
+// another with HBM idle between them (reference: the score -> top-k ->
+// attention sequence of src/cuda/sparse_batched_attention.cu:665-762 and
+// its k > 16 path, :703-731).
+//
+// Tickets.  A workgroup takes the next item from a counter as it starts,
+// and the grid holds half as many spare workgroups again, which find the
+// items gone and only count themselves out.  Workgroup i goes to XCD i mod
+// 8 and each XCD runs its own share of the grid: with items tied to
+// workgroup ids, the XCDs whose CUs ran the selects (each holds its CU for
+// about 47 us) finished up to 25 us after the others; with tickets an XCD
+// that frees up early takes more items (config 3: 381 against 395 us per
+// step; spares of 1 and 2 per item measured 383 and 388 us).
 //
 // Intervals, selected ids and counts cross workgroups as epoch-tagged
 // words (score_slice.h): no fences.
@@ -1053,29 +1063,38 @@ __global__ __launch_bounds__(WAVES * kWave) void AttentionFastKernel(
 // Every wait ends.  A score slice never waits; the select that follows a
 // request's last slice waits only for interval words that the request's
 // slices wrote before they arrived.  An attention item waits for its
-// request's select, that is for score slices with lower ids.  Workgroup i
-// goes to XCD i mod 8 and each XCD dispatches its share in id order.  Take
-// the lowest-id attention item that waits: on every XCD, everything before
-// the slices it waits for is a score slice (which finishes) or an attention
-// item with a lower id (which, by the choice, does not wait forever), so
-// those slices are dispatched, run and arrive, and the select runs.  The
-// polls are bounded anyway (kFailWait, zero outputs, never a hang).  The
-// last workgroup to finish resets the arrival counters for the next launch.
+// request's select, that is for score slices with lower tickets, which
+// workgroups already running took: they finish without waiting, the last
+// of them runs the select, and the select ends.  (Without tickets, the
+// lowest-id attention item that waits has, on every XCD, only score slices
+// and attention items that do not wait forever ahead of it in dispatch
+// order, and the same follows.)  The polls are bounded anyway (kFailWait,
+// zero outputs, never a hang).  The last workgroup to finish resets the
+// ticket and arrival counters for the next launch.
 //
 // A persistent form (one workgroup per CU taking items from a counter)
 // spilled 188 bytes per lane: values the compiler hoisted out of the item
 // loop stay live across all three item kinds.
 // ---------------------------------------------------------------------------
-constexpr int kWideAttnWaves = kFWaves / 2;  // one head per half-workgroup
-constexpr int kWideStamps = 5;  // per workgroup in timing mode
+constexpr int kWideStamps = 5;  // per item in timing mode
+
+// An attention item is one head of one request, all kFWaves waves on it,
+// with the lane split of the three-kernel step's attention for the same
+// batches (kWideAttnLpt, kWideAttnUnroll; LaunchAttention with
+// wide_partition): both step forms give bit-identical outputs.  Two heads
+// per item (8 waves each) measured 10 us slower at 32 requests of 2048
+// pages: the attention of the requests selected last ends later.
+constexpr int kWideAttnLpt = 16;
+constexpr int kWideAttnUnroll = 4;
 
 struct WideShared {
   union {
     ScoreShared score;
     CertShared cert;
-    AttnFastShared<kWideAttnWaves, 128> attn[2];
+    AttnFastShared<kFWaves, 128> attn;
   };
   int page[kCertMaxKeys];  // an attention item's selected pages
+  int item;
   int last;
   int count;
   unsigned long long stamp[3];  // timing mode: start, select start and end
@@ -1095,10 +1114,10 @@ __device__ __forceinline__ bool AwaitTagged(unsigned long long* p, unsigned tag,
   return true;
 }
 
-// Item i's kind (0 score slice, 1 attention), request and slice or head
-// pair: request r's G slices, then (for r >= lag) request r - lag's Q head
-// pairs, request by request; after the last request the remaining lag
-// requests' head pairs.
+// Item i's kind (0 score slice, 1 attention), request and slice or head:
+// request r's G slices, then (for r >= lag) request r - lag's Q heads,
+// request by request; after the last request the remaining lag requests'
+// heads.  (lag = batch: all slices, then all heads; DSD_WIDE_LAG.)
 __device__ __forceinline__ int WideItemOf(int i, int batch, int G, int Q, int lag, int* r,
                                           int* sub) {
   const int head = lag * G;
@@ -1126,15 +1145,14 @@ __device__ __forceinline__ int WideItemOf(int i, int batch, int G, int Q, int la
   return 1;
 }
 
-__global__ __launch_bounds__(kFThreads) void WideStepKernel(PoolView pool, WideArgs w) {
-  __shared__ WideShared sh;
-  // (no captured form: the host runs captured steps in three kernels)
+// Item `item` of the step (WideItemOf), by the whole workgroup.
+__device__ __forceinline__ void WideStepItem(const PoolView& pool, const WideArgs& w, int item,
+                                             WideShared& sh) {
   const FusedArgs& a = w.a;
-  const int pairs = pool.num_heads / 2;
   const int stride = a.sel_stride;
   int item_r, item_sub;
-  const int kind = WideItemOf(static_cast<int>(blockIdx.x), a.batch, w.groups, pairs, w.lag,
-                              &item_r, &item_sub);
+  const int kind =
+      WideItemOf(item, a.batch, w.groups, pool.num_heads, w.lag, &item_r, &item_sub);
   // Timing mode: thread 0's clocks (start, select start and end, end) and
   // the item kind, written out at the end.
   // (kept in LDS: a register would stay live across the whole item)
@@ -1193,7 +1211,7 @@ __global__ __launch_bounds__(kFThreads) void WideStepKernel(PoolView pool, WideA
     }
   } else {
     const int r = item_r;
-    const int hp = item_sub;
+    const int head = item_sub;
     if (threadIdx.x == 0) {
       unsigned long long word = 0;
       int count = 0;
@@ -1222,27 +1240,43 @@ __global__ __launch_bounds__(kFThreads) void WideStepKernel(PoolView pool, WideA
     args.queries = a.queries;
     args.scale = a.scale;
     args.outputs = a.outputs;
-    const int half = threadIdx.x / (kWideAttnWaves * kWave);
-    AttentionFastHead<128, 16, kWideAttnWaves, 4>(pool, args, 2 * hp + half, r,
-                                                  threadIdx.x - half * kWideAttnWaves * kWave,
-                                                  sh.page, count, sh.attn[half]);
+    AttentionFastHead<128, kWideAttnLpt, kFWaves, kWideAttnUnroll>(
+        pool, args, head, r, threadIdx.x, sh.page, count, sh.attn);
   }
   if (a.stamps != nullptr && threadIdx.x == 0) {
-    unsigned long long* st = a.stamps + static_cast<size_t>(kWideStamps) * blockIdx.x;
+    unsigned long long* st = a.stamps + static_cast<size_t>(kWideStamps) * item;
     st[0] = sh.stamp[0];
-    st[1] = static_cast<unsigned long long>(kind) | (static_cast<unsigned long long>(item_r) << 8);
+    st[1] = static_cast<unsigned long long>(kind) | (static_cast<unsigned long long>(item_r) << 8) |
+            (static_cast<unsigned long long>(blockIdx.x) << 32);
     st[2] = sh.stamp[1];
     st[3] = sh.stamp[2];
     st[4] = wall_clock64();
   }
+}
+
+__global__ __launch_bounds__(kFThreads) void WideStepKernel(PoolView pool, WideArgs w) {
+  __shared__ WideShared sh;
+  // (no captured form: the host runs captured steps in three kernels)
+  int item = static_cast<int>(blockIdx.x);
+  if (w.tickets) {
+    if (threadIdx.x == 0) {
+      sh.item = static_cast<int>(__hip_atomic_fetch_add(w.counters, 1u, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT));
+    }
+    __syncthreads();
+    item = sh.item;
+  }
+  // (a spare workgroup, started after every item was taken, only counts)
+  if (item < w.items) WideStepItem(pool, w, item, sh);
   if (threadIdx.x == 0) {
     // The last workgroup to finish: every slice has arrived.
     const unsigned prev =
         __hip_atomic_fetch_add(w.counters + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == gridDim.x - 1) {
-      for (int q = 0; q < a.batch; ++q) {
+      for (int q = 0; q < w.a.batch; ++q) {
         __hip_atomic_store(w.counters + 2 + q, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
+      __hip_atomic_store(w.counters, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(w.counters + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -1262,6 +1296,7 @@ const AttnVariant kAttnVariants[] = {
     DSD_ATTN_VARIANT(8, 4, 1),  DSD_ATTN_VARIANT(8, 4, 2),  DSD_ATTN_VARIANT(8, 4, 4),
     DSD_ATTN_VARIANT(8, 8, 1),  DSD_ATTN_VARIANT(8, 8, 2),  DSD_ATTN_VARIANT(16, 4, 2),
     DSD_ATTN_VARIANT(16, 4, 4), DSD_ATTN_VARIANT(16, 8, 2), DSD_ATTN_VARIANT(16, 8, 4),
+    DSD_ATTN_VARIANT(16, 16, 4),
 };
 #undef DSD_ATTN_VARIANT
 
@@ -1378,7 +1413,7 @@ void LaunchSelectCertified(const PoolView& pool, const float* d_mid, const float
 int SelectMaxCandidates() { return kSelectMaxKeys; }
 
 bool WideStepSupported(const PoolView& pool, int max_candidates, int top_k) {
-  return pool.elements == kFE && pool.head_dim == 128 && pool.num_heads % 2 == 0 &&
+  return pool.elements == kFE && pool.head_dim == 128 &&
          pool.page_size > 0 && max_candidates > 0 && max_candidates <= kCertMaxKeys &&
          top_k <= kCertMaxKeys;
 }
@@ -1387,15 +1422,17 @@ int WideStepMaxCandidates() { return kCertMaxKeys; }
 
 int WideStepStampsPerGroup() { return kWideStamps; }
 
-int WideStepGrid(const PoolView& pool, int batch, int groups) {
-  return batch * groups + batch * (pool.num_heads / 2);
+int WideStepItems(const PoolView& pool, int batch, int groups) {
+  return batch * groups + batch * pool.num_heads;
 }
+
+int WideStepGrid(int items, bool tickets) { return tickets ? items + items / 2 : items; }
 
 void LaunchWideStep(const PoolView& pool, const WideArgs& w, hipStream_t stream) {
   if (w.a.batch <= 0) return;
   if (!WideStepSupported(pool, w.a.max_candidates, w.a.top_k)) {
-    throw std::invalid_argument("the wide step needs E = 4096, head_dim 128, an even head "
-                                "count and at most 2048 candidates per request");
+    throw std::invalid_argument("the wide step needs E = 4096, head_dim 128 and at most 2048 "
+                                "candidates per request");
   }
   if (w.pages_per_group <= 0 || w.pages_per_group % kFPagesPerPass != 0 ||
       static_cast<long long>(w.groups) * w.pages_per_group < w.a.max_candidates) {
@@ -1408,7 +1445,10 @@ void LaunchWideStep(const PoolView& pool, const WideArgs& w, hipStream_t stream)
   if (w.a.epoch_src != nullptr) {
     throw std::invalid_argument("the wide step takes its epoch from the host (not captured)");
   }
-  const int grid = WideStepGrid(pool, w.a.batch, w.groups);
+  if (w.items != WideStepItems(pool, w.a.batch, w.groups)) {
+    throw std::invalid_argument("wide step item count does not match its slices");
+  }
+  const int grid = WideStepGrid(w.items, w.tickets);
   hipLaunchKernelGGL(WideStepKernel, dim3(grid), dim3(kFThreads), 0, stream, pool, w);
   DSD_HIP_CHECK(hipGetLastError());
 }
@@ -1442,6 +1482,13 @@ void LaunchAttention(const PoolView& pool, const AttentionArgs& args,
   if (D <= 0 || D > 256) {
     throw std::invalid_argument("head_dim must be in (0, 256]");
   }
+  if (D == 128 && args.wide_partition && pool.elements == kFE) {
+    // the wide step's partition of a head (kFWaves waves)
+    hipLaunchKernelGGL((AttentionFastKernel<128, kWideAttnLpt, kFWaves, kWideAttnUnroll>),
+                       dim3(pool.num_heads, args.batch), dim3(kFThreads), 0, stream, pool, args);
+    DSD_HIP_CHECK(hipGetLastError());
+    return;
+  }
   if (D == 128) {
     const AttnVariant& v = SelectAttnVariant();
     hipLaunchKernelGGL(v.fn, dim3(pool.num_heads, args.batch), dim3(v.waves * kWave), 0,
@@ -1465,6 +1512,7 @@ void LaunchAttention(const PoolView& pool, const AttentionArgs& args,
 
 void PreloadStepKernels() {
   PreloadKernel(WideStepKernel);
+  PreloadKernel(AttentionFastKernel<128, kWideAttnLpt, kFWaves, kWideAttnUnroll>);
   PreloadKernel(SelectAttnVariant().fn);
   PreloadKernel(SelectCertifiedKernel);
   PreloadKernel(SelectCertifiedRankKernel);

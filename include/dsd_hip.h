@@ -323,7 +323,8 @@ typedef struct dsd_launch_info {
   int certified;             /* 1: certified scoring, 0: exact chains */
   int multi_pass;            /* fused: slices span several 8-page passes */
   int heads_per_group;       /* fused: heads per 1024-thread workgroup */
-  int grid;                  /* fused, wide: workgroups; three-kernel at
+  int grid;                  /* fused, wide: workgroups launched (wide:
+                                items plus spares); three-kernel at
                                 E = 4096: score workgroups */
   int score_pages_per_group; /* wide, three-kernel at E = 4096: pages per
                                 score workgroup */
@@ -340,10 +341,11 @@ int dsd_sparse_last_launch(const dsd_sparse_ctx* ctx, dsd_launch_info* out);
  * *per_group stamps each -- start, slice scored, intervals ready, intervals
  * read, ranked, selected, end, refinement begun and ended (0 when none ran),
  * then the hardware ids (HW_ID, XCC_ID << 32) -- at *khz ticks per
- * millisecond.  For the wide launch (dsd_launch_info.wide) the stamps are
- * start, item kind (0 score slice, 1 attention), select start and end (0
- * when the workgroup selected nothing), end.  out == NULL queries the sizes
- * only.
+ * millisecond.  For the wide launch (dsd_launch_info.wide) *grid counts
+ * items (score slices, then attention items) and each item's stamps are
+ * start; kind (bits 0-7: 0 score slice, 1 attention), request (bits 8-31)
+ * and the workgroup that ran it (bits 32+); select start and end (0 when
+ * the item selected nothing); end.  out == NULL queries the sizes only.
  * For profiling; no reference counterpart. */
 int dsd_sparse_step_stamps(const dsd_sparse_ctx* ctx, int* grid, int* per_group, double* khz,
                            uint64_t* out, size_t capacity);
@@ -576,7 +578,8 @@ typedef struct dsd_async_step {
   double score_ms;     /* DSD_TIMING_EVENTS only, as dsd_step_timings */
   double topk_ms;
   double attention_ms;
-  double kernel_ms;
+  double kernel_ms;    /* the wide launch: its whole time (no stage split) */
+  int wide;            /* 1: the wide single launch ran the step */
 } dsd_async_step;
 int dsd_sparse_run_table_async(dsd_sparse_ctx* ctx, dsd_table* table, int batch,
                                const int* slots, const float* queries,

@@ -13,6 +13,8 @@ step reports is raised by the call that waits for it, and the context keeps
 working afterwards."""
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -189,11 +191,22 @@ def test_async_steps_read_query_rows_in_device_blocks(gpu):
         pool.close()
 
 
-def test_async_timed_three_kernel_steps(gpu):
-    """Requests of more than 256 pages take the three-kernel step, timed by
-    stage events; their records carry the stage times."""
+@pytest.mark.parametrize("wide", [True, False])
+def test_async_timed_wide_and_three_kernel_steps(gpu, wide):
+    """Requests of more than 256 pages take the wide single launch, timed
+    as a whole (its stages overlap), or with DSD_WIDE_STEP=0 the
+    three-kernel step, timed by stage events."""
     rng = np.random.default_rng(75)
-    pool, table, mirror, ctx = setup(gpu, rng, [300 * PS + 5, 20 * PS], cap=800, max_pages=400)
+    old = os.environ.get("DSD_WIDE_STEP")
+    os.environ["DSD_WIDE_STEP"] = "1" if wide else "0"
+    try:
+        pool, table, mirror, ctx = setup(gpu, rng, [300 * PS + 5, 20 * PS], cap=800,
+                                         max_pages=400)
+    finally:
+        if old is None:
+            del os.environ["DSD_WIDE_STEP"]
+        else:
+            os.environ["DSD_WIDE_STEP"] = old
     try:
         slots = [0, 1]
         tickets = []
@@ -203,13 +216,17 @@ def test_async_timed_three_kernel_steps(gpu):
             tickets.append(ctx.run_table_async(table, slots, queries=q,
                                                timing_mode=gpu.TIMING_EVENTS))
             append_behind(rng, table, mirror, slots, fresh=False)
-        print("three-kernel async steps: collecting", flush=True)
+        print(f"timed async steps (wide={wide}): collecting", flush=True)
         recs = ctx.async_collect()
         check(ctx, 2, expected)
         assert [r["ticket"] for r in recs] == tickets
         for r in recs:
-            assert r["fused"] == 0
-            assert min(r["score_ms"], r["topk_ms"], r["attention_ms"]) > 0.0
+            assert r["fused"] == 0 and r["wide"] == int(wide)
+            if wide:
+                assert r["score_ms"] == r["topk_ms"] == r["attention_ms"] == 0.0
+                assert r["kernel_ms"] > 0.0
+            else:
+                assert min(r["score_ms"], r["topk_ms"], r["attention_ms"]) > 0.0
             assert r["kernel_ms"] <= r["done_ms"] - r["start_ms"] + 2e-3
     finally:
         ctx.close()

@@ -4,7 +4,7 @@ bench times, against the oracle.
     config 3: B=32, 32768 tokens each (2048 pages of 16), top-k 64, seed 11
               -> the wide single launch: 128 pages per score slice, the
                  2048-candidate certified select by each request's last
-                 slice, attention by head pairs; bit-equal to the same step
+                 slice, attention one head per item; bit-equal to the same step
                  in three kernels; also dense over the same pages (the
                  crossover's dense side) against dense_cpu
     config 4: B=64, contexts U[4096, 16384] (seed 13), page 64, top-k 32
@@ -106,8 +106,9 @@ def test_config3_full_batch_wide_step(gpu):
     assert batch.total_candidates == 65536
     info = ctx.last_launch()
     assert info["wide"] == 1 and info["fused"] == 0 and info["certified"] == 1, info
-    # 16 score slices of 128 pages and 16 head pairs per request
-    assert info["score_pages_per_group"] == 128 and info["grid"] == 32 * 16 + 32 * 16, info
+    # 16 score slices of 128 pages and 32 heads per request (1536 items),
+    # launched with 768 spare workgroups
+    assert info["score_pages_per_group"] == 128 and info["grid"] == 2304, info
     assert device_step_equals_host_step(gpu, batch, ctx, res) == info
     # The same step in three kernels (DSD_WIDE_STEP=0): bit-equal.
     sel_total = int(sum(min(64, int(n)) for n in np.diff(batch.cand_offsets)))
