@@ -1347,6 +1347,7 @@ struct StepLaunch {
   float* lo = nullptr;
   float* hi = nullptr;
   unsigned long long* rec = nullptr;  // [3 * total] publication words
+  unsigned long long* refined = nullptr;  // [batch][8][3] refined-interval words
   unsigned long long* sel_rec = nullptr;  // wide step: tagged ids, then counts
   unsigned long long* cnt_rec = nullptr;
   unsigned* wide_counters = nullptr;
@@ -1442,6 +1443,7 @@ dsdk::FusedArgs FusedStepArgs(const PoolView& v, const StepLaunch& L) {
   a.counts = L.counts;
   a.outputs = L.outputs;
   a.rec = L.rec;
+  a.refined = L.refined;
   a.epoch = L.epoch;
   a.wait_mask = L.never_ready ? 0x80000000u : 0u;
   a.wait_tag = L.epoch | a.wait_mask;
@@ -1533,6 +1535,7 @@ struct dsd_sparse_ctx {
   DeviceBuffer<int> d_offsets, d_ids, d_selected, d_counts, d_exact_pages;
   // fused-step publication words (see fused_step.hip)
   DeviceBuffer<unsigned long long> d_rec;
+  DeviceBuffer<unsigned long long> d_refined;
   // The epoch counter of captured fused launches (advanced on the device).
   DeviceBuffer<unsigned> d_epoch;
   // The wide step's tagged selections ([max_batch][k] ids, then
@@ -1660,6 +1663,7 @@ struct dsd_sparse_ctx {
     L.lo = d_lo.ptr;
     L.hi = d_hi.ptr;
     L.rec = d_rec.ptr;
+    L.refined = d_refined.ptr;
     L.exact_pages = d_exact_pages.ptr;
     L.fail_word = h_fail.ptr;
     return L;
@@ -1811,6 +1815,9 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
       ctx->d_rec.Reserve(rec);
       ctx->h_stamps.Reserve(stamps, hipHostMallocCoherent);
       DSD_HIP_CHECK(hipMemset(ctx->d_rec.ptr, 0, rec * sizeof(unsigned long long)));
+      const size_t refined = 3 * dsdk::kFRefineSlots * B;
+      ctx->d_refined.Reserve(refined);
+      DSD_HIP_CHECK(hipMemset(ctx->d_refined.ptr, 0, refined * sizeof(unsigned long long)));
     }
     ctx->h_fail.Reserve(1, hipHostMallocCoherent);
     ctx->h_fail.ptr[0] = 0;
@@ -2663,7 +2670,9 @@ constexpr int kStaticMaxSelected = 65536;    // batch * max(1, top_k) held for
                                              // a caller that passes no ids
 constexpr size_t Align256(size_t bytes) { return (bytes + 255) / 256 * 256; }
 // Byte offsets of the scratch's parts: publication words (3 per candidate),
-// midpoints, lower and upper bounds, selected ids, selected counts.
+// midpoints, lower and upper bounds, selected ids, selected counts, the
+// device epoch, refined-interval words (3 per flagged-page slot of each
+// request).
 constexpr size_t kStaticRec = 0;
 constexpr size_t kStaticMid =
     Align256(kStaticRec + sizeof(unsigned long long) * 3 * kStaticMaxCandidates);
@@ -2672,11 +2681,13 @@ constexpr size_t kStaticHi = Align256(kStaticLo + sizeof(float) * kStaticMaxCand
 constexpr size_t kStaticSel = Align256(kStaticHi + sizeof(float) * kStaticMaxCandidates);
 constexpr size_t kStaticCounts = Align256(kStaticSel + sizeof(int) * kStaticMaxSelected);
 constexpr size_t kStaticEpoch = Align256(kStaticCounts + sizeof(int) * kStaticMaxBatch);
-constexpr size_t kStaticBytes = Align256(kStaticEpoch + sizeof(unsigned));
+constexpr size_t kStaticRefined = Align256(kStaticEpoch + sizeof(unsigned));
+constexpr size_t kStaticBytes = Align256(
+    kStaticRefined + sizeof(unsigned long long) * 3 * dsdk::kFRefineSlots * kStaticMaxBatch);
 
 }  // namespace
 
-// The scratch of dsd_sparse_run_batch_device_static (2.5 MiB): one copy per
+// The scratch of dsd_sparse_run_batch_device_static (2.7 MiB): one copy per
 // GPU, held until the process ends, shared by every call on that GPU.  Host
 // code never names it except to look up its device address.
 static __device__ __align__(256) unsigned char scratch[kStaticBytes];
@@ -2778,6 +2789,7 @@ int dsd_sparse_run_batch_device_static(dsd_pool* pool, int top_k, int batch,
     L.ids = d_cand_ids;
     L.outputs = d_outputs;
     L.rec = reinterpret_cast<unsigned long long*>(st.ptr + kStaticRec);
+    L.refined = reinterpret_cast<unsigned long long*>(st.ptr + kStaticRefined);
     L.scores = d_scores != nullptr ? d_scores : reinterpret_cast<float*>(st.ptr + kStaticMid);
     L.lo = reinterpret_cast<float*>(st.ptr + kStaticLo);
     L.hi = reinterpret_cast<float*>(st.ptr + kStaticHi);

@@ -274,6 +274,10 @@ struct FusedArgs {
   int* counts = nullptr;              // [batch]
   float* outputs = nullptr;           // [batch][E]
   unsigned long long* rec = nullptr;
+  // [batch][kFRefineSlots][3] tagged refined intervals that a request's
+  // workgroups exchange (each refines a share of the flagged pages); null:
+  // every workgroup refines all of them.
+  unsigned long long* refined = nullptr;
   unsigned epoch = 0;
   int* exact_pages = nullptr;         // may be null
   FailReport fail;                    // kFailWait / kFailShape / kFailPageId / kFailSelect
@@ -291,6 +295,10 @@ struct FusedArgs {
                                          // ready, records read, ranked, selected,
                                          // end; then the hardware ids
 };
+
+// Flagged pages a request refines at most (RefineWorthwhile with 1024
+// threads) and so the refined-interval slots per request.
+constexpr int kFRefineSlots = 8;
 
 // E = 4096, head_dim = 128, max_candidates <= 256, top_k <= 256.
 bool FusedStepSupported(const PoolView& pool, int max_candidates, int top_k);

@@ -487,9 +487,11 @@ __device__ __forceinline__ int FastSelectSlots(int n, int kk, const float (&mid)
 //      cover every overlapping pair.
 //   4. Only if some pair is flagged: those pages are rescored with the exact
 //      sequential chain (as SelectCertifiedRankKernel) and ranked again.
-// The workgroup with `writer` set also writes the selection out.
+// Workgroup `group` of the request's `groups` (group 0 also writes the
+// selection out).
 __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const FusedArgs& a, int r, int begin,
-                                int n, bool writer, FusedShared& sh) {
+                                int n, int group, int groups, FusedShared& sh) {
+  const bool writer = group == 0;
   int kk = a.top_k <= 0 ? 0 : (a.top_k < n ? a.top_k : n);
   if (n > a.max_candidates || n > kFMaxCand) {
     // The caller's max_candidates understated the CSR: select nothing (the
@@ -648,30 +650,83 @@ __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const Fuse
       // flagged pages than that pays for go straight to the exact chains
       // (sh.nflag read after the barrier: wave 0 wrote it).
       __syncthreads();
-      if (!RefineWorthwhile(sh.nflag)) break;
+      const int nflag = sh.nflag;
+      if (!RefineWorthwhile(nflag)) break;
       StampAt(a, sh, kRefine);
+      // The request's workgroups share the work: flagged page f is refined
+      // by workgroup f mod groups, which publishes its interval as tagged
+      // words (a.refined, slot f of the request); the others read it.  Every
+      // workgroup of the request holds the same intervals and so forms the
+      // same flag list (ballots over the same values), and each page's
+      // interval is computed once: all of them certify from identical
+      // intervals.  (The refinement is VALU-bound: at 8 flagged pages one
+      // workgroup took 11 us for all of them.)
+      const bool share = a.refined != nullptr && groups > 1 && nflag <= kFRefineSlots;
+      const int stride = share ? groups : 1;
+      const int first = share ? group : 0;
+      const int nmine = first < nflag ? (nflag - first + stride - 1) / stride : 0;
+      unsigned long long* xr =
+          share ? a.refined + static_cast<size_t>(r) * (3 * kFRefineSlots) : nullptr;
       RefineScores(
-          sh.nflag,
+          nmine,
           [&](int f) -> const float* {
-            const int i = sh.flag[f];
+            const int i = sh.flag[first + f * stride];
             const int pg = sh.cpage[i];
             const bool live = pg >= 0 && pg < pool.capacity && sh.cntok[i] != 0;
             return live ? pool.summaries + static_cast<size_t>(pg) * kFE : nullptr;
           },
           [&](int f) {
-            const int i = sh.flag[f];
+            const int i = sh.flag[first + f * stride];
             return dsd_refine::FirstPassBound(sh.lo[i], sh.hi[i], a.scale, kFE);
           },
           [&](int f, float m, float l, float h) {
-            // Only in LDS: the score passes of the request's other workgroups
-            // wrote the global intervals, with no ordering against this one.
-            const int i = sh.flag[f];
+            // In LDS (the score passes of the request's other workgroups
+            // wrote the global intervals, with no ordering against this
+            // one), and for the other workgroups in the request's slot.
+            const int ff = first + f * stride;
+            const int i = sh.flag[ff];
             sh.mid[i] = m;
             sh.lo[i] = l;
             sh.hi[i] = h;
+            if (xr != nullptr) {
+              PutTagged(xr + 3 * ff + 0, a.epoch, __float_as_uint(m));
+              PutTagged(xr + 3 * ff + 1, a.epoch, __float_as_uint(l));
+              PutTagged(xr + 3 * ff + 2, a.epoch, __float_as_uint(h));
+            }
           },
           a.queries + static_cast<size_t>(r) * kFE, kFE, a.scale,
           reinterpret_cast<double*>(sh.tile));
+      if (share) {
+        // The other workgroups' pages.  A wait that gives up keeps that
+        // page's first-pass interval (still sound: the certification then
+        // flags it again and the exact chain decides) and is reported.
+        const int f = static_cast<int>(threadIdx.x);
+        if (f < nflag && f % groups != group) {
+          unsigned long long w[3];
+          bool ok = true;
+          for (int x = 0; x < 3; ++x) {
+            unsigned spins = 0;
+            w[x] = LoadWord(xr + 3 * f + x);
+            while (ok && !Current(w[x], a.wait_tag)) {
+              if (++spins >= a.spin_limit) {
+                ok = false;
+                break;
+              }
+              __builtin_amdgcn_s_sleep(1);
+              w[x] = LoadWord(xr + 3 * f + x);
+            }
+          }
+          const int i = sh.flag[f];
+          if (ok) {
+            sh.mid[i] = __uint_as_float(static_cast<uint32_t>(w[0]));
+            sh.lo[i] = __uint_as_float(static_cast<uint32_t>(w[1]));
+            sh.hi[i] = __uint_as_float(static_cast<uint32_t>(w[2]));
+          } else {
+            ReportFailure(a.fail, kFailWait);
+          }
+        }
+        __syncthreads();
+      }
       StampAt(a, sh, kRefined);
     }
     if (any) {
@@ -732,7 +787,8 @@ __device__ __forceinline__ void AttentionItem(const PoolView& pool, const FusedA
   const int g = lane / kFLpt;
   const int j = lane % kFLpt;
   const int head_off = h * kFD + j * kFDq;
-  const int kk = SelectForRequest(pool, a, r, begin, n, group == 0, sh);
+  const int kk =
+      SelectForRequest(pool, a, r, begin, n, group, pool.num_heads / a.heads_per_group, sh);
   StampAt(a, sh, kSelected);
   // The query row loads with the first K/V rows (it is not held through the
   // selection, whose registers it would take).

@@ -380,7 +380,7 @@ int dsd_sparse_set_wait_limit(dsd_sparse_ctx* ctx, unsigned spin_limit, int neve
  * src/cuda/sparse_batched_attention.cu:444-528).
  * The step's scratch (publication words, score intervals, and ids / counts
  * when d_selected / d_selected_counts are NULL) lives in a static device
- * array of 2.5 MiB that each GPU holds until the process ends; the call
+ * array of 2.7 MiB that each GPU holds until the process ends; the call
  * makes no hipMalloc / hipFree and no allocating library call.  Limits:
  * batch <= 1024, total_candidates <= 65536 and, when d_selected is NULL,
  * batch * max(1, top_k) <= 65536; larger calls fail with
