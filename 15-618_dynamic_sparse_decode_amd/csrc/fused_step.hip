@@ -651,7 +651,7 @@ __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const Fuse
       // (sh.nflag read after the barrier: wave 0 wrote it).
       __syncthreads();
       const int nflag = sh.nflag;
-      if (!RefineWorthwhile(nflag)) break;
+      if (!RefineWorthwhile<kFThreads>(nflag)) break;
       StampAt(a, sh, kRefine);
       // The request's workgroups share the work: flagged page f is refined
       // by workgroup f mod groups, which publishes its interval as tagged
@@ -667,7 +667,7 @@ __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const Fuse
       const int nmine = first < nflag ? (nflag - first + stride - 1) / stride : 0;
       unsigned long long* xr =
           share ? a.refined + static_cast<size_t>(r) * (3 * kFRefineSlots) : nullptr;
-      RefineScores(
+      RefineScores<kFThreads>(
           nmine,
           [&](int f) -> const float* {
             const int i = sh.flag[first + f * stride];
@@ -737,7 +737,7 @@ __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const Fuse
       if (writer && threadIdx.x == 0 && a.exact_pages != nullptr) {
         atomicAdd(a.exact_pages, nflag);
       }
-      RescoreChains<kFRescoreGroup>(
+      RescoreChains<kFRescoreGroup, kFThreads>(
           nflag, [&](int f) { return sh.cpage[sh.flag[f]]; },
           [&](int f, float score) {
             const int i = sh.flag[f];

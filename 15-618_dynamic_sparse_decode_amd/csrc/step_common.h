@@ -328,11 +328,11 @@ __device__ __forceinline__ float ChainAdd(const float* row, int len, float acc) 
 // an all-zero summary: src/paged_kv_cache.cpp:457-459), emit(f, score)
 // receives its exact score.  q is the request's query (E floats, 16-byte
 // aligned), E % 64 == 0, tile holds RescoreFloats<kMaxGroup>() floats of
-// LDS (kMaxGroup a multiple of 4).  Must be
-// called by the whole workgroup; emit runs in lanes of wave 0 only.  A
+// LDS (kMaxGroup a multiple of 4).  Must be called by the whole workgroup
+// of kThreads threads; emit runs in lanes of wave 0 only.  A
 // one-wave workgroup fills each stretch itself after adding the previous one
 // (no overlap).
-template <int kMaxGroup, class PageOf, class Emit>
+template <int kMaxGroup, int kThreads, class PageOf, class Emit>
 __device__ void RescoreChains(int nflag, PageOf page_of, Emit emit, const float* __restrict__ q,
                               const float* __restrict__ summaries,
                               const int* __restrict__ token_counts, int capacity, int E,
@@ -341,10 +341,10 @@ __device__ void RescoreChains(int nflag, PageOf page_of, Emit emit, const float*
   constexpr int kBuf = RescoreFloats<kMaxGroup>() / 2;  // floats per buffer
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const bool one_wave = blockDim.x <= kWave;
+  constexpr bool one_wave = kThreads <= kWave;
   // Threads that form the stretch after the one being added.
   const int fill_first = one_wave ? 0 : kWave;
-  const int fill_count = static_cast<int>(blockDim.x) - fill_first;
+  const int fill_count = kThreads - fill_first;
   for (int g0 = 0; g0 < nflag; ) {
     const int left = nflag - g0;
     const int width = left <= kMaxGroup / 4 ? kMaxGroup / 4
@@ -376,7 +376,7 @@ __device__ void RescoreChains(int nflag, PageOf page_of, Emit emit, const float*
         reinterpret_cast<float4*>(buf + f * stride)[e4] = p;
       }
     };
-    fill(0, 0, 0, blockDim.x);
+    fill(0, 0, 0, kThreads);
     __syncthreads();
     float acc = 0.0f;
     for (int t = 0; t < stretches; ++t) {
@@ -415,8 +415,15 @@ __device__ void RescoreChains(int nflag, PageOf page_of, Emit emit, const float*
 // flagged pages a request): refining every flagged set took the select
 // kernel from 31 to 45 us; with this rule it stays within 1 us of never
 // refining, and small flagged sets still settle without the chain.
+//
+// The thread counts here and below are compile-time constants, not
+// blockDim.x: that reads the dispatch's group size from memory (code
+// object v5), and where the compiler re-reads it mid-kernel (it did so just
+// before the single-launch step's refinement) the read waits for every
+// outstanding load.
+template <int kThreads>
 __device__ __forceinline__ bool RefineWorthwhile(int nflag) {
-  return 2 * nflag <= static_cast<int>(blockDim.x) / kWave;
+  return 2 * nflag <= kThreads / kWave;
 }
 
 // Refined intervals of nflag pages: page_of(f) gives the f-th page's summary
@@ -436,13 +443,13 @@ __device__ __forceinline__ bool RefineWorthwhile(int nflag) {
 // barrier).  Sweep 2: every step through dsd_refine::Sweep2Step,
 // straight-line code with no divergence between lanes; each wave's sums go
 // to LDS (one barrier) and each page's first wave combines its parts.
-template <class PageOf, class BoundOf, class Emit>
+template <int kThreads, class PageOf, class BoundOf, class Emit>
 __device__ void RefineScores(int nflag, PageOf page_of, BoundOf bound_of, Emit emit,
                              const float* __restrict__ q, int E, float scale, double* scratch) {
   constexpr int kKeep = 2;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int nwaves = static_cast<int>(blockDim.x) / kWave;
+  constexpr int nwaves = kThreads / kWave;
   const int busy = nflag < nwaves ? nflag : nwaves;
   int parts = 1;
   while (parts < 8 && parts * 2 * busy <= nwaves && (E / (kWave * parts * 2)) % 4 == 0) parts *= 2;

@@ -243,9 +243,9 @@ __device__ void RadixSelectKth(const uint64_t* keys, int n, int kk, int* hist,
   bool all = false;
   for (int round = 0; round < 8; ++round) {
     shift = 56 - 8 * round;
-    for (int b = threadIdx.x; b < 256; b += blockDim.x) hist[b] = 0;
+    for (int b = threadIdx.x; b < 256; b += kSelThreads) hist[b] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    for (int i = threadIdx.x; i < n; i += kSelThreads) {
       const uint64_t key = keys[i];
       if (round == 0 || (key >> (shift + 8)) == prefix) {
         atomicAdd(&hist[static_cast<int>((key >> shift) & 255u)], 1);
@@ -295,7 +295,7 @@ __device__ void RadixSelectKth(const uint64_t* keys, int n, int kk, int* hist,
 // workgroup; the outputs are complete after the closing barrier.
 __device__ void RankSortDesc(const uint64_t* keys, const int* idx, int count,
                              uint64_t* out_keys, int* out_idx) {
-  for (int i = threadIdx.x; i < count; i += blockDim.x) {
+  for (int i = threadIdx.x; i < count; i += kSelThreads) {
     const uint64_t key = keys[i];
     int rank = 0;
     int j = 0;
@@ -380,7 +380,7 @@ __device__ __forceinline__ void SelectCertifiedRequest(
     if (threadIdx.x == 0) sh.s_bad = 0;
     __syncthreads();
   }
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+  for (int i = threadIdx.x; i < n; i += kSelThreads) {
     float m, l, h;
     if (!load(begin + i, &m, &l, &h)) sh.s_bad = 1;
     keys[i] = SelectKey(m, cand[i]);
@@ -404,7 +404,7 @@ __device__ __forceinline__ void SelectCertifiedRequest(
   }
 
   const int wave = threadIdx.x / kWave;
-  const int nwaves = (blockDim.x + kWave - 1) / kWave;
+  constexpr int nwaves = kSelThreads / kWave;
   uint64_t* tkeys = reinterpret_cast<uint64_t*>(tile);
   int* tidx = reinterpret_cast<int*>(tile + 2 * kCertMaxKeys);
   // Pass 0 certifies with the score kernel's intervals; the candidates it
@@ -421,7 +421,7 @@ __device__ __forceinline__ void SelectCertifiedRequest(
     RadixSelectKth(keys, n, kk, hist, &s_prefix, &s_need, &s_all, &shift, &prefix, &need, &all);
     // The members, unordered, into the rescoring tile (idle until step 3),
     // then in key order into skeys / sidx.
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    for (int i = threadIdx.x; i < n; i += kSelThreads) {
       const uint64_t top = keys[i] >> shift;
       bool in = top > prefix;
       if (top == prefix) in = all || atomicAdd(&s_tie, 1) < need;
@@ -440,13 +440,13 @@ __device__ __forceinline__ void SelectCertifiedRequest(
     float* mlo = tile;
     float* mhi = tile + kCertMaxKeys;
     float my_min = INFINITY, my_max = -INFINITY;
-    for (int t = threadIdx.x; t < kk; t += blockDim.x) {
+    for (int t = threadIdx.x; t < kk; t += kSelThreads) {
       const int c = sidx[t];
       mlo[t] = s_lo[c];
       mhi[t] = s_hi[c];
       my_min = fminf(my_min, s_lo[c]);
     }
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    for (int i = threadIdx.x; i < n; i += kSelThreads) {
       if (!member[i]) my_max = fmaxf(my_max, s_hi[i]);
     }
     for (int o = 1; o < kWave; o <<= 1) {
@@ -466,10 +466,10 @@ __device__ __forceinline__ void SelectCertifiedRequest(
     // An outsider is flagged when its hi reaches the members' smallest lo; a
     // member when its lo reaches the outsiders' largest hi or its interval
     // meets another member's.
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    for (int i = threadIdx.x; i < n; i += kSelThreads) {
       if (!member[i] && s_hi[i] >= min_t_lo) flagged[atomicAdd(&s_nflag, 1)] = i;
     }
-    for (int t = threadIdx.x; t < kk; t += blockDim.x) {
+    for (int t = threadIdx.x; t < kk; t += kSelThreads) {
       const float l = mlo[t];
       const float h = mhi[t];
       bool flag = l <= max_o_hi;
@@ -487,8 +487,8 @@ __device__ __forceinline__ void SelectCertifiedRequest(
       if (flag) flagged[atomicAdd(&s_nflag, 1)] = sidx[t];
     }
     __syncthreads();
-    if (s_nflag == 0 || pass == 1 || E % 256 != 0 || !RefineWorthwhile(s_nflag)) break;
-    RefineScores(
+    if (s_nflag == 0 || pass == 1 || E % 256 != 0 || !RefineWorthwhile<kSelThreads>(s_nflag)) break;
+    RefineScores<kSelThreads>(
         s_nflag,
         [&](int f) -> const float* {
           const int pg = cand[flagged[f]];
@@ -522,7 +522,7 @@ __device__ __forceinline__ void SelectCertifiedRequest(
     //    the members and the flagged outsiders: every other outsider's hi
     //    is below every member's lo, so it cannot enter the top kk.
     if (threadIdx.x == 0 && exact_pages != nullptr) atomicAdd(exact_pages, nflag);
-    RescoreChains<kSelRescoreGroup>(
+    RescoreChains<kSelRescoreGroup, kSelThreads>(
         nflag, [&](int f) { return cand[flagged[f]]; },
         [&](int f, float score) {
           const int c = flagged[f];
@@ -531,8 +531,8 @@ __device__ __forceinline__ void SelectCertifiedRequest(
         queries + static_cast<size_t>(r) * E, summaries, token_counts, capacity, E, scale, tile);
     if (threadIdx.x == 0) s_count = kk;
     __syncthreads();
-    for (int t = threadIdx.x; t < kk; t += blockDim.x) skeys[t] = keys[sidx[t]];
-    for (int f = threadIdx.x; f < nflag; f += blockDim.x) {
+    for (int t = threadIdx.x; t < kk; t += kSelThreads) skeys[t] = keys[sidx[t]];
+    for (int f = threadIdx.x; f < nflag; f += kSelThreads) {
       const int c = flagged[f];
       if (!member[c]) {
         const int pos = atomicAdd(&s_count, 1);
@@ -544,7 +544,7 @@ __device__ __forceinline__ void SelectCertifiedRequest(
     RankSortDesc(skeys, sidx, s_count, tkeys, tidx);
   }
   const uint64_t* final_keys = nflag > 0 ? tkeys : skeys;
-  for (int i = threadIdx.x; i < kk; i += blockDim.x) emit(i, KeyPage(final_keys[i]));
+  for (int i = threadIdx.x; i < kk; i += kSelThreads) emit(i, KeyPage(final_keys[i]));
   if constexpr (kPolled) __syncthreads();  // every member out before the count
   if (threadIdx.x == 0) emit_count(kk);
 }
@@ -636,7 +636,7 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
     return rank;
   };
   const int wave = threadIdx.x / kWave;
-  const int nwaves = (blockDim.x + kWave - 1) / kWave;
+  constexpr int nwaves = kRankMax / kWave;
   const int* cand = cand_ids + begin;
   int rank = n;
   int nflag = 0;
@@ -681,8 +681,8 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
     }
     __syncthreads();
     nflag = s_nflag;
-    if (nflag == 0 || pass == 1 || E % 256 != 0 || !RefineWorthwhile(nflag)) break;
-    RefineScores(
+    if (nflag == 0 || pass == 1 || E % 256 != 0 || !RefineWorthwhile<kRankMax>(nflag)) break;
+    RefineScores<kRankMax>(
         nflag,
         [&](int f) -> const float* {
           const int pg = cand[s_flag[f]];
@@ -706,7 +706,7 @@ __global__ __launch_bounds__(kRankMax) void SelectCertifiedRankKernel(
   }
   if (nflag > 0) {
     if (threadIdx.x == 0 && exact_pages != nullptr) atomicAdd(exact_pages, nflag);
-    RescoreChains<kSelRescoreGroup>(
+    RescoreChains<kSelRescoreGroup, kRankMax>(
         nflag, [&](int f) { return cand[s_flag[f]]; },
         [&](int f, float score) {
           const int c = s_flag[f];
@@ -1225,7 +1225,7 @@ __device__ __forceinline__ void WideStepItem(const PoolView& pool, const WideArg
     __syncthreads();
     const int count = sh.count;
     unsigned long long* sel = w.sel_rec + static_cast<size_t>(r) * stride;
-    for (int i = threadIdx.x; i < count; i += blockDim.x) {
+    for (int i = threadIdx.x; i < count; i += kFThreads) {
       unsigned long long word = 0;
       int page = -1;  // never attended (InPool fails)
       if (AwaitTagged(sel + i, a.wait_tag, a.spin_limit, &word)) {
