@@ -1350,7 +1350,9 @@ struct StepLaunch {
   unsigned long long* refined = nullptr;  // [batch][8][3] refined-interval words
   unsigned long long* sel_rec = nullptr;  // wide step: tagged ids, then counts
   unsigned long long* cnt_rec = nullptr;
-  unsigned* wide_counters = nullptr;
+  unsigned* wide_counters = nullptr;  // two sets of wide_counter_words
+  int wide_counter_words = 0;
+  unsigned* wide_launches = nullptr;  // host: wide launches so far (picks the set)
   int* exact_pages = nullptr;         // may be null
   unsigned long long* fail_word = nullptr;
   unsigned epoch = 0;  // fresh (non-zero, below 2^30) for every launch
@@ -1477,10 +1479,21 @@ dsdk::WideArgs WideStepArgs(const PoolView& v, const StepLaunch& L) {
   return w;
 }
 
+// The counter set of this launch: launches alternate between the two sets,
+// and each zeroes the other for the next.
+void UseWideCounters(dsdk::WideArgs* w, const StepLaunch& L) {
+  const unsigned n = (*L.wide_launches)++;
+  w->counter_words = L.wide_counter_words;
+  w->counters = L.wide_counters + (n & 1u) * static_cast<size_t>(L.wide_counter_words);
+  w->next_counters = L.wide_counters + ((n + 1u) & 1u) * static_cast<size_t>(L.wide_counter_words);
+}
+
 // The whole step: one launch (fused) or score, select and attention.
 void EnqueueStep(const PoolView& v, const StepLaunch& L, hipStream_t s) {
   if (L.wide) {
-    dsdk::LaunchWideStep(v, WideStepArgs(v, L), s);
+    dsdk::WideArgs w = WideStepArgs(v, L);
+    UseWideCounters(&w, L);
+    dsdk::LaunchWideStep(v, w, s);
     return;
   }
   if (L.fused) {
@@ -1543,6 +1556,7 @@ struct dsd_sparse_ctx {
   // launches).
   DeviceBuffer<unsigned long long> d_sel_rec;
   DeviceBuffer<unsigned> d_wide_counters;
+  mutable unsigned wide_launches = 0;  // host count of wide launches (picks the counter set)
   // The epoch of the step being enqueued: it tags the fused step's
   // publication words and every failure report of the step's kernels.
   unsigned epoch = 0;
@@ -1657,6 +1671,8 @@ struct dsd_sparse_ctx {
     L.sel_rec = d_sel_rec.ptr;
     L.cnt_rec = d_sel_rec.ptr + static_cast<size_t>(max_batch) * std::max(1, top_k);
     L.wide_counters = d_wide_counters.ptr;
+    L.wide_counter_words = static_cast<int>(d_wide_counters.count / 2);
+    L.wide_launches = &wide_launches;
     L.scores = d_scores.ptr;
     L.selected = d_selected.ptr;
     L.counts = d_counts.ptr;
@@ -1736,6 +1752,7 @@ struct dsd_sparse_ctx {
       } else {
         *stamped = 0;
       }
+      UseWideCounters(&w, *L);
       dsdk::LaunchWideStep(v, w, s);
       DSD_HIP_CHECK(hipEventRecord(k[3], s));
       return;
@@ -1804,8 +1821,8 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     DSD_HIP_CHECK(hipMemset(ctx->d_epoch.ptr, 0, sizeof(unsigned)));
     ctx->d_sel_rec.Reserve(B * K + B);
     DSD_HIP_CHECK(hipMemset(ctx->d_sel_rec.ptr, 0, (B * K + B) * sizeof(unsigned long long)));
-    ctx->d_wide_counters.Reserve(B + 2);
-    DSD_HIP_CHECK(hipMemset(ctx->d_wide_counters.ptr, 0, (B + 2) * sizeof(unsigned)));
+    ctx->d_wide_counters.Reserve(2 * (B + 1));
+    DSD_HIP_CHECK(hipMemset(ctx->d_wide_counters.ptr, 0, 2 * (B + 1) * sizeof(unsigned)));
     {
       const size_t rec = 3 * P;
       // The largest fused grid: one head per workgroup.

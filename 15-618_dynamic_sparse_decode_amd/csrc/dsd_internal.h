@@ -322,14 +322,17 @@ void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t st
 // the last slice of a request to finish selects it.  a: as for
 // LaunchFusedStep (rec: the interval words, 3 per candidate; sel_stride =
 // top_k; no epoch_src).  sel_rec: [batch][sel_stride] tagged selected ids;
-// cnt_rec: [batch] tagged counts; counters: [0] item tickets, [1] finished
-// workgroups, [2 .. 2 + batch) arrivals, zero between launches (the
-// kernel's last workgroup resets them).
+// cnt_rec: [batch] tagged counts; counters: this launch's set, [0] item
+// tickets, [1 .. 1 + batch) arrivals, zero at the launch; next_counters:
+// the other set (counter_words words), which workgroup 0 zeroes for the
+// next launch.  Launches alternate between the two sets.
 struct WideArgs {
   FusedArgs a;
   unsigned long long* sel_rec = nullptr;
   unsigned long long* cnt_rec = nullptr;
   unsigned* counters = nullptr;
+  unsigned* next_counters = nullptr;
+  int counter_words = 0;    // words per set, at least batch + 1
   int pages_per_group = 0;  // candidates per score item (a multiple of 8)
   int groups = 0;           // score items per request
   int lag = 0;              // a request's attention items follow the score

@@ -1050,7 +1050,7 @@ __global__ __launch_bounds__(WAVES * kWave) void AttentionFastKernel(
 //
 // Tickets.  A workgroup takes the next item from a counter as it starts,
 // and the grid holds half as many spare workgroups again, which find the
-// items gone and only count themselves out.  Workgroup i goes to XCD i mod
+// items gone and leave.  Workgroup i goes to XCD i mod
 // 8 and each XCD runs its own share of the grid: with items tied to
 // workgroup ids, the XCDs whose CUs ran the selects (each holds its CU for
 // about 47 us) finished up to 25 us after the others; with tickets an XCD
@@ -1069,8 +1069,11 @@ __global__ __launch_bounds__(WAVES * kWave) void AttentionFastKernel(
 // lowest-id attention item that waits has, on every XCD, only score slices
 // and attention items that do not wait forever ahead of it in dispatch
 // order, and the same follows.)  The polls are bounded anyway (kFailWait,
-// zero outputs, never a hang).  The last workgroup to finish resets the
-// ticket and arrival counters for the next launch.
+// zero outputs, never a hang).  The ticket and arrival counters come in two
+// sets that launches use in turn; workgroup 0 of each launch zeroes the set
+// the next launch will use (the previous launch used it and has finished),
+// so no workgroup waits at the end to reset anything and a spare leaves
+// after one load.
 //
 // A persistent form (one workgroup per CU taking items from a counter)
 // spilled 188 bytes per lane: values the compiler hoisted out of the item
@@ -1174,7 +1177,7 @@ __device__ __forceinline__ void WideStepItem(const PoolView& pool, const WideArg
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-      const unsigned prev = __hip_atomic_fetch_add(w.counters + 2 + r, 1u, __ATOMIC_RELAXED,
+      const unsigned prev = __hip_atomic_fetch_add(w.counters + 1 + r, 1u, __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_AGENT);
       sh.last = prev == static_cast<unsigned>(w.groups - 1) ? 1 : 0;
     }
@@ -1257,29 +1260,29 @@ __device__ __forceinline__ void WideStepItem(const PoolView& pool, const WideArg
 __global__ __launch_bounds__(kFThreads) void WideStepKernel(PoolView pool, WideArgs w) {
   __shared__ WideShared sh;
   // (no captured form: the host runs captured steps in three kernels)
+  if (blockIdx.x == 0) {
+    // Zero the other counter set for the next launch (the launch before
+    // this one used it and has finished).
+    for (int t = static_cast<int>(threadIdx.x); t < w.counter_words; t += kFThreads) {
+      __hip_atomic_store(w.next_counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
   int item = static_cast<int>(blockIdx.x);
   if (w.tickets) {
     if (threadIdx.x == 0) {
-      sh.item = static_cast<int>(__hip_atomic_fetch_add(w.counters, 1u, __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT));
+      // A spare workgroup that starts after every item was taken sees so
+      // with a load and leaves without touching the counter.
+      unsigned t = static_cast<unsigned>(w.items);
+      if (__hip_atomic_load(w.counters, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+          static_cast<unsigned>(w.items)) {
+        t = __hip_atomic_fetch_add(w.counters, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      sh.item = t < static_cast<unsigned>(w.items) ? static_cast<int>(t) : w.items;
     }
     __syncthreads();
     item = sh.item;
   }
-  // (a spare workgroup, started after every item was taken, only counts)
   if (item < w.items) WideStepItem(pool, w, item, sh);
-  if (threadIdx.x == 0) {
-    // The last workgroup to finish: every slice has arrived.
-    const unsigned prev =
-        __hip_atomic_fetch_add(w.counters + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == gridDim.x - 1) {
-      for (int q = 0; q < w.a.batch; ++q) {
-        __hip_atomic_store(w.counters + 2 + q, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      __hip_atomic_store(w.counters, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(w.counters + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
 }
 
 using AttnKernelFn = void (*)(PoolView, AttentionArgs);
@@ -1439,7 +1442,8 @@ void LaunchWideStep(const PoolView& pool, const WideArgs& w, hipStream_t stream)
     throw std::invalid_argument("wide step slices do not cover max_candidates");
   }
   if (w.a.rec == nullptr || w.sel_rec == nullptr || w.cnt_rec == nullptr ||
-      w.counters == nullptr || w.a.sel_stride < (w.a.top_k > 0 ? w.a.top_k : 1)) {
+      w.counters == nullptr || w.next_counters == nullptr || w.counter_words < w.a.batch + 1 ||
+      w.a.sel_stride < (w.a.top_k > 0 ? w.a.top_k : 1)) {
     throw std::invalid_argument("wide step scratch missing");
   }
   if (w.a.epoch_src != nullptr) {
