@@ -421,3 +421,65 @@ def test_midpoint_order_reversed_by_certification(gpu, k):
     assert orc.max_abs_diff(cert["outputs"], outs) <= 1e-4
     assert reversed_pairs > 0, "no request had its midpoint order reversed by certification"
     pool.close()
+
+
+@pytest.mark.parametrize("batch,tie_request,near_count", [
+    (1, 0, 8),     # one head per workgroup: 32 workgroups share the request
+    (16, 5, 8),    # two heads: 16 workgroups
+    (16, 15, 3),
+    (40, 0, 8),    # eight heads: 4 workgroups, two flagged pages each
+    (64, 63, 8),
+])
+def test_refinement_shared_by_the_requests_workgroups(gpu, batch, tie_request, near_count):
+    """One request of the batch has near_count pages within about 1e-3 of
+    each other at its top-8 boundary; in the single-launch step its
+    workgroups refine the flagged pages between them (page f by workgroup f
+    mod the request's workgroups) and exchange the intervals.  Every
+    request's ids must equal the oracle's, no page may need the exact chain
+    (the refined intervals settle it), and the outputs must be within 1e-4."""
+    rng = np.random.default_rng(1000 + batch + tie_request)
+    H, D, ps, k = 32, 128, 16, 8
+    E = H * D
+    scale = 1.0 / np.sqrt(np.float32(D))
+    sizes = [40 if r == tie_request else 9 for r in range(batch)]
+    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    n_pages = int(offs[-1])
+    queries = rng.standard_normal((batch, E)).astype(np.float32)
+    summ = (0.25 * rng.standard_normal((n_pages, E))).astype(np.float32)
+    q = queries[tie_request]
+    m = int(np.argmax(np.abs(q)))
+    base = (0.2 * q + 0.25 * rng.standard_normal(E)).astype(np.float32)
+    first = int(offs[tie_request])
+    for j in range(near_count):
+        row = base.copy()
+        row[m] = np.float32(row[m] + j * 1e-3 / (q[m] * scale))
+        summ[first + j] = row
+    keys = rng.standard_normal((n_pages, ps, E)).astype(np.float32)
+    values = rng.standard_normal((n_pages, ps, E)).astype(np.float32)
+    pool = gpu.DevicePagePool(H, D, ps, n_pages)
+    try:
+        page_ids = np.arange(n_pages, dtype=np.int32)
+        counts = np.full(n_pages, ps, np.int32)
+        pool.upload_pages(page_ids, counts, page_ids.astype(np.int64) * ps * E, keys, values,
+                          summ)
+        ids = np.concatenate([rng.permutation(np.arange(offs[r], offs[r + 1]))
+                              for r in range(batch)]).astype(np.int32)
+        print(f"shared refinement: batch {batch}, near-tie request {tie_request}", flush=True)
+        with gpu.SparseContext(pool, k, batch, n_pages, selected_total(offs, k)) as ctx:
+            res = ctx.run_batch(queries, offs, ids, output_mode=gpu.OUTPUT_OUTPUTS,
+                                want_ids=True)
+            info = ctx.last_launch()
+            rescored = ctx.exact_rescored_pages()
+            ctx.device_status()
+        assert info["fused"] == 1, info
+        _, selected, outs = orc.sparse_batch(queries, keys, values, summ, counts, offs, ids,
+                                             H, D, ps, k)
+        for r in range(batch):
+            assert res["selected"][r].tolist() == selected[r].tolist(), r
+        if near_count >= k:
+            assert sorted(selected[tie_request].tolist()) == list(
+                range(first + near_count - k, first + near_count))
+        assert rescored == 0, f"{rescored} pages took the exact chain"
+        assert orc.max_abs_diff(res["outputs"], outs) <= 1e-4
+    finally:
+        pool.close()
