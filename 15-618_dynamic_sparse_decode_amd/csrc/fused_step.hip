@@ -605,154 +605,162 @@ __device__ __forceinline__ int SelectForRequest(const PoolView& pool, const Fuse
     kk = 0;
   }
   if (kk > 0) {
-    // 2-3 with the slot counts fixed at compile time (straight-line code).
-    const int cs = (n + kWave - 1) / kWave;    // candidate slots, 1..4
-    const int rs = (kk + kWave - 1) / kWave;   // rank slots, 1..cs
-    bool any = false;
-    bool ballot = kk > kFFastK;  // the ballot ranks (every wave) or FastSelect
-    for (int pass = 0; pass < 2; ++pass) {
-      if (!ballot) {
-        if (pass == 1) {
-          // Select again from the refined intervals.
-          if (wave == 0) {
-            float mid[kFSlots], hi[kFSlots];
-#pragma unroll
-            for (int m = 0; m < kFSlots; ++m) {
-              const int i = lane + kWave * m;  // < kFMaxCand: in bounds
-              mid[m] = sh.mid[i];
-              hi[m] = sh.hi[i];
+    // The common case, FastSelect's intervals certified the selection
+    // (sh.certified > 0, wave 0 wrote it before the barrier): nothing to
+    // rank, refine or rescore.  It skips the block below, whose loop the
+    // compiler prepares with a few hundred instructions of hoisted masks:
+    // about 1 us, run cold, of every step that took them.
+    const bool settled = kk <= kFFastK && sh.certified > 0;
+    if (!settled) {
+      // 2-3 with the slot counts fixed at compile time (straight-line code).
+      const int cs = (n + kWave - 1) / kWave;    // candidate slots, 1..4
+      const int rs = (kk + kWave - 1) / kWave;   // rank slots, 1..cs
+      bool any = false;
+      bool ballot = kk > kFFastK;  // the ballot ranks (every wave) or FastSelect
+      for (int pass = 0; pass < 2; ++pass) {
+        if (!ballot) {
+          if (pass == 1) {
+            // Select again from the refined intervals.
+            if (wave == 0) {
+              float mid[kFSlots], hi[kFSlots];
+  #pragma unroll
+              for (int m = 0; m < kFSlots; ++m) {
+                const int i = lane + kWave * m;  // < kFMaxCand: in bounds
+                mid[m] = sh.mid[i];
+                hi[m] = sh.hi[i];
+              }
+              const int verdict = FastSelectSlots(n, kk, mid, hi, sh, false);
+              if (lane == 0) sh.certified = verdict;
             }
-            const int verdict = FastSelectSlots(n, kk, mid, hi, sh, false);
-            if (lane == 0) sh.certified = verdict;
+            __syncthreads();
+          }
+          const int verdict = sh.certified;
+          ballot = verdict < 0;  // equal midpoints: rank with ballots instead
+          any = verdict == 0;
+        }
+        if (ballot) switch (cs * 8 + rs) {
+          case 1 * 8 + 1: any = RankAndCertify<1, 1>(a, n, kk, page, ntok, sh); break;
+          case 2 * 8 + 1: any = RankAndCertify<2, 1>(a, n, kk, page, ntok, sh); break;
+          case 2 * 8 + 2: any = RankAndCertify<2, 2>(a, n, kk, page, ntok, sh); break;
+          case 3 * 8 + 1: any = RankAndCertify<3, 1>(a, n, kk, page, ntok, sh); break;
+          case 3 * 8 + 2: any = RankAndCertify<3, 2>(a, n, kk, page, ntok, sh); break;
+          case 3 * 8 + 3: any = RankAndCertify<3, 3>(a, n, kk, page, ntok, sh); break;
+          case 4 * 8 + 1: any = RankAndCertify<4, 1>(a, n, kk, page, ntok, sh); break;
+          case 4 * 8 + 2: any = RankAndCertify<4, 2>(a, n, kk, page, ntok, sh); break;
+          case 4 * 8 + 3: any = RankAndCertify<4, 3>(a, n, kk, page, ntok, sh); break;
+          default: any = RankAndCertify<4, 4>(a, n, kk, page, ntok, sh); break;
+        }
+        if (!any || pass == 1) break;
+        // 4a. Some order is not decided by the intervals: the flagged pages
+        // get refined intervals (RefineScores, the whole workgroup, several
+        // waves per page), and the ranks and certification run again; more
+        // flagged pages than that pays for go straight to the exact chains
+        // (sh.nflag read after the barrier: wave 0 wrote it).
+        __syncthreads();
+        const int nflag = sh.nflag;
+        if (!RefineWorthwhile<kFThreads>(nflag)) break;
+        StampAt(a, sh, kRefine);
+        // The request's workgroups share the work: flagged page f is refined
+        // by workgroup f mod groups, which publishes its interval as tagged
+        // words (a.refined, slot f of the request); the others read it.  Every
+        // workgroup of the request holds the same intervals and so forms the
+        // same flag list (ballots over the same values), and each page's
+        // interval is computed once: all of them certify from identical
+        // intervals.  (The refinement is VALU-bound: at 8 flagged pages one
+        // workgroup took 11 us for all of them.)
+        const bool share = a.refined != nullptr && groups > 1 && nflag <= kFRefineSlots;
+        const int stride = share ? groups : 1;
+        const int first = share ? group : 0;
+        const int nmine = first < nflag ? (nflag - first + stride - 1) / stride : 0;
+        unsigned long long* xr =
+            share ? a.refined + static_cast<size_t>(r) * (3 * kFRefineSlots) : nullptr;
+        RefineScores<kFThreads>(
+            nmine,
+            [&](int f) -> const float* {
+              const int i = sh.flag[first + f * stride];
+              const int pg = sh.cpage[i];
+              const bool live = pg >= 0 && pg < pool.capacity && sh.cntok[i] != 0;
+              return live ? pool.summaries + static_cast<size_t>(pg) * kFE : nullptr;
+            },
+            [&](int f) {
+              const int i = sh.flag[first + f * stride];
+              return dsd_refine::FirstPassBound(sh.lo[i], sh.hi[i], a.scale, kFE);
+            },
+            [&](int f, float m, float l, float h) {
+              // In LDS (the score passes of the request's other workgroups
+              // wrote the global intervals, with no ordering against this
+              // one), and for the other workgroups in the request's slot.
+              const int ff = first + f * stride;
+              const int i = sh.flag[ff];
+              sh.mid[i] = m;
+              sh.lo[i] = l;
+              sh.hi[i] = h;
+              if (xr != nullptr) {
+                PutTagged(xr + 3 * ff + 0, a.epoch, __float_as_uint(m));
+                PutTagged(xr + 3 * ff + 1, a.epoch, __float_as_uint(l));
+                PutTagged(xr + 3 * ff + 2, a.epoch, __float_as_uint(h));
+              }
+            },
+            a.queries + static_cast<size_t>(r) * kFE, kFE, a.scale,
+            reinterpret_cast<double*>(sh.tile));
+        if (share) {
+          // The other workgroups' pages.  A wait that gives up keeps that
+          // page's first-pass interval (still sound: the certification then
+          // flags it again and the exact chain decides) and is reported.
+          const int f = static_cast<int>(threadIdx.x);
+          if (f < nflag && f % groups != group) {
+            unsigned long long w[3];
+            bool ok = true;
+            for (int x = 0; x < 3; ++x) {
+              unsigned spins = 0;
+              w[x] = LoadWord(xr + 3 * f + x);
+              while (ok && !Current(w[x], a.wait_tag)) {
+                if (++spins >= a.spin_limit) {
+                  ok = false;
+                  break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                w[x] = LoadWord(xr + 3 * f + x);
+              }
+            }
+            const int i = sh.flag[f];
+            if (ok) {
+              sh.mid[i] = __uint_as_float(static_cast<uint32_t>(w[0]));
+              sh.lo[i] = __uint_as_float(static_cast<uint32_t>(w[1]));
+              sh.hi[i] = __uint_as_float(static_cast<uint32_t>(w[2]));
+            } else {
+              ReportFailure(a.fail, kFailWait);
+            }
           }
           __syncthreads();
         }
-        const int verdict = sh.certified;
-        ballot = verdict < 0;  // equal midpoints: rank with ballots instead
-        any = verdict == 0;
+        StampAt(a, sh, kRefined);
       }
-      if (ballot) switch (cs * 8 + rs) {
-        case 1 * 8 + 1: any = RankAndCertify<1, 1>(a, n, kk, page, ntok, sh); break;
-        case 2 * 8 + 1: any = RankAndCertify<2, 1>(a, n, kk, page, ntok, sh); break;
-        case 2 * 8 + 2: any = RankAndCertify<2, 2>(a, n, kk, page, ntok, sh); break;
-        case 3 * 8 + 1: any = RankAndCertify<3, 1>(a, n, kk, page, ntok, sh); break;
-        case 3 * 8 + 2: any = RankAndCertify<3, 2>(a, n, kk, page, ntok, sh); break;
-        case 3 * 8 + 3: any = RankAndCertify<3, 3>(a, n, kk, page, ntok, sh); break;
-        case 4 * 8 + 1: any = RankAndCertify<4, 1>(a, n, kk, page, ntok, sh); break;
-        case 4 * 8 + 2: any = RankAndCertify<4, 2>(a, n, kk, page, ntok, sh); break;
-        case 4 * 8 + 3: any = RankAndCertify<4, 3>(a, n, kk, page, ntok, sh); break;
-        default: any = RankAndCertify<4, 4>(a, n, kk, page, ntok, sh); break;
-      }
-      if (!any || pass == 1) break;
-      // 4a. Some order is not decided by the intervals: the flagged pages
-      // get refined intervals (RefineScores, the whole workgroup, several
-      // waves per page), and the ranks and certification run again; more
-      // flagged pages than that pays for go straight to the exact chains
-      // (sh.nflag read after the barrier: wave 0 wrote it).
-      __syncthreads();
-      const int nflag = sh.nflag;
-      if (!RefineWorthwhile<kFThreads>(nflag)) break;
-      StampAt(a, sh, kRefine);
-      // The request's workgroups share the work: flagged page f is refined
-      // by workgroup f mod groups, which publishes its interval as tagged
-      // words (a.refined, slot f of the request); the others read it.  Every
-      // workgroup of the request holds the same intervals and so forms the
-      // same flag list (ballots over the same values), and each page's
-      // interval is computed once: all of them certify from identical
-      // intervals.  (The refinement is VALU-bound: at 8 flagged pages one
-      // workgroup took 11 us for all of them.)
-      const bool share = a.refined != nullptr && groups > 1 && nflag <= kFRefineSlots;
-      const int stride = share ? groups : 1;
-      const int first = share ? group : 0;
-      const int nmine = first < nflag ? (nflag - first + stride - 1) / stride : 0;
-      unsigned long long* xr =
-          share ? a.refined + static_cast<size_t>(r) * (3 * kFRefineSlots) : nullptr;
-      RefineScores<kFThreads>(
-          nmine,
-          [&](int f) -> const float* {
-            const int i = sh.flag[first + f * stride];
-            const int pg = sh.cpage[i];
-            const bool live = pg >= 0 && pg < pool.capacity && sh.cntok[i] != 0;
-            return live ? pool.summaries + static_cast<size_t>(pg) * kFE : nullptr;
-          },
-          [&](int f) {
-            const int i = sh.flag[first + f * stride];
-            return dsd_refine::FirstPassBound(sh.lo[i], sh.hi[i], a.scale, kFE);
-          },
-          [&](int f, float m, float l, float h) {
-            // In LDS (the score passes of the request's other workgroups
-            // wrote the global intervals, with no ordering against this
-            // one), and for the other workgroups in the request's slot.
-            const int ff = first + f * stride;
-            const int i = sh.flag[ff];
-            sh.mid[i] = m;
-            sh.lo[i] = l;
-            sh.hi[i] = h;
-            if (xr != nullptr) {
-              PutTagged(xr + 3 * ff + 0, a.epoch, __float_as_uint(m));
-              PutTagged(xr + 3 * ff + 1, a.epoch, __float_as_uint(l));
-              PutTagged(xr + 3 * ff + 2, a.epoch, __float_as_uint(h));
-            }
-          },
-          a.queries + static_cast<size_t>(r) * kFE, kFE, a.scale,
-          reinterpret_cast<double*>(sh.tile));
-      if (share) {
-        // The other workgroups' pages.  A wait that gives up keeps that
-        // page's first-pass interval (still sound: the certification then
-        // flags it again and the exact chain decides) and is reported.
-        const int f = static_cast<int>(threadIdx.x);
-        if (f < nflag && f % groups != group) {
-          unsigned long long w[3];
-          bool ok = true;
-          for (int x = 0; x < 3; ++x) {
-            unsigned spins = 0;
-            w[x] = LoadWord(xr + 3 * f + x);
-            while (ok && !Current(w[x], a.wait_tag)) {
-              if (++spins >= a.spin_limit) {
-                ok = false;
-                break;
-              }
-              __builtin_amdgcn_s_sleep(1);
-              w[x] = LoadWord(xr + 3 * f + x);
-            }
-          }
-          const int i = sh.flag[f];
-          if (ok) {
-            sh.mid[i] = __uint_as_float(static_cast<uint32_t>(w[0]));
-            sh.lo[i] = __uint_as_float(static_cast<uint32_t>(w[1]));
-            sh.hi[i] = __uint_as_float(static_cast<uint32_t>(w[2]));
-          } else {
-            ReportFailure(a.fail, kFailWait);
-          }
+      if (any) {
+        // 4b. What the refined intervals leave open: rescore those pages with
+        // the exact chain, rank again and rewrite the members.
+        __syncthreads();
+        const int nflag = sh.nflag;
+        if (writer && threadIdx.x == 0 && a.exact_pages != nullptr) {
+          atomicAdd(a.exact_pages, nflag);
+        }
+        RescoreChains<kFRescoreGroup, kFThreads>(
+            nflag, [&](int f) { return sh.cpage[sh.flag[f]]; },
+            [&](int f, float score) {
+              const int i = sh.flag[f];
+              sh.key[i] = SelectKey(score, sh.cpage[i]);
+            },
+            a.queries + static_cast<size_t>(r) * kFE, pool.summaries, pool.token_counts,
+            pool.capacity, kFE, a.scale, sh.tile);
+        ParallelRanks(sh, n);
+        const int i = threadIdx.x;
+        if (i < n && sh.rank[i] < kk) {
+          sh.top[sh.rank[i]] = i;
+          sh.page[sh.rank[i]] = sh.cpage[i];
+          sh.ntok[sh.rank[i]] = sh.cntok[i];
         }
         __syncthreads();
       }
-      StampAt(a, sh, kRefined);
-    }
-    if (any) {
-      // 4b. What the refined intervals leave open: rescore those pages with
-      // the exact chain, rank again and rewrite the members.
-      __syncthreads();
-      const int nflag = sh.nflag;
-      if (writer && threadIdx.x == 0 && a.exact_pages != nullptr) {
-        atomicAdd(a.exact_pages, nflag);
-      }
-      RescoreChains<kFRescoreGroup, kFThreads>(
-          nflag, [&](int f) { return sh.cpage[sh.flag[f]]; },
-          [&](int f, float score) {
-            const int i = sh.flag[f];
-            sh.key[i] = SelectKey(score, sh.cpage[i]);
-          },
-          a.queries + static_cast<size_t>(r) * kFE, pool.summaries, pool.token_counts,
-          pool.capacity, kFE, a.scale, sh.tile);
-      ParallelRanks(sh, n);
-      const int i = threadIdx.x;
-      if (i < n && sh.rank[i] < kk) {
-        sh.top[sh.rank[i]] = i;
-        sh.page[sh.rank[i]] = sh.cpage[i];
-        sh.ntok[sh.rank[i]] = sh.cntok[i];
-      }
-      __syncthreads();
     }
     if (writer && static_cast<int>(threadIdx.x) < kk) {
       // Every rank below kk holds the page of one of the request's
