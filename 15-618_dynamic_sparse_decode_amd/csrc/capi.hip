@@ -1479,21 +1479,29 @@ dsdk::WideArgs WideStepArgs(const PoolView& v, const StepLaunch& L) {
   return w;
 }
 
-// The counter set of this launch: launches alternate between the two sets,
-// and each zeroes the other for the next.
+// The counter set of the next launch: launches alternate between the two
+// sets, and each zeroes the other for the one after it.  The count advances
+// only once a launch was enqueued (LaunchWideCounted), so a launch that
+// throws leaves the sets in turn.
 void UseWideCounters(dsdk::WideArgs* w, const StepLaunch& L) {
-  const unsigned n = (*L.wide_launches)++;
+  const unsigned n = *L.wide_launches;
   w->counter_words = L.wide_counter_words;
   w->counters = L.wide_counters + (n & 1u) * static_cast<size_t>(L.wide_counter_words);
   w->next_counters = L.wide_counters + ((n + 1u) & 1u) * static_cast<size_t>(L.wide_counter_words);
+}
+
+void LaunchWideCounted(const PoolView& v, dsdk::WideArgs* w, const StepLaunch& L,
+                       hipStream_t s) {
+  UseWideCounters(w, L);
+  dsdk::LaunchWideStep(v, *w, s);
+  ++*L.wide_launches;
 }
 
 // The whole step: one launch (fused) or score, select and attention.
 void EnqueueStep(const PoolView& v, const StepLaunch& L, hipStream_t s) {
   if (L.wide) {
     dsdk::WideArgs w = WideStepArgs(v, L);
-    UseWideCounters(&w, L);
-    dsdk::LaunchWideStep(v, w, s);
+    LaunchWideCounted(v, &w, L, s);
     return;
   }
   if (L.fused) {
@@ -1752,8 +1760,7 @@ struct dsd_sparse_ctx {
       } else {
         *stamped = 0;
       }
-      UseWideCounters(&w, *L);
-      dsdk::LaunchWideStep(v, w, s);
+      LaunchWideCounted(v, &w, *L, s);
       DSD_HIP_CHECK(hipEventRecord(k[3], s));
       return;
     }
