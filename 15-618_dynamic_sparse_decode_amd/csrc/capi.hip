@@ -1471,10 +1471,19 @@ dsdk::WideArgs WideStepArgs(const PoolView& v, const StepLaunch& L) {
   // launch on while it waits for its request's select; on 32 requests of
   // 2048 pages the step spanned 379 us with all slices first and 427-489 us
   // with 4 to 16 requests between a request's slices and its attention.
-  int lag = L.batch;
-  if (const char* env = std::getenv("DSD_WIDE_LAG")) lag = std::atoi(env);
+  // (DSD_WIDE_LAG and DSD_WIDE_TICKETS=0, tuning switches read once per
+  // process, give the other orders)
+  static const int lag_env = [] {
+    const char* env = std::getenv("DSD_WIDE_LAG");
+    return env != nullptr ? std::atoi(env) : -1;
+  }();
+  static const bool tickets = [] {
+    const char* env = std::getenv("DSD_WIDE_TICKETS");
+    return env == nullptr || std::atoi(env) != 0;
+  }();
+  const int lag = lag_env >= 0 ? lag_env : L.batch;
   w.lag = std::max(0, std::min(lag, L.batch));
-  if (const char* env = std::getenv("DSD_WIDE_TICKETS")) w.tickets = std::atoi(env) != 0;
+  w.tickets = tickets;
   w.items = dsdk::WideStepItems(v, L.batch, w.groups);
   return w;
 }
