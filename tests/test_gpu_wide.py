@@ -10,9 +10,10 @@ runs the same score pass, select and attention code in three launches, ids
 and outputs must be bit-equal.  Cases: ragged batches mixing short and long
 requests, k from 1 to 64 (and k above a request's candidate count), near
 ties that the select settles by refinement or the exact chain, an empty
-request, the device-buffer entry, back-to-back replays of the launch, and a
-forced wait failure (the test hook, set from the host) that must be
-reported and leave the context usable."""
+request, the device-buffer entry, back-to-back replays of the launch, pages
+of 64 tokens with a partial last page, and a forced wait failure (the test
+hook, set from the host) that must be reported and leave the context
+usable."""
 from __future__ import annotations
 
 import os
@@ -190,5 +191,45 @@ def test_wide_step_wait_that_gives_up_raises_and_recovers(gpu):
                 assert res["selected"][r].tolist() == selected[r].tolist(), r
             assert orc.max_abs_diff(res["outputs"], outs) <= 1e-4
             ctx.device_status()
+    finally:
+        pool.close()
+
+
+def test_wide_step_page_size_64_with_partial_pages(gpu):
+    """Pages of 64 tokens (BASELINE config 4's size), a request of 300
+    pages whose last page is partial next to a short one: the wide launch
+    against the oracle and, bit for bit, against the three-kernel form."""
+    ps = 64
+    lengths = [300 * ps - 5, 40 * ps + 7]
+    batch = gpu.SyntheticBatch(H, D, ps, lengths, seed=12)
+    pool = gpu.DevicePagePool(H, D, ps, batch.capacity)
+    k = 32
+    try:
+        batch.upload(pool)
+        print(f"wide step, page size {ps}: lengths {lengths}", flush=True)
+        total = int(batch.cand_offsets[-1])
+
+        def run_form(wide):
+            with make_ctx(gpu, pool, k, batch.batch, total, wide) as ctx:
+                res = ctx.run_batch(batch.queries, batch.cand_offsets, batch.cand_ids,
+                                    output_mode=gpu.OUTPUT_OUTPUTS, want_ids=True)
+                res["launch"] = ctx.last_launch()
+                ctx.device_status()
+            return res
+
+        wide = run_form(True)
+        three = run_form(False)
+        assert wide["launch"]["wide"] == 1 and three["launch"]["wide"] == 0
+        summ = np.zeros((batch.capacity, E), np.float32)
+        live = batch.live_page_ids()
+        summ[live] = orc.pool_summaries(batch.key_pool, batch.token_counts, E, live)
+        _, selected, outs = orc.sparse_batch(batch.queries, batch.key_pool, batch.value_pool,
+                                             summ, batch.token_counts, batch.cand_offsets,
+                                             batch.cand_ids, H, D, ps, k)
+        for r in range(batch.batch):
+            assert wide["selected"][r].tolist() == selected[r].tolist(), r
+            assert three["selected"][r].tolist() == selected[r].tolist(), r
+        assert orc.max_abs_diff(wide["outputs"], outs) <= 1e-4
+        assert np.array_equal(wide["outputs"].view(np.uint32), three["outputs"].view(np.uint32))
     finally:
         pool.close()
