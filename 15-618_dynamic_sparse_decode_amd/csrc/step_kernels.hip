@@ -1215,6 +1215,13 @@ __device__ __forceinline__ void WideStepItem(const PoolView& pool, const WideArg
   } else {
     const int r = item_r;
     const int head = item_sub;
+    unsigned long long* sel = w.sel_rec + static_cast<size_t>(r) * stride;
+    // Each thread reads its id word along with thread 0's read of the count:
+    // when the select finished before this item started (most items), the
+    // ids arrive in the same round trip; a word not yet current is polled
+    // below.
+    const unsigned long long early =
+        static_cast<int>(threadIdx.x) < stride ? LoadWord(sel + threadIdx.x) : 0ull;
     if (threadIdx.x == 0) {
       unsigned long long word = 0;
       int count = 0;
@@ -1227,11 +1234,11 @@ __device__ __forceinline__ void WideStepItem(const PoolView& pool, const WideArg
     }
     __syncthreads();
     const int count = sh.count;
-    unsigned long long* sel = w.sel_rec + static_cast<size_t>(r) * stride;
     for (int i = threadIdx.x; i < count; i += kFThreads) {
-      unsigned long long word = 0;
+      unsigned long long word = i == static_cast<int>(threadIdx.x) ? early : 0ull;
       int page = -1;  // never attended (InPool fails)
-      if (AwaitTagged(sel + i, a.wait_tag, a.spin_limit, &word)) {
+      if (static_cast<unsigned>(word >> 32) == a.wait_tag ||
+          AwaitTagged(sel + i, a.wait_tag, a.spin_limit, &word)) {
         page = static_cast<int>(static_cast<uint32_t>(word));
       } else {
         ReportFailure(a.fail, kFailWait);
