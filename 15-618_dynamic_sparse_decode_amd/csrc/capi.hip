@@ -1350,7 +1350,9 @@ struct StepLaunch {
   unsigned long long* refined = nullptr;  // [batch][8][3] refined-interval words
   unsigned long long* sel_rec = nullptr;  // wide step: tagged ids, then counts
   unsigned long long* cnt_rec = nullptr;
-  unsigned* wide_counters = nullptr;  // two sets of wide_counter_words
+  unsigned* wide_counters = nullptr;  // two sets of wide_counter_words (eager launches),
+                                      // then two for captured ones
+  unsigned* wide_seq = nullptr;       // device: captured wide launches so far
   int wide_counter_words = 0;
   unsigned* wide_launches = nullptr;  // host: wide launches so far (picks the set)
   int* exact_pages = nullptr;         // may be null
@@ -1495,6 +1497,9 @@ dsdk::WideArgs WideStepArgs(const PoolView& v, const StepLaunch& L) {
 void UseWideCounters(dsdk::WideArgs* w, const StepLaunch& L) {
   const unsigned n = *L.wide_launches;
   w->counter_words = L.wide_counter_words;
+  // (a captured launch picks one of the other two sets on the device)
+  w->seq_src = L.wide_seq;
+  w->capture_counters = L.wide_counters + 2 * static_cast<size_t>(L.wide_counter_words);
   w->counters = L.wide_counters + (n & 1u) * static_cast<size_t>(L.wide_counter_words);
   w->next_counters = L.wide_counters + ((n + 1u) & 1u) * static_cast<size_t>(L.wide_counter_words);
 }
@@ -1503,7 +1508,7 @@ void LaunchWideCounted(const PoolView& v, dsdk::WideArgs* w, const StepLaunch& L
                        hipStream_t s) {
   UseWideCounters(w, L);
   dsdk::LaunchWideStep(v, *w, s);
-  ++*L.wide_launches;
+  if (w->a.epoch_src == nullptr) ++*L.wide_launches;
 }
 
 // The whole step: one launch (fused) or score, select and attention.
@@ -1573,6 +1578,7 @@ struct dsd_sparse_ctx {
   // launches).
   DeviceBuffer<unsigned long long> d_sel_rec;
   DeviceBuffer<unsigned> d_wide_counters;
+  DeviceBuffer<unsigned> d_wide_seq;
   mutable unsigned wide_launches = 0;  // host count of wide launches (picks the counter set)
   // The epoch of the step being enqueued: it tags the fused step's
   // publication words and every failure report of the step's kernels.
@@ -1688,7 +1694,8 @@ struct dsd_sparse_ctx {
     L.sel_rec = d_sel_rec.ptr;
     L.cnt_rec = d_sel_rec.ptr + static_cast<size_t>(max_batch) * std::max(1, top_k);
     L.wide_counters = d_wide_counters.ptr;
-    L.wide_counter_words = static_cast<int>(d_wide_counters.count / 2);
+    L.wide_counter_words = static_cast<int>(d_wide_counters.count / 4);
+    L.wide_seq = d_wide_seq.ptr;
     L.wide_launches = &wide_launches;
     L.scores = d_scores.ptr;
     L.selected = d_selected.ptr;
@@ -1837,8 +1844,10 @@ int dsd_sparse_create(dsd_pool* pool, int top_k, int max_batch,
     DSD_HIP_CHECK(hipMemset(ctx->d_epoch.ptr, 0, sizeof(unsigned)));
     ctx->d_sel_rec.Reserve(B * K + B);
     DSD_HIP_CHECK(hipMemset(ctx->d_sel_rec.ptr, 0, (B * K + B) * sizeof(unsigned long long)));
-    ctx->d_wide_counters.Reserve(2 * (B + 1));
-    DSD_HIP_CHECK(hipMemset(ctx->d_wide_counters.ptr, 0, 2 * (B + 1) * sizeof(unsigned)));
+    ctx->d_wide_counters.Reserve(4 * (B + 1));
+    DSD_HIP_CHECK(hipMemset(ctx->d_wide_counters.ptr, 0, 4 * (B + 1) * sizeof(unsigned)));
+    ctx->d_wide_seq.Reserve(1);
+    DSD_HIP_CHECK(hipMemset(ctx->d_wide_seq.ptr, 0, sizeof(unsigned)));
     {
       const size_t rec = 3 * P;
       // The largest fused grid: one head per workgroup.
@@ -2561,7 +2570,6 @@ int dsd_sparse_run_batch_device(dsd_sparse_ctx* ctx, int batch,
             "a pool append is still pending: synchronise before capturing a step");
       }
       L.epoch_src = ctx->d_epoch.ptr;
-      L.wide = false;  // the wide step takes its epoch from the host: three kernels
       ctx->last_stream = nullptr;
     } else {
       ctx->pool->OrderAfterPending(s);

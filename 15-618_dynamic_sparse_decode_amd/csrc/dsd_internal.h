@@ -321,17 +321,22 @@ void LaunchFusedStep(const PoolView& pool, const FusedArgs& args, hipStream_t st
 // attention item per (request, head), taken by workgroups in start order;
 // the last slice of a request to finish selects it.  a: as for
 // LaunchFusedStep (rec: the interval words, 3 per candidate; sel_stride =
-// top_k; no epoch_src).  sel_rec: [batch][sel_stride] tagged selected ids;
-// cnt_rec: [batch] tagged counts; counters: this launch's set, [0] item
-// tickets, [1 .. 1 + batch) arrivals, zero at the launch; next_counters:
-// the other set (counter_words words), which workgroup 0 zeroes for the
-// next launch.  Launches alternate between the two sets.
+// top_k).  sel_rec: [batch][sel_stride] tagged selected ids; cnt_rec:
+// [batch] tagged counts; counters: this launch's set, [0] item tickets,
+// [1 .. 1 + batch) arrivals, zero at the launch; next_counters: the other
+// set (counter_words words), which workgroup 0 zeroes for the next launch.
+// Launches alternate between the two sets.  A launch captured into a graph
+// (a.epoch_src set) takes its epoch there and its set from the parity of
+// *seq_src, one of the two sets at capture_counters; LaunchWideStep then
+// first advances both counters in a one-thread kernel.
 struct WideArgs {
   FusedArgs a;
   unsigned long long* sel_rec = nullptr;
   unsigned long long* cnt_rec = nullptr;
   unsigned* counters = nullptr;
   unsigned* next_counters = nullptr;
+  unsigned* seq_src = nullptr;           // captured launches: the device launch count
+  unsigned* capture_counters = nullptr;  // captured launches: their two sets
   int counter_words = 0;    // words per set, at least batch + 1
   int pages_per_group = 0;  // candidates per score item (a multiple of 8)
   int groups = 0;           // score items per request

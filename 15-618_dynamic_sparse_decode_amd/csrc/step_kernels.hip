@@ -1264,9 +1264,28 @@ __device__ __forceinline__ void WideStepItem(const PoolView& pool, const WideArg
   }
 }
 
+// One thread advances a captured wide step's epoch (as EpochBumpKernel:
+// within [2^30, 2^31)) and its launch count (the parity picks the counter
+// set).
+__global__ void WideBumpKernel(unsigned* epoch, unsigned* seq) {
+  if (threadIdx.x == 0) {
+    *epoch = ((*epoch + 1u) & 0x3FFFFFFFu) | 0x40000000u;
+    *seq = *seq + 1u;
+  }
+}
+
 __global__ __launch_bounds__(kFThreads) void WideStepKernel(PoolView pool, WideArgs w) {
   __shared__ WideShared sh;
-  // (no captured form: the host runs captured steps in three kernels)
+  if (w.a.epoch_src != nullptr) {
+    // Replayed from a captured graph: the epoch and the counter set that
+    // the bump kernel just before this launch advanced.
+    w.a.epoch = *w.a.epoch_src;
+    w.a.wait_tag = w.a.epoch | w.a.wait_mask;
+    w.a.fail.epoch = w.a.epoch;
+    const unsigned n = *w.seq_src;
+    w.counters = w.capture_counters + (n & 1u) * static_cast<size_t>(w.counter_words);
+    w.next_counters = w.capture_counters + ((n + 1u) & 1u) * static_cast<size_t>(w.counter_words);
+  }
   if (blockIdx.x == 0) {
     // Zero the other counter set for the next launch (the launch before
     // this one used it and has finished).
@@ -1454,7 +1473,12 @@ void LaunchWideStep(const PoolView& pool, const WideArgs& w, hipStream_t stream)
     throw std::invalid_argument("wide step scratch missing");
   }
   if (w.a.epoch_src != nullptr) {
-    throw std::invalid_argument("the wide step takes its epoch from the host (not captured)");
+    if (w.seq_src == nullptr || w.capture_counters == nullptr) {
+      throw std::invalid_argument("a captured wide step needs its device launch count");
+    }
+    hipLaunchKernelGGL(WideBumpKernel, dim3(1), dim3(kWave), 0, stream,
+                       const_cast<unsigned*>(w.a.epoch_src), w.seq_src);
+    DSD_HIP_CHECK(hipGetLastError());
   }
   if (w.items != WideStepItems(pool, w.a.batch, w.groups)) {
     throw std::invalid_argument("wide step item count does not match its slices");
@@ -1523,6 +1547,7 @@ void LaunchAttention(const PoolView& pool, const AttentionArgs& args,
 
 void PreloadStepKernels() {
   PreloadKernel(WideStepKernel);
+  PreloadKernel(WideBumpKernel);
   PreloadKernel(AttentionFastKernel<128, kWideAttnLpt, kFWaves, kWideAttnUnroll>);
   PreloadKernel(SelectAttnVariant().fn);
   PreloadKernel(SelectCertifiedKernel);

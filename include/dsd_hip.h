@@ -301,10 +301,12 @@ int dsd_synthetic_batch(int num_heads, int head_dim, int page_size, int batch,
  * previous step's first waits for the previous stream's work, so that
  * stream must still be valid then (it is used for an event record).
  * Graph capture: on a stream that is capturing, the call records the step
- * into the graph.  A captured single-launch step takes its epoch (the tag
- * of the words its workgroups exchange) from a device counter that a
- * one-thread kernel, captured with it, advances on every replay, so each
- * replay reads its own inputs.  The caller orders the graph's replays
+ * into the graph.  A captured single-launch step (fused or wide) takes its
+ * epoch (the tag of the words its workgroups exchange) from a device
+ * counter that a one-thread kernel, captured with it, advances on every
+ * replay, so each replay reads its own inputs; the wide step's item
+ * counters alternate between two sets by a device count the same kernel
+ * advances.  The caller orders the graph's replays
  * against the context's other steps (no event wait is captured), and a
  * pool append must have completed (dsd_pool_* synchronised) before the
  * capture, or the call fails with DSD_ERR_INVALID_ARGUMENT. */

@@ -1,12 +1,15 @@
 """The device step captured into a HIP graph (torch.cuda.CUDAGraph on a side
 stream) and replayed: the context entry point (dsd_sparse_run_batch_device)
 and the allocation-free one (dsd_sparse_run_batch_device_static), for the
-single-launch step and the three-kernel step.
+single-launch step and the three-kernel step.  For 600-page requests the
+context runs the wide single launch (captured too); the static entry runs
+three kernels there.
 
-The fused step's workgroups exchange their score intervals through words
-tagged with the launch's epoch.  A captured launch takes its epoch from a
-device counter that a one-thread kernel, captured with it, advances on
-every replay; with an epoch frozen at capture, a replay would read the
+The fused and wide steps' workgroups exchange their score intervals through
+words tagged with the launch's epoch.  A captured launch takes its epoch from
+a device counter that a one-thread kernel, captured with it, advances on
+every replay (for the wide step the same kernel also advances the count that
+picks which of two item-counter sets the replay uses); with an epoch frozen at capture, a replay would read the
 previous replay's intervals as current.  So the queries change between
 replays (and an eager step on other data runs between two of them), and
 every replay must give, bit for bit, the ids and outputs of an eager step
@@ -32,7 +35,7 @@ def device(a):
 @pytest.mark.parametrize("entry", ["context", "static"])
 @pytest.mark.parametrize("lengths,fused", [
     ([629, 861, 1710, 1002, 1185, 2015], True),       # the single-launch step
-    ([600 * PS, 40, 2100, 16 * PS], False),           # > 512 candidates: three kernels
+    ([600 * PS, 40, 2100, 16 * PS], False),           # > 512 candidates: wide / three kernels
 ])
 def test_graph_replays_follow_new_inputs(gpu, entry, lengths, fused):
     import torch
@@ -88,6 +91,7 @@ def test_graph_replays_follow_new_inputs(gpu, entry, lengths, fused):
         if ctx is not None:
             info = ctx.last_launch()
             assert bool(info["fused"]) == fused, info
+            assert bool(info["wide"]) == (not fused), info
         # the first set against the oracle
         summ = orc.pool_summaries(batch.key_pool, batch.token_counts, E)
         _, want_sel, want_out = orc.sparse_batch(query_sets[0], batch.key_pool, batch.value_pool,
@@ -102,6 +106,9 @@ def test_graph_replays_follow_new_inputs(gpu, entry, lengths, fused):
         with torch.cuda.graph(graph, stream=side):
             step(side.cuda_stream)
         torch.cuda.synchronize()
+        if ctx is not None:
+            info = ctx.last_launch()
+            assert bool(info["fused"]) == fused and bool(info["wide"]) == (not fused), info
         for rep, idx in enumerate([1, 2, 0, 3, 1, 2]):
             q.copy_(torch.from_numpy(query_sets[idx]))
             out.fill_(7.0)
