@@ -427,16 +427,18 @@ def test_midpoint_order_reversed_by_certification(gpu, k):
     (1, 0, 8),     # one head per workgroup: 32 workgroups share the request
     (16, 5, 8),    # two heads: 16 workgroups
     (16, 15, 3),
+    (16, 9, 2),    # two flagged pages
     (40, 0, 8),    # eight heads: 4 workgroups, two flagged pages each
     (64, 63, 8),
 ])
 def test_refinement_shared_by_the_requests_workgroups(gpu, batch, tie_request, near_count):
     """One request of the batch has near_count pages within about 1e-3 of
-    each other at its top-8 boundary; in the single-launch step its
-    workgroups refine the flagged pages between them (page f by workgroup f
-    mod the request's workgroups) and exchange the intervals.  Every
-    request's ids must equal the oracle's, no page may need the exact chain
-    (the refined intervals settle it), and the outputs must be within 1e-4."""
+    each other among its top-8; in the single-launch step its workgroups
+    refine the flagged pages between them (page f by workgroup f mod the
+    request's workgroups) and exchange the intervals.  Every request's ids
+    must equal the oracle's, no page may need the exact chain (the refined
+    intervals settle it), and the outputs must be within 1e-4; the near
+    pages' first-pass intervals must overlap (the step had to refine)."""
     rng = np.random.default_rng(1000 + batch + tie_request)
     H, D, ps, k = 32, 128, 16, 8
     E = H * D
@@ -471,7 +473,12 @@ def test_refinement_shared_by_the_requests_workgroups(gpu, batch, tie_request, n
             info = ctx.last_launch()
             rescored = ctx.exact_rescored_pages()
             ctx.device_status()
+            _, lo, hi = ctx.score_bounds(n_pages)
         assert info["fused"] == 1, info
+        at = {int(p): i for i, p in enumerate(ids)}
+        near = [at[first + j] for j in range(near_count)]
+        assert any(lo[x] <= hi[y] and lo[y] <= hi[x] for x in near for y in near if x != y), \
+            "the near pages' first-pass intervals do not overlap"
         _, selected, outs = orc.sparse_batch(queries, keys, values, summ, counts, offs, ids,
                                              H, D, ps, k)
         for r in range(batch):
