@@ -2,8 +2,8 @@
 stream) and replayed: the context entry point (dsd_sparse_run_batch_device)
 and the allocation-free one (dsd_sparse_run_batch_device_static), for the
 single-launch step and the three-kernel step.  For 600-page requests the
-context runs the wide single launch (captured too); the static entry runs
-three kernels there.
+context runs the wide single launch (captured too), or three kernels when
+created with DSD_WIDE_STEP=0; the static entry runs three kernels there.
 
 The fused and wide steps' workgroups exchange their score intervals through
 words tagged with the launch's epoch.  A captured launch takes its epoch from
@@ -15,6 +15,8 @@ replays (and an eager step on other data runs between two of them), and
 every replay must give, bit for bit, the ids and outputs of an eager step
 on the same queries; the first set is also checked against the oracle."""
 from __future__ import annotations
+
+import os
 
 import numpy as np
 import pytest
@@ -32,7 +34,7 @@ def device(a):
     return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
 
 
-@pytest.mark.parametrize("entry", ["context", "static"])
+@pytest.mark.parametrize("entry", ["context", "context_three", "static"])
 @pytest.mark.parametrize("lengths,fused", [
     ([629, 861, 1710, 1002, 1185, 2015], True),       # the single-launch step
     ([600 * PS, 40, 2100, 16 * PS], False),           # > 512 candidates: wide / three kernels
@@ -57,7 +59,19 @@ def test_graph_replays_follow_new_inputs(gpu, entry, lengths, fused):
         sel = torch.full((B, k), -1, dtype=torch.int32, device="cuda:0")
         cnt = torch.full((B,), -1, dtype=torch.int32, device="cuda:0")
         fail = torch.zeros(1, dtype=torch.int64, device="cuda:0")
-        ctx = gpu.SparseContext(pool, k, B, total, sel_total) if entry == "context" else None
+        ctx = None
+        if entry != "static":
+            # context_three: DSD_WIDE_STEP=0 at the context's creation, so a
+            # wide-shaped step captures the three kernels
+            old = os.environ.get("DSD_WIDE_STEP")
+            os.environ["DSD_WIDE_STEP"] = "0" if entry == "context_three" else "1"
+            try:
+                ctx = gpu.SparseContext(pool, k, B, total, sel_total)
+            finally:
+                if old is None:
+                    del os.environ["DSD_WIDE_STEP"]
+                else:
+                    os.environ["DSD_WIDE_STEP"] = old
 
         def step(stream):
             if ctx is not None:
@@ -88,10 +102,11 @@ def test_graph_replays_follow_new_inputs(gpu, entry, lengths, fused):
             step(main)
             torch.cuda.synchronize()
             eager.append(result())
+        wide = not fused and entry == "context"
         if ctx is not None:
             info = ctx.last_launch()
             assert bool(info["fused"]) == fused, info
-            assert bool(info["wide"]) == (not fused), info
+            assert bool(info["wide"]) == wide, info
         # the first set against the oracle
         summ = orc.pool_summaries(batch.key_pool, batch.token_counts, E)
         _, want_sel, want_out = orc.sparse_batch(query_sets[0], batch.key_pool, batch.value_pool,
@@ -108,7 +123,7 @@ def test_graph_replays_follow_new_inputs(gpu, entry, lengths, fused):
         torch.cuda.synchronize()
         if ctx is not None:
             info = ctx.last_launch()
-            assert bool(info["fused"]) == fused and bool(info["wide"]) == (not fused), info
+            assert bool(info["fused"]) == fused and bool(info["wide"]) == wide, info
         for rep, idx in enumerate([1, 2, 0, 3, 1, 2]):
             q.copy_(torch.from_numpy(query_sets[idx]))
             out.fill_(7.0)
